@@ -1,0 +1,443 @@
+// libgsample C ABI: contexts, scratch, launches and error mapping.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cmath>
+#include <cstdio>
+#include <cstring>
+#include <string>
+#include <vector>
+
+#include "gs_internal.h"
+
+using namespace gs;
+
+struct gs_context {
+  int device = 0;
+  int32_t vocab = 0;
+  int32_t max_rows = 0;
+  int32_t n_chunks = 0;
+  int32_t mask_words = 0;
+  hipStream_t stream = nullptr;
+  ChunkStat* d_stats = nullptr;
+  uint64_t* d_lists = nullptr;
+  ExactQueue* d_queue = nullptr;
+  uint8_t* d_exact = nullptr;
+  int64_t exact_cap = 0;
+  int64_t exact_slot_bytes = 0;
+  int32_t exact_slots = 0;
+  // constraint tables
+  int64_t* d_vocab_offsets = nullptr;
+  uint8_t* d_vocab_bytes = nullptr;
+  std::vector<int64_t> vocab_offsets;
+  std::vector<uint8_t> vocab_bytes;
+  int32_t n_states = 0;
+  int16_t* d_next = nullptr;
+  std::vector<int32_t> next;      // viability folded in
+  std::vector<uint8_t> finals;
+  std::vector<uint8_t> viable;
+  int32_t* d_states = nullptr;
+  int32_t states_cap = 0;
+  int32_t* d_tokens = nullptr;
+  double* d_logprob = nullptr;
+  int32_t tokens_cap = 0;
+  std::string error;
+};
+
+namespace {
+
+// message of the last failure of a call made without a context
+thread_local std::string g_no_context_error = "no context";
+
+int fail(gs_context* ctx, int status, const std::string& msg) {
+  if (ctx) ctx->error = msg;
+  else g_no_context_error = msg;
+  return status;
+}
+
+#define GS_HIP(ctx, expr)                                                                  \
+  do {                                                                                    \
+    hipError_t e_ = (expr);                                                               \
+    if (e_ != hipSuccess) return fail((ctx), GS_ERR_HIP, std::string(#expr ": ") + hipGetErrorString(e_)); \
+  } while (0)
+
+void free_dev(void* p) {
+  if (p) (void)hipFree(p);
+}
+
+hipStream_t pick_stream(gs_context* ctx, void* stream) {
+  return stream ? (hipStream_t)stream : ctx->stream;
+}
+
+bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
+
+}  // namespace
+
+extern "C" {
+
+int gs_abi_version(void) { return GSAMPLE_ABI_VERSION; }
+
+int gs_device_count(int* out) {
+  if (!out) return GS_ERR_INVALID_ARGUMENT;
+  int n = 0;
+  if (hipGetDeviceCount(&n) != hipSuccess) n = 0;
+  *out = n;
+  return GS_OK;
+}
+
+double gs_seeded_random(int64_t seed, uint64_t index) { return gsm::mulberry32_draw(seed, index); }
+
+double gs_js_exp(double x) { return gsm::js_exp(x); }
+double gs_js_log(double x) { return gsm::js_log(x); }
+float gs_softcap(float x, double cap) { return gsm::softcap_f32(x, cap); }
+
+int gs_create(int device, int32_t vocab_size, int32_t max_rows, gs_context** out) {
+  if (!out) return GS_ERR_INVALID_ARGUMENT;
+  *out = nullptr;
+  if (vocab_size <= 0 || max_rows <= 0) return GS_ERR_INVALID_ARGUMENT;
+  int n = 0;
+  if (hipGetDeviceCount(&n) != hipSuccess || n <= 0) return GS_ERR_NO_DEVICE;
+  if (device < 0 || device >= n) return GS_ERR_NO_DEVICE;
+  gs_context* ctx = new gs_context();
+  ctx->device = device;
+  ctx->vocab = vocab_size;
+  ctx->max_rows = max_rows;
+  ctx->n_chunks = (vocab_size + kChunk - 1) / kChunk;
+  ctx->mask_words = (vocab_size + 31) / 32;
+  ctx->exact_cap = 1;
+  while (ctx->exact_cap < vocab_size) ctx->exact_cap <<= 1;
+  ctx->exact_slot_bytes = 36 * ctx->exact_cap;
+  ctx->exact_slots = std::min<int32_t>(max_rows, 64);
+  auto cleanup = [&](int status, const char* what) {
+    gs_destroy(ctx);
+    (void)what;
+    return status;
+  };
+  if (hipSetDevice(device) != hipSuccess) return cleanup(GS_ERR_HIP, "hipSetDevice");
+  if (hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking) != hipSuccess) return cleanup(GS_ERR_HIP, "stream");
+  const size_t stats_bytes = (size_t)max_rows * ctx->n_chunks * sizeof(ChunkStat);
+  const size_t list_bytes = (size_t)max_rows * ctx->n_chunks * kGatherCap * sizeof(uint64_t);
+  const size_t queue_bytes = sizeof(ExactQueue) + (size_t)max_rows * sizeof(uint32_t);
+  if (hipMalloc(&ctx->d_stats, stats_bytes) != hipSuccess) return cleanup(GS_ERR_HIP, "stats");
+  if (hipMalloc(&ctx->d_lists, list_bytes) != hipSuccess) return cleanup(GS_ERR_HIP, "lists");
+  if (hipMalloc(&ctx->d_queue, queue_bytes) != hipSuccess) return cleanup(GS_ERR_HIP, "queue");
+  if (hipMalloc(&ctx->d_exact, (size_t)ctx->exact_slot_bytes * ctx->exact_slots) != hipSuccess)
+    return cleanup(GS_ERR_HIP, "exact scratch");
+  *out = ctx;
+  return GS_OK;
+}
+
+int gs_destroy(gs_context* ctx) {
+  if (!ctx) return GS_OK;
+  (void)hipSetDevice(ctx->device);
+  if (ctx->stream) (void)hipStreamSynchronize(ctx->stream);
+  free_dev(ctx->d_stats);
+  free_dev(ctx->d_lists);
+  free_dev(ctx->d_queue);
+  free_dev(ctx->d_exact);
+  free_dev(ctx->d_vocab_offsets);
+  free_dev(ctx->d_vocab_bytes);
+  free_dev(ctx->d_next);
+  free_dev(ctx->d_states);
+  free_dev(ctx->d_tokens);
+  free_dev(ctx->d_logprob);
+  if (ctx->stream) (void)hipStreamDestroy(ctx->stream);
+  delete ctx;
+  return GS_OK;
+}
+
+const char* gs_last_error(const gs_context* ctx) { return ctx ? ctx->error.c_str() : g_no_context_error.c_str(); }
+
+int gs_synchronize(gs_context* ctx) {
+  if (!ctx) return GS_ERR_INVALID_ARGUMENT;
+  GS_HIP(ctx, hipSetDevice(ctx->device));
+  GS_HIP(ctx, hipStreamSynchronize(ctx->stream));
+  return GS_OK;
+}
+
+void* gs_stream(gs_context* ctx) { return ctx ? (void*)ctx->stream : nullptr; }
+
+// validateDecodingConfig (src/runtime/decoding.ts:31-59) for the fields a row
+// config carries, with the reference's messages joined as
+// resolveGemmaGenerationConfig does (src/runtime/generation-config.ts:65).
+int gs_validate_configs(gs_context* ctx, const gs_row_config* configs, int32_t n) {
+  if (!configs || n < 0) return fail(ctx, GS_ERR_INVALID_ARGUMENT, "configs must be a host array");
+  for (int32_t i = 0; i < n; ++i) {
+    const gs_row_config& c = configs[i];
+    std::vector<std::string> errors;
+    if (!std::isfinite(c.temperature) || c.temperature < 0) errors.push_back("temperature must be >= 0");
+    if (c.top_k < 0) errors.push_back("topK must be a non-negative integer");
+    const double probs[3] = {c.top_p, c.min_p, c.typical_p};
+    const char* names[3] = {"topP", "minP", "typicalP"};
+    for (int k = 0; k < 3; ++k) {
+      if (!std::isfinite(probs[k]) || probs[k] < 0 || probs[k] > 1) errors.push_back(std::string(names[k]) + " must be between 0 and 1");
+    }
+    if (!std::isfinite(c.repetition_penalty) || c.repetition_penalty <= 0) errors.push_back("repetitionPenalty must be > 0");
+    if (c.repetition_window < 0) errors.push_back("repetitionWindow must be a non-negative integer");
+    if (!std::isfinite(c.frequency_penalty) || c.frequency_penalty < 0) errors.push_back("frequencyPenalty must be finite and non-negative");
+    if (!std::isfinite(c.presence_penalty) || c.presence_penalty < 0) errors.push_back("presencePenalty must be finite and non-negative");
+    if (!errors.empty()) {
+      std::string msg = "Invalid Gemma decoding config: ";
+      for (size_t k = 0; k < errors.size(); ++k) msg += (k ? "; " : "") + errors[k];
+      return fail(ctx, GS_ERR_INVALID_CONFIG, msg);
+    }
+    if (c.rng_mode == GS_RNG_SEEDED && c.draw_index > gsm::mulberry32_index_limit(c.seed)) {
+      return fail(ctx, GS_ERR_UNSUPPORTED, "draw_index is beyond the exactly representable SeededRandom state");
+    }
+  }
+  return GS_OK;
+}
+
+int gs_sample(gs_context* ctx, const gs_batch* b, void* stream) {
+  if (!ctx || !b) return fail(ctx, GS_ERR_INVALID_ARGUMENT, "null context or batch");
+  if (b->rows == 0) return GS_OK;
+  if (b->rows < 0 || b->rows > ctx->max_rows) return fail(ctx, GS_ERR_INVALID_ARGUMENT, "rows outside [0, max_rows]");
+  if (!b->logits || !b->configs || !b->results) return fail(ctx, GS_ERR_INVALID_ARGUMENT, "logits, configs and results are required");
+  if (b->dtype != GS_F32 && b->dtype != GS_BF16) return fail(ctx, GS_ERR_INVALID_ARGUMENT, "dtype must be f32 or bf16");
+  if (b->row_stride < ctx->vocab) return fail(ctx, GS_ERR_INVALID_ARGUMENT, "row_stride is smaller than the vocab");
+  if (b->history_offsets && !b->history_ids) return fail(ctx, GS_ERR_INVALID_ARGUMENT, "history_ids missing");
+  if (b->forced_offsets && (!b->forced_ids || !b->forced_kinds)) return fail(ctx, GS_ERR_INVALID_ARGUMENT, "forced ids missing");
+  if (b->mask_slots > 0 && !b->mask_table) return fail(ctx, GS_ERR_INVALID_ARGUMENT, "mask_table missing");
+  GS_HIP(ctx, hipSetDevice(ctx->device));
+  hipStream_t s = pick_stream(ctx, stream);
+  const size_t esize = b->dtype == GS_BF16 ? 2 : 4;
+  SampleArgs a{};
+  a.logits = b->logits;
+  a.row_stride = b->row_stride;
+  a.dtype = b->dtype;
+  a.rows = b->rows;
+  a.vocab = ctx->vocab;
+  a.n_chunks = ctx->n_chunks;
+  a.vector_ok = aligned16(b->logits) && ((b->row_stride * esize) % 16 == 0);
+  a.mask_words = ctx->mask_words;
+  a.configs = b->configs;
+  a.history_offsets = b->history_offsets;
+  a.history_ids = b->history_ids;
+  a.forced_offsets = b->forced_offsets;
+  a.forced_ids = b->forced_ids;
+  a.forced_kinds = b->forced_kinds;
+  a.mask_table = b->mask_table;
+  a.mask_slots = b->mask_table ? b->mask_slots : 0;
+  a.exact_slots = ctx->exact_slots;
+  a.results = b->results;
+  a.stats = ctx->d_stats;
+  a.lists = ctx->d_lists;
+  a.queue = ctx->d_queue;
+  a.exact_scratch = ctx->d_exact;
+  a.exact_slot_bytes = ctx->exact_slot_bytes;
+  a.exact_capacity = ctx->exact_cap;
+  GS_HIP(ctx, hipMemsetAsync(ctx->d_queue, 0, 2 * sizeof(uint32_t), s));
+  launch_scan(a, s);
+  GS_HIP(ctx, hipGetLastError());
+  launch_finish(a, s);
+  GS_HIP(ctx, hipGetLastError());
+  launch_exact(a, s);
+  GS_HIP(ctx, hipGetLastError());
+  return GS_OK;
+}
+
+int gs_sample_sync(gs_context* ctx, const gs_batch* b, gs_row_result* host_out) {
+  int st = gs_sample(ctx, b, nullptr);
+  if (st != GS_OK) return st;
+  std::vector<gs_row_result> tmp;
+  gs_row_result* dst = host_out;
+  if (!dst) {
+    tmp.resize(b->rows);
+    dst = tmp.data();
+  }
+  GS_HIP(ctx, hipMemcpyAsync(dst, b->results, sizeof(gs_row_result) * b->rows, hipMemcpyDeviceToHost, ctx->stream));
+  GS_HIP(ctx, hipStreamSynchronize(ctx->stream));
+  for (int32_t r = 0; r < b->rows; ++r) {
+    const uint32_t f = dst[r].flags;
+    if (f & GS_FLAG_DEAD_END) return fail(ctx, GS_ERR_DEAD_END, "Generation constraint reached a tokenization dead end");
+    if (f & GS_FLAG_EMPTY_CANDIDATES)
+      return fail(ctx, GS_ERR_EMPTY_CANDIDATES, "min-p left no candidate token (row " + std::to_string(r) + ")");
+    if (f & GS_FLAG_UNSUPPORTED)
+      return fail(ctx, GS_ERR_UNSUPPORTED, "row " + std::to_string(r) + ": more than 2048 distinct penalty-window and forced ids");
+  }
+  return GS_OK;
+}
+
+int gs_token_log_prob(gs_context* ctx, const void* logits, int32_t dtype, int32_t rows, int64_t row_stride,
+                      const int32_t* tokens, double* out, void* stream) {
+  if (!ctx || !logits || !tokens || !out || rows < 0) return fail(ctx, GS_ERR_INVALID_ARGUMENT, "bad arguments");
+  if (dtype != GS_F32 && dtype != GS_BF16) return fail(ctx, GS_ERR_INVALID_ARGUMENT, "dtype must be f32 or bf16");
+  if (row_stride < ctx->vocab) return fail(ctx, GS_ERR_INVALID_ARGUMENT, "row_stride is smaller than the vocab");
+  if (rows == 0) return GS_OK;
+  GS_HIP(ctx, hipSetDevice(ctx->device));
+  launch_logprob(logits, dtype, rows, row_stride, ctx->vocab, tokens, out, pick_stream(ctx, stream));
+  GS_HIP(ctx, hipGetLastError());
+  return GS_OK;
+}
+
+// Host convenience: tokenLogProbability with host buffers and the reference's range error.
+int gs_token_log_prob_host(gs_context* ctx, const float* logits, int32_t rows, const int32_t* tokens, double* out) {
+  if (!ctx || !logits || !tokens || !out || rows < 0) return fail(ctx, GS_ERR_INVALID_ARGUMENT, "bad arguments");
+  for (int32_t r = 0; r < rows; ++r) {
+    if (tokens[r] < 0 || tokens[r] >= ctx->vocab) {
+      return fail(ctx, GS_ERR_TOKEN_RANGE,
+                  "Token " + std::to_string(tokens[r]) + " is outside logits length " + std::to_string(ctx->vocab));
+    }
+  }
+  if (rows == 0) return GS_OK;
+  GS_HIP(ctx, hipSetDevice(ctx->device));
+  float* d_logits = nullptr;
+  GS_HIP(ctx, hipMalloc(&d_logits, sizeof(float) * (size_t)rows * ctx->vocab));
+  if (rows > ctx->tokens_cap) {
+    free_dev(ctx->d_tokens);
+    free_dev(ctx->d_logprob);
+    ctx->d_tokens = nullptr;
+    ctx->d_logprob = nullptr;
+    GS_HIP(ctx, hipMalloc(&ctx->d_tokens, sizeof(int32_t) * rows));
+    GS_HIP(ctx, hipMalloc(&ctx->d_logprob, sizeof(double) * rows));
+    ctx->tokens_cap = rows;
+  }
+  int st = GS_OK;
+  if (hipMemcpyAsync(d_logits, logits, sizeof(float) * (size_t)rows * ctx->vocab, hipMemcpyHostToDevice, ctx->stream) !=
+          hipSuccess ||
+      hipMemcpyAsync(ctx->d_tokens, tokens, sizeof(int32_t) * rows, hipMemcpyHostToDevice, ctx->stream) != hipSuccess) {
+    st = fail(ctx, GS_ERR_HIP, "copy to device failed");
+  } else {
+    launch_logprob(d_logits, GS_F32, rows, ctx->vocab, ctx->vocab, ctx->d_tokens, ctx->d_logprob, ctx->stream);
+    if (hipGetLastError() != hipSuccess ||
+        hipMemcpyAsync(out, ctx->d_logprob, sizeof(double) * rows, hipMemcpyDeviceToHost, ctx->stream) != hipSuccess ||
+        hipStreamSynchronize(ctx->stream) != hipSuccess) {
+      st = fail(ctx, GS_ERR_HIP, "log-probability kernel failed");
+    }
+  }
+  (void)hipStreamSynchronize(ctx->stream);
+  free_dev(d_logits);
+  return st;
+}
+
+int gs_set_vocab(gs_context* ctx, const int64_t* offsets, const uint8_t* bytes, int64_t n_bytes) {
+  if (!ctx || !offsets || (n_bytes > 0 && !bytes) || n_bytes < 0) return fail(ctx, GS_ERR_INVALID_ARGUMENT, "bad vocab");
+  const int64_t V = ctx->vocab;
+  if (offsets[0] != 0 || offsets[V] != n_bytes) return fail(ctx, GS_ERR_INVALID_ARGUMENT, "offsets must run 0..n_bytes");
+  for (int64_t t = 0; t < V; ++t) {
+    if (offsets[t + 1] < offsets[t]) return fail(ctx, GS_ERR_INVALID_ARGUMENT, "offsets must be non-decreasing");
+  }
+  GS_HIP(ctx, hipSetDevice(ctx->device));
+  ctx->vocab_offsets.assign(offsets, offsets + V + 1);
+  ctx->vocab_bytes.assign(bytes, bytes + n_bytes);
+  free_dev(ctx->d_vocab_offsets);
+  free_dev(ctx->d_vocab_bytes);
+  ctx->d_vocab_offsets = nullptr;
+  ctx->d_vocab_bytes = nullptr;
+  GS_HIP(ctx, hipMalloc(&ctx->d_vocab_offsets, sizeof(int64_t) * (V + 1)));
+  GS_HIP(ctx, hipMalloc(&ctx->d_vocab_bytes, std::max<int64_t>(n_bytes, 16)));
+  GS_HIP(ctx, hipMemcpy(ctx->d_vocab_offsets, offsets, sizeof(int64_t) * (V + 1), hipMemcpyHostToDevice));
+  if (n_bytes) GS_HIP(ctx, hipMemcpy(ctx->d_vocab_bytes, bytes, n_bytes, hipMemcpyHostToDevice));
+  return GS_OK;
+}
+
+int gs_set_dfa(gs_context* ctx, int32_t n_states, const int32_t* next, const uint8_t* finals) {
+  if (!ctx || n_states <= 0 || n_states > 32767 || !next || !finals)
+    return fail(ctx, GS_ERR_INVALID_ARGUMENT, "DFA needs 1..32767 states, a next table and finals");
+  for (int64_t i = 0; i < (int64_t)n_states * 256; ++i) {
+    if (next[i] < -1 || next[i] >= n_states) return fail(ctx, GS_ERR_INVALID_ARGUMENT, "next-state out of range");
+  }
+  // findViableStates (constraints.ts:300-322): reverse reachability from finals
+  std::vector<std::vector<int32_t>> preds(n_states);
+  for (int32_t s = 0; s < n_states; ++s)
+    for (int c = 0; c < 256; ++c)
+      if (next[(int64_t)s * 256 + c] >= 0) preds[next[(int64_t)s * 256 + c]].push_back(s);
+  std::vector<uint8_t> viable(n_states, 0);
+  std::vector<int32_t> stack;
+  for (int32_t s = 0; s < n_states; ++s)
+    if (finals[s]) { viable[s] = 1; stack.push_back(s); }
+  while (!stack.empty()) {
+    const int32_t t = stack.back();
+    stack.pop_back();
+    for (int32_t p : preds[t])
+      if (!viable[p]) { viable[p] = 1; stack.push_back(p); }
+  }
+  std::vector<int16_t> folded((size_t)n_states * 256);
+  ctx->next.assign(next, next + (size_t)n_states * 256);
+  for (size_t i = 0; i < folded.size(); ++i) {
+    const int32_t t = next[i];
+    folded[i] = (int16_t)((t >= 0 && viable[t]) ? t : -1);
+  }
+  GS_HIP(ctx, hipSetDevice(ctx->device));
+  free_dev(ctx->d_next);
+  ctx->d_next = nullptr;
+  GS_HIP(ctx, hipMalloc(&ctx->d_next, folded.size() * sizeof(int16_t)));
+  GS_HIP(ctx, hipMemcpy(ctx->d_next, folded.data(), folded.size() * sizeof(int16_t), hipMemcpyHostToDevice));
+  ctx->n_states = n_states;
+  ctx->finals.assign(finals, finals + n_states);
+  ctx->viable = viable;
+  return GS_OK;
+}
+
+int gs_build_masks(gs_context* ctx, const int32_t* states, int32_t n, uint32_t* mask_table, void* stream) {
+  if (!ctx || (n > 0 && (!states || !mask_table)) || n < 0) return fail(ctx, GS_ERR_INVALID_ARGUMENT, "bad arguments");
+  if (!ctx->d_next || !ctx->d_vocab_offsets) return fail(ctx, GS_ERR_INVALID_ARGUMENT, "set the vocab and the DFA first");
+  for (int32_t i = 0; i < n; ++i) {
+    if (states[i] < 0 || states[i] >= ctx->n_states) return fail(ctx, GS_ERR_INVALID_ARGUMENT, "state out of range");
+  }
+  if (n == 0) return GS_OK;
+  GS_HIP(ctx, hipSetDevice(ctx->device));
+  hipStream_t s = pick_stream(ctx, stream);
+  if (n > ctx->states_cap) {
+    GS_HIP(ctx, hipStreamSynchronize(s));
+    free_dev(ctx->d_states);
+    ctx->d_states = nullptr;
+    GS_HIP(ctx, hipMalloc(&ctx->d_states, sizeof(int32_t) * n));
+    ctx->states_cap = n;
+  }
+  GS_HIP(ctx, hipMemcpyAsync(ctx->d_states, states, sizeof(int32_t) * n, hipMemcpyHostToDevice, s));
+  launch_masks(ctx->d_vocab_offsets, ctx->d_vocab_bytes, ctx->vocab, ctx->d_next, ctx->d_states, n, mask_table,
+               ctx->mask_words, ctx->n_states, s);
+  GS_HIP(ctx, hipGetLastError());
+  GS_HIP(ctx, hipStreamSynchronize(s));  // the state list is reused by the next call
+  return GS_OK;
+}
+
+int gs_dfa_advance(gs_context* ctx, const int32_t* states_in, const int32_t* tokens, int32_t n, int32_t* states_out) {
+  if (!ctx || n < 0 || (n > 0 && (!states_in || !tokens || !states_out))) return fail(ctx, GS_ERR_INVALID_ARGUMENT, "bad arguments");
+  if (ctx->next.empty() || ctx->vocab_offsets.empty()) return fail(ctx, GS_ERR_INVALID_ARGUMENT, "set the vocab and the DFA first");
+  for (int32_t i = 0; i < n; ++i) {
+    int32_t s = states_in[i];
+    const int32_t t = tokens[i];
+    if (s < 0 || s >= ctx->n_states || t < 0 || t >= ctx->vocab)
+      return fail(ctx, GS_ERR_INVALID_ARGUMENT, "state or token out of range");
+    for (int64_t k = ctx->vocab_offsets[t]; k < ctx->vocab_offsets[t + 1]; ++k) {
+      s = ctx->next[(size_t)s * 256 + ctx->vocab_bytes[k]];
+      if (s < 0 || !ctx->viable[s]) return fail(ctx, GS_ERR_CONSTRAINT_VIOLATION, "Selected token violates the generation constraint");
+    }
+    states_out[i] = s;
+  }
+  return GS_OK;
+}
+
+int gs_dfa_accepting(gs_context* ctx, int32_t state, int32_t* out) {
+  if (!ctx || !out || state < 0 || state >= ctx->n_states) return fail(ctx, GS_ERR_INVALID_ARGUMENT, "bad state");
+  *out = ctx->finals[state] ? 1 : 0;
+  return GS_OK;
+}
+
+int gs_lmhead(gs_context* ctx, const void* hidden, const void* weight, int32_t m_rows, int32_t width, float softcap,
+              float* logits, void* stream) {
+  if (!ctx || !hidden || !weight || !logits || m_rows <= 0 || width <= 0) return fail(ctx, GS_ERR_INVALID_ARGUMENT, "bad arguments");
+  if (width % 64 != 0) return fail(ctx, GS_ERR_UNSUPPORTED, "lm_head width must be a multiple of 64");
+  if (!aligned16(hidden) || !aligned16(weight)) return fail(ctx, GS_ERR_INVALID_ARGUMENT, "hidden and weight must be 16-byte aligned");
+  GS_HIP(ctx, hipSetDevice(ctx->device));
+  launch_lmhead((const uint16_t*)hidden, (const uint16_t*)weight, m_rows, width, ctx->vocab, softcap, logits,
+                pick_stream(ctx, stream));
+  GS_HIP(ctx, hipGetLastError());
+  return GS_OK;
+}
+
+int gs_lmhead_sample(gs_context* ctx, const void* hidden, const void* weight, int32_t width, float softcap,
+                     float* logits_scratch, const gs_batch* batch, void* stream) {
+  if (!batch) return fail(ctx, GS_ERR_INVALID_ARGUMENT, "null batch");
+  int st = gs_lmhead(ctx, hidden, weight, batch->rows, width, softcap, logits_scratch, stream);
+  if (st != GS_OK) return st;
+  gs_batch b = *batch;
+  b.logits = logits_scratch;
+  b.dtype = GS_F32;
+  b.row_stride = ctx->vocab;
+  return gs_sample(ctx, &b, stream);
+}
+
+}  // extern "C"

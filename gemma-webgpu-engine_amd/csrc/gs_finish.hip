@@ -1,0 +1,513 @@
+// Row finish: the per-row half of the batched sampler (one 1024-thread
+// workgroup per row, after the chunk scan).
+//
+// It rebuilds, for one row, exactly the part of the reference's sorted
+// candidate list that the filters can reach (src/runtime/sampling.ts:33-64):
+//   1. merges the chunk maxima and partial sums into the softmax normaliser;
+//   2. evaluates the row's distinct special ids exactly: penalty-window ids
+//      with their counts (sampling.ts:21-30) and, for constrained rows, the
+//      termination / extra ids of selectConstrainedToken
+//      (src/runtime/gemma-session.ts:1305-1329);
+//   3. keeps the chunk-list entries whose key is at or above the highest
+//      truncated chunk's threshold -- the region where the union of the
+//      lists is complete -- sorts them by (value desc, id asc) and merges in
+//      the specials of that region;
+//   4. applies top-k, min-p and top-p and draws, with the reference's
+//      comparisons, on binary64 probabilities from the bit-exact js_exp.
+// The normaliser is summed in a different order from the reference's
+// sequential loop, so every comparison that decides the outcome is checked
+// against a 1e-10 relative margin; rows that fail a margin, need candidates
+// outside the complete region, or hold non-finite logits are queued for the
+// exact kernel, which replays the reference step by step.
+#include "gs_internal.h"
+
+namespace gs {
+namespace {
+
+constexpr int kWaves = kFinishThreads / 64;
+
+__device__ __forceinline__ double block_scan_f64(double v, double* s_w, double* total) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const double incl = wave_scan_f64(v, lane);
+  if (lane == 63) s_w[wave] = incl;
+  __syncthreads();
+  double off = 0.0, tot = 0.0;
+  for (int w = 0; w < kWaves; ++w) {
+    const double x = s_w[w];
+    if (w < wave) off += x;
+    tot += x;
+  }
+  __syncthreads();
+  *total = tot;
+  return incl + off;
+}
+
+__device__ void block_sort_desc(uint64_t* s, int n) {
+  for (int k = 2; k <= n; k <<= 1) {
+    for (int j = k >> 1; j > 0; j >>= 1) {
+      for (int i = threadIdx.x; i < n; i += kFinishThreads) {
+        const int p = i ^ j;
+        if (p > i) {
+          const uint64_t x = s[i], y = s[p];
+          const bool desc = (i & k) == 0;
+          if (desc ? (x < y) : (x > y)) { s[i] = y; s[p] = x; }
+        }
+      }
+      __syncthreads();
+    }
+  }
+}
+
+// (value key desc, id asc) on parallel arrays
+__device__ __forceinline__ bool ranks_before(uint64_t ka, uint32_t ia, uint64_t kb, uint32_t ib) {
+  return ka > kb || (ka == kb && ia < ib);
+}
+
+__device__ void block_sort_pairs_desc(uint64_t* key, uint32_t* id, int n) {
+  for (int k = 2; k <= n; k <<= 1) {
+    for (int j = k >> 1; j > 0; j >>= 1) {
+      for (int i = threadIdx.x; i < n; i += kFinishThreads) {
+        const int p = i ^ j;
+        if (p > i) {
+          const bool desc = (i & k) == 0;
+          const bool swap = desc ? ranks_before(key[p], id[p], key[i], id[i])
+                                 : ranks_before(key[i], id[i], key[p], id[p]);
+          if (swap) {
+            const uint64_t tk = key[i]; key[i] = key[p]; key[p] = tk;
+            const uint32_t ti = id[i]; id[i] = id[p]; id[p] = ti;
+          }
+        }
+      }
+      __syncthreads();
+    }
+  }
+}
+
+__device__ __forceinline__ int pow2_at_least(int n) {
+  int p = 1;
+  while (p < n) p <<= 1;
+  return p;
+}
+
+struct Shared {
+  uint64_t sorted[kFinishCap];        // non-special entries of the complete region
+  uint32_t hash_ids[kHashSize];
+  uint32_t hash_counts[kHashSize];
+  uint64_t sp_key[kSpecialCap];       // specials: f64 key of their value
+  uint32_t sp_id[kSpecialCap];
+  double cand_p[kFinishCap];          // merged candidates: probability
+  uint32_t cand_id[kFinishCap];
+  double wsum[kWaves];
+  double wtmp[kWaves];
+  double total;
+  double vmax;
+  uint32_t flags;
+  uint32_t max_key;
+  uint32_t thr_max;
+  uint32_t any_truncated;
+  uint32_t n_sorted;
+  uint32_t n_special;
+  uint32_t n_sp_in;
+  uint32_t n_cand;
+  uint32_t route_exact;
+  uint32_t status_flags;
+  uint32_t first_idx;
+  uint32_t legal_bits;
+  uint32_t special_legal;
+  uint64_t best_entry;
+};
+
+__device__ void enqueue_exact(const SampleArgs& a, int64_t row, uint32_t flags) {
+  const uint32_t q = atomicAdd(&a.queue->count, 1u);
+  a.queue->rows[q] = (uint32_t)row;
+  a.results[row].flags = flags;
+}
+
+__global__ __launch_bounds__(kFinishThreads) void finish_kernel(SampleArgs a) {
+  __shared__ Shared S;
+  const int tid = threadIdx.x;
+  const int64_t row = blockIdx.x;
+  const gs_row_config cfg = a.configs[row];
+  const Plan plan = plan_row(cfg);
+  if (plan.route == kRouteExact) {
+    if (tid == 0) enqueue_exact(a, row, 0u);
+    return;
+  }
+  const bool greedy = plan.route == kRouteGreedy;
+  const int32_t slot = cfg.mask_slot;
+  const bool constrained = slot >= 0 && slot < a.mask_slots;
+  const double T = cfg.temperature;
+
+  if (tid == 0) {
+    S.flags = 0; S.max_key = 0; S.thr_max = 0; S.any_truncated = 0; S.n_sorted = 0; S.n_special = 0;
+    S.n_sp_in = 0; S.route_exact = 0; S.status_flags = 0; S.first_idx = 0xFFFFFFFFu; S.legal_bits = 0;
+    S.special_legal = 0; S.best_entry = 0;
+  }
+  for (int h = tid; h < kHashSize; h += kFinishThreads) { S.hash_ids[h] = 0xFFFFFFFFu; S.hash_counts[h] = 0; }
+  __syncthreads();
+
+  // ---- 1. chunk statistics
+  const ChunkStat* st = a.stats + row * a.n_chunks;
+  for (int c = tid; c < a.n_chunks; c += kFinishThreads) {
+    const ChunkStat s = st[c];
+    atomicOr(&S.flags, s.flags);
+    atomicMax(&S.max_key, s.max_key);
+    if (s.truncated) { atomicMax(&S.thr_max, s.threshold); atomicOr(&S.any_truncated, 1u); }
+  }
+  // ---- 2. distinct special ids
+  {
+    int64_t w0, w1;
+    history_window(a, row, cfg, &w0, &w1);
+    SpecialTable tab{S.hash_ids, S.hash_counts};
+    for (int64_t j = w0 + tid; j < w1; j += kFinishThreads) {
+      const int32_t id = a.history_ids[j];
+      if (id >= 0 && id < a.vocab) special_insert(tab, (uint32_t)id, 0u);
+    }
+    if (constrained && a.forced_offsets) {
+      const int64_t f0 = a.forced_offsets[row], f1 = a.forced_offsets[row + 1];
+      for (int64_t j = f0 + tid; j < f1; j += kFinishThreads) {
+        const int32_t id = a.forced_ids[j];
+        if (id >= 0 && id < a.vocab) special_insert(tab, (uint32_t)id, (uint32_t)a.forced_kinds[j] & 3u);
+      }
+    }
+  }
+  __syncthreads();
+  if (S.flags & kChunkNonFinite) {
+    if (tid == 0) enqueue_exact(a, row, GS_FLAG_NONFINITE);
+    return;
+  }
+  if (!greedy && (S.flags & kChunkOverflow)) {
+    if (tid == 0) enqueue_exact(a, row, 0u);
+    return;
+  }
+  // evaluate every special exactly: mask / termination rules, then penalties
+  for (int h = tid; h < kHashSize; h += kFinishThreads) {
+    const uint32_t id = S.hash_ids[h];
+    if (id == 0xFFFFFFFFu) continue;
+    const uint32_t packed = S.hash_counts[h];
+    const uint32_t count = packed & 0xFFFFFFu, kinds = packed >> 24;
+    const uint32_t idx = atomicAdd(&S.n_special, 1u);
+    if (idx >= (uint32_t)kSpecialCap) continue;
+    float raw = load_logit(a, row, id);
+    if (cfg.softcap > 0) raw = gsm::softcap_f32(raw, cfg.softcap);
+    bool allowed = true;
+    if (constrained) {
+      const bool term = kinds & GS_FORCED_TERMINATION;
+      const bool extra = kinds & GS_FORCED_EXTRA;
+      allowed = term ? cfg.accepting != 0 : (extra || mask_allows(a, slot, id));
+    }
+    if (allowed) atomicOr(&S.special_legal, 1u);
+    if (allowed && !(raw < __builtin_inff())) atomicOr(&S.flags, kChunkNonFinite);
+    double x = allowed ? (double)raw : -__builtin_inf();
+    if (count > 0) {
+      x = x < 0 ? x * cfg.repetition_penalty : x / cfg.repetition_penalty;
+      x -= cfg.presence_penalty + (double)count * cfg.frequency_penalty;
+    }
+    const double v = greedy ? x : x / T;
+    S.sp_key[idx] = f64_key(v);
+    S.sp_id[idx] = id;
+  }
+  __syncthreads();
+  if (S.n_special > (uint32_t)kSpecialCap) {
+    if (tid == 0) {
+      a.results[row].token = -1;
+      a.results[row].flags = GS_FLAG_UNSUPPORTED;
+      a.results[row].probability = 0.0;
+    }
+    return;
+  }
+  if (S.flags & kChunkNonFinite) {
+    if (tid == 0) enqueue_exact(a, row, GS_FLAG_NONFINITE);
+    return;
+  }
+  const int n_sp = (int)S.n_special;
+
+  // ---- constrained dead end: no legal id at all (gemma-session.ts:1322-1326)
+  if (constrained && S.max_key <= kKeyNegInf && !S.special_legal) {
+    // a non-special id is legal iff its mask bit is set; count those bits
+    const uint32_t* m = a.mask_table + (int64_t)slot * a.mask_words;
+    uint32_t bits = 0;
+    for (int w = tid; w < a.mask_words; w += kFinishThreads) bits |= m[w];
+    if (bits) atomicOr(&S.legal_bits, 1u);
+    __syncthreads();
+    const uint32_t any_bits = S.legal_bits;
+    __syncthreads();
+    // specials' own mask bits may be the only set bits: those ids are not legal
+    // (termination) or were evaluated above; count non-special legal bits exactly
+    if (any_bits) {
+      if (tid == 0) S.legal_bits = 0;
+      __syncthreads();
+      for (int w = tid; w < a.mask_words; w += kFinishThreads) {
+        uint32_t word = m[w];
+        for (int i = 0; i < n_sp; ++i) {
+          const uint32_t id = S.sp_id[i];
+          if ((int)(id >> 5) == w) word &= ~(1u << (id & 31));
+        }
+        if (word) atomicOr(&S.legal_bits, 1u);
+      }
+      __syncthreads();
+    }
+    if (!S.legal_bits) {
+      if (tid == 0) {
+        a.results[row].token = -1;
+        a.results[row].flags = GS_FLAG_DEAD_END;
+        a.results[row].probability = 0.0;
+      }
+      return;
+    }
+  }
+
+  // ---- greedy: first maximum of the penalised logits (sampling.ts:31,92-96)
+  if (greedy) {
+    const uint64_t* lists = a.lists + row * a.n_chunks * kGatherCap;
+    for (int c = tid; c < a.n_chunks; c += kFinishThreads) {
+      if (st[c].n_list) atomicMax((unsigned long long*)&S.best_entry, (unsigned long long)lists[(int64_t)c * kGatherCap]);
+    }
+    __syncthreads();
+    if (tid == 0) {
+      // best special by (value desc, id asc)
+      int bs = -1;
+      for (int i = 0; i < n_sp; ++i) {
+        if (bs < 0 || ranks_before(S.sp_key[i], S.sp_id[i], S.sp_key[bs], S.sp_id[bs])) bs = i;
+      }
+      int32_t token;
+      if (S.best_entry == 0) {
+        token = bs >= 0 ? (int32_t)S.sp_id[bs] : 0;
+      } else {
+        const uint32_t nid = entry_id(S.best_entry);
+        const uint64_t nkey = f64_key((double)key_f32(entry_key(S.best_entry)));
+        token = (bs >= 0 && ranks_before(S.sp_key[bs], S.sp_id[bs], nkey, nid)) ? (int32_t)S.sp_id[bs]
+                                                                                 : (int32_t)nid;
+      }
+      a.results[row].token = token;
+      a.results[row].flags = GS_FLAG_GREEDY;
+      a.results[row].probability = 1.0;
+    }
+    return;
+  }
+
+  // ---- 3. the complete region of the chunk lists
+  const uint32_t thr = S.thr_max;  // 0 when no chunk was truncated: every finite logit is listed
+  {
+    const uint64_t* lists = a.lists + row * a.n_chunks * kGatherCap;
+    for (int c = 0; c < a.n_chunks; ++c) {
+      const uint32_t n = st[c].n_list;
+      for (uint32_t i = tid; i < n; i += kFinishThreads) {
+        const uint64_t e = lists[(int64_t)c * kGatherCap + i];
+        if (entry_key(e) >= thr) {
+          const uint32_t p = atomicAdd(&S.n_sorted, 1u);
+          if (p < (uint32_t)kFinishCap) S.sorted[p] = e;
+        }
+      }
+    }
+  }
+  __syncthreads();
+  if (S.n_sorted > (uint32_t)kFinishCap) {
+    if (tid == 0) enqueue_exact(a, row, 0u);
+    return;
+  }
+  const int n_ns = (int)S.n_sorted;
+  {
+    const int n2 = pow2_at_least(n_ns);
+    for (int i = n_ns + tid; i < n2; i += kFinishThreads) S.sorted[i] = 0;
+    __syncthreads();
+    block_sort_desc(S.sorted, n2);
+    const int m2 = pow2_at_least(n_sp);
+    for (int i = n_sp + tid; i < m2; i += kFinishThreads) { S.sp_key[i] = 0; S.sp_id[i] = 0xFFFFFFFFu; }
+    __syncthreads();
+    block_sort_pairs_desc(S.sp_key, S.sp_id, m2);
+  }
+  // specials inside the complete region: value >= value of the threshold key
+  const uint64_t region_floor = thr ? f64_key((double)key_f32(thr) / T) : 0;
+  for (int i = tid; i < n_sp; i += kFinishThreads) {
+    if (S.sp_key[i] >= region_floor) atomicAdd(&S.n_sp_in, 1u);
+  }
+  __syncthreads();
+  const int n_sp_in = (int)S.n_sp_in;  // specials are sorted, so these are the first n_sp_in
+  const int n_cand = n_ns + n_sp_in;
+  if (n_cand > kFinishCap || n_cand == 0) {
+    if (tid == 0) enqueue_exact(a, row, 0u);
+    return;
+  }
+
+  // ---- merge by rank into (probability, id); value first, probability below
+  // the maximum value is the first entry of either list
+  if (tid == 0) {
+    double v0 = -__builtin_inf();
+    if (n_ns) v0 = (double)key_f32(entry_key(S.sorted[0])) / T;
+    if (n_sp && key_f64(S.sp_key[0]) > v0) v0 = key_f64(S.sp_key[0]);
+    S.vmax = v0;
+  }
+  for (int i = tid; i < n_ns; i += kFinishThreads) {
+    const uint64_t e = S.sorted[i];
+    const uint32_t id = entry_id(e);
+    const uint64_t k = f64_key((double)key_f32(entry_key(e)) / T);
+    int lo = 0, hi = n_sp_in;  // specials ranked before this entry
+    while (lo < hi) {
+      const int mid = (lo + hi) >> 1;
+      if (ranks_before(S.sp_key[mid], S.sp_id[mid], k, id)) lo = mid + 1; else hi = mid;
+    }
+    S.cand_p[i + lo] = key_f64(k);
+    S.cand_id[i + lo] = id;
+  }
+  for (int j = tid; j < n_sp_in; j += kFinishThreads) {
+    const uint64_t k = S.sp_key[j];
+    const uint32_t id = S.sp_id[j];
+    int lo = 0, hi = n_ns;  // non-specials ranked before this special
+    while (lo < hi) {
+      const int mid = (lo + hi) >> 1;
+      const uint64_t e = S.sorted[mid];
+      const uint64_t ek = f64_key((double)key_f32(entry_key(e)) / T);
+      if (ranks_before(ek, entry_id(e), k, id)) lo = mid + 1; else hi = mid;
+    }
+    S.cand_p[j + lo] = key_f64(k);
+    S.cand_id[j + lo] = id;
+  }
+  __syncthreads();
+  const double M = S.vmax;
+  if (!(M > -__builtin_inf())) {
+    // every logit is -inf: the reference's arithmetic turns NaN; replay it exactly
+    if (tid == 0) enqueue_exact(a, row, 0u);
+    return;
+  }
+
+  // ---- normaliser: chunk partial sums rescaled to M, plus every special
+  double part = 0.0;
+  for (int c = tid; c < a.n_chunks; c += kFinishThreads) {
+    const ChunkStat s = st[c];
+    if (s.max_key > kKeyNegInf && s.sum > 0) {
+      part += s.sum * gsm::js_exp((double)key_f32(s.max_key) / T - M);
+    }
+  }
+  for (int i = tid; i < n_sp; i += kFinishThreads) part += gsm::js_exp(key_f64(S.sp_key[i]) - M);
+  double total;
+  block_scan_f64(part, S.wsum, &total);
+
+  // probabilities in candidate order (sampling.ts:39,42)
+  for (int i = tid; i < n_cand; i += kFinishThreads) S.cand_p[i] = gsm::js_exp(S.cand_p[i] - M) / total;
+  __syncthreads();
+
+  // ---- top-k (sampling.ts:44)
+  const bool complete = !S.any_truncated;  // no finite logit outside the candidates
+  int n = n_cand;
+  bool n_complete = complete;
+  if (cfg.top_k > 0) {
+    if (cfg.top_k < n) n = cfg.top_k;
+    n_complete = true;  // the first topK of the sorted list are all present
+  }
+  // ---- min-p (sampling.ts:45-48): p is non-increasing along the list
+  if (cfg.min_p > 0) {
+    const double floor_p = S.cand_p[0] * cfg.min_p;
+    for (int i = tid; i < n; i += kFinishThreads) {
+      const double p = S.cand_p[i];
+      if (i + 1 < n && S.cand_p[i + 1] > p) atomicOr(&S.route_exact, 1u);  // not monotone: replay
+      if (!(p >= floor_p)) atomicMin(&S.first_idx, (uint32_t)i);
+      const double margin = p >= floor_p ? p - floor_p : floor_p - p;
+      if (margin < kNearTie * floor_p) atomicOr(&S.route_exact, 2u);
+    }
+    __syncthreads();
+    if (S.first_idx != 0xFFFFFFFFu) {
+      n = (int)S.first_idx;
+      n_complete = true;
+    }
+    __syncthreads();
+    if (tid == 0) S.first_idx = 0xFFFFFFFFu;
+    __syncthreads();
+    if (n == 0) {
+      if (tid == 0) {
+        a.results[row].token = -1;
+        a.results[row].flags = GS_FLAG_EMPTY_CANDIDATES;
+        a.results[row].probability = 0.0;
+      }
+      return;
+    }
+  }
+  // ---- top-p (sampling.ts:56,82-90) on inclusive prefix sums
+  constexpr int kPer = kFinishCap / kFinishThreads;
+  uint32_t tie_report = 0;
+  if (cfg.top_p < 1) {
+    double local[kPer];
+    double s = 0.0;
+    for (int q = 0; q < kPer; ++q) {
+      const int i = tid * kPer + q;
+      s += i < n ? S.cand_p[i] : 0.0;
+      local[q] = s;
+    }
+    double tot;
+    const double base = block_scan_f64(s, S.wtmp, &tot) - s;
+    for (int q = 0; q < kPer; ++q) {
+      const int i = tid * kPer + q;
+      if (i >= n) break;
+      const double cum = base + local[q];
+      if (cum >= cfg.top_p) atomicMin(&S.first_idx, (uint32_t)i);
+      const double d = cum >= cfg.top_p ? cum - cfg.top_p : cfg.top_p - cum;
+      if (d < kNearTie) atomicOr(&S.route_exact, 4u);
+    }
+    __syncthreads();
+    int cut = (int)S.first_idx;  // index of the item that reached topP
+    if (S.first_idx == 0xFFFFFFFFu) {
+      if (!n_complete) {
+        if (tid == 0) enqueue_exact(a, row, 0u);
+        return;
+      }
+      cut = n - 1;
+    } else if (tid == cut / kPer) {
+      // 1e-6 boundary ties, as reported by the reference comparison plan
+      const double cum = base + local[cut % kPer];
+      const double prev = cum - S.cand_p[cut];
+      if (cum - cfg.top_p <= kTieReport * cfg.top_p || (cut > 0 && cfg.top_p - prev <= kTieReport * cfg.top_p)) {
+        atomicOr(&S.status_flags, GS_FLAG_TOPP_TIE);
+      }
+    }
+    n = cut + 1;
+    __syncthreads();
+    if (tid == 0) S.first_idx = 0xFFFFFFFFu;
+    __syncthreads();
+  } else if (!n_complete) {
+    if (tid == 0) enqueue_exact(a, row, 0u);
+    return;
+  }
+  tie_report = S.status_flags;
+
+  // ---- draw (sampling.ts:58-64): first i with prefix_i >= u * sum_{j<n} p_j
+  {
+    double local[kPer];
+    double s = 0.0;
+    for (int q = 0; q < kPer; ++q) {
+      const int i = tid * kPer + q;
+      s += i < n ? S.cand_p[i] : 0.0;
+      local[q] = s;
+    }
+    double ctotal;
+    const double base = block_scan_f64(s, S.wtmp, &ctotal) - s;
+    const double u = cfg.rng_mode == GS_RNG_EXPLICIT ? cfg.uniform : gsm::mulberry32_draw(cfg.seed, cfg.draw_index);
+    const double cursor = u * ctotal;
+    for (int q = 0; q < kPer; ++q) {
+      const int i = tid * kPer + q;
+      if (i >= n) break;
+      const double pre = base + local[q];
+      if (pre >= cursor) atomicMin(&S.first_idx, (uint32_t)i);
+      const double d = pre >= cursor ? pre - cursor : cursor - pre;
+      if (d < kNearTie * ctotal) atomicOr(&S.route_exact, 8u);
+    }
+    __syncthreads();
+    if (tid == 0) {
+      if (S.route_exact || S.first_idx == 0xFFFFFFFFu) {
+        enqueue_exact(a, row, S.route_exact ? GS_FLAG_NEAR_TIE : 0u);
+      } else {
+        const int i = (int)S.first_idx;
+        a.results[row].token = (int32_t)S.cand_id[i];
+        a.results[row].flags = tie_report;
+        a.results[row].probability = S.cand_p[i];
+      }
+    }
+  }
+}
+
+}  // namespace
+
+void launch_finish(const SampleArgs& a, hipStream_t s) {
+  hipLaunchKernelGGL(finish_kernel, dim3(a.rows), dim3(kFinishThreads), 0, s, a);
+}
+
+}  // namespace gs

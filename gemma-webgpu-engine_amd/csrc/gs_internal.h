@@ -1,0 +1,247 @@
+// Internal declarations shared by libgsample's kernels and host code.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/gsample.h"
+#include "gs_math.h"
+
+namespace gs {
+
+// ---------------------------------------------------------------- layout
+constexpr int kScanThreads = 256;                 // one workgroup = 4 wave64
+constexpr int kElemsPerThread = 32;
+constexpr int kChunk = kScanThreads * kElemsPerThread;  // 8192 logits per chunk
+constexpr int kGatherCap = 256;                   // list entries a chunk may emit
+constexpr int kMaxFastK = 64;                     // top-k handled by the one-pass path
+constexpr int kTopPListL = 64;                    // rank depth per chunk in top-p mode
+constexpr int kFinishThreads = 1024;
+constexpr int kFinishCap = 4096;                  // sorted candidate region in the finish kernel
+constexpr int kSpecialCap = 2048;                 // distinct (history window + forced) ids per row
+constexpr int kHashSize = 4096;                   // open-addressing table for those ids
+constexpr int kExactThreads = 1024;
+constexpr int kExactTile = 4096;                  // LDS tile of the exact path's bitonic sort
+
+// relative margin under which a fast-path decision is re-resolved exactly;
+// it bounds the reference's own sequential-sum error (V * 2^-53 ~ 3e-11)
+constexpr double kNearTie = 1.0e-10;
+// the north star's reporting tolerance for top-p boundary ties
+constexpr double kTieReport = 1.0e-6;
+
+// ------------------------------------------------------- orderable keys
+// 32-bit key of an f32 value, increasing with the value; -0 and +0 share a
+// key (they are equal to the reference's comparator). 0 is never produced
+// for a non-NaN value and marks "no element".
+constexpr uint32_t kKeyNegInf = 0x007FFFFFu;    // key of -inf
+constexpr uint32_t kKeyPosInf = 0xFF800000u;    // key of +inf
+
+__host__ __device__ __forceinline__ uint32_t f32_key(float x) {
+  uint32_t b = __builtin_bit_cast(uint32_t, x);
+  if (b == 0x80000000u) b = 0;
+  return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+}
+__host__ __device__ __forceinline__ float key_f32(uint32_t k) {
+  const uint32_t b = (k & 0x80000000u) ? (k & 0x7fffffffu) : ~k;
+  return __builtin_bit_cast(float, b);
+}
+// 64-bit key of an f64 value (same conventions).
+__host__ __device__ __forceinline__ uint64_t f64_key(double x) {
+  uint64_t b = __builtin_bit_cast(uint64_t, x);
+  if (b == 0x8000000000000000ull) b = 0;
+  return (b >> 63) ? ~b : (b | 0x8000000000000000ull);
+}
+__host__ __device__ __forceinline__ double key_f64(uint64_t k) {
+  const uint64_t b = (k >> 63) ? (k & 0x7fffffffffffffffull) : ~k;
+  return __builtin_bit_cast(double, b);
+}
+// list entry: value key high, inverted id low -> descending order is
+// (value desc, id asc), the reference's stable-sort order
+__host__ __device__ __forceinline__ uint64_t pack_entry(uint32_t key, uint32_t id) {
+  return ((uint64_t)key << 32) | (uint32_t)~id;
+}
+__host__ __device__ __forceinline__ uint32_t entry_key(uint64_t e) { return (uint32_t)(e >> 32); }
+__host__ __device__ __forceinline__ uint32_t entry_id(uint64_t e) { return ~(uint32_t)e; }
+
+// ---------------------------------------------------------- row routing
+enum Route : int32_t {
+  kRouteGreedy = 0,  // temperature 0: argmax, first maximum wins
+  kRouteTopK = 1,    // 0 < topK <= kMaxFastK
+  kRouteTopP = 2,    // topK 0 with a top-p or min-p cut
+  kRouteExact = 3,   // sequential replay of the reference (everything else)
+};
+
+struct Plan {
+  int32_t route;
+  int32_t depth;  // per-chunk rank depth of the one-pass path
+};
+
+__host__ __device__ __forceinline__ Plan plan_row(const gs_row_config& c) {
+  if (c.temperature == 0) return Plan{kRouteGreedy, 1};
+  if (c.options & GS_ROW_FORCE_EXACT) return Plan{kRouteExact, 0};
+  // between these bounds l/T keeps the order and the ties of the f32 logits
+  if (!(c.temperature >= 1.0e-200 && c.temperature <= 1.0e200)) return Plan{kRouteExact, 0};
+  if (c.typical_p < 1) return Plan{kRouteExact, 0};
+  if (c.top_k > 0) return c.top_k <= kMaxFastK ? Plan{kRouteTopK, c.top_k} : Plan{kRouteExact, 0};
+  if (c.top_p < 1 || c.min_p > 0) return Plan{kRouteTopP, kTopPListL};
+  return Plan{kRouteExact, 0};
+}
+
+// ------------------------------------------------------- per-chunk state
+struct ChunkStat {
+  double sum;          // sum of e^((l - lmax)/T) over finite non-special logits of the chunk
+  uint32_t max_key;    // key of lmax (0: no non-special logit, kKeyNegInf: all masked)
+  uint32_t n_list;     // entries written to the chunk's list
+  uint32_t n_finite;   // finite non-special logits
+  uint32_t threshold;  // the list holds every finite non-special logit with key >= threshold
+  uint32_t truncated;  // some finite logit lies below the threshold
+  uint32_t flags;      // kChunkOverflow | kChunkNonFinite
+};
+constexpr uint32_t kChunkOverflow = 1u;
+constexpr uint32_t kChunkNonFinite = 2u;
+
+struct ExactQueue {
+  uint32_t count;  // rows appended by the finish kernel
+  uint32_t next;   // rows taken by the exact kernel
+  uint32_t rows[1];
+};
+
+// Arguments every sampling kernel reads.
+struct SampleArgs {
+  const void* logits;
+  int64_t row_stride;
+  int32_t dtype;
+  int32_t rows;
+  int32_t vocab;
+  int32_t n_chunks;
+  int32_t vector_ok;  // 16-byte aligned rows
+  int32_t mask_words;
+  const gs_row_config* configs;
+  const int64_t* history_offsets;
+  const int32_t* history_ids;
+  const int64_t* forced_offsets;
+  const int32_t* forced_ids;
+  const uint8_t* forced_kinds;
+  const uint32_t* mask_table;
+  int32_t mask_slots;
+  int32_t exact_slots;
+  gs_row_result* results;
+  ChunkStat* stats;     // [rows][n_chunks]
+  uint64_t* lists;      // [rows][n_chunks][kGatherCap]
+  ExactQueue* queue;
+  uint8_t* exact_scratch;
+  int64_t exact_slot_bytes;
+  int64_t exact_capacity;  // entries per slot (power of two >= vocab)
+};
+
+// --------------------------------------------------------- wave helpers
+__device__ __forceinline__ uint32_t shfl_xor_u32(uint32_t v, int m) { return (uint32_t)__shfl_xor((int)v, m, 64); }
+__device__ __forceinline__ uint64_t shfl_xor_u64(uint64_t v, int m) {
+  const uint32_t lo = shfl_xor_u32((uint32_t)v, m), hi = shfl_xor_u32((uint32_t)(v >> 32), m);
+  return ((uint64_t)hi << 32) | lo;
+}
+__device__ __forceinline__ double shfl_xor_f64(double v, int m) {
+  return __builtin_bit_cast(double, shfl_xor_u64(__builtin_bit_cast(uint64_t, v), m));
+}
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
+  for (int m = 32; m > 0; m >>= 1) { const uint32_t o = shfl_xor_u32(v, m); v = o > v ? o : v; }
+  return v;
+}
+__device__ __forceinline__ uint32_t wave_sum_u32(uint32_t v) {
+  for (int m = 32; m > 0; m >>= 1) v += shfl_xor_u32(v, m);
+  return v;
+}
+__device__ __forceinline__ double wave_sum_f64(double v) {
+  for (int m = 32; m > 0; m >>= 1) v += shfl_xor_f64(v, m);
+  return v;
+}
+// inclusive prefix sum of u32 across the wave
+__device__ __forceinline__ uint32_t wave_scan_u32(uint32_t v, int lane) {
+  for (int d = 1; d < 64; d <<= 1) {
+    const uint32_t o = (uint32_t)__shfl_up((int)v, d, 64);
+    if (lane >= d) v += o;
+  }
+  return v;
+}
+__device__ __forceinline__ double wave_scan_f64(double v, int lane) {
+  for (int d = 1; d < 64; d <<= 1) {
+    const double o = __shfl_up(v, d, 64);
+    if (lane >= d) v += o;
+  }
+  return v;
+}
+// bitonic sort of one u64 per lane, descending across the wave
+__device__ __forceinline__ uint64_t wave_sort_desc(uint64_t x, int lane) {
+  for (int k = 2; k <= 64; k <<= 1) {
+    for (int j = k >> 1; j > 0; j >>= 1) {
+      const uint64_t y = shfl_xor_u64(x, j);
+      const uint64_t hi = x > y ? x : y, lo = x > y ? y : x;
+      const bool lower = (lane & j) == 0;
+      const bool desc_seg = (lane & k) == 0;
+      x = (lower == desc_seg) ? hi : lo;
+    }
+  }
+  return x;
+}
+
+// ----------------------------------------------------------- row inputs
+__device__ __forceinline__ float load_logit(const SampleArgs& a, int64_t row, int64_t i) {
+  if (a.dtype == GS_BF16) {
+    const uint16_t* p = (const uint16_t*)a.logits + row * a.row_stride + i;
+    return __builtin_bit_cast(float, (uint32_t)(*p) << 16);
+  }
+  return ((const float*)a.logits)[row * a.row_stride + i];
+}
+
+__device__ __forceinline__ bool mask_allows(const SampleArgs& a, int32_t slot, int64_t id) {
+  return (a.mask_table[(int64_t)slot * a.mask_words + (id >> 5)] >> (id & 31)) & 1u;
+}
+
+// Window of the history that penalties read (sampling.ts:22-24).
+__device__ __forceinline__ void history_window(const SampleArgs& a, int64_t row, const gs_row_config& c,
+                                               int64_t* begin, int64_t* end) {
+  *begin = *end = 0;
+  if (!a.history_offsets || c.repetition_window <= 0) return;
+  const int64_t h0 = a.history_offsets[row], h1 = a.history_offsets[row + 1];
+  const int64_t s = h1 - (int64_t)c.repetition_window;
+  *begin = s > h0 ? s : h0;
+  *end = h1;
+}
+
+// -------------------------------------------- distinct ids of one row
+// Hash of the row's distinct special ids (window ids with counts, forced
+// ids with kinds), built in LDS by one workgroup.
+struct SpecialTable {
+  uint32_t* ids;     // kHashSize, 0xFFFFFFFF = empty
+  uint32_t* counts;  // kHashSize: window count | kinds << 24
+};
+
+__device__ __forceinline__ uint32_t hash_id(uint32_t id) { return (id * 2654435761u) >> 20; }
+
+// window ids add 1 to the low 24 bits; forced ids OR their kind into the top 8
+__device__ __forceinline__ void special_insert(SpecialTable t, uint32_t id, uint32_t kind) {
+  uint32_t h = hash_id(id) & (kHashSize - 1);
+  for (int probe = 0; probe < kHashSize; ++probe) {
+    const uint32_t prev = atomicCAS(&t.ids[h], 0xFFFFFFFFu, id);
+    if (prev == 0xFFFFFFFFu || prev == id) {
+      if (kind == 0) atomicAdd(&t.counts[h], 1u);
+      else atomicOr(&t.counts[h], kind << 24);
+      return;
+    }
+    h = (h + 1) & (kHashSize - 1);
+  }
+}
+
+// ---------------------------------------------------- kernel launchers
+void launch_scan(const SampleArgs& a, hipStream_t s);
+void launch_finish(const SampleArgs& a, hipStream_t s);
+void launch_exact(const SampleArgs& a, hipStream_t s);
+void launch_logprob(const void* logits, int32_t dtype, int32_t rows, int64_t stride, int32_t vocab,
+                    const int32_t* tokens, double* out, hipStream_t s);
+void launch_masks(const int64_t* offsets, const uint8_t* bytes, int32_t vocab, const int16_t* next,
+                  const int32_t* states, int32_t n, uint32_t* masks, int32_t mask_words, int32_t n_states,
+                  hipStream_t s);
+void launch_lmhead(const uint16_t* hidden, const uint16_t* weight, int32_t m, int32_t width, int32_t vocab,
+                   float softcap, float* out, hipStream_t s);
+
+}  // namespace gs

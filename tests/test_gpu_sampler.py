@@ -1,0 +1,327 @@
+"""GPU parity of the batched sampler (gs_sample through the C ABI) against the
+oracle: token ids bit-exact on every row; probabilities identical on rows the
+exact path resolved and within 1e-12 relative on one-pass rows."""
+import math
+
+import numpy as np
+import pytest
+
+from oracle.oracle import Decoding
+
+pytestmark = pytest.mark.gpu
+
+PROB_RTOL = 1e-12
+
+
+def _gs():
+    import gsample
+
+    return gsample
+
+
+def to_oracle_cfg(c):
+    return Decoding(temperature=c.temperature, topK=c.topK, topP=c.topP, minP=c.minP, typicalP=c.typicalP,
+                    repetitionPenalty=c.repetitionPenalty, repetitionWindow=c.repetitionWindow,
+                    frequencyPenalty=c.frequencyPenalty, presencePenalty=c.presencePenalty)
+
+
+def assert_rows_match(out, expected, flags_ok=None, label=""):
+    gs = _gs()
+    for i, (t, p) in enumerate(expected):
+        assert out.tokens[i] == t, f"{label} row {i}: token {out.tokens[i]} != {t} (flags {out.flags[i]})"
+        if out.flags[i] & gs.GS_FLAG_EXACT_PATH:
+            assert out.probabilities[i] == p or (math.isnan(p) and math.isnan(out.probabilities[i])), (label, i)
+        else:
+            assert abs(out.probabilities[i] - p) <= PROB_RTOL * abs(p), (label, i, out.probabilities[i], p)
+
+
+# ------------------------------------------------------------ reference tests
+
+
+def test_reference_known_answers_on_gpu():
+    """tests/sampling.spec.ts:13-139 through the drop-in sample_token."""
+    gs = _gs()
+    D = gs.DEFAULT_DECODING_CONFIG
+    assert gs.sample_token([0.2, 4, 1], [], D.merged(temperature=0), lambda: 0.5) == 1
+    assert gs.sample_token([0.2, 4, 1], [], D.merged(topK=1), lambda: 0.99) == 1
+    cfg = D.merged(topK=0, topP=1)
+    r1, r2 = gs.SeededRandom(71), gs.SeededRandom(71)
+    a = [gs.sample_token([1, 1, 1], [], cfg, r1.next) for _ in range(20)]
+    b = [gs.sample_token([1, 1, 1], [], cfg, r2.next) for _ in range(20)]
+    assert a == b
+    assert gs.sample_token([2, 1.5], [0], D.merged(temperature=0, repetitionPenalty=2), lambda: 0) == 1
+    assert gs.sample_token([2, 1.5], [0], D.merged(temperature=0, repetitionPenalty=2, repetitionWindow=0),
+                           lambda: 0) == 0
+    pf = D.merged(temperature=0, repetitionPenalty=1, repetitionWindow=2, presencePenalty=0.1, frequencyPenalty=0.3)
+    assert gs.sample_token([2, 1.5], [0, 0], pf, lambda: 0) == 1
+    assert gs.sample_token([2, 2.1], [0, 1], pf.merged(repetitionWindow=1, presencePenalty=0.5, frequencyPenalty=0),
+                           lambda: 0) == 0
+    l3 = [math.log(0.6), math.log(0.3), math.log(0.1)]
+    assert gs.sample_token(l3, [], D.merged(temperature=1, topK=0, topP=1, typicalP=1, minP=0.6), lambda: 0.99) == 0
+    assert gs.sample_token(l3, [], D.merged(temperature=1, topK=0, topP=0.5, minP=0, typicalP=1), lambda: 0.99) == 0
+    lt = [math.log(0.45), math.log(0.4), math.log(0.15)]
+    assert gs.sample_token(lt, [], D.merged(temperature=1, topK=0, topP=1, minP=0, typicalP=0.3), lambda: 0.5) == 1
+    assert gs.token_log_probability(l3, 0) == pytest.approx(math.log(0.6), abs=1e-6)
+    assert gs.token_log_probability(l3, 2) == pytest.approx(math.log(0.1), abs=1e-6)
+    with pytest.raises(gs.GSampleError, match="outside logits length"):
+        gs.token_log_probability(l3, 3)
+
+
+def test_random_never_called_for_greedy():
+    gs = _gs()
+    calls = []
+
+    def rnd():
+        calls.append(1)
+        return 0.5
+
+    gs.sample_token([0.1, 0.2], [], gs.DEFAULT_DECODING_CONFIG.merged(temperature=0), rnd)
+    assert calls == []
+    gs.sample_token([0.1, 0.2], [], gs.DEFAULT_DECODING_CONFIG, rnd)
+    assert calls == [1]
+
+
+# ------------------------------------------------------- random small vocabs
+
+
+def _random_batch(seed, rows, V):
+    rng = np.random.default_rng(seed)
+    gs = _gs()
+    logits = np.empty((rows, V), dtype=np.float32)
+    hists, cfgs, us = [], [], []
+    for r in range(rows):
+        x = rng.normal(0, rng.uniform(0.5, 4), V).astype(np.float32)
+        if rng.random() < 0.3:
+            x = (np.round(x * 4) / 4).astype(np.float32)
+        if rng.random() < 0.15:
+            x[rng.random(V) < 0.8] = -np.inf
+        logits[r] = x
+        hists.append(rng.integers(-2, V + 2, int(rng.integers(0, 80))).tolist())
+        cfgs.append(gs.DecodingConfig(
+            temperature=float(rng.choice([0.0, 0.5, 0.8, 1.0, 1.7])),
+            topK=int(rng.choice([0, 1, 5, 40, 64, 300])),
+            topP=float(rng.choice([1.0, 0.95, 0.5, 0.9, 0.1])),
+            minP=float(rng.choice([0.0, 0.0, 0.05, 0.3])),
+            typicalP=float(rng.choice([1.0, 1.0, 1.0, 0.9, 0.3])),
+            repetitionPenalty=float(rng.choice([1.0, 1.1, 2.0])),
+            repetitionWindow=int(rng.choice([0, 8, 64])),
+            frequencyPenalty=float(rng.choice([0.0, 0.3])),
+            presencePenalty=float(rng.choice([0.0, 0.5]))))
+        us.append(float(rng.random()))
+    return logits, hists, cfgs, us
+
+
+@pytest.mark.parametrize("V,seed", [(3000, 1), (8192 + 77, 2), (40000, 3)])
+@pytest.mark.parametrize("force_exact", [False, True])
+def test_random_batches_match_oracle(oracle, V, seed, force_exact):
+    import torch
+
+    gs = _gs()
+    rows = 96
+    logits, hists, cfgs, us = _random_batch(seed, rows, V)
+    s = gs.Sampler(vocab_size=V, max_rows=rows)
+    try:
+        conf = np.stack([gs.runtime.row_config(c, uniform=u, force_exact=force_exact) for c, u in zip(cfgs, us)])
+        out = s.sample(torch.from_numpy(logits).cuda(), conf, histories=hists, raise_on_failure=False)
+    finally:
+        s.close()
+    expected = []
+    for r in range(rows):
+        t, tr = oracle.sample_token(logits[r], hists[r], to_oracle_cfg(cfgs[r]), us[r])
+        expected.append((t, tr.probability if t >= 0 else 0.0))
+    for r, (t, p) in enumerate(expected):
+        if t < 0:
+            assert out.flags[r] & gs.GS_FLAG_EMPTY_CANDIDATES
+            expected[r] = (int(out.tokens[r]), float(out.probabilities[r]))
+    assert_rows_match(out, expected, label=f"V={V}")
+    if force_exact:
+        for r in range(rows):
+            if cfgs[r].temperature > 0:
+                assert out.flags[r] & gs.GS_FLAG_EXACT_PATH
+
+
+# ------------------------------------------------------------- full-size rows
+
+
+def test_single_row_config(sampler, oracle):
+    import torch
+
+    gs = _gs()
+    w = gs.workloads.single_row()
+    conf = gs.runtime.row_config(w.configs[0], seed=42).reshape(1)
+    out = sampler.sample(torch.from_numpy(w.logits).cuda(), conf)
+    t, tr = oracle.sample_token(w.logits[0], [], to_oracle_cfg(w.configs[0]), oracle.draw(42, 0))
+    assert_rows_match(out, [(t, tr.probability)], label="single_row")
+
+
+def test_penalties_batch(sampler, oracle):
+    import torch
+
+    gs = _gs()
+    w = gs.workloads.penalties()
+    conf = np.stack([gs.runtime.row_config(c, seed=s) for c, s in zip(w.configs, w.seeds)])
+    out = sampler.sample(torch.from_numpy(w.logits).cuda(), conf, histories=w.histories)
+    pick = list(range(0, 256, 8))
+    exp = []
+    for r in pick:
+        t, tr = oracle.sample_token(w.logits[r], w.histories[r], to_oracle_cfg(w.configs[r]), oracle.draw(w.seeds[r], 0))
+        exp.append((t, tr.probability))
+    sub = gs.runtime.SampleOutput(out.tokens[pick], out.probabilities[pick], out.flags[pick])
+    assert_rows_match(sub, exp, label="penalties")
+    # every row was settled by the one-pass path (no margin within 1e-10)
+    assert not np.any(out.flags & gs.GS_FLAG_EXACT_PATH), out.flags
+
+
+def test_heavy_tail_bf16(sampler, oracle):
+    import torch
+
+    gs = _gs()
+    rows = list(range(0, 1024, 64))
+    w = gs.workloads.heavy_tail(rows=rows)
+    conf = np.stack([gs.runtime.row_config(c, seed=s) for c, s in zip(w.configs, w.seeds)])
+    x = torch.from_numpy(w.logits.view(np.int16)).cuda().view(torch.bfloat16)
+    out = sampler.sample(x, conf)
+    exp = []
+    for i, r in enumerate(rows):
+        f = gs.workloads.bf16_bits_to_f32(w.logits[i])
+        t, tr = oracle.sample_token(f, [], to_oracle_cfg(w.configs[i]), oracle.draw(w.seeds[i], 0))
+        exp.append((t, tr.probability))
+    assert_rows_match(out, exp, label="heavy_tail")
+
+
+def test_constrained_masks_and_samples(sampler, oracle):
+    import torch
+
+    gs = _gs()
+    offsets, data = gs.workloads.synthetic_vocab()
+    nxt, finals = gs.workloads.synthetic_dfa()
+    sampler.set_vocab(offsets, data)
+    sampler.set_dfa(nxt, finals)
+    viable = oracle.viable_states(nxt, finals)
+    states = list(range(64))
+    table = sampler.build_masks(states).cpu().numpy().view(np.uint32)
+    for s in states[::7]:
+        ref = oracle.dfa_legal_mask(nxt, viable, offsets, data, s)
+        assert np.array_equal(table[s], ref), s
+    frac = np.mean([oracle.mask_bits_to_ids(table[s], 262144).size for s in states]) / 262144
+    assert 0.005 < frac < 0.1
+    rows = list(range(0, 128, 8))
+    for greedy in (True, False):
+        w = gs.workloads.constrained(rows=rows, greedy=greedy)
+        masks = torch.from_numpy(table.view(np.int32)).cuda()
+        conf = np.stack([gs.runtime.row_config(c, seed=s, mask_slot=int(st))
+                         for c, s, st in zip(w.configs, w.seeds, w.states)])
+        out = sampler.sample(torch.from_numpy(w.logits).cuda(), conf, mask_table=masks)
+        exp = []
+        for i in range(len(rows)):
+            legal = oracle.mask_bits_to_ids(table[w.states[i]], 262144)
+            masked = oracle.mask_logits(w.logits[i], legal, [])
+            t, tr = oracle.sample_token(masked, [], to_oracle_cfg(w.configs[i]), oracle.draw(w.seeds[i], 0))
+            exp.append((t, tr.probability))
+        assert_rows_match(out, exp, label=f"constrained greedy={greedy}")
+
+
+# ---------------------------------------------------------------- edge cases
+
+
+def test_edge_cases(oracle):
+    import torch
+
+    gs = _gs()
+    V = 10000
+    s = gs.Sampler(vocab_size=V, max_rows=16)
+    try:
+        base = gs.DecodingConfig(temperature=1.0, topK=0, topP=0.9, minP=0, typicalP=1, repetitionPenalty=1,
+                                 repetitionWindow=0)
+        rows = []
+        # all equal logits (one giant tie), greedy and sampled
+        rows.append((np.zeros(V, np.float32), [], base, 0.37))
+        rows.append((np.zeros(V, np.float32), [], base.merged(temperature=0), 0.0))
+        rows.append((np.zeros(V, np.float32), [], base.merged(topK=10), 0.99))
+        # -0 and +0 tie by id
+        z = np.zeros(V, np.float32)
+        z[5] = -0.0
+        z[3] = -0.0
+        rows.append((z, [], base.merged(temperature=0), 0.0))
+        # a single finite logit among -inf
+        one = np.full(V, -np.inf, np.float32)
+        one[777] = -3.0
+        rows.append((one, [], base, 0.5))
+        rows.append((one, [], base.merged(topK=5), 0.999))
+        # top-k larger than the finite set
+        few = np.full(V, -np.inf, np.float32)
+        few[[10, 20, 30]] = [1.0, 2.0, 3.0]
+        rows.append((few, [], base.merged(topK=50, topP=1.0), 0.75))
+        # huge spread: exp underflow in the normaliser
+        wide = np.linspace(-2000, 10, V).astype(np.float32)
+        rows.append((wide, [], base.merged(topP=0.999999), 0.8))
+        # extreme temperatures go to the exact path
+        x = np.random.default_rng(0).normal(0, 3, V).astype(np.float32)
+        rows.append((x, [], base.merged(temperature=1e-250), 0.3))
+        rows.append((x, [], base.merged(temperature=1e250), 0.3))
+        # penalties on every id of a long window
+        rows.append((x, list(range(V)) * 2, base.merged(repetitionPenalty=1.3, repetitionWindow=2000, topK=20), 0.6))
+        # u = 0 and u just below 1
+        rows.append((x, [], base.merged(topK=40, topP=0.95), 0.0))
+        rows.append((x, [], base.merged(topK=40, topP=0.95), 1 - 2 ** -32))
+        logits = np.stack([r[0] for r in rows])
+        conf = np.stack([gs.runtime.row_config(r[2], uniform=r[3]) for r in rows])
+        out = s.sample(torch.from_numpy(logits).cuda(), conf, histories=[r[1] for r in rows])
+        exp = []
+        for r in rows:
+            t, tr = oracle.sample_token(r[0], r[1], to_oracle_cfg(r[2]), r[3])
+            exp.append((t, tr.probability))
+        assert_rows_match(out, exp, label="edge")
+    finally:
+        s.close()
+
+
+def test_dead_end_and_termination_rules():
+    """selectConstrainedToken (gemma-session.ts:1305-1329): termination ids only
+    when accepting, extra ids legal unless also termination, empty -> dead end."""
+    import torch
+
+    gs = _gs()
+    V = 4096
+    s = gs.Sampler(vocab_size=V, max_rows=8)
+    try:
+        tokens = [None] * V
+        tokens[10], tokens[11], tokens[12] = b"a", b"b", b"ab"
+        vocab = gs.VocabBytes.from_tokens(tokens)
+        nxt = np.full((3, 256), -1, np.int32)
+        nxt[0, ord("a")] = 1
+        nxt[1, ord("b")] = 2
+        finals = np.array([0, 0, 1], np.uint8)
+        s.set_vocab(vocab.offsets, vocab.data)
+        s.set_dfa(nxt, finals)
+        table = s.build_masks([0, 1, 2])
+        assert np.nonzero(np.unpackbits(table[0].cpu().numpy().view(np.uint8), bitorder="little"))[0].tolist() == [10, 12]
+        x = np.linspace(0, 1, V).astype(np.float32)
+        base = gs.DecodingConfig(temperature=0, topK=0, topP=1, repetitionWindow=0)
+        term = [1, 50, 106]
+        forced = gs.constraint.forced_ids_csr(3, term, [100])
+        conf = np.stack([
+            gs.runtime.row_config(base, uniform=0.0, mask_slot=0),                   # legal {10,12,100}
+            gs.runtime.row_config(base, uniform=0.0, mask_slot=2, accepting=True),   # only termination + extra
+            gs.runtime.row_config(base, uniform=0.0, mask_slot=2, accepting=False),  # only the extra id
+        ])
+        out = s.sample(torch.from_numpy(np.stack([x, x, x])).cuda(), conf, forced=forced, mask_table=table)
+        assert out.tokens.tolist() == [100, 106, 100]
+        forced2 = gs.constraint.forced_ids_csr(1, term, [])
+        conf2 = gs.runtime.row_config(base, uniform=0.0, mask_slot=2, accepting=False).reshape(1)
+        with pytest.raises(gs.GSampleError, match="tokenization dead end"):
+            s.sample(torch.from_numpy(x[None]).cuda(), conf2, forced=forced2, mask_table=table)
+    finally:
+        s.close()
+
+
+def test_token_log_probability_rows(sampler):
+    import torch
+
+    x = np.random.default_rng(9).normal(0, 3, (4, 262144)).astype(np.float32)
+    toks = [0, 5, 262143, 1234]
+    got = sampler.token_log_probability(torch.from_numpy(x).cuda(), toks)
+    for r in range(4):
+        v = x[r].astype(np.float64)
+        ref = v[toks[r]] - v.max() - np.log(np.exp(v - v.max()).sum())
+        assert got[r] == pytest.approx(ref, abs=1e-12)
