@@ -58,6 +58,8 @@ struct Lds {
   int32_t result_token;
   uint32_t result_flags;
   double dtmp;
+  double bcast_d[2];
+  int64_t bcast_n;
 };
 
 __device__ __forceinline__ bool before(uint64_t ka, uint32_t ia, uint64_t kb, uint32_t ib) {
@@ -135,7 +137,10 @@ __device__ double sequential_sum(Lds& L, const double* prob, const uint32_t* ord
   return acc;
 }
 
-// cumulativeCut (sampling.ts:82-90): number of items kept.
+// cumulativeCut (sampling.ts:82-90): number of items kept. Lane 0 of the
+// workgroup walks the list; the running sum, the previous sum and the count
+// are broadcast through LDS after every block so that all threads leave with
+// the same values (every loop below with a barrier depends on them).
 __device__ int64_t cumulative_cut(Lds& L, const double* prob, const uint32_t* order, int64_t n, double threshold,
                                   double* at_cut, double* before_cut) {
   double cum = 0.0, prev = 0.0;
@@ -156,13 +161,15 @@ __device__ int64_t cumulative_cut(Lds& L, const double* prob, const uint32_t* or
         if (!(end < n && cum < threshold)) { stop = true; break; }
       }
       L.flag = stop ? 1u : 0u;
-      L.stage[0] = cum;
-      L.stage[1] = prev;
+      L.bcast_d[0] = cum;
+      L.bcast_d[1] = prev;
+      L.bcast_n = end;
     }
     __syncthreads();
     done = L.flag != 0;
-    cum = L.stage[0];
-    prev = L.stage[1];
+    cum = L.bcast_d[0];
+    prev = L.bcast_d[1];
+    end = L.bcast_n;
     __syncthreads();
   }
   *at_cut = cum;

@@ -305,7 +305,8 @@ class Sampler:
         keep.append(d_cfg)
         b = Batch()
         b.logits = logits.data_ptr()
-        b.row_stride = logits.stride(0)
+        # a one-row view may carry any leading stride; only its row is read
+        b.row_stride = logits.stride(0) if rows > 1 else max(logits.stride(0), int(logits.shape[1]))
         b.dtype = dtype
         b.rows = rows
         b.configs = d_cfg.data_ptr()
