@@ -41,6 +41,13 @@ struct gs_context {
   int32_t* d_tokens = nullptr;
   double* d_logprob = nullptr;
   int32_t tokens_cap = 0;
+  // kernel timing (gs_timing_begin / gs_timing_end): per timed call, one event
+  // before each stage and one after it
+  std::vector<hipEvent_t> t_events;  // [max_calls][GS_STAGE_COUNT][2]
+  std::vector<uint8_t> t_ran;        // [max_calls][GS_STAGE_COUNT]
+  int32_t t_cap = 0;
+  int32_t t_calls = 0;
+  bool t_on = false;
   std::string error;
 };
 
@@ -70,6 +77,26 @@ hipStream_t pick_stream(gs_context* ctx, void* stream) {
 }
 
 bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
+
+// Slot of the current call in the timing tables, or -1 when not timing.
+int32_t timing_slot(gs_context* ctx) {
+  if (!ctx->t_on || ctx->t_calls >= ctx->t_cap) return -1;
+  return ctx->t_calls;
+}
+
+void stage_mark(gs_context* ctx, int32_t slot, int stage, int edge, hipStream_t s) {
+  if (slot < 0) return;
+  (void)hipEventRecord(ctx->t_events[((size_t)slot * GS_STAGE_COUNT + stage) * 2 + edge], s);
+  if (edge == 0) ctx->t_ran[(size_t)slot * GS_STAGE_COUNT + stage] = 1;
+}
+
+void destroy_timing(gs_context* ctx) {
+  for (hipEvent_t e : ctx->t_events) (void)hipEventDestroy(e);
+  ctx->t_events.clear();
+  ctx->t_ran.clear();
+  ctx->t_cap = ctx->t_calls = 0;
+  ctx->t_on = false;
+}
 
 }  // namespace
 
@@ -141,6 +168,7 @@ int gs_destroy(gs_context* ctx) {
   free_dev(ctx->d_states);
   free_dev(ctx->d_tokens);
   free_dev(ctx->d_logprob);
+  destroy_timing(ctx);
   if (ctx->stream) (void)hipStreamDestroy(ctx->stream);
   delete ctx;
   return GS_OK;
@@ -227,12 +255,20 @@ int gs_sample(gs_context* ctx, const gs_batch* b, void* stream) {
   a.exact_slot_bytes = ctx->exact_slot_bytes;
   a.exact_capacity = ctx->exact_cap;
   GS_HIP(ctx, hipMemsetAsync(ctx->d_queue, 0, 2 * sizeof(uint32_t), s));
+  const int32_t slot = timing_slot(ctx);
+  stage_mark(ctx, slot, GS_STAGE_SCAN, 0, s);
   launch_scan(a, s);
   GS_HIP(ctx, hipGetLastError());
+  stage_mark(ctx, slot, GS_STAGE_SCAN, 1, s);
+  stage_mark(ctx, slot, GS_STAGE_FINISH, 0, s);
   launch_finish(a, s);
   GS_HIP(ctx, hipGetLastError());
+  stage_mark(ctx, slot, GS_STAGE_FINISH, 1, s);
+  stage_mark(ctx, slot, GS_STAGE_EXACT, 0, s);
   launch_exact(a, s);
   GS_HIP(ctx, hipGetLastError());
+  stage_mark(ctx, slot, GS_STAGE_EXACT, 1, s);
+  if (slot >= 0) ctx->t_calls++;
   return GS_OK;
 }
 
@@ -422,9 +458,12 @@ int gs_lmhead(gs_context* ctx, const void* hidden, const void* weight, int32_t m
   if (width % 64 != 0) return fail(ctx, GS_ERR_UNSUPPORTED, "lm_head width must be a multiple of 64");
   if (!aligned16(hidden) || !aligned16(weight)) return fail(ctx, GS_ERR_INVALID_ARGUMENT, "hidden and weight must be 16-byte aligned");
   GS_HIP(ctx, hipSetDevice(ctx->device));
-  launch_lmhead((const uint16_t*)hidden, (const uint16_t*)weight, m_rows, width, ctx->vocab, softcap, logits,
-                pick_stream(ctx, stream));
+  hipStream_t s = pick_stream(ctx, stream);
+  const int32_t slot = timing_slot(ctx);
+  stage_mark(ctx, slot, GS_STAGE_LMHEAD, 0, s);
+  launch_lmhead((const uint16_t*)hidden, (const uint16_t*)weight, m_rows, width, ctx->vocab, softcap, logits, s);
   GS_HIP(ctx, hipGetLastError());
+  stage_mark(ctx, slot, GS_STAGE_LMHEAD, 1, s);
   return GS_OK;
 }
 
@@ -438,6 +477,48 @@ int gs_lmhead_sample(gs_context* ctx, const void* hidden, const void* weight, in
   b.dtype = GS_F32;
   b.row_stride = ctx->vocab;
   return gs_sample(ctx, &b, stream);
+}
+
+int gs_timing_begin(gs_context* ctx, int32_t max_calls) {
+  if (!ctx || max_calls <= 0 || max_calls > 100000) return fail(ctx, GS_ERR_INVALID_ARGUMENT, "max_calls must be 1..100000");
+  GS_HIP(ctx, hipSetDevice(ctx->device));
+  destroy_timing(ctx);
+  ctx->t_events.assign((size_t)max_calls * GS_STAGE_COUNT * 2, nullptr);
+  ctx->t_ran.assign((size_t)max_calls * GS_STAGE_COUNT, 0);
+  for (hipEvent_t& e : ctx->t_events) {
+    if (hipEventCreate(&e) != hipSuccess) {
+      destroy_timing(ctx);
+      return fail(ctx, GS_ERR_HIP, "hipEventCreate failed");
+    }
+  }
+  ctx->t_cap = max_calls;
+  ctx->t_calls = 0;
+  ctx->t_on = true;
+  return GS_OK;
+}
+
+int gs_timing_end(gs_context* ctx, double* stage_ms, int32_t* calls) {
+  if (!ctx || !stage_ms || !calls) return fail(ctx, GS_ERR_INVALID_ARGUMENT, "bad arguments");
+  if (!ctx->t_on) return fail(ctx, GS_ERR_INVALID_ARGUMENT, "timing was not started");
+  GS_HIP(ctx, hipSetDevice(ctx->device));
+  for (int k = 0; k < GS_STAGE_COUNT; ++k) { stage_ms[k] = 0.0; calls[k] = 0; }
+  int st = GS_OK;
+  for (int32_t c = 0; c < ctx->t_calls && st == GS_OK; ++c) {
+    for (int k = 0; k < GS_STAGE_COUNT; ++k) {
+      if (!ctx->t_ran[(size_t)c * GS_STAGE_COUNT + k]) continue;
+      hipEvent_t e0 = ctx->t_events[((size_t)c * GS_STAGE_COUNT + k) * 2];
+      hipEvent_t e1 = ctx->t_events[((size_t)c * GS_STAGE_COUNT + k) * 2 + 1];
+      float ms = 0.0f;
+      if (hipEventSynchronize(e1) != hipSuccess || hipEventElapsedTime(&ms, e0, e1) != hipSuccess) {
+        st = fail(ctx, GS_ERR_HIP, "reading a timing event failed");
+        break;
+      }
+      stage_ms[k] += ms;
+      calls[k] += 1;
+    }
+  }
+  destroy_timing(ctx);
+  return st;
 }
 
 }  // extern "C"

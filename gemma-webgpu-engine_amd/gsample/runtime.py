@@ -105,8 +105,12 @@ EXPORTED_SYMBOLS = (
     "gs_abi_version", "gs_device_count", "gs_seeded_random", "gs_js_exp", "gs_js_log", "gs_softcap",
     "gs_validate_configs", "gs_create", "gs_destroy", "gs_last_error", "gs_synchronize", "gs_stream",
     "gs_sample", "gs_sample_sync", "gs_token_log_prob", "gs_token_log_prob_host", "gs_set_vocab", "gs_set_dfa",
-    "gs_build_masks", "gs_dfa_advance", "gs_dfa_accepting", "gs_lmhead", "gs_lmhead_sample",
+    "gs_build_masks", "gs_dfa_advance", "gs_dfa_accepting", "gs_lmhead", "gs_lmhead_sample", "gs_timing_begin",
+    "gs_timing_end",
 )
+
+# kernel stages reported by gs_timing_end (include/gsample.h GS_STAGE_*)
+STAGES = ("lmhead", "scan", "finish", "exact")
 
 _lib = None
 
@@ -149,6 +153,8 @@ def library():
     L.gs_dfa_accepting.argtypes = [vp, i32, C.POINTER(C.c_int32)]
     L.gs_lmhead.argtypes = [vp, vp, vp, i32, i32, C.c_float, vp, vp]
     L.gs_lmhead_sample.argtypes = [vp, vp, vp, i32, C.c_float, vp, C.POINTER(Batch), vp]
+    L.gs_timing_begin.argtypes = [vp, i32]
+    L.gs_timing_end.argtypes = [vp, vp, vp]
     _lib = L
     return L
 
@@ -391,15 +397,36 @@ class Sampler:
         self._check(self.lib.gs_dfa_accepting(self.ctx, int(state), C.byref(v)))
         return bool(v.value)
 
+    # -- kernel timing ---------------------------------------------------
+    def timing_begin(self, max_calls: int):
+        """Record HIP events around every kernel of the next `max_calls` calls."""
+        self._check(self.lib.gs_timing_begin(self.ctx, int(max_calls)))
+
+    def timing_end(self) -> dict:
+        """{stage: (summed ms, calls)} for the calls timed since timing_begin."""
+        ms = np.zeros(len(STAGES), dtype=np.float64)
+        calls = np.zeros(len(STAGES), dtype=np.int32)
+        self._check(self.lib.gs_timing_end(self.ctx, _np_ptr(ms), _np_ptr(calls)))
+        return {name: (float(ms[i]), int(calls[i])) for i, name in enumerate(STAGES)}
+
     # -- lm_head ---------------------------------------------------------
-    def lmhead(self, hidden, weight, softcap_value: float = 0.0, out=None):
+    def lmhead(self, hidden, weight, softcap_value: float = 0.0, out=None, stream: Optional[int] = None):
         torch = self.torch
         m, width = int(hidden.shape[0]), int(hidden.shape[1])
         if out is None:
             out = torch.empty((m, self.vocab), dtype=torch.float32, device=self.device)
         self._check(self.lib.gs_lmhead(self.ctx, C.c_void_p(hidden.data_ptr()), C.c_void_p(weight.data_ptr()), m,
-                                       width, float(softcap_value), C.c_void_p(out.data_ptr()), None))
+                                       width, float(softcap_value), C.c_void_p(out.data_ptr()),
+                                       C.c_void_p(stream or 0)))
         return out
+
+    def lmhead_sample_launch(self, hidden, weight, softcap_value: float, logits_scratch, batch: Batch,
+                             stream: Optional[int] = None):
+        """gs_lmhead_sample: lm_head into `logits_scratch`, then the sampler on it."""
+        width = int(hidden.shape[1])
+        self._check(self.lib.gs_lmhead_sample(self.ctx, C.c_void_p(hidden.data_ptr()), C.c_void_p(weight.data_ptr()),
+                                              width, float(softcap_value), C.c_void_p(logits_scratch.data_ptr()),
+                                              C.byref(batch), C.c_void_p(stream or 0)))
 
 
 _default_sampler: Optional[Sampler] = None

@@ -200,6 +200,22 @@ int gs_lmhead(gs_context* ctx, const void* hidden, const void* weight, int32_t m
 int gs_lmhead_sample(gs_context* ctx, const void* hidden, const void* weight, int32_t width, float softcap,
                      float* logits_scratch, const gs_batch* batch, void* stream);
 
+/* Kernel timing with HIP events: replaces the WebGPU timestamp queries of
+ * measureGpuDispatches (src/webgpu/gpu-timestamp.ts:1-56). After
+ * gs_timing_begin(ctx, max_calls), the next max_calls gs_sample /
+ * gs_lmhead_sample calls record an event before and after each of their
+ * kernels, on the stream they launch on. gs_timing_end waits for those
+ * events, writes per stage the summed milliseconds (stage_ms[GS_STAGE_COUNT])
+ * and the number of calls that ran that stage (calls[GS_STAGE_COUNT]), and
+ * stops timing. The events add a few microseconds per call. */
+#define GS_STAGE_LMHEAD 0 /* lmhead_kernel */
+#define GS_STAGE_SCAN 1   /* scan_kernel: the one HBM pass over the logits */
+#define GS_STAGE_FINISH 2 /* finish_kernel: per-row merge, filters and draw */
+#define GS_STAGE_EXACT 3  /* exact_kernel: sequential replay of queued rows */
+#define GS_STAGE_COUNT 4
+int gs_timing_begin(gs_context* ctx, int32_t max_calls);
+int gs_timing_end(gs_context* ctx, double* stage_ms, int32_t* calls);
+
 #ifdef __cplusplus
 }
 #endif
