@@ -122,6 +122,7 @@ int gs_create(int device, int32_t vocab_size, int32_t max_rows, gs_context** out
   if (!out) return GS_ERR_INVALID_ARGUMENT;
   *out = nullptr;
   if (vocab_size <= 0 || max_rows <= 0) return GS_ERR_INVALID_ARGUMENT;
+  if (vocab_size > kMaxVocab) return GS_ERR_UNSUPPORTED;
   int n = 0;
   if (hipGetDeviceCount(&n) != hipSuccess || n <= 0) return GS_ERR_NO_DEVICE;
   if (device < 0 || device >= n) return GS_ERR_NO_DEVICE;
@@ -254,7 +255,8 @@ int gs_sample(gs_context* ctx, const gs_batch* b, void* stream) {
   a.exact_scratch = ctx->d_exact;
   a.exact_slot_bytes = ctx->exact_slot_bytes;
   a.exact_capacity = ctx->exact_cap;
-  GS_HIP(ctx, hipMemsetAsync(ctx->d_queue, 0, 2 * sizeof(uint32_t), s));
+  // the exact-path queue is reset by the chunk scan's first workgroup: no
+  // memset node, so the call stays capturable and one launch cheaper
   const int32_t slot = timing_slot(ctx);
   stage_mark(ctx, slot, GS_STAGE_SCAN, 0, s);
   launch_scan(a, s);

@@ -42,22 +42,6 @@ __device__ __forceinline__ double block_scan_f64(double v, double* s_w, double* 
   return incl + off;
 }
 
-__device__ void block_sort_desc(uint64_t* s, int n) {
-  for (int k = 2; k <= n; k <<= 1) {
-    for (int j = k >> 1; j > 0; j >>= 1) {
-      for (int i = threadIdx.x; i < n; i += kFinishThreads) {
-        const int p = i ^ j;
-        if (p > i) {
-          const uint64_t x = s[i], y = s[p];
-          const bool desc = (i & k) == 0;
-          if (desc ? (x < y) : (x > y)) { s[i] = y; s[p] = x; }
-        }
-      }
-      __syncthreads();
-    }
-  }
-}
-
 // (value key desc, id asc) on parallel arrays
 __device__ __forceinline__ bool ranks_before(uint64_t ka, uint32_t ia, uint64_t kb, uint32_t ib) {
   return ka > kb || (ka == kb && ia < ib);
@@ -83,6 +67,75 @@ __device__ void block_sort_pairs_desc(uint64_t* key, uint32_t* id, int n) {
   }
 }
 
+// Bitonic sort, descending, of kFinishThreads * E entries; thread t holds
+// entries t*E .. t*E+E-1 in v[]. Stages whose partner is in the same thread
+// compare registers, stages within a wave exchange through cross-lane
+// shuffles, and only the stages that cross waves go through LDS -- two
+// buffers alternate, so each such stage needs one barrier.
+template <int E>
+__device__ void sort_desc_regs(uint64_t (&v)[E], uint64_t* buf0, uint64_t* buf1) {
+  const int t = threadIdx.x;
+  constexpr int n2 = kFinishThreads * E;
+  int lds_stage = 0;
+  for (int k = 2; k <= n2; k <<= 1) {
+    for (int j = k >> 1; j > 0; j >>= 1) {
+      if (j < E) {
+#pragma unroll
+        for (int q = 0; q < E; ++q) {
+          const int qp = q ^ j;
+          if (qp > q) {
+            const int i = t * E + q;
+            const uint64_t x = v[q], y = v[qp];
+            const uint64_t hi = x > y ? x : y, lo = x > y ? y : x;
+            const bool desc = (i & k) == 0;
+            v[q] = desc ? hi : lo;
+            v[qp] = desc ? lo : hi;
+          }
+        }
+      } else if (j < 64 * E) {
+        const int m = j / E;  // partner lane distance
+#pragma unroll
+        for (int q = 0; q < E; ++q) {
+          const int i = t * E + q;
+          const uint64_t y = shfl_xor_u64(v[q], m);
+          const bool keep_max = ((i & j) == 0) == ((i & k) == 0);
+          v[q] = keep_max ? (v[q] > y ? v[q] : y) : (v[q] > y ? y : v[q]);
+        }
+      } else {
+        uint64_t* buf = (lds_stage++ & 1) ? buf1 : buf0;
+#pragma unroll
+        for (int q = 0; q < E; ++q) buf[t * E + q] = v[q];
+        __syncthreads();
+#pragma unroll
+        for (int q = 0; q < E; ++q) {
+          const int i = t * E + q;
+          const uint64_t y = buf[i ^ j];
+          const bool keep_max = ((i & j) == 0) == ((i & k) == 0);
+          v[q] = keep_max ? (v[q] > y ? v[q] : y) : (v[q] > y ? y : v[q]);
+        }
+      }
+    }
+  }
+}
+
+// Sorts s[0..n) descending (n <= kFinishCap), zero-padded; buf is kFinishCap
+// entries of scratch. Ends with a barrier.
+template <int E>
+__device__ void sort_region(uint64_t* s, int n, uint64_t* buf) {
+  uint64_t v[E];
+#pragma unroll
+  for (int q = 0; q < E; ++q) {
+    const int i = threadIdx.x * E + q;
+    v[q] = i < n ? s[i] : 0ull;
+  }
+  __syncthreads();  // s is the first LDS buffer of the sort
+  sort_desc_regs<E>(v, s, buf);
+  __syncthreads();
+#pragma unroll
+  for (int q = 0; q < E; ++q) s[threadIdx.x * E + q] = v[q];
+  __syncthreads();
+}
+
 __device__ __forceinline__ int pow2_at_least(int n) {
   int p = 1;
   while (p < n) p <<= 1;
@@ -91,15 +144,17 @@ __device__ __forceinline__ int pow2_at_least(int n) {
 
 struct Shared {
   uint64_t sorted[kFinishCap];        // non-special entries of the complete region
-  uint32_t hash_ids[kHashSize];
-  uint32_t hash_counts[kHashSize];
+  uint32_t hash_ids[kHashSize];       // after the specials are evaluated: the in-region
+  uint32_t hash_counts[kHashSize];    // specials (keys in hash_ids, ids in hash_counts)
   uint64_t sp_key[kSpecialCap];       // specials: f64 key of their value
   uint32_t sp_id[kSpecialCap];
-  double cand_p[kFinishCap];          // merged candidates: probability
+  double cand_p[kFinishCap];          // merged candidates: probability (sort scratch before)
   uint32_t cand_id[kFinishCap];
+  double c_sum[kFinishMaxChunks];     // chunk statistics
+  uint32_t c_max[kFinishMaxChunks];
+  uint16_t c_nsub[kFinishMaxChunks * kScanWaves];
   double wsum[kWaves];
   double wtmp[kWaves];
-  double total;
   double vmax;
   uint32_t flags;
   uint32_t max_key;
@@ -108,7 +163,6 @@ struct Shared {
   uint32_t n_sorted;
   uint32_t n_special;
   uint32_t n_sp_in;
-  uint32_t n_cand;
   uint32_t route_exact;
   uint32_t status_flags;
   uint32_t first_idx;
@@ -123,9 +177,13 @@ __device__ void enqueue_exact(const SampleArgs& a, int64_t row, uint32_t flags) 
   a.results[row].flags = flags;
 }
 
+constexpr int kSubThreads = 8;                        // threads that read one wave sub-list
+constexpr int kSubPerThread = kSubCap / kSubThreads;  // slots each of them reads
+constexpr int kSlotsPerThread = kHashSize / kFinishThreads;
+
 __global__ __launch_bounds__(kFinishThreads) void finish_kernel(SampleArgs a) {
   __shared__ Shared S;
-  const int tid = threadIdx.x;
+  const int tid = threadIdx.x, lane = tid & 63;
   const int64_t row = blockIdx.x;
   const gs_row_config cfg = a.configs[row];
   const Plan plan = plan_row(cfg);
@@ -146,15 +204,17 @@ __global__ __launch_bounds__(kFinishThreads) void finish_kernel(SampleArgs a) {
   for (int h = tid; h < kHashSize; h += kFinishThreads) { S.hash_ids[h] = 0xFFFFFFFFu; S.hash_counts[h] = 0; }
   __syncthreads();
 
-  // ---- 1. chunk statistics
+  // ---- 1. chunk statistics into LDS, and the row's distinct special ids
   const ChunkStat* st = a.stats + row * a.n_chunks;
   for (int c = tid; c < a.n_chunks; c += kFinishThreads) {
     const ChunkStat s = st[c];
+    S.c_sum[c] = s.sum;
+    S.c_max[c] = s.max_key;
+    for (int w = 0; w < kScanWaves; ++w) S.c_nsub[c * kScanWaves + w] = s.n_sub[w];
     atomicOr(&S.flags, s.flags);
     atomicMax(&S.max_key, s.max_key);
     if (s.truncated) { atomicMax(&S.thr_max, s.threshold); atomicOr(&S.any_truncated, 1u); }
   }
-  // ---- 2. distinct special ids
   {
     int64_t w0, w1;
     history_window(a, row, cfg, &w0, &w1);
@@ -180,32 +240,49 @@ __global__ __launch_bounds__(kFinishThreads) void finish_kernel(SampleArgs a) {
     if (tid == 0) enqueue_exact(a, row, 0u);
     return;
   }
-  // evaluate every special exactly: mask / termination rules, then penalties
-  for (int h = tid; h < kHashSize; h += kFinishThreads) {
-    const uint32_t id = S.hash_ids[h];
-    if (id == 0xFFFFFFFFu) continue;
-    const uint32_t packed = S.hash_counts[h];
-    const uint32_t count = packed & 0xFFFFFFu, kinds = packed >> 24;
-    const uint32_t idx = atomicAdd(&S.n_special, 1u);
-    if (idx >= (uint32_t)kSpecialCap) continue;
-    float raw = load_logit(a, row, id);
-    if (cfg.softcap > 0) raw = gsm::softcap_f32(raw, cfg.softcap);
-    bool allowed = true;
-    if (constrained) {
-      const bool term = kinds & GS_FORCED_TERMINATION;
-      const bool extra = kinds & GS_FORCED_EXTRA;
-      allowed = term ? cfg.accepting != 0 : (extra || mask_allows(a, slot, id));
+  // evaluate every special exactly: mask / termination rules, then penalties.
+  // Each thread owns kSlotsPerThread hash slots; their logits and mask words
+  // are loaded together before any is used.
+  {
+    uint32_t hid[kSlotsPerThread], hpk[kSlotsPerThread], mw[kSlotsPerThread];
+    float raw[kSlotsPerThread];
+#pragma unroll
+    for (int r = 0; r < kSlotsPerThread; ++r) {
+      hid[r] = S.hash_ids[tid + r * kFinishThreads];
+      hpk[r] = S.hash_counts[tid + r * kFinishThreads];
     }
-    if (allowed) atomicOr(&S.special_legal, 1u);
-    if (allowed && !(raw < __builtin_inff())) atomicOr(&S.flags, kChunkNonFinite);
-    double x = allowed ? (double)raw : -__builtin_inf();
-    if (count > 0) {
-      x = x < 0 ? x * cfg.repetition_penalty : x / cfg.repetition_penalty;
-      x -= cfg.presence_penalty + (double)count * cfg.frequency_penalty;
+#pragma unroll
+    for (int r = 0; r < kSlotsPerThread; ++r) {
+      const bool used = hid[r] != 0xFFFFFFFFu;
+      raw[r] = used ? load_logit(a, row, hid[r]) : 0.0f;
+      mw[r] = used && constrained ? a.mask_table[(int64_t)slot * a.mask_words + (hid[r] >> 5)] : 0u;
     }
-    const double v = greedy ? x : x / T;
-    S.sp_key[idx] = f64_key(v);
-    S.sp_id[idx] = id;
+#pragma unroll
+    for (int r = 0; r < kSlotsPerThread; ++r) {
+      const uint32_t id = hid[r];
+      if (id == 0xFFFFFFFFu) continue;
+      const uint32_t count = hpk[r] & 0xFFFFFFu, kinds = hpk[r] >> 24;
+      const uint32_t idx = atomicAdd(&S.n_special, 1u);
+      if (idx >= (uint32_t)kSpecialCap) continue;
+      float x32 = raw[r];
+      if (cfg.softcap > 0) x32 = gsm::softcap_f32(x32, cfg.softcap);
+      bool allowed = true;
+      if (constrained) {
+        const bool term = kinds & GS_FORCED_TERMINATION;
+        const bool extra = kinds & GS_FORCED_EXTRA;
+        allowed = term ? cfg.accepting != 0 : (extra || ((mw[r] >> (id & 31)) & 1u));
+      }
+      if (allowed) atomicOr(&S.special_legal, 1u);
+      if (allowed && !(x32 < __builtin_inff())) atomicOr(&S.flags, kChunkNonFinite);
+      double x = allowed ? (double)x32 : -__builtin_inf();
+      if (count > 0) {
+        x = x < 0 ? x * cfg.repetition_penalty : x / cfg.repetition_penalty;
+        x -= cfg.presence_penalty + (double)count * cfg.frequency_penalty;
+      }
+      const double v = greedy ? x : x / T;
+      S.sp_key[idx] = f64_key(v);
+      S.sp_id[idx] = id;
+    }
   }
   __syncthreads();
   if (S.n_special > (uint32_t)kSpecialCap) {
@@ -257,11 +334,14 @@ __global__ __launch_bounds__(kFinishThreads) void finish_kernel(SampleArgs a) {
     }
   }
 
+  const uint64_t* lists = a.lists + row * a.n_chunks * kGatherCap;
+
   // ---- greedy: first maximum of the penalised logits (sampling.ts:31,92-96)
   if (greedy) {
-    const uint64_t* lists = a.lists + row * a.n_chunks * kGatherCap;
     for (int c = tid; c < a.n_chunks; c += kFinishThreads) {
-      if (st[c].n_list) atomicMax((unsigned long long*)&S.best_entry, (unsigned long long)lists[(int64_t)c * kGatherCap]);
+      if (S.c_nsub[c * kScanWaves]) {
+        atomicMax((unsigned long long*)&S.best_entry, (unsigned long long)list_rank(lists[(int64_t)c * kGatherCap]));
+      }
     }
     __syncthreads();
     if (tid == 0) {
@@ -286,17 +366,43 @@ __global__ __launch_bounds__(kFinishThreads) void finish_kernel(SampleArgs a) {
     return;
   }
 
-  // ---- 3. the complete region of the chunk lists
-  const uint32_t thr = S.thr_max;  // 0 when no chunk was truncated: every finite logit is listed
+  // ---- 2. the complete region of the chunk lists: every listed entry with
+  // key >= the highest truncated chunk's threshold (0 when no chunk was
+  // truncated: every finite logit is listed). kSubThreads threads read each
+  // wave sub-list, all their loads in flight together; kept entries are
+  // appended with one LDS atomic per wave.
+  const uint32_t thr = S.thr_max;
   {
-    const uint64_t* lists = a.lists + row * a.n_chunks * kGatherCap;
-    for (int c = 0; c < a.n_chunks; ++c) {
-      const uint32_t n = st[c].n_list;
-      for (uint32_t i = tid; i < n; i += kFinishThreads) {
-        const uint64_t e = lists[(int64_t)c * kGatherCap + i];
-        if (entry_key(e) >= thr) {
-          const uint32_t p = atomicAdd(&S.n_sorted, 1u);
-          if (p < (uint32_t)kFinishCap) S.sorted[p] = e;
+    const int n_subs = a.n_chunks * kScanWaves;
+    for (int s0 = 0; s0 < n_subs; s0 += kFinishThreads / kSubThreads) {
+      const int sl = s0 + tid / kSubThreads;
+      const int k0 = tid % kSubThreads;
+      const int cnt = sl < n_subs ? (int)S.c_nsub[sl] : 0;
+      uint64_t v[kSubPerThread];
+#pragma unroll
+      for (int q = 0; q < kSubPerThread; ++q) {
+        const int k = k0 + q * kSubThreads;
+        v[q] = k < cnt ? lists[(int64_t)sl * kSubCap + k] : 0ull;
+      }
+      uint32_t keep = 0;
+#pragma unroll
+      for (int q = 0; q < kSubPerThread; ++q) {
+        if (k0 + q * kSubThreads < cnt) {
+          v[q] = list_rank(v[q]);
+          if (entry_key(v[q]) >= thr) keep |= 1u << q;
+        }
+      }
+      const uint32_t mine = (uint32_t)__popc(keep);
+      const uint32_t incl = wave_scan_u32(mine, lane);
+      uint32_t base = 0;
+      if (lane == 63) base = atomicAdd(&S.n_sorted, incl);
+      base = (uint32_t)__shfl((int)base, 63, 64);
+      uint32_t pos = base + incl - mine;
+#pragma unroll
+      for (int q = 0; q < kSubPerThread; ++q) {
+        if ((keep >> q) & 1u) {
+          if (pos < (uint32_t)kFinishCap) S.sorted[pos] = v[q];
+          ++pos;
         }
       }
     }
@@ -307,23 +413,31 @@ __global__ __launch_bounds__(kFinishThreads) void finish_kernel(SampleArgs a) {
     return;
   }
   const int n_ns = (int)S.n_sorted;
-  {
-    const int n2 = pow2_at_least(n_ns);
-    for (int i = n_ns + tid; i < n2; i += kFinishThreads) S.sorted[i] = 0;
-    __syncthreads();
-    block_sort_desc(S.sorted, n2);
-    const int m2 = pow2_at_least(n_sp);
-    for (int i = n_sp + tid; i < m2; i += kFinishThreads) { S.sp_key[i] = 0; S.sp_id[i] = 0xFFFFFFFFu; }
-    __syncthreads();
-    block_sort_pairs_desc(S.sp_key, S.sp_id, m2);
-  }
-  // specials inside the complete region: value >= value of the threshold key
+  uint64_t* scratch = (uint64_t*)S.cand_p;
+  if (n_ns <= kFinishThreads) sort_region<1>(S.sorted, n_ns, scratch);
+  else if (n_ns <= 2 * kFinishThreads) sort_region<2>(S.sorted, n_ns, scratch);
+  else sort_region<4>(S.sorted, n_ns, scratch);
+
+  // specials inside the complete region (value >= the threshold's value),
+  // moved into the dead hash table and sorted there; usually none or a few
+  uint64_t* in_key = (uint64_t*)S.hash_ids;
+  uint32_t* in_id = S.hash_counts;
   const uint64_t region_floor = thr ? f64_key((double)key_f32(thr) / T) : 0;
   for (int i = tid; i < n_sp; i += kFinishThreads) {
-    if (S.sp_key[i] >= region_floor) atomicAdd(&S.n_sp_in, 1u);
+    if (S.sp_key[i] >= region_floor) {
+      const uint32_t p = atomicAdd(&S.n_sp_in, 1u);
+      in_key[p] = S.sp_key[i];
+      in_id[p] = S.sp_id[i];
+    }
   }
   __syncthreads();
-  const int n_sp_in = (int)S.n_sp_in;  // specials are sorted, so these are the first n_sp_in
+  const int n_sp_in = (int)S.n_sp_in;
+  {
+    const int m2 = pow2_at_least(n_sp_in);
+    for (int i = n_sp_in + tid; i < m2; i += kFinishThreads) { in_key[i] = 0; in_id[i] = 0xFFFFFFFFu; }
+    __syncthreads();
+    if (m2 > 1) block_sort_pairs_desc(in_key, in_id, m2);
+  }
   const int n_cand = n_ns + n_sp_in;
   if (n_cand > kFinishCap || n_cand == 0) {
     if (tid == 0) enqueue_exact(a, row, 0u);
@@ -335,7 +449,7 @@ __global__ __launch_bounds__(kFinishThreads) void finish_kernel(SampleArgs a) {
   if (tid == 0) {
     double v0 = -__builtin_inf();
     if (n_ns) v0 = (double)key_f32(entry_key(S.sorted[0])) / T;
-    if (n_sp && key_f64(S.sp_key[0]) > v0) v0 = key_f64(S.sp_key[0]);
+    if (n_sp_in && key_f64(in_key[0]) > v0) v0 = key_f64(in_key[0]);
     S.vmax = v0;
   }
   for (int i = tid; i < n_ns; i += kFinishThreads) {
@@ -345,14 +459,14 @@ __global__ __launch_bounds__(kFinishThreads) void finish_kernel(SampleArgs a) {
     int lo = 0, hi = n_sp_in;  // specials ranked before this entry
     while (lo < hi) {
       const int mid = (lo + hi) >> 1;
-      if (ranks_before(S.sp_key[mid], S.sp_id[mid], k, id)) lo = mid + 1; else hi = mid;
+      if (ranks_before(in_key[mid], in_id[mid], k, id)) lo = mid + 1; else hi = mid;
     }
     S.cand_p[i + lo] = key_f64(k);
     S.cand_id[i + lo] = id;
   }
   for (int j = tid; j < n_sp_in; j += kFinishThreads) {
-    const uint64_t k = S.sp_key[j];
-    const uint32_t id = S.sp_id[j];
+    const uint64_t k = in_key[j];
+    const uint32_t id = in_id[j];
     int lo = 0, hi = n_ns;  // non-specials ranked before this special
     while (lo < hi) {
       const int mid = (lo + hi) >> 1;
@@ -370,14 +484,18 @@ __global__ __launch_bounds__(kFinishThreads) void finish_kernel(SampleArgs a) {
     if (tid == 0) enqueue_exact(a, row, 0u);
     return;
   }
+  // Margin for the comparisons that depend on the normaliser (the top-p cut):
+  // this total and the reference's differ by summation order (kNearTie) and by
+  // the reference's rounding of l/T and of l/T - M in every term, at most
+  // 2^-52 (2|M| + 60) relative for the terms that matter.
+  const double margin = kNearTie + 0x1p-52 * (2.0 * (M < 0 ? -M : M) + 60.0);
 
   // ---- normaliser: chunk partial sums rescaled to M, plus every special
   double part = 0.0;
   for (int c = tid; c < a.n_chunks; c += kFinishThreads) {
-    const ChunkStat s = st[c];
-    if (s.max_key > kKeyNegInf && s.sum > 0) {
-      part += s.sum * gsm::js_exp((double)key_f32(s.max_key) / T - M);
-    }
+    const double csum = S.c_sum[c];
+    const uint32_t cmax = S.c_max[c];
+    if (cmax > kKeyNegInf && csum > 0) part += csum * gsm::js_exp((double)key_f32(cmax) / T - M);
   }
   for (int i = tid; i < n_sp; i += kFinishThreads) part += gsm::js_exp(key_f64(S.sp_key[i]) - M);
   double total;
@@ -441,7 +559,7 @@ __global__ __launch_bounds__(kFinishThreads) void finish_kernel(SampleArgs a) {
       const double cum = base + local[q];
       if (cum >= cfg.top_p) atomicMin(&S.first_idx, (uint32_t)i);
       const double d = cum >= cfg.top_p ? cum - cfg.top_p : cfg.top_p - cum;
-      if (d < kNearTie) atomicOr(&S.route_exact, 4u);
+      if (d < margin) atomicOr(&S.route_exact, 4u);
     }
     __syncthreads();
     int cut = (int)S.first_idx;  // index of the item that reached topP

@@ -11,13 +11,17 @@ namespace gs {
 
 // ---------------------------------------------------------------- layout
 constexpr int kScanThreads = 256;                 // one workgroup = 4 wave64
+constexpr int kScanWaves = kScanThreads / 64;
 constexpr int kElemsPerThread = 32;
 constexpr int kChunk = kScanThreads * kElemsPerThread;  // 8192 logits per chunk
-constexpr int kGatherCap = 256;                   // list entries a chunk may emit
+constexpr int kSubCap = 128;                      // list entries each wave of a chunk may emit
+constexpr int kGatherCap = kSubCap * kScanWaves;  // 512 list slots per chunk
 constexpr int kMaxFastK = 64;                     // top-k handled by the one-pass path
 constexpr int kTopPListL = 64;                    // rank depth per chunk in top-p mode
 constexpr int kFinishThreads = 1024;
 constexpr int kFinishCap = 4096;                  // sorted candidate region in the finish kernel
+constexpr int kFinishMaxChunks = 256;             // chunk statistics the finish keeps in LDS
+constexpr int64_t kMaxVocab = (int64_t)kFinishMaxChunks * kChunk;  // 2097152 ids
 constexpr int kSpecialCap = 2048;                 // distinct (history window + forced) ids per row
 constexpr int kHashSize = 4096;                   // open-addressing table for those ids
 constexpr int kExactThreads = 1024;
@@ -90,13 +94,23 @@ __host__ __device__ __forceinline__ Plan plan_row(const gs_row_config& c) {
 // ------------------------------------------------------- per-chunk state
 struct ChunkStat {
   double sum;          // sum of e^((l - lmax)/T) over finite non-special logits of the chunk
-  uint32_t max_key;    // key of lmax (0: no non-special logit, kKeyNegInf: all masked)
-  uint32_t n_list;     // entries written to the chunk's list
+  uint32_t max_key;    // key of lmax (kKeyNegInf or below: no finite non-special logit)
+  uint32_t n_list;     // entries written to the chunk's list (all sub-lists)
   uint32_t n_finite;   // finite non-special logits
   uint32_t threshold;  // the list holds every finite non-special logit with key >= threshold
   uint32_t truncated;  // some finite logit lies below the threshold
   uint32_t flags;      // kChunkOverflow | kChunkNonFinite
+  uint16_t n_sub[kScanWaves];  // entries of wave w's sub-list, which starts at slot w * kSubCap
 };
+
+// A list slot holds the logit's f32 bits (after softcap) high and its id low;
+// list_rank turns it into a pack_entry (value desc, id asc) ordering key.
+__host__ __device__ __forceinline__ uint64_t list_slot(uint32_t bits, uint32_t id) {
+  return ((uint64_t)bits << 32) | id;
+}
+__host__ __device__ __forceinline__ uint64_t list_rank(uint64_t slot) {
+  return pack_entry(f32_key(__builtin_bit_cast(float, (uint32_t)(slot >> 32))), (uint32_t)slot);
+}
 constexpr uint32_t kChunkOverflow = 1u;
 constexpr uint32_t kChunkNonFinite = 2u;
 

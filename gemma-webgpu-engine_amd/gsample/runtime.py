@@ -341,11 +341,16 @@ class Sampler:
         return b, keep
 
     def launch(self, batch: Batch, stream: Optional[int] = None):
+        """gs_sample on `stream` (a hipStream_t handle), else on the context's
+        stream after torch's current stream has drained."""
+        if stream is None:
+            self.torch.cuda.current_stream(self.device).synchronize()
         self._check(self.lib.gs_sample(self.ctx, C.byref(batch), C.c_void_p(stream or 0)))
 
     def sample(self, logits, configs: np.ndarray, histories=None, forced=None, mask_table=None,
                raise_on_failure: bool = True) -> SampleOutput:
         b, keep = self.prepare(logits, configs, histories, forced, mask_table)
+        self.torch.cuda.current_stream(self.device).synchronize()
         out = np.zeros(b.rows, dtype=RESULT_DTYPE)
         st = self.lib.gs_sample_sync(self.ctx, C.byref(b), _np_ptr(out))
         if st != GS_OK and raise_on_failure:
@@ -415,15 +420,23 @@ class Sampler:
         m, width = int(hidden.shape[0]), int(hidden.shape[1])
         if out is None:
             out = torch.empty((m, self.vocab), dtype=torch.float32, device=self.device)
+        if stream is None:
+            # the context's stream does not order against torch's: finish torch's
+            # work on the inputs first and the kernel before `out` is handed back
+            torch.cuda.current_stream(self.device).synchronize()
         self._check(self.lib.gs_lmhead(self.ctx, C.c_void_p(hidden.data_ptr()), C.c_void_p(weight.data_ptr()), m,
                                        width, float(softcap_value), C.c_void_p(out.data_ptr()),
                                        C.c_void_p(stream or 0)))
+        if stream is None:
+            self.synchronize()
         return out
 
     def lmhead_sample_launch(self, hidden, weight, softcap_value: float, logits_scratch, batch: Batch,
                              stream: Optional[int] = None):
         """gs_lmhead_sample: lm_head into `logits_scratch`, then the sampler on it."""
         width = int(hidden.shape[1])
+        if stream is None:
+            self.torch.cuda.current_stream(self.device).synchronize()
         self._check(self.lib.gs_lmhead_sample(self.ctx, C.c_void_p(hidden.data_ptr()), C.c_void_p(weight.data_ptr()),
                                               width, float(softcap_value), C.c_void_p(logits_scratch.data_ptr()),
                                               C.byref(batch), C.c_void_p(stream or 0)))

@@ -135,7 +135,9 @@ float gs_softcap(float x, double cap);
  * be NULL; gs_last_error(NULL) then holds the message. */
 int gs_validate_configs(gs_context* ctx, const gs_row_config* configs, int32_t n);
 
-/* Context: device ordinal, vocab size V, the largest batch it will see.
+/* Context: device ordinal, vocab size V (1 .. 2097152; larger returns
+ * GS_ERR_UNSUPPORTED), the largest batch it will see. Calls on one context
+ * share its scratch memory, so they must be ordered on one stream.
  * (no reference counterpart: the reference keeps its WebGPU device in a
  *  module singleton, src/webgpu/device.ts:4-40) */
 int gs_create(int device, int32_t vocab_size, int32_t max_rows, gs_context** out);
