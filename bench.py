@@ -57,6 +57,9 @@ def parse_args():
                     choices=["penalties", "single_row", "heavy_tail", "constrained", "lmhead"])
     ap.add_argument("--cpu-rows", type=int, default=64, help="rows of the CPU baseline sample")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--copy-probe", action="store_true",
+                    help="also time a plain device copy of the logits' byte count (achievable HBM bandwidth; "
+                         "the reference kernel for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE)")
     return ap.parse_args()
 
 
@@ -297,6 +300,25 @@ def main():
     if mfma_tflops is not None:
         roofline["mfma_tflops"] = round(mfma_tflops, 1)
         roofline["mfma_frac_bf16_dense"] = round(mfma_tflops / BF16_PEAK_TFLOPS, 4)
+
+    if args.copy_probe:
+        # a plain copy of the same byte count: reads and writes each byte once
+        src = wl["keep"][0]
+        dst = torch.empty_like(src)
+        with torch.cuda.stream(stream):
+            for _ in range(3):
+                dst.copy_(src)
+            c0, c1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            c0.record(stream)
+            for _ in range(args.steps):
+                dst.copy_(src)
+            c1.record(stream)
+        torch.cuda.synchronize()
+        copy_ms = c0.elapsed_time(c1) / args.steps
+        nbytes = src.numel() * src.element_size()
+        roofline["copy_probe"] = {"bytes_read": nbytes, "bytes_written": nbytes, "avg_us": round(copy_ms * 1000, 2),
+                                  "gbps_read_plus_write": round(2 * nbytes / (copy_ms * 1e6), 1)}
+        del dst
 
     base, parity = (None, None)
     if not args.no_cpu:

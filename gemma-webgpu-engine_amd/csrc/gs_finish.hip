@@ -3,28 +3,40 @@
 //
 // It rebuilds, for one row, exactly the part of the reference's sorted
 // candidate list that the filters can reach (src/runtime/sampling.ts:33-64):
-//   1. merges the chunk maxima and partial sums into the softmax normaliser;
-//   2. evaluates the row's distinct special ids exactly: penalty-window ids
+//   1. evaluates the row's distinct special ids exactly: penalty-window ids
 //      with their counts (sampling.ts:21-30) and, for constrained rows, the
 //      termination / extra ids of selectConstrainedToken
 //      (src/runtime/gemma-session.ts:1305-1329);
-//   3. keeps the chunk-list entries whose key is at or above the highest
+//   2. keeps the chunk-list entries whose key is at or above the highest
 //      truncated chunk's threshold -- the region where the union of the
-//      lists is complete -- sorts them by (value desc, id asc) and merges in
-//      the specials of that region;
-//   4. applies top-k, min-p and top-p and draws, with the reference's
-//      comparisons, on binary64 probabilities from the bit-exact js_exp.
+//      lists is complete -- and merges the chunk maxima and partial sums
+//      with the specials into the softmax normaliser;
+//   3. ranks the top 64 of that region (per-wave register sorts, then a
+//      bitonic tree merge), merges in the specials of the region, and applies
+//      top-k, min-p and top-p and the draw in one wave, with the reference's
+//      comparisons on binary64 probabilities from the bit-exact js_exp;
+//   4. when the filters reach past the top 64 (top-p or min-p cuts deep in
+//      the list), sorts the whole region and repeats step 3 block-wide.
 // The normaliser is summed in a different order from the reference's
 // sequential loop, so every comparison that decides the outcome is checked
-// against a 1e-10 relative margin; rows that fail a margin, need candidates
-// outside the complete region, or hold non-finite logits are queued for the
-// exact kernel, which replays the reference step by step.
+// against a margin that bounds the difference; rows that fail a margin, need
+// candidates outside the complete region, or hold non-finite logits are
+// queued for the exact kernel, which replays the reference step by step.
+//
+// Global loads are issued in two rounds (row inputs, then the list entries
+// and special logits that LDS data locates), so the row's latency is a few
+// memory round trips plus the rank work.
 #include "gs_internal.h"
 
 namespace gs {
 namespace {
 
 constexpr int kWaves = kFinishThreads / 64;
+constexpr int kTopR = 64;                             // entries the fast path ranks exactly
+constexpr int kSubThreads = 8;                        // threads that read one wave sub-list
+constexpr int kSubPerThread = kSubCap / kSubThreads;  // slots each of them reads
+constexpr int kSlotsPerThread = kHashSize / kFinishThreads;
+constexpr int kIdsPerThread = 2;                      // window ids loaded ahead per thread
 
 __device__ __forceinline__ double block_scan_f64(double v, double* s_w, double* total) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -67,6 +79,9 @@ __device__ void block_sort_pairs_desc(uint64_t* key, uint32_t* id, int n) {
   }
 }
 
+__device__ __forceinline__ uint64_t umax64(uint64_t a, uint64_t b) { return a > b ? a : b; }
+__device__ __forceinline__ uint64_t umin64(uint64_t a, uint64_t b) { return a > b ? b : a; }
+
 // Bitonic sort, descending, of kFinishThreads * E entries; thread t holds
 // entries t*E .. t*E+E-1 in v[]. Stages whose partner is in the same thread
 // compare registers, stages within a wave exchange through cross-lane
@@ -86,10 +101,9 @@ __device__ void sort_desc_regs(uint64_t (&v)[E], uint64_t* buf0, uint64_t* buf1)
           if (qp > q) {
             const int i = t * E + q;
             const uint64_t x = v[q], y = v[qp];
-            const uint64_t hi = x > y ? x : y, lo = x > y ? y : x;
             const bool desc = (i & k) == 0;
-            v[q] = desc ? hi : lo;
-            v[qp] = desc ? lo : hi;
+            v[q] = desc ? umax64(x, y) : umin64(x, y);
+            v[qp] = desc ? umin64(x, y) : umax64(x, y);
           }
         }
       } else if (j < 64 * E) {
@@ -99,7 +113,7 @@ __device__ void sort_desc_regs(uint64_t (&v)[E], uint64_t* buf0, uint64_t* buf1)
           const int i = t * E + q;
           const uint64_t y = shfl_xor_u64(v[q], m);
           const bool keep_max = ((i & j) == 0) == ((i & k) == 0);
-          v[q] = keep_max ? (v[q] > y ? v[q] : y) : (v[q] > y ? y : v[q]);
+          v[q] = keep_max ? umax64(v[q], y) : umin64(v[q], y);
         }
       } else {
         uint64_t* buf = (lds_stage++ & 1) ? buf1 : buf0;
@@ -111,7 +125,7 @@ __device__ void sort_desc_regs(uint64_t (&v)[E], uint64_t* buf0, uint64_t* buf1)
           const int i = t * E + q;
           const uint64_t y = buf[i ^ j];
           const bool keep_max = ((i & j) == 0) == ((i & k) == 0);
-          v[q] = keep_max ? (v[q] > y ? v[q] : y) : (v[q] > y ? y : v[q]);
+          v[q] = keep_max ? umax64(v[q], y) : umin64(v[q], y);
         }
       }
     }
@@ -136,6 +150,80 @@ __device__ void sort_region(uint64_t* s, int n, uint64_t* buf) {
   __syncthreads();
 }
 
+// Descending bitonic sort of the 64*E entries one wave holds (lane l holds
+// entries l*E .. l*E+E-1); every stage is a register or cross-lane step.
+template <int E>
+__device__ __forceinline__ void wave_sort_desc_regs(uint64_t (&v)[E]) {
+  const int lane = threadIdx.x & 63;
+#pragma unroll
+  for (int k = 2; k <= 64 * E; k <<= 1) {
+#pragma unroll
+    for (int j = k >> 1; j > 0; j >>= 1) {
+      if (j < E) {
+#pragma unroll
+        for (int q = 0; q < E; ++q) {
+          const int qp = q ^ j;
+          if (qp > q) {
+            const int i = lane * E + q;
+            const uint64_t x = v[q], y = v[qp];
+            const bool desc = (i & k) == 0;
+            v[q] = desc ? umax64(x, y) : umin64(x, y);
+            v[qp] = desc ? umin64(x, y) : umax64(x, y);
+          }
+        }
+      } else {
+#pragma unroll
+        for (int q = 0; q < E; ++q) {
+          const int i = lane * E + q;
+          const uint64_t y = shfl_xor_u64(v[q], j / E);
+          const bool keep_max = ((i & j) == 0) == ((i & k) == 0);
+          v[q] = keep_max ? umax64(v[q], y) : umin64(v[q], y);
+        }
+      }
+    }
+  }
+}
+
+// The kTopR largest entries of s[0..n) (n <= kWaves * 64 * E), descending,
+// into top[0..kTopR) (zero-padded). Each wave sorts its 64*E entries in
+// registers; the 16 wave lists then meet in a tree of bitonic merges (the
+// element-wise maximum of a descending list and a reversed descending list
+// holds the top half as a bitonic sequence, which six half-cleaner steps
+// sort). tmp holds kWaves * 64 entries. Ends with a barrier.
+template <int E>
+__device__ void top_r(const uint64_t* s, int n, uint64_t* tmp, uint64_t* top) {
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  uint64_t v[E];
+#pragma unroll
+  for (int q = 0; q < E; ++q) {
+    const int i = wave * 64 * E + lane * E + q;
+    v[q] = i < n ? s[i] : 0ull;
+  }
+  wave_sort_desc_regs<E>(v);
+#pragma unroll
+  for (int q = 0; q < E; ++q) {
+    const int i = lane * E + q;
+    if (i < 64) tmp[wave * 64 + i] = v[q];
+  }
+  __syncthreads();
+  for (int half = kWaves / 2; half >= 1; half >>= 1) {
+    uint64_t x = 0;
+    if (wave < half) {
+      x = umax64(tmp[wave * 64 + lane], tmp[(wave + half) * 64 + 63 - lane]);
+#pragma unroll
+      for (int j = 32; j > 0; j >>= 1) {
+        const uint64_t y = shfl_xor_u64(x, j);
+        x = (lane & j) == 0 ? umax64(x, y) : umin64(x, y);
+      }
+    }
+    __syncthreads();
+    if (wave < half) tmp[wave * 64 + lane] = x;
+    __syncthreads();
+  }
+  if (tid < kTopR) top[tid] = tmp[tid];
+  __syncthreads();
+}
+
 __device__ __forceinline__ int pow2_at_least(int n) {
   int p = 1;
   while (p < n) p <<= 1;
@@ -153,9 +241,11 @@ struct Shared {
   double c_sum[kFinishMaxChunks];     // chunk statistics
   uint32_t c_max[kFinishMaxChunks];
   uint16_t c_nsub[kFinishMaxChunks * kScanWaves];
+  uint64_t top[kTopR];                // the fast path's ranked non-specials
   double wsum[kWaves];
   double wtmp[kWaves];
-  double vmax;
+  double total;
+  uint64_t sp_max;
   uint32_t flags;
   uint32_t max_key;
   uint32_t thr_max;
@@ -168,6 +258,7 @@ struct Shared {
   uint32_t first_idx;
   uint32_t legal_bits;
   uint32_t special_legal;
+  uint32_t fast_done;
   uint64_t best_entry;
 };
 
@@ -177,13 +268,154 @@ __device__ void enqueue_exact(const SampleArgs& a, int64_t row, uint32_t flags) 
   a.results[row].flags = flags;
 }
 
-constexpr int kSubThreads = 8;                        // threads that read one wave sub-list
-constexpr int kSubPerThread = kSubCap / kSubThreads;  // slots each of them reads
-constexpr int kSlotsPerThread = kHashSize / kFinishThreads;
+__device__ void write_result(const SampleArgs& a, int64_t row, int32_t token, uint32_t flags, double p) {
+  a.results[row].token = token;
+  a.results[row].flags = flags;
+  a.results[row].probability = p;
+}
+
+// value l / T of a non-special list entry, in binary64 as the reference
+// computes it (sampling.ts:34)
+__device__ __forceinline__ double nonspecial_value(uint64_t e, double T) { return (double)key_f32(entry_key(e)) / T; }
+
+// The filters and the draw over the first n_avail (<= 128) candidates, whose
+// probabilities p[] and ids ids[] sit in LDS in list order, evaluated by the
+// calling wave alone. Returns 0 when the row is settled (result written or
+// queued for the exact path), 1 when the cut lies past the candidates and the
+// caller must widen them. `complete`: the candidates are the row's whole list.
+__device__ int filters_and_draw_wave(const SampleArgs& a, int64_t row, const gs_row_config& cfg, const double* p,
+                                     const uint32_t* ids, int n_avail, bool complete, double margin) {
+  const int lane = threadIdx.x & 63;
+  constexpr int kPerLane = 2;  // list index lane*2 + q
+  double pl[kPerLane];
+#pragma unroll
+  for (int q = 0; q < kPerLane; ++q) {
+    const int i = lane * kPerLane + q;
+    pl[q] = i < n_avail ? p[i] : 0.0;
+  }
+  int n = n_avail;
+  bool n_complete = complete;
+  uint32_t exact_why = 0;
+  // ---- top-k (sampling.ts:44)
+  if (cfg.top_k > 0) {
+    if (cfg.top_k < n) n = cfg.top_k;
+    n_complete = true;
+  }
+  // ---- min-p (sampling.ts:45-48)
+  if (cfg.min_p > 0) {
+    const double floor_p = __shfl(pl[0], 0, 64) * cfg.min_p;
+    int first = 0x7FFFFFFF;
+    bool bad = false;
+#pragma unroll
+    for (int q = kPerLane - 1; q >= 0; --q) {
+      const int i = lane * kPerLane + q;
+      if (i < n) {
+        if (!(pl[q] >= floor_p)) first = i;
+        const double d = pl[q] >= floor_p ? pl[q] - floor_p : floor_p - pl[q];
+        if (d < kNearTie * floor_p) bad = true;
+      }
+    }
+    // the list is sorted by value, so probabilities must not increase
+    const double next = __shfl_down(pl[0], 1, 64);
+    if (lane * kPerLane + 1 < n && pl[1] > pl[0]) bad = true;
+    if (lane * kPerLane + 2 < n && next > pl[1]) bad = true;
+    if (__ballot(bad)) exact_why |= 2u;
+    for (int m = 32; m > 0; m >>= 1) {
+      const int o = __shfl_xor(first, m, 64);
+      first = o < first ? o : first;
+    }
+    if (first != 0x7FFFFFFF) {
+      n = first;
+      n_complete = true;
+    }
+    if (n == 0) {
+      if (lane == 0) write_result(a, row, -1, GS_FLAG_EMPTY_CANDIDATES, 0.0);
+      return 0;
+    }
+  }
+  // inclusive prefix sums of the first n probabilities
+  double pre[kPerLane];
+  {
+    double s = 0.0;
+#pragma unroll
+    for (int q = 0; q < kPerLane; ++q) {
+      s += lane * kPerLane + q < n ? pl[q] : 0.0;
+      pre[q] = s;
+    }
+    const double incl = wave_scan_f64(s, lane);
+#pragma unroll
+    for (int q = 0; q < kPerLane; ++q) pre[q] += incl - s;
+  }
+  uint32_t tie = 0;
+  // ---- top-p (sampling.ts:56,82-90)
+  if (cfg.top_p < 1) {
+    int cut = 0x7FFFFFFF;
+    bool near = false;
+#pragma unroll
+    for (int q = kPerLane - 1; q >= 0; --q) {
+      const int i = lane * kPerLane + q;
+      if (i < n) {
+        if (pre[q] >= cfg.top_p) cut = i;
+        const double d = pre[q] >= cfg.top_p ? pre[q] - cfg.top_p : cfg.top_p - pre[q];
+        if (d < margin) near = true;
+      }
+    }
+    for (int m = 32; m > 0; m >>= 1) {
+      const int o = __shfl_xor(cut, m, 64);
+      cut = o < cut ? o : cut;
+    }
+    if (__ballot(near)) exact_why |= 4u;
+    if (cut == 0x7FFFFFFF) {
+      if (!n_complete) return 1;
+      cut = n - 1;
+    } else {
+      // 1e-6 boundary ties, as the reference comparison plan reports them
+      const int cl = cut / kPerLane, cq = cut % kPerLane;
+      const double cum = __shfl(cq == 0 ? pre[0] : pre[1], cl, 64);
+      const double pc = __shfl(cq == 0 ? pl[0] : pl[1], cl, 64);
+      const double prev = cum - pc;
+      if (cum - cfg.top_p <= kTieReport * cfg.top_p || (cut > 0 && cfg.top_p - prev <= kTieReport * cfg.top_p)) {
+        tie = GS_FLAG_TOPP_TIE;
+      }
+    }
+    n = cut + 1;  // prefix sums below the cut are unchanged
+  } else if (!n_complete) {
+    return 1;
+  }
+  // ---- draw (sampling.ts:58-64): first i with prefix_i >= u * sum_{j<n} p_j
+  const int last_lane = (n - 1) / kPerLane, last_q = (n - 1) % kPerLane;
+  const double ctotal = __shfl(last_q == 0 ? pre[0] : pre[1], last_lane, 64);
+  const double u = cfg.rng_mode == GS_RNG_EXPLICIT ? cfg.uniform : gsm::mulberry32_draw(cfg.seed, cfg.draw_index);
+  const double cursor = u * ctotal;
+  int pick = 0x7FFFFFFF;
+  bool near = false;
+#pragma unroll
+  for (int q = kPerLane - 1; q >= 0; --q) {
+    const int i = lane * kPerLane + q;
+    if (i < n) {
+      if (pre[q] >= cursor) pick = i;
+      const double d = pre[q] >= cursor ? pre[q] - cursor : cursor - pre[q];
+      if (d < kNearTie * ctotal) near = true;
+    }
+  }
+  for (int m = 32; m > 0; m >>= 1) {
+    const int o = __shfl_xor(pick, m, 64);
+    pick = o < pick ? o : pick;
+  }
+  if (__ballot(near)) exact_why |= 8u;
+  if (lane == 0) {
+    if (exact_why || pick == 0x7FFFFFFF) {
+      enqueue_exact(a, row, exact_why ? GS_FLAG_NEAR_TIE : 0u);
+    } else {
+      write_result(a, row, (int32_t)ids[pick], tie, p[pick]);
+    }
+  }
+  return 0;
+}
 
 __global__ __launch_bounds__(kFinishThreads) void finish_kernel(SampleArgs a) {
   __shared__ Shared S;
-  const int tid = threadIdx.x, lane = tid & 63;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int64_t row = blockIdx.x;
   const gs_row_config cfg = a.configs[row];
   const Plan plan = plan_row(cfg);
@@ -196,39 +428,51 @@ __global__ __launch_bounds__(kFinishThreads) void finish_kernel(SampleArgs a) {
   const bool constrained = slot >= 0 && slot < a.mask_slots;
   const double T = cfg.temperature;
 
+  // ---- round 1 of global loads: chunk statistics, window and forced ids
+  const ChunkStat* st = a.stats + row * a.n_chunks;
+  ChunkStat cs{};
+  if (tid < a.n_chunks) cs = st[tid];
+  int64_t w0, w1;
+  history_window(a, row, cfg, &w0, &w1);
+  int32_t wid[kIdsPerThread];
+#pragma unroll
+  for (int r = 0; r < kIdsPerThread; ++r) {
+    const int64_t j = w0 + tid + (int64_t)r * kFinishThreads;
+    wid[r] = j < w1 ? a.history_ids[j] : -1;
+  }
+  int64_t f0 = 0, f1 = 0;
+  if (constrained && a.forced_offsets) { f0 = a.forced_offsets[row]; f1 = a.forced_offsets[row + 1]; }
+
   if (tid == 0) {
     S.flags = 0; S.max_key = 0; S.thr_max = 0; S.any_truncated = 0; S.n_sorted = 0; S.n_special = 0;
     S.n_sp_in = 0; S.route_exact = 0; S.status_flags = 0; S.first_idx = 0xFFFFFFFFu; S.legal_bits = 0;
-    S.special_legal = 0; S.best_entry = 0;
+    S.special_legal = 0; S.best_entry = 0; S.sp_max = 0; S.fast_done = 0;
   }
   for (int h = tid; h < kHashSize; h += kFinishThreads) { S.hash_ids[h] = 0xFFFFFFFFu; S.hash_counts[h] = 0; }
   __syncthreads();
 
-  // ---- 1. chunk statistics into LDS, and the row's distinct special ids
-  const ChunkStat* st = a.stats + row * a.n_chunks;
-  for (int c = tid; c < a.n_chunks; c += kFinishThreads) {
-    const ChunkStat s = st[c];
-    S.c_sum[c] = s.sum;
-    S.c_max[c] = s.max_key;
-    for (int w = 0; w < kScanWaves; ++w) S.c_nsub[c * kScanWaves + w] = s.n_sub[w];
-    atomicOr(&S.flags, s.flags);
-    atomicMax(&S.max_key, s.max_key);
-    if (s.truncated) { atomicMax(&S.thr_max, s.threshold); atomicOr(&S.any_truncated, 1u); }
+  // ---- 1. statistics into LDS, distinct special ids into the hash
+  if (tid < a.n_chunks) {
+    S.c_sum[tid] = cs.sum;
+    S.c_max[tid] = cs.max_key;
+    for (int w = 0; w < kScanWaves; ++w) S.c_nsub[tid * kScanWaves + w] = cs.n_sub[w];
+    atomicOr(&S.flags, cs.flags);
+    atomicMax(&S.max_key, cs.max_key);
+    if (cs.truncated) { atomicMax(&S.thr_max, cs.threshold); atomicOr(&S.any_truncated, 1u); }
   }
   {
-    int64_t w0, w1;
-    history_window(a, row, cfg, &w0, &w1);
     SpecialTable tab{S.hash_ids, S.hash_counts};
-    for (int64_t j = w0 + tid; j < w1; j += kFinishThreads) {
+#pragma unroll
+    for (int r = 0; r < kIdsPerThread; ++r) {
+      if (wid[r] >= 0 && wid[r] < a.vocab) special_insert(tab, (uint32_t)wid[r], 0u);
+    }
+    for (int64_t j = w0 + tid + (int64_t)kIdsPerThread * kFinishThreads; j < w1; j += kFinishThreads) {
       const int32_t id = a.history_ids[j];
       if (id >= 0 && id < a.vocab) special_insert(tab, (uint32_t)id, 0u);
     }
-    if (constrained && a.forced_offsets) {
-      const int64_t f0 = a.forced_offsets[row], f1 = a.forced_offsets[row + 1];
-      for (int64_t j = f0 + tid; j < f1; j += kFinishThreads) {
-        const int32_t id = a.forced_ids[j];
-        if (id >= 0 && id < a.vocab) special_insert(tab, (uint32_t)id, (uint32_t)a.forced_kinds[j] & 3u);
-      }
+    for (int64_t j = f0 + tid; j < f1; j += kFinishThreads) {
+      const int32_t id = a.forced_ids[j];
+      if (id >= 0 && id < a.vocab) special_insert(tab, (uint32_t)id, (uint32_t)a.forced_kinds[j] & 3u);
     }
   }
   __syncthreads();
@@ -240,57 +484,109 @@ __global__ __launch_bounds__(kFinishThreads) void finish_kernel(SampleArgs a) {
     if (tid == 0) enqueue_exact(a, row, 0u);
     return;
   }
-  // evaluate every special exactly: mask / termination rules, then penalties.
-  // Each thread owns kSlotsPerThread hash slots; their logits and mask words
-  // are loaded together before any is used.
-  {
-    uint32_t hid[kSlotsPerThread], hpk[kSlotsPerThread], mw[kSlotsPerThread];
-    float raw[kSlotsPerThread];
+
+  // ---- round 2 of global loads: the specials' logits and mask words and
+  // every list entry, all in flight together
+  const uint32_t thr = S.thr_max;  // 0 when no chunk was truncated: every finite logit is listed
+  const uint64_t* lists = a.lists + row * a.n_chunks * kGatherCap;
+  const int n_subs = a.n_chunks * kScanWaves;
+  uint32_t hid[kSlotsPerThread], hpk[kSlotsPerThread], mw[kSlotsPerThread];
+  float raw[kSlotsPerThread];
 #pragma unroll
-    for (int r = 0; r < kSlotsPerThread; ++r) {
-      hid[r] = S.hash_ids[tid + r * kFinishThreads];
-      hpk[r] = S.hash_counts[tid + r * kFinishThreads];
+  for (int r = 0; r < kSlotsPerThread; ++r) {
+    hid[r] = S.hash_ids[tid + r * kFinishThreads];
+    hpk[r] = S.hash_counts[tid + r * kFinishThreads];
+  }
+#pragma unroll
+  for (int r = 0; r < kSlotsPerThread; ++r) {
+    const bool used = hid[r] != 0xFFFFFFFFu;
+    raw[r] = used ? load_logit(a, row, hid[r]) : 0.0f;
+    mw[r] = used && constrained ? a.mask_table[(int64_t)slot * a.mask_words + (hid[r] >> 5)] : 0u;
+  }
+  // list entries of the first kFinishThreads / kSubThreads sub-lists (every
+  // sub-list up to 32 chunks, V <= 262144); wider rows loop below
+  uint64_t lv[kSubPerThread];
+  const int sl0 = tid / kSubThreads, k0 = tid % kSubThreads;
+  const int cnt0 = (!greedy && sl0 < n_subs) ? (int)S.c_nsub[sl0] : 0;
+#pragma unroll
+  for (int q = 0; q < kSubPerThread; ++q) {
+    const int k = k0 + q * kSubThreads;
+    lv[q] = k < cnt0 ? lists[(int64_t)sl0 * kSubCap + k] : 0ull;
+  }
+
+  // evaluate every special exactly: mask / termination rules, then penalties
+#pragma unroll
+  for (int r = 0; r < kSlotsPerThread; ++r) {
+    const uint32_t id = hid[r];
+    if (id == 0xFFFFFFFFu) continue;
+    const uint32_t count = hpk[r] & 0xFFFFFFu, kinds = hpk[r] >> 24;
+    const uint32_t idx = atomicAdd(&S.n_special, 1u);
+    if (idx >= (uint32_t)kSpecialCap) continue;
+    float x32 = raw[r];
+    if (cfg.softcap > 0) x32 = gsm::softcap_f32(x32, cfg.softcap);
+    bool allowed = true;
+    if (constrained) {
+      const bool term = kinds & GS_FORCED_TERMINATION;
+      const bool extra = kinds & GS_FORCED_EXTRA;
+      allowed = term ? cfg.accepting != 0 : (extra || ((mw[r] >> (id & 31)) & 1u));
     }
-#pragma unroll
-    for (int r = 0; r < kSlotsPerThread; ++r) {
-      const bool used = hid[r] != 0xFFFFFFFFu;
-      raw[r] = used ? load_logit(a, row, hid[r]) : 0.0f;
-      mw[r] = used && constrained ? a.mask_table[(int64_t)slot * a.mask_words + (hid[r] >> 5)] : 0u;
+    if (allowed) atomicOr(&S.special_legal, 1u);
+    if (allowed && !(x32 < __builtin_inff())) atomicOr(&S.flags, kChunkNonFinite);
+    double x = allowed ? (double)x32 : -__builtin_inf();
+    if (count > 0) {
+      x = x < 0 ? x * cfg.repetition_penalty : x / cfg.repetition_penalty;
+      x -= cfg.presence_penalty + (double)count * cfg.frequency_penalty;
     }
+    const double v = greedy ? x : x / T;
+    S.sp_key[idx] = f64_key(v);
+    S.sp_id[idx] = id;
+    atomicMax((unsigned long long*)&S.sp_max, (unsigned long long)f64_key(v));
+  }
+
+  // the complete region: listed entries with key >= thr, appended with one
+  // LDS atomic per wave
+  auto append = [&](const uint64_t (&v)[kSubPerThread], int cnt) {
+    uint64_t e[kSubPerThread];
+    uint32_t keep = 0;
 #pragma unroll
-    for (int r = 0; r < kSlotsPerThread; ++r) {
-      const uint32_t id = hid[r];
-      if (id == 0xFFFFFFFFu) continue;
-      const uint32_t count = hpk[r] & 0xFFFFFFu, kinds = hpk[r] >> 24;
-      const uint32_t idx = atomicAdd(&S.n_special, 1u);
-      if (idx >= (uint32_t)kSpecialCap) continue;
-      float x32 = raw[r];
-      if (cfg.softcap > 0) x32 = gsm::softcap_f32(x32, cfg.softcap);
-      bool allowed = true;
-      if (constrained) {
-        const bool term = kinds & GS_FORCED_TERMINATION;
-        const bool extra = kinds & GS_FORCED_EXTRA;
-        allowed = term ? cfg.accepting != 0 : (extra || ((mw[r] >> (id & 31)) & 1u));
+    for (int q = 0; q < kSubPerThread; ++q) {
+      e[q] = 0;
+      if (k0 + q * kSubThreads < cnt) {
+        e[q] = list_rank(v[q]);
+        if (entry_key(e[q]) >= thr) keep |= 1u << q;
       }
-      if (allowed) atomicOr(&S.special_legal, 1u);
-      if (allowed && !(x32 < __builtin_inff())) atomicOr(&S.flags, kChunkNonFinite);
-      double x = allowed ? (double)x32 : -__builtin_inf();
-      if (count > 0) {
-        x = x < 0 ? x * cfg.repetition_penalty : x / cfg.repetition_penalty;
-        x -= cfg.presence_penalty + (double)count * cfg.frequency_penalty;
+    }
+    const uint32_t mine = (uint32_t)__popc(keep);
+    const uint32_t incl = wave_scan_u32(mine, lane);
+    uint32_t base = 0;
+    if (lane == 63) base = atomicAdd(&S.n_sorted, incl);
+    base = (uint32_t)__shfl((int)base, 63, 64);
+    uint32_t pos = base + incl - mine;
+#pragma unroll
+    for (int q = 0; q < kSubPerThread; ++q) {
+      if ((keep >> q) & 1u) {
+        if (pos < (uint32_t)kFinishCap) S.sorted[pos] = e[q];
+        ++pos;
       }
-      const double v = greedy ? x : x / T;
-      S.sp_key[idx] = f64_key(v);
-      S.sp_id[idx] = id;
+    }
+  };
+  if (!greedy) {
+    append(lv, cnt0);
+    for (int s0 = kFinishThreads / kSubThreads; s0 < n_subs; s0 += kFinishThreads / kSubThreads) {
+      const int sl = s0 + tid / kSubThreads;
+      const int cnt = sl < n_subs ? (int)S.c_nsub[sl] : 0;
+      uint64_t v[kSubPerThread];
+#pragma unroll
+      for (int q = 0; q < kSubPerThread; ++q) {
+        const int k = k0 + q * kSubThreads;
+        v[q] = k < cnt ? lists[(int64_t)sl * kSubCap + k] : 0ull;
+      }
+      append(v, cnt);
     }
   }
   __syncthreads();
   if (S.n_special > (uint32_t)kSpecialCap) {
-    if (tid == 0) {
-      a.results[row].token = -1;
-      a.results[row].flags = GS_FLAG_UNSUPPORTED;
-      a.results[row].probability = 0.0;
-    }
+    if (tid == 0) write_result(a, row, -1, GS_FLAG_UNSUPPORTED, 0.0);
     return;
   }
   if (S.flags & kChunkNonFinite) {
@@ -325,16 +621,10 @@ __global__ __launch_bounds__(kFinishThreads) void finish_kernel(SampleArgs a) {
       __syncthreads();
     }
     if (!S.legal_bits) {
-      if (tid == 0) {
-        a.results[row].token = -1;
-        a.results[row].flags = GS_FLAG_DEAD_END;
-        a.results[row].probability = 0.0;
-      }
+      if (tid == 0) write_result(a, row, -1, GS_FLAG_DEAD_END, 0.0);
       return;
     }
   }
-
-  const uint64_t* lists = a.lists + row * a.n_chunks * kGatherCap;
 
   // ---- greedy: first maximum of the penalised logits (sampling.ts:31,92-96)
   if (greedy) {
@@ -359,64 +649,49 @@ __global__ __launch_bounds__(kFinishThreads) void finish_kernel(SampleArgs a) {
         token = (bs >= 0 && ranks_before(S.sp_key[bs], S.sp_id[bs], nkey, nid)) ? (int32_t)S.sp_id[bs]
                                                                                  : (int32_t)nid;
       }
-      a.results[row].token = token;
-      a.results[row].flags = GS_FLAG_GREEDY;
-      a.results[row].probability = 1.0;
+      write_result(a, row, token, GS_FLAG_GREEDY, 1.0);
     }
     return;
   }
 
-  // ---- 2. the complete region of the chunk lists: every listed entry with
-  // key >= the highest truncated chunk's threshold (0 when no chunk was
-  // truncated: every finite logit is listed). kSubThreads threads read each
-  // wave sub-list, all their loads in flight together; kept entries are
-  // appended with one LDS atomic per wave.
-  const uint32_t thr = S.thr_max;
-  {
-    const int n_subs = a.n_chunks * kScanWaves;
-    for (int s0 = 0; s0 < n_subs; s0 += kFinishThreads / kSubThreads) {
-      const int sl = s0 + tid / kSubThreads;
-      const int k0 = tid % kSubThreads;
-      const int cnt = sl < n_subs ? (int)S.c_nsub[sl] : 0;
-      uint64_t v[kSubPerThread];
-#pragma unroll
-      for (int q = 0; q < kSubPerThread; ++q) {
-        const int k = k0 + q * kSubThreads;
-        v[q] = k < cnt ? lists[(int64_t)sl * kSubCap + k] : 0ull;
-      }
-      uint32_t keep = 0;
-#pragma unroll
-      for (int q = 0; q < kSubPerThread; ++q) {
-        if (k0 + q * kSubThreads < cnt) {
-          v[q] = list_rank(v[q]);
-          if (entry_key(v[q]) >= thr) keep |= 1u << q;
-        }
-      }
-      const uint32_t mine = (uint32_t)__popc(keep);
-      const uint32_t incl = wave_scan_u32(mine, lane);
-      uint32_t base = 0;
-      if (lane == 63) base = atomicAdd(&S.n_sorted, incl);
-      base = (uint32_t)__shfl((int)base, 63, 64);
-      uint32_t pos = base + incl - mine;
-#pragma unroll
-      for (int q = 0; q < kSubPerThread; ++q) {
-        if ((keep >> q) & 1u) {
-          if (pos < (uint32_t)kFinishCap) S.sorted[pos] = v[q];
-          ++pos;
-        }
-      }
-    }
-  }
-  __syncthreads();
   if (S.n_sorted > (uint32_t)kFinishCap) {
     if (tid == 0) enqueue_exact(a, row, 0u);
     return;
   }
   const int n_ns = (int)S.n_sorted;
-  uint64_t* scratch = (uint64_t*)S.cand_p;
-  if (n_ns <= kFinishThreads) sort_region<1>(S.sorted, n_ns, scratch);
-  else if (n_ns <= 2 * kFinishThreads) sort_region<2>(S.sorted, n_ns, scratch);
-  else sort_region<4>(S.sorted, n_ns, scratch);
+
+  // ---- the maximum value M = scaled[0].logit (sampling.ts:36): the best
+  // finite non-special logit / T, or the best special value
+  double M = -__builtin_inf();
+  if (S.max_key > kKeyNegInf) M = (double)key_f32(S.max_key) / T;
+  if (S.sp_max) {
+    const double sm = key_f64(S.sp_max);
+    if (sm > M) M = sm;
+  }
+  if (!(M > -__builtin_inf())) {
+    // every logit is -inf: the reference's arithmetic turns NaN; replay it exactly
+    if (tid == 0) enqueue_exact(a, row, 0u);
+    return;
+  }
+  // Margin for the comparisons that depend on the normaliser (the top-p cut):
+  // this total and the reference's differ by summation order (kNearTie) and by
+  // the reference's rounding of l/T and of l/T - M in every term, at most
+  // 2^-52 (2|M| + 60) relative for the terms that matter.
+  const double margin = kNearTie + 0x1p-52 * (2.0 * (M < 0 ? -M : M) + 60.0);
+
+  // ---- normaliser: chunk partial sums rescaled to M, plus every special
+  {
+    double part = 0.0;
+    for (int c = tid; c < a.n_chunks; c += kFinishThreads) {
+      const double csum = S.c_sum[c];
+      const uint32_t cmax = S.c_max[c];
+      if (cmax > kKeyNegInf && csum > 0) part += csum * gsm::js_exp((double)key_f32(cmax) / T - M);
+    }
+    for (int i = tid; i < n_sp; i += kFinishThreads) part += gsm::js_exp(key_f64(S.sp_key[i]) - M);
+    double total;
+    block_scan_f64(part, S.wsum, &total);
+    if (tid == 0) S.total = total;
+  }
 
   // specials inside the complete region (value >= the threshold's value),
   // moved into the dead hash table and sorted there; usually none or a few
@@ -438,24 +713,92 @@ __global__ __launch_bounds__(kFinishThreads) void finish_kernel(SampleArgs a) {
     __syncthreads();
     if (m2 > 1) block_sort_pairs_desc(in_key, in_id, m2);
   }
-  const int n_cand = n_ns + n_sp_in;
-  if (n_cand > kFinishCap || n_cand == 0) {
+  if (n_ns + n_sp_in == 0) {
     if (tid == 0) enqueue_exact(a, row, 0u);
     return;
   }
+  const double total = S.total;
+  const bool region_complete = !S.any_truncated;
 
-  // ---- merge by rank into (probability, id); value first, probability below
-  // the maximum value is the first entry of either list
-  if (tid == 0) {
-    double v0 = -__builtin_inf();
-    if (n_ns) v0 = (double)key_f32(entry_key(S.sorted[0])) / T;
-    if (n_sp_in && key_f64(in_key[0]) > v0) v0 = key_f64(in_key[0]);
-    S.vmax = v0;
+  // ---- fast path: the top kTopR non-specials, merged with the region's
+  // specials, settle every cut the filters make within them (when the
+  // specials fit beside them in 2 * kTopR candidates)
+  const int n_top_all = n_ns < kTopR ? n_ns : kTopR;
+  if (n_sp_in <= 2 * kTopR - n_top_all) {
+    uint64_t* tmp = (uint64_t*)S.cand_p;  // kWaves * 64 entries of merge scratch
+    if (n_ns <= kWaves * 64) top_r<1>(S.sorted, n_ns, tmp, S.top);
+    else if (n_ns <= kWaves * 128) top_r<2>(S.sorted, n_ns, tmp, S.top);
+    else top_r<4>(S.sorted, n_ns, tmp, S.top);
+    if (wave == 0) {
+      const int n_top = n_ns < kTopR ? n_ns : kTopR;
+      double* fp = S.cand_p + kWaves * 64;  // past the merge scratch
+      uint32_t* fid = S.cand_id;
+      const int n_sp_use = n_sp_in;
+      for (int i = lane; i < n_top; i += 64) {
+        const uint64_t e = S.top[i];
+        const uint32_t id = entry_id(e);
+        const uint64_t k = f64_key(nonspecial_value(e, T));
+        int lo = 0, hi = n_sp_use;  // specials ranked before this entry
+        while (lo < hi) {
+          const int mid = (lo + hi) >> 1;
+          if (ranks_before(in_key[mid], in_id[mid], k, id)) lo = mid + 1; else hi = mid;
+        }
+        fp[i + lo] = key_f64(k);
+        fid[i + lo] = id;
+      }
+      for (int j = lane; j < n_sp_use; j += 64) {
+        const uint64_t k = in_key[j];
+        const uint32_t id = in_id[j];
+        int lo = 0, hi = n_top;  // ranked non-specials before this special
+        while (lo < hi) {
+          const int mid = (lo + hi) >> 1;
+          const uint64_t e = S.top[mid];
+          if (ranks_before(f64_key(nonspecial_value(e, T)), entry_id(e), k, id)) lo = mid + 1; else hi = mid;
+        }
+        fp[j + lo] = key_f64(k);
+        fid[j + lo] = id;
+      }
+      // the merged list equals the row's list up to the last ranked
+      // non-special; specials below it may sit under unranked non-specials
+      int n_valid = n_top + n_sp_use;
+      const bool complete = region_complete && n_ns <= kTopR;
+      if (n_ns > kTopR) {
+        const uint64_t e = S.top[kTopR - 1];
+        const uint64_t lk = f64_key(nonspecial_value(e, T));
+        int after = 0;
+        for (int j = lane; j < n_sp_use; j += 64) {
+          if (!ranks_before(in_key[j], in_id[j], lk, entry_id(e))) ++after;
+        }
+        for (int m = 32; m > 0; m >>= 1) after += __shfl_xor(after, m, 64);
+        n_valid -= after;
+      }
+      __builtin_amdgcn_wave_barrier();
+      for (int i = lane; i < n_valid; i += 64) fp[i] = gsm::js_exp(fp[i] - M) / total;
+      __builtin_amdgcn_wave_barrier();
+      const int r = filters_and_draw_wave(a, row, cfg, fp, fid, n_valid, complete, margin);
+      if (lane == 0) S.fast_done = r == 0 ? 1u : 0u;
+    }
+    __syncthreads();
+    if (S.fast_done) return;
   }
+
+  // ---- slow path: the whole region sorted, then the filters block-wide
+  {
+    uint64_t* scratch = (uint64_t*)S.cand_p;
+    if (n_ns <= kFinishThreads) sort_region<1>(S.sorted, n_ns, scratch);
+    else if (n_ns <= 2 * kFinishThreads) sort_region<2>(S.sorted, n_ns, scratch);
+    else sort_region<4>(S.sorted, n_ns, scratch);
+  }
+  const int n_cand = n_ns + n_sp_in;
+  if (n_cand > kFinishCap) {
+    if (tid == 0) enqueue_exact(a, row, 0u);
+    return;
+  }
+  // merge by rank into (value, id), then probabilities (sampling.ts:39,42)
   for (int i = tid; i < n_ns; i += kFinishThreads) {
     const uint64_t e = S.sorted[i];
     const uint32_t id = entry_id(e);
-    const uint64_t k = f64_key((double)key_f32(entry_key(e)) / T);
+    const uint64_t k = f64_key(nonspecial_value(e, T));
     int lo = 0, hi = n_sp_in;  // specials ranked before this entry
     while (lo < hi) {
       const int mid = (lo + hi) >> 1;
@@ -471,44 +814,18 @@ __global__ __launch_bounds__(kFinishThreads) void finish_kernel(SampleArgs a) {
     while (lo < hi) {
       const int mid = (lo + hi) >> 1;
       const uint64_t e = S.sorted[mid];
-      const uint64_t ek = f64_key((double)key_f32(entry_key(e)) / T);
-      if (ranks_before(ek, entry_id(e), k, id)) lo = mid + 1; else hi = mid;
+      if (ranks_before(f64_key(nonspecial_value(e, T)), entry_id(e), k, id)) lo = mid + 1; else hi = mid;
     }
     S.cand_p[j + lo] = key_f64(k);
     S.cand_id[j + lo] = id;
   }
   __syncthreads();
-  const double M = S.vmax;
-  if (!(M > -__builtin_inf())) {
-    // every logit is -inf: the reference's arithmetic turns NaN; replay it exactly
-    if (tid == 0) enqueue_exact(a, row, 0u);
-    return;
-  }
-  // Margin for the comparisons that depend on the normaliser (the top-p cut):
-  // this total and the reference's differ by summation order (kNearTie) and by
-  // the reference's rounding of l/T and of l/T - M in every term, at most
-  // 2^-52 (2|M| + 60) relative for the terms that matter.
-  const double margin = kNearTie + 0x1p-52 * (2.0 * (M < 0 ? -M : M) + 60.0);
-
-  // ---- normaliser: chunk partial sums rescaled to M, plus every special
-  double part = 0.0;
-  for (int c = tid; c < a.n_chunks; c += kFinishThreads) {
-    const double csum = S.c_sum[c];
-    const uint32_t cmax = S.c_max[c];
-    if (cmax > kKeyNegInf && csum > 0) part += csum * gsm::js_exp((double)key_f32(cmax) / T - M);
-  }
-  for (int i = tid; i < n_sp; i += kFinishThreads) part += gsm::js_exp(key_f64(S.sp_key[i]) - M);
-  double total;
-  block_scan_f64(part, S.wsum, &total);
-
-  // probabilities in candidate order (sampling.ts:39,42)
   for (int i = tid; i < n_cand; i += kFinishThreads) S.cand_p[i] = gsm::js_exp(S.cand_p[i] - M) / total;
   __syncthreads();
 
   // ---- top-k (sampling.ts:44)
-  const bool complete = !S.any_truncated;  // no finite logit outside the candidates
   int n = n_cand;
-  bool n_complete = complete;
+  bool n_complete = region_complete;
   if (cfg.top_k > 0) {
     if (cfg.top_k < n) n = cfg.top_k;
     n_complete = true;  // the first topK of the sorted list are all present
@@ -520,8 +837,8 @@ __global__ __launch_bounds__(kFinishThreads) void finish_kernel(SampleArgs a) {
       const double p = S.cand_p[i];
       if (i + 1 < n && S.cand_p[i + 1] > p) atomicOr(&S.route_exact, 1u);  // not monotone: replay
       if (!(p >= floor_p)) atomicMin(&S.first_idx, (uint32_t)i);
-      const double margin = p >= floor_p ? p - floor_p : floor_p - p;
-      if (margin < kNearTie * floor_p) atomicOr(&S.route_exact, 2u);
+      const double d = p >= floor_p ? p - floor_p : floor_p - p;
+      if (d < kNearTie * floor_p) atomicOr(&S.route_exact, 2u);
     }
     __syncthreads();
     if (S.first_idx != 0xFFFFFFFFu) {
@@ -532,11 +849,7 @@ __global__ __launch_bounds__(kFinishThreads) void finish_kernel(SampleArgs a) {
     if (tid == 0) S.first_idx = 0xFFFFFFFFu;
     __syncthreads();
     if (n == 0) {
-      if (tid == 0) {
-        a.results[row].token = -1;
-        a.results[row].flags = GS_FLAG_EMPTY_CANDIDATES;
-        a.results[row].probability = 0.0;
-      }
+      if (tid == 0) write_result(a, row, -1, GS_FLAG_EMPTY_CANDIDATES, 0.0);
       return;
     }
   }
@@ -570,7 +883,7 @@ __global__ __launch_bounds__(kFinishThreads) void finish_kernel(SampleArgs a) {
       }
       cut = n - 1;
     } else if (tid == cut / kPer) {
-      // 1e-6 boundary ties, as reported by the reference comparison plan
+      // 1e-6 boundary ties, as the reference comparison plan reports them
       const double cum = base + local[cut % kPer];
       const double prev = cum - S.cand_p[cut];
       if (cum - cfg.top_p <= kTieReport * cfg.top_p || (cut > 0 && cfg.top_p - prev <= kTieReport * cfg.top_p)) {
@@ -614,9 +927,7 @@ __global__ __launch_bounds__(kFinishThreads) void finish_kernel(SampleArgs a) {
         enqueue_exact(a, row, S.route_exact ? GS_FLAG_NEAR_TIE : 0u);
       } else {
         const int i = (int)S.first_idx;
-        a.results[row].token = (int32_t)S.cand_id[i];
-        a.results[row].flags = tie_report;
-        a.results[row].probability = S.cand_p[i];
+        write_result(a, row, (int32_t)S.cand_id[i], tie_report, S.cand_p[i]);
       }
     }
   }

@@ -244,7 +244,9 @@ __device__ __forceinline__ void scan_chunk(const SampleArgs& a, const gs_row_con
   const bool use_cap = cfg.softcap > 0;
 
   // values: excluded (special / out of range) and masked ids become -inf,
-  // which neither the normaliser nor the candidate list admits
+  // which neither the normaliser nor the candidate list admits. Most load
+  // groups hold no such id: the per-element masking runs only for groups
+  // where some lane of the wave has one.
   float x[kElemsPerThread];
 #pragma unroll
   for (int v = 0; v < kLoads; ++v) {
@@ -253,20 +255,24 @@ __device__ __forceinline__ void scan_chunk(const SampleArgs& a, const gs_row_con
     for (int j = 0; j < kVec; ++j) {
       float y = __builtin_bit_cast(float, VT::bits(raw[v], j));
       if (use_cap) y = capped(y, cfg.softcap);
-      x[v * kVec + j] = ((live >> j) & 1u) ? y : -__builtin_inff();
+      x[v * kVec + j] = y;
+    }
+    if (__ballot(live != kLaneBits)) {
+#pragma unroll
+      for (int j = 0; j < kVec; ++j) {
+        if (!((live >> j) & 1u)) x[v * kVec + j] = -__builtin_inff();
+      }
     }
   }
 
-  // pass 1: the thread's maximum (NaN-propagating) and the wave's finite count
+  // pass 1: the thread's maximum (NaN-propagating: NaN or +inf flags the row)
   float tmax = -__builtin_inff();
-  uint32_t wfin = 0;
 #pragma unroll
-  for (int e = 0; e < kElemsPerThread; ++e) {
-    tmax = __builtin_elementwise_maximum(tmax, x[e]);
-    wfin += (uint32_t)__popcll(__ballot(x[e] > -__builtin_inff()));
-  }
+  for (int e = 0; e < kElemsPerThread; ++e) tmax = __builtin_elementwise_maximum(tmax, x[e]);
   const bool finite_max = tmax > -__builtin_inff() && tmax < __builtin_inff();
-  const bool thread_bad = !(tmax < __builtin_inff());  // NaN or +inf
+  // the normaliser below reads -inf as -FLT_MAX, which adds exactly 0 unless
+  // the thread's maximum is -FLT_MAX itself: such rows take the exact path
+  const bool thread_bad = !(tmax < __builtin_inff()) || tmax == -__FLT_MAX__;
 
   // ------------------------------------------------------------ greedy rows
   if (greedy) {
@@ -318,17 +324,21 @@ __device__ __forceinline__ void scan_chunk(const SampleArgs& a, const gs_row_con
   if (finite_max) {
     const double m = (double)tmax;
     // groups of four terms, so the table reads of a group overlap; a group is
-    // skipped when no lane of the wave has a term above e^-60, and inside a
-    // group such terms are clamped to e^-60 (within the bound stated above)
+    // skipped when no lane of the wave has a term above e^-60. -inf enters as
+    // -FLT_MAX (one med3; +inf rows are already flagged): its exponent is
+    // finite and so negative that the term is 0.
 #pragma unroll
     for (int g = 0; g < kElemsPerThread; g += 4) {
       double y[4];
 #pragma unroll
-      for (int q = 0; q < 4; ++q) y[q] = ((double)x[g + q] - m) * A;
+      for (int q = 0; q < 4; ++q) {
+        const float xe = __builtin_amdgcn_fmed3f(x[g + q], -__FLT_MAX__, __FLT_MAX__);
+        y[q] = ((double)xe - m) * A;
+      }
       const bool need = y[0] > kSkipY || y[1] > kSkipY || y[2] > kSkipY || y[3] > kSkipY;
       if (__ballot(need)) {
 #pragma unroll
-        for (int q = 0; q < 4; ++q) sum += exp2_256(__builtin_fmax(y[q], kSkipY), s_tab);
+        for (int q = 0; q < 4; ++q) sum += exp2_256(y[q], s_tab);
       }
     }
   }
@@ -343,18 +353,16 @@ __device__ __forceinline__ void scan_chunk(const SampleArgs& a, const gs_row_con
     if (lane == 0) {
       s_wmax[wave] = wm;
       s_wbad[wave] = wb != 0;
-      s_wfin[wave] = wfin;
       s_wlanes[wave] = (uint32_t)__popcll(wl);
     }
   }
   __syncthreads();
-  uint32_t cmax = 0, cbad = 0, lanes = 0, cfin = 0;
+  uint32_t cmax = 0, cbad = 0, lanes = 0;
 #pragma unroll
   for (int w = 0; w < kScanWaves; ++w) {
     cmax = s_wmax[w] > cmax ? s_wmax[w] : cmax;
     cbad |= s_wbad[w];
     lanes += s_wlanes[w];
-    cfin += s_wfin[w];
   }
   if (cbad) {
     // NaN or +inf among the live logits: outside the one-pass contract
@@ -381,7 +389,8 @@ __device__ __forceinline__ void scan_chunk(const SampleArgs& a, const gs_row_con
   // tau: at least `depth` per-thread maxima are >= tau
   const uint32_t depth = (uint32_t)plan.depth;
   uint32_t tau = 0;
-  if (lanes > depth + 32u) tau = radix_floor(s_keys, s_hist, s_sel, depth, 32u);
+  const bool selected = lanes > depth + 32u;
+  if (selected) tau = radix_floor(s_keys, s_hist, s_sel, depth, 32u);
   const uint32_t thr = tau > kKeyNegInf ? tau : kKeyNegInf + 1u;
   const float tf = key_f32(thr);
 
@@ -424,9 +433,10 @@ __device__ __forceinline__ void scan_chunk(const SampleArgs& a, const gs_row_con
     st.sum = csum;
     st.max_key = cmax;
     st.n_list = listed;
-    st.n_finite = cfin;
+    st.n_finite = 0;
     st.threshold = thr;
-    st.truncated = cfin > gathered ? 1u : 0u;
+    // with a tau, lanes whose maximum lies below it left finite logits out
+    st.truncated = selected ? 1u : 0u;
     st.flags = overflow ? kChunkOverflow : 0u;
     *stat = st;
   }
