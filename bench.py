@@ -12,6 +12,12 @@ The same run reports
   roofline      the dominant kernel's algorithmic bytes per launch over its
                 mean duration, timed with HIP events around every launch of
                 the timed region (gs_timing_begin / gs_timing_end);
+  traffic       HBM bytes the dominant kernel moves per launch, taken from the
+                PMC summary committed under profiles/ for this workload (a
+                line "bench-traffic: workload=<w> kernel=<k> bytes=<B>" that
+                scales rocprofv3's FETCH_SIZE + WRITE_SIZE per dispatch by
+                what those counters read for a copy of known size); null when
+                no such summary exists;
   cpu_baseline  the JavaScript restatement of the reference sampler run by
                 Node on one host core over a bounded sample of the same rows
                 (falls back to the C restatement when node is absent), and a
@@ -42,6 +48,25 @@ METRIC = "sampled rows/sec at vocab 262144, batch 256; achieved HBM GB/s (% of p
 HBM_PEAK_GBPS = 8000.0       # MI355X HBM3E, AMD public specification
 BF16_PEAK_TFLOPS = 2500.0    # MI355X dense bf16 MFMA
 V = 262144
+
+
+def profiled_traffic(workload: str, kernel: str):
+    """HBM bytes per launch of `kernel` on `workload` from the committed PMC
+    summaries (profiles/*.md, lines "bench-traffic: workload=.. kernel=.. bytes=..")."""
+    pdir = os.path.join(ROOT, "profiles")
+    if not os.path.isdir(pdir):
+        return None
+    for name in sorted(os.listdir(pdir)):
+        if not name.endswith(".md"):
+            continue
+        with open(os.path.join(pdir, name)) as f:
+            for line in f:
+                if not line.startswith("bench-traffic:"):
+                    continue
+                kv = dict(t.split("=", 1) for t in line.split()[1:] if "=" in t)
+                if kv.get("workload") == workload and kv.get("kernel") == kernel:
+                    return int(kv["bytes"])
+    return None
 
 
 def log(*a):
@@ -292,9 +317,11 @@ def main():
     else:
         achieved = rows * wl["scan_bytes_per_row"] / (dom_avg_ms * 1e6)
         mfma_tflops = None
+    kname = {"scan": "scan_kernel", "lmhead": "lmhead_kernel"}[dom]
     roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
-                "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": None,
-                "kernel": {"scan": "scan_kernel", "lmhead": "lmhead_kernel"}[dom],
+                "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": profiled_traffic(wl["name"], kname),
+                "kernel": kname, "algorithmic_bytes_per_launch": int(
+                    wl["lm_bytes"] if dom == "lmhead" else rows * wl["scan_bytes_per_row"]),
                 "kernel_avg_us": round(dom_avg_ms * 1000, 2),
                 "stage_avg_us": {k: round(v[0] / v[1] * 1000, 2) for k, v in stages.items() if v[1]}}
     if mfma_tflops is not None:
@@ -302,8 +329,8 @@ def main():
         roofline["mfma_frac_bf16_dense"] = round(mfma_tflops / BF16_PEAK_TFLOPS, 4)
 
     if args.copy_probe:
-        # a plain copy of the same byte count: reads and writes each byte once
-        src = wl["keep"][0]
+        # a plain 256 MiB device-to-device copy: reads and writes each byte once
+        src = torch.ones(64 << 20, dtype=torch.float32, device=device)
         dst = torch.empty_like(src)
         with torch.cuda.stream(stream):
             for _ in range(3):
@@ -318,7 +345,7 @@ def main():
         nbytes = src.numel() * src.element_size()
         roofline["copy_probe"] = {"bytes_read": nbytes, "bytes_written": nbytes, "avg_us": round(copy_ms * 1000, 2),
                                   "gbps_read_plus_write": round(2 * nbytes / (copy_ms * 1e6), 1)}
-        del dst
+        del dst, src
 
     base, parity = (None, None)
     if not args.no_cpu:

@@ -673,11 +673,13 @@ __global__ __launch_bounds__(kFinishThreads) void finish_kernel(SampleArgs a) {
     if (tid == 0) enqueue_exact(a, row, 0u);
     return;
   }
-  // Margin for the comparisons that depend on the normaliser (the top-p cut):
-  // this total and the reference's differ by summation order (kNearTie) and by
-  // the reference's rounding of l/T and of l/T - M in every term, at most
-  // 2^-52 (2|M| + 60) relative for the terms that matter.
-  const double margin = kNearTie + 0x1p-52 * (2.0 * (M < 0 ? -M : M) + 60.0);
+  // Margin for the comparisons that depend on the normaliser (the top-p cut).
+  // This total and the reference's differ by: the scan's exponential (4.2e-10
+  // relative per term), summation order (under V 2^-53 < 3e-11), the
+  // reference's rounding of l/T and of l/T - M in every term (2^-52 (2|M| + 60)
+  // for the terms that matter) and the scan's rounding of its exponent
+  // argument (2^-53 |M|, for the threads whose terms matter).
+  const double margin = kNormaliserRel + 0x1p-52 * (3.0 * (M < 0 ? -M : M) + 60.0);
 
   // ---- normaliser: chunk partial sums rescaled to M, plus every special
   {
@@ -691,6 +693,11 @@ __global__ __launch_bounds__(kFinishThreads) void finish_kernel(SampleArgs a) {
     double total;
     block_scan_f64(part, S.wsum, &total);
     if (tid == 0) S.total = total;
+  }
+  if (!(S.total < __builtin_inf())) {
+    // an exponent argument beyond the double range (|l/T| near 1e18 or more)
+    if (tid == 0) enqueue_exact(a, row, 0u);
+    return;
   }
 
   // specials inside the complete region (value >= the threshold's value),

@@ -30,6 +30,9 @@ constexpr int kExactTile = 4096;                  // LDS tile of the exact path'
 // relative margin under which a fast-path decision is re-resolved exactly;
 // it bounds the reference's own sequential-sum error (V * 2^-53 ~ 3e-11)
 constexpr double kNearTie = 1.0e-10;
+// relative margin of decisions that depend on the softmax normaliser: the
+// scan's exponential (4.2e-10 per term) and summation order, with room
+constexpr double kNormaliserRel = 2.0e-9;
 // the north star's reporting tolerance for top-p boundary ties
 constexpr double kTieReport = 1.0e-6;
 

@@ -21,9 +21,11 @@
 // (src/runtime/constraints.ts:159-173).
 //
 // The normaliser's exponential is 2^(y/256) = 2^(j/256) * 2^k * e^r with a
-// correctly rounded 256-entry table and a cubic in r, |r| <= ln2/512: relative
-// error below 1.5e-13 per term. Only the normaliser sees it; every ordering
-// and every probability the filters compare is recomputed exactly later.
+// correctly rounded 256-entry table and a quadratic in r, |r| <= ln2/512:
+// relative error below 4.2e-10 per term. Only the normaliser sees it, and only
+// the top-p cut depends on the normaliser (its margin in the finish kernel
+// covers this); every ordering and every probability the filters compare is
+// recomputed exactly later.
 #include "gs_exp2_table.h"
 #include "gs_internal.h"
 
@@ -40,9 +42,7 @@ constexpr double kSkipY = -22160.0;
 __device__ __forceinline__ double exp2_256(double y, const double* tab) {
   const double n = __builtin_rint(y);
   const double s = y - n;  // |s| <= 1/2
-  double p = __builtin_fma(s, GS_EXP2_256_C3, GS_EXP2_256_C2);
-  p = __builtin_fma(s, p, GS_EXP2_256_C1);
-  p = __builtin_fma(s, p, 1.0);
+  const double p = __builtin_fma(s, __builtin_fma(s, GS_EXP2_256_C2, GS_EXP2_256_C1), 1.0);
   const int ni = (int)n;
   return __builtin_ldexp(tab[ni & 255] * p, ni >> 8);
 }
@@ -122,7 +122,6 @@ struct ScanShared {
   uint32_t sel[4];
   double wsum[kScanWaves];
   uint32_t wmax[kScanWaves];
-  uint32_t wfin[kScanWaves];
   uint32_t wbad[kScanWaves];
   uint32_t wlanes[kScanWaves];
   uint32_t wgather[kScanWaves];
@@ -147,7 +146,6 @@ __device__ __forceinline__ void scan_chunk(const SampleArgs& a, const gs_row_con
   uint32_t* s_sel = S.sel;
   double* s_wsum = S.wsum;
   uint32_t* s_wmax = S.wmax;
-  uint32_t* s_wfin = S.wfin;
   uint32_t* s_wbad = S.wbad;
   uint32_t* s_wlanes = S.wlanes;
   uint32_t* s_wgather = S.wgather;
@@ -315,30 +313,32 @@ __device__ __forceinline__ void scan_chunk(const SampleArgs& a, const gs_row_con
     return;
   }
 
-  // pass 2: sum of e^((l - tmax)/T) against the thread's own maximum. The
-  // difference of two binary32 values is exact or correctly rounded in
-  // binary64 (and exactly 0 at the maximum), so each exponent carries only the
-  // rounding of one product.
-  const double A = (1.0 / cfg.temperature) * GS_256_LOG2E;  // y = 256 log2(e) (l - m) / T
+  // pass 2: sum of e^((l - tmax)/T) against the thread's own maximum, with
+  // y = 256 log2(e) (l - tmax) / T formed by one fma; its rounding (of
+  // tmax * A) is of the order of the reference's own rounding of l/T - M,
+  // which the finish kernel's top-p margin already covers.
+  const double A = (1.0 / cfg.temperature) * GS_256_LOG2E;
   double sum = 0.0;
   if (finite_max) {
-    const double m = (double)tmax;
+    const double B = -(double)tmax * A;
+    // logits below lim have (l - tmax)/T < -60 (lim is rounded down)
+    const double lim64 = (double)tmax - 60.0 * cfg.temperature;
+    // 1e-6 relative below lim64 before rounding to binary32 (half an ulp)
+    const float lim = (float)(lim64 - (lim64 < 0 ? -lim64 : lim64) * 1.0e-6 - 1.0e-37);
     // groups of four terms, so the table reads of a group overlap; a group is
     // skipped when no lane of the wave has a term above e^-60. -inf enters as
     // -FLT_MAX (one med3; +inf rows are already flagged): its exponent is
     // finite and so negative that the term is 0.
 #pragma unroll
     for (int g = 0; g < kElemsPerThread; g += 4) {
-      double y[4];
+      const float gmax = __builtin_elementwise_maximum(__builtin_elementwise_maximum(x[g], x[g + 1]),
+                                                       __builtin_elementwise_maximum(x[g + 2], x[g + 3]));
+      if (__ballot(gmax >= lim)) {
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const float xe = __builtin_amdgcn_fmed3f(x[g + q], -__FLT_MAX__, __FLT_MAX__);
-        y[q] = ((double)xe - m) * A;
-      }
-      const bool need = y[0] > kSkipY || y[1] > kSkipY || y[2] > kSkipY || y[3] > kSkipY;
-      if (__ballot(need)) {
-#pragma unroll
-        for (int q = 0; q < 4; ++q) sum += exp2_256(y[q], s_tab);
+        for (int q = 0; q < 4; ++q) {
+          const float xe = __builtin_amdgcn_fmed3f(x[g + q], -__FLT_MAX__, __FLT_MAX__);
+          sum += exp2_256(__builtin_fma((double)xe, A, B), s_tab);
+        }
       }
     }
   }
@@ -380,7 +380,7 @@ __device__ __forceinline__ void scan_chunk(const SampleArgs& a, const gs_row_con
     double part = 0.0;
     if (finite_max && sum > 0.0) {
       const double y = ((double)tmax - (double)key_f32(cmax)) * A;
-      part = y > kSkipY ? sum * exp2_256(y, s_tab) : 0.0;
+      part = y > kSkipY ? sum * exp2_256(y, s_tab) : 0.0;  // the chunk maximum's own factor is exactly 1
     }
     part = wave_sum_f64(part);
     if (lane == 0) s_wsum[wave] = part;
@@ -420,11 +420,10 @@ __device__ __forceinline__ void scan_chunk(const SampleArgs& a, const gs_row_con
   if (tid == 0) {
     ChunkStat st;
     double csum = 0.0;
-    uint32_t gathered = 0, listed = 0, overflow = 0;
+    uint32_t listed = 0, overflow = 0;
     for (int w = 0; w < kScanWaves; ++w) {
       csum += s_wsum[w];
       const uint32_t g = s_wgather[w];
-      gathered += g;
       const uint32_t n = g < (uint32_t)kSubCap ? g : (uint32_t)kSubCap;
       listed += n;
       overflow |= g > (uint32_t)kSubCap;
@@ -444,7 +443,7 @@ __device__ __forceinline__ void scan_chunk(const SampleArgs& a, const gs_row_con
 
 
 template <typename In>
-__global__ __launch_bounds__(kScanThreads) void scan_kernel(SampleArgs a) {
+__global__ __launch_bounds__(kScanThreads, 5) void scan_kernel(SampleArgs a) {
   __shared__ ScanShared S;
   const int64_t row = blockIdx.y;
   const int chunk = blockIdx.x;

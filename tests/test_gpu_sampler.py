@@ -1,6 +1,11 @@
 """GPU parity of the batched sampler (gs_sample through the C ABI) against the
 oracle: token ids bit-exact on every row; probabilities identical on rows the
-exact path resolved and within 1e-12 relative on one-pass rows."""
+exact path resolved and within PROB_RTOL relative on one-pass rows.
+
+One-pass rows take their softmax normaliser from the chunk scan, which sums
+exp through a 256-entry 2^(j/256) table and a quadratic (relative error at
+most 4.2e-10 per term), so one-pass probabilities carry up to that relative
+error; the path's stated bound is 1e-6 relative."""
 import math
 
 import numpy as np
@@ -10,7 +15,7 @@ from oracle.oracle import Decoding
 
 pytestmark = pytest.mark.gpu
 
-PROB_RTOL = 1e-12
+PROB_RTOL = 1e-9
 
 
 def _gs():
