@@ -41,6 +41,9 @@ struct gs_context {
   int32_t* d_tokens = nullptr;
   double* d_logprob = nullptr;
   int32_t tokens_cap = 0;
+  // device staging for the host-array entry points (grown on demand)
+  uint8_t* d_stage = nullptr;
+  size_t stage_cap = 0;
   // kernel timing (gs_timing_begin / gs_timing_end): per timed call, one event
   // before each stage and one after it
   std::vector<hipEvent_t> t_events;  // [max_calls][GS_STAGE_COUNT][2]
@@ -88,6 +91,43 @@ void stage_mark(gs_context* ctx, int32_t slot, int stage, int edge, hipStream_t 
   if (slot < 0) return;
   (void)hipEventRecord(ctx->t_events[((size_t)slot * GS_STAGE_COUNT + stage) * 2 + edge], s);
   if (edge == 0) ctx->t_ran[(size_t)slot * GS_STAGE_COUNT + stage] = 1;
+}
+
+// Grows the context's device staging buffer to at least `bytes`. Waits for
+// the stream first: queued work may still read the old buffer.
+int ensure_stage(gs_context* ctx, size_t bytes) {
+  if (bytes <= ctx->stage_cap) return GS_OK;
+  GS_HIP(ctx, hipStreamSynchronize(ctx->stream));
+  free_dev(ctx->d_stage);
+  ctx->d_stage = nullptr;
+  ctx->stage_cap = 0;
+  GS_HIP(ctx, hipMalloc(&ctx->d_stage, bytes));
+  ctx->stage_cap = bytes;
+  return GS_OK;
+}
+
+size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
+
+// Per-row failures of a finished batch, mapped to the reference's errors
+// (the first failing row decides).
+int map_row_failures(gs_context* ctx, const gs_row_result* res, int32_t rows) {
+  for (int32_t r = 0; r < rows; ++r) {
+    const uint32_t f = res[r].flags;
+    if (f & GS_FLAG_DEAD_END) return fail(ctx, GS_ERR_DEAD_END, "Generation constraint reached a tokenization dead end");
+    if (f & GS_FLAG_EMPTY_CANDIDATES)
+      return fail(ctx, GS_ERR_EMPTY_CANDIDATES, "min-p left no candidate token (row " + std::to_string(r) + ")");
+    if (f & GS_FLAG_UNSUPPORTED)
+      return fail(ctx, GS_ERR_UNSUPPORTED, "row " + std::to_string(r) + ": more than 2048 distinct penalty-window and forced ids");
+  }
+  return GS_OK;
+}
+
+// A host CSR offsets array [rows+1]: starts at 0 and never decreases.
+bool csr_ok(const int64_t* off, int32_t rows) {
+  if (off[0] != 0) return false;
+  for (int32_t r = 0; r < rows; ++r)
+    if (off[r + 1] < off[r]) return false;
+  return true;
 }
 
 void destroy_timing(gs_context* ctx) {
@@ -169,6 +209,7 @@ int gs_destroy(gs_context* ctx) {
   free_dev(ctx->d_states);
   free_dev(ctx->d_tokens);
   free_dev(ctx->d_logprob);
+  free_dev(ctx->d_stage);
   destroy_timing(ctx);
   if (ctx->stream) (void)hipStreamDestroy(ctx->stream);
   delete ctx;
@@ -285,14 +326,154 @@ int gs_sample_sync(gs_context* ctx, const gs_batch* b, gs_row_result* host_out) 
   }
   GS_HIP(ctx, hipMemcpyAsync(dst, b->results, sizeof(gs_row_result) * b->rows, hipMemcpyDeviceToHost, ctx->stream));
   GS_HIP(ctx, hipStreamSynchronize(ctx->stream));
-  for (int32_t r = 0; r < b->rows; ++r) {
-    const uint32_t f = dst[r].flags;
-    if (f & GS_FLAG_DEAD_END) return fail(ctx, GS_ERR_DEAD_END, "Generation constraint reached a tokenization dead end");
-    if (f & GS_FLAG_EMPTY_CANDIDATES)
-      return fail(ctx, GS_ERR_EMPTY_CANDIDATES, "min-p left no candidate token (row " + std::to_string(r) + ")");
-    if (f & GS_FLAG_UNSUPPORTED)
-      return fail(ctx, GS_ERR_UNSUPPORTED, "row " + std::to_string(r) + ": more than 2048 distinct penalty-window and forced ids");
+  return map_row_failures(ctx, dst, b->rows);
+}
+
+int gs_sample_host(gs_context* ctx, const gs_batch* b, int32_t logits_on_device, gs_row_result* host_results) {
+  if (!ctx || !b || !host_results) return fail(ctx, GS_ERR_INVALID_ARGUMENT, "null context, batch or results");
+  if (b->rows == 0) return GS_OK;
+  if (b->rows < 0 || b->rows > ctx->max_rows) return fail(ctx, GS_ERR_INVALID_ARGUMENT, "rows outside [0, max_rows]");
+  if (!b->logits || !b->configs) return fail(ctx, GS_ERR_INVALID_ARGUMENT, "logits and configs are required");
+  if (b->dtype != GS_F32 && b->dtype != GS_BF16) return fail(ctx, GS_ERR_INVALID_ARGUMENT, "dtype must be f32 or bf16");
+  if (b->row_stride < ctx->vocab) return fail(ctx, GS_ERR_INVALID_ARGUMENT, "row_stride is smaller than the vocab");
+  if (b->history_offsets && !b->history_ids) return fail(ctx, GS_ERR_INVALID_ARGUMENT, "history_ids missing");
+  if (b->forced_offsets && (!b->forced_ids || !b->forced_kinds)) return fail(ctx, GS_ERR_INVALID_ARGUMENT, "forced ids missing");
+  if (b->mask_slots > 0 && !b->mask_table) return fail(ctx, GS_ERR_INVALID_ARGUMENT, "mask_table missing");
+  const int32_t R = b->rows;
+  if (b->history_offsets && !csr_ok(b->history_offsets, R))
+    return fail(ctx, GS_ERR_INVALID_ARGUMENT, "history_offsets must start at 0 and never decrease");
+  if (b->forced_offsets && !csr_ok(b->forced_offsets, R))
+    return fail(ctx, GS_ERR_INVALID_ARGUMENT, "forced_offsets must start at 0 and never decrease");
+  for (int32_t r = 0; r < R; ++r) {
+    const int32_t slot = b->configs[r].mask_slot;
+    if (slot >= 0 && (b->mask_slots <= 0 || slot >= b->mask_slots))
+      return fail(ctx, GS_ERR_INVALID_ARGUMENT, "row " + std::to_string(r) + ": mask_slot outside the mask table");
   }
+  const size_t esize = b->dtype == GS_BF16 ? 2 : 4;
+  const size_t logit_bytes = logits_on_device ? 0 : ((size_t)(R - 1) * b->row_stride + ctx->vocab) * esize;
+  const int64_t n_hist = b->history_offsets ? b->history_offsets[R] : 0;
+  const int64_t n_forced = b->forced_offsets ? b->forced_offsets[R] : 0;
+  size_t off = 0;
+  const size_t o_logits = off;
+  off = align256(off + logit_bytes);
+  const size_t o_cfg = off;
+  off = align256(off + sizeof(gs_row_config) * R);
+  const size_t o_hoff = off;
+  off = align256(off + (b->history_offsets ? sizeof(int64_t) * (R + 1) : 0));
+  const size_t o_hids = off;
+  off = align256(off + sizeof(int32_t) * n_hist);
+  const size_t o_foff = off;
+  off = align256(off + (b->forced_offsets ? sizeof(int64_t) * (R + 1) : 0));
+  const size_t o_fids = off;
+  off = align256(off + sizeof(int32_t) * n_forced);
+  const size_t o_fk = off;
+  off = align256(off + n_forced);
+  const size_t o_res = off;
+  off = align256(off + sizeof(gs_row_result) * R);
+  GS_HIP(ctx, hipSetDevice(ctx->device));
+  int st = ensure_stage(ctx, off);
+  if (st != GS_OK) return st;
+  uint8_t* d = ctx->d_stage;
+  hipStream_t s = ctx->stream;
+  gs_batch db = *b;
+  if (!logits_on_device) {
+    GS_HIP(ctx, hipMemcpyAsync(d + o_logits, b->logits, logit_bytes, hipMemcpyHostToDevice, s));
+    db.logits = d + o_logits;
+  }
+  GS_HIP(ctx, hipMemcpyAsync(d + o_cfg, b->configs, sizeof(gs_row_config) * R, hipMemcpyHostToDevice, s));
+  db.configs = (const gs_row_config*)(d + o_cfg);
+  if (b->history_offsets) {
+    GS_HIP(ctx, hipMemcpyAsync(d + o_hoff, b->history_offsets, sizeof(int64_t) * (R + 1), hipMemcpyHostToDevice, s));
+    if (n_hist) GS_HIP(ctx, hipMemcpyAsync(d + o_hids, b->history_ids, sizeof(int32_t) * n_hist, hipMemcpyHostToDevice, s));
+    db.history_offsets = (const int64_t*)(d + o_hoff);
+    db.history_ids = (const int32_t*)(d + o_hids);
+  }
+  if (b->forced_offsets) {
+    GS_HIP(ctx, hipMemcpyAsync(d + o_foff, b->forced_offsets, sizeof(int64_t) * (R + 1), hipMemcpyHostToDevice, s));
+    if (n_forced) {
+      GS_HIP(ctx, hipMemcpyAsync(d + o_fids, b->forced_ids, sizeof(int32_t) * n_forced, hipMemcpyHostToDevice, s));
+      GS_HIP(ctx, hipMemcpyAsync(d + o_fk, b->forced_kinds, n_forced, hipMemcpyHostToDevice, s));
+    }
+    db.forced_offsets = (const int64_t*)(d + o_foff);
+    db.forced_ids = (const int32_t*)(d + o_fids);
+    db.forced_kinds = d + o_fk;
+  }
+  db.results = (gs_row_result*)(d + o_res);
+  st = gs_sample(ctx, &db, s);
+  if (st != GS_OK) return st;
+  GS_HIP(ctx, hipMemcpyAsync(host_results, d + o_res, sizeof(gs_row_result) * R, hipMemcpyDeviceToHost, s));
+  GS_HIP(ctx, hipStreamSynchronize(s));
+  return map_row_failures(ctx, host_results, R);
+}
+
+int gs_device_alloc(gs_context* ctx, size_t bytes, void** out) {
+  if (!ctx || !out) return fail(ctx, GS_ERR_INVALID_ARGUMENT, "null context or output");
+  *out = nullptr;
+  GS_HIP(ctx, hipSetDevice(ctx->device));
+  GS_HIP(ctx, hipMalloc(out, bytes ? bytes : 1));
+  return GS_OK;
+}
+
+int gs_device_free(gs_context* ctx, void* ptr) {
+  if (!ctx) return fail(ctx, GS_ERR_INVALID_ARGUMENT, "null context");
+  if (!ptr) return GS_OK;
+  GS_HIP(ctx, hipSetDevice(ctx->device));
+  GS_HIP(ctx, hipStreamSynchronize(ctx->stream));
+  GS_HIP(ctx, hipFree(ptr));
+  return GS_OK;
+}
+
+int gs_copy_to_device(gs_context* ctx, void* dst, const void* src, size_t bytes) {
+  if (!ctx || (bytes && (!dst || !src))) return fail(ctx, GS_ERR_INVALID_ARGUMENT, "bad copy arguments");
+  if (!bytes) return GS_OK;
+  GS_HIP(ctx, hipSetDevice(ctx->device));
+  GS_HIP(ctx, hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, ctx->stream));
+  GS_HIP(ctx, hipStreamSynchronize(ctx->stream));
+  return GS_OK;
+}
+
+int gs_copy_to_host(gs_context* ctx, void* dst, const void* src, size_t bytes) {
+  if (!ctx || (bytes && (!dst || !src))) return fail(ctx, GS_ERR_INVALID_ARGUMENT, "bad copy arguments");
+  if (!bytes) return GS_OK;
+  GS_HIP(ctx, hipSetDevice(ctx->device));
+  GS_HIP(ctx, hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, ctx->stream));
+  GS_HIP(ctx, hipStreamSynchronize(ctx->stream));
+  return GS_OK;
+}
+
+int gs_mask_logits(gs_context* ctx, const float* raw, int64_t n, const int32_t* ids, int64_t n_ids, float* out,
+                   void* stream) {
+  if (!ctx || n < 0 || n_ids < 0 || (n > 0 && (!raw || !out)) || (n_ids > 0 && !ids))
+    return fail(ctx, GS_ERR_INVALID_ARGUMENT, "bad arguments");
+  GS_HIP(ctx, hipSetDevice(ctx->device));
+  launch_mask_logits(raw, n, ids, n_ids, out, pick_stream(ctx, stream));
+  GS_HIP(ctx, hipGetLastError());
+  return GS_OK;
+}
+
+int gs_mask_logits_host(gs_context* ctx, const float* raw, int64_t n, const int32_t* legal, int64_t n_legal,
+                        const int32_t* termination, int64_t n_termination, float* out) {
+  if (!ctx || n < 0 || n_legal < 0 || n_termination < 0 || (n > 0 && (!raw || !out)) || (n_legal > 0 && !legal) ||
+      (n_termination > 0 && !termination))
+    return fail(ctx, GS_ERR_INVALID_ARGUMENT, "bad arguments");
+  if (n == 0) return GS_OK;
+  const size_t o_raw = 0, o_out = align256(sizeof(float) * n), o_ids = o_out + align256(sizeof(float) * n);
+  const size_t total = o_ids + sizeof(int32_t) * (n_legal + n_termination);
+  GS_HIP(ctx, hipSetDevice(ctx->device));
+  int st = ensure_stage(ctx, total);
+  if (st != GS_OK) return st;
+  uint8_t* d = ctx->d_stage;
+  hipStream_t s = ctx->stream;
+  GS_HIP(ctx, hipMemcpyAsync(d + o_raw, raw, sizeof(float) * n, hipMemcpyHostToDevice, s));
+  if (n_legal) GS_HIP(ctx, hipMemcpyAsync(d + o_ids, legal, sizeof(int32_t) * n_legal, hipMemcpyHostToDevice, s));
+  if (n_termination)
+    GS_HIP(ctx, hipMemcpyAsync(d + o_ids + sizeof(int32_t) * n_legal, termination, sizeof(int32_t) * n_termination,
+                               hipMemcpyHostToDevice, s));
+  launch_mask_logits((const float*)(d + o_raw), n, (const int32_t*)(d + o_ids), n_legal + n_termination,
+                     (float*)(d + o_out), s);
+  GS_HIP(ctx, hipGetLastError());
+  GS_HIP(ctx, hipMemcpyAsync(out, d + o_out, sizeof(float) * n, hipMemcpyDeviceToHost, s));
+  GS_HIP(ctx, hipStreamSynchronize(s));
   return GS_OK;
 }
 
@@ -445,6 +626,45 @@ int gs_dfa_advance(gs_context* ctx, const int32_t* states_in, const int32_t* tok
     }
     states_out[i] = s;
   }
+  return GS_OK;
+}
+
+int gs_dfa_advance_bytes(gs_context* ctx, int32_t state, const uint8_t* bytes, int64_t n, int32_t* state_out) {
+  if (!ctx || !state_out || n < 0 || (n > 0 && !bytes)) return fail(ctx, GS_ERR_INVALID_ARGUMENT, "bad arguments");
+  if (ctx->next.empty()) return fail(ctx, GS_ERR_INVALID_ARGUMENT, "set the DFA first");
+  if (state < 0 || state >= ctx->n_states) return fail(ctx, GS_ERR_INVALID_ARGUMENT, "state out of range");
+  int32_t s = state;
+  for (int64_t k = 0; k < n; ++k) {
+    s = ctx->next[(size_t)s * 256 + bytes[k]];
+    if (s < 0 || !ctx->viable[s]) return fail(ctx, GS_ERR_CONSTRAINT_VIOLATION, "Selected token violates the generation constraint");
+  }
+  *state_out = s;
+  return GS_OK;
+}
+
+int gs_legal_token_ids(gs_context* ctx, int32_t state, int32_t* ids, int32_t cap, int32_t* n_out) {
+  if (!ctx || !n_out || cap < 0 || (cap > 0 && !ids)) return fail(ctx, GS_ERR_INVALID_ARGUMENT, "bad arguments");
+  if (!ctx->d_next || !ctx->d_vocab_offsets) return fail(ctx, GS_ERR_INVALID_ARGUMENT, "set the vocab and the DFA first");
+  if (state < 0 || state >= ctx->n_states) return fail(ctx, GS_ERR_INVALID_ARGUMENT, "state out of range");
+  GS_HIP(ctx, hipSetDevice(ctx->device));
+  int st = ensure_stage(ctx, sizeof(uint32_t) * ctx->mask_words);
+  if (st != GS_OK) return st;
+  st = gs_build_masks(ctx, &state, 1, (uint32_t*)ctx->d_stage, ctx->stream);
+  if (st != GS_OK) return st;
+  std::vector<uint32_t> words(ctx->mask_words);
+  GS_HIP(ctx, hipMemcpyAsync(words.data(), ctx->d_stage, sizeof(uint32_t) * words.size(), hipMemcpyDeviceToHost,
+                             ctx->stream));
+  GS_HIP(ctx, hipStreamSynchronize(ctx->stream));
+  int32_t count = 0;
+  for (int32_t w = 0; w < ctx->mask_words; ++w) {
+    for (uint32_t bits = words[w]; bits; bits &= bits - 1) {
+      const int32_t id = w * 32 + __builtin_ctz(bits);
+      if (id >= ctx->vocab) break;
+      if (count < cap) ids[count] = id;
+      ++count;
+    }
+  }
+  *n_out = count;
   return GS_OK;
 }
 

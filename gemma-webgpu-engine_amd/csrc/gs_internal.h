@@ -255,6 +255,7 @@ void launch_finish(const SampleArgs& a, hipStream_t s);
 void launch_exact(const SampleArgs& a, hipStream_t s);
 void launch_logprob(const void* logits, int32_t dtype, int32_t rows, int64_t stride, int32_t vocab,
                     const int32_t* tokens, double* out, hipStream_t s);
+void launch_mask_logits(const float* raw, int64_t n, const int32_t* ids, int64_t n_ids, float* out, hipStream_t s);
 void launch_masks(const int64_t* offsets, const uint8_t* bytes, int32_t vocab, const int16_t* next,
                   const int32_t* states, int32_t n, uint32_t* masks, int32_t mask_words, int32_t n_states,
                   hipStream_t s);

@@ -12,6 +12,11 @@
 // gives two mask words.
 //
 // logprob_kernel: tokenLogProbability (src/runtime/sampling.ts:67-80).
+//
+// mask_fill_kernel + mask_copy_kernel: maskConstraintLogits
+// (src/runtime/constraints.ts:159-173): a row of -Infinity, then the raw
+// logit copied back at every listed id inside [0, n). Listed ids may repeat
+// (legal and termination lists overlap); repeats store the same value.
 #include "gs_internal.h"
 
 namespace gs {
@@ -97,7 +102,33 @@ __global__ __launch_bounds__(kLogThreads) void logprob_kernel(const void* logits
   }
 }
 
+constexpr int kFillThreads = 256;
+
+__global__ __launch_bounds__(kFillThreads) void mask_fill_kernel(float* out, int64_t n) {
+  const int64_t i = (int64_t)blockIdx.x * kFillThreads + threadIdx.x;
+  if (i < n) out[i] = -__builtin_inff();
+}
+
+__global__ __launch_bounds__(kFillThreads) void mask_copy_kernel(const float* raw, int64_t n, const int32_t* ids,
+                                                                 int64_t n_ids, float* out) {
+  const int64_t k = (int64_t)blockIdx.x * kFillThreads + threadIdx.x;
+  if (k >= n_ids) return;
+  const int32_t id = ids[k];
+  if (id >= 0 && id < n) out[id] = raw[id];
+}
+
 }  // namespace
+
+void launch_mask_logits(const float* raw, int64_t n, const int32_t* ids, int64_t n_ids, float* out, hipStream_t s) {
+  if (n > 0) {
+    hipLaunchKernelGGL(mask_fill_kernel, dim3((unsigned)((n + kFillThreads - 1) / kFillThreads)), dim3(kFillThreads),
+                       0, s, out, n);
+  }
+  if (n > 0 && n_ids > 0) {
+    hipLaunchKernelGGL(mask_copy_kernel, dim3((unsigned)((n_ids + kFillThreads - 1) / kFillThreads)),
+                       dim3(kFillThreads), 0, s, raw, n, ids, n_ids, out);
+  }
+}
 
 void launch_masks(const int64_t* offsets, const uint8_t* bytes, int32_t vocab, const int16_t* next,
                   const int32_t* states, int32_t n, uint32_t* masks, int32_t mask_words, int32_t n_states,

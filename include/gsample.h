@@ -159,6 +159,41 @@ int gs_sample(gs_context* ctx, const gs_batch* batch, void* stream);
  * (may be NULL). */
 int gs_sample_sync(gs_context* ctx, const gs_batch* batch, gs_row_result* host_out);
 
+/* Batched sampleToken over HOST arrays, for hosts that hold the logits in
+ * host memory as the reference does (its per-token readback copy,
+ * src/webgpu/decode-model.ts:183-188, handed to sampleToken,
+ * src/runtime/sampling.ts:18-65): every pointer of `batch` is a host pointer
+ * except `logits` when logits_on_device != 0 (device memory, e.g. the output
+ * of gs_lmhead) and `mask_table` (device memory filled by gs_build_masks);
+ * batch->results is ignored. The arrays are staged into context-owned device
+ * memory, the batch is sampled on the context's stream, and the call waits,
+ * writes the rows' results to host_results[rows] and maps the first failing
+ * row to its reference error as gs_sample_sync does. CSR offsets must start
+ * at 0 and never decrease, and every mask_slot must lie in the mask table
+ * (GS_ERR_INVALID_ARGUMENT otherwise). */
+int gs_sample_host(gs_context* ctx, const gs_batch* batch, int32_t logits_on_device, gs_row_result* host_results);
+
+/* Device memory for hosts without a GPU array library (the Node addon):
+ * hipMalloc / hipFree on the context's device, and copies on the context's
+ * stream that return when the bytes have arrived.
+ * (no reference counterpart: the reference's buffers are WebGPU GPUBuffers,
+ *  src/webgpu/decode-model.ts:127-188) */
+int gs_device_alloc(gs_context* ctx, size_t bytes, void** out);
+int gs_device_free(gs_context* ctx, void* ptr);
+int gs_copy_to_device(gs_context* ctx, void* dst_device, const void* src_host, size_t bytes);
+int gs_copy_to_host(gs_context* ctx, void* dst_host, const void* src_device, size_t bytes);
+
+/* maskConstraintLogits (src/runtime/constraints.ts:159-173) on the device:
+ * out[i] = raw[i] for every listed id i in [0, n) (ids outside are ignored),
+ * -Infinity elsewhere. raw, ids and out are DEVICE pointers; enqueued on
+ * `stream` (NULL: the context's). */
+int gs_mask_logits(gs_context* ctx, const float* raw, int64_t n, const int32_t* ids, int64_t n_ids, float* out,
+                   void* stream);
+/* The same over HOST arrays with the reference's two id lists (legal ids,
+ * termination ids); returns when out[n] holds the masked row. */
+int gs_mask_logits_host(gs_context* ctx, const float* raw, int64_t n, const int32_t* legal, int64_t n_legal,
+                        const int32_t* termination, int64_t n_termination, float* out);
+
 /* tokenLogProbability (src/runtime/sampling.ts:67-80) per row:
  * out[r] = logits[r][token[r]] - max - log(sum exp(logits - max)), raw logits. */
 int gs_token_log_prob(gs_context* ctx, const void* logits, int32_t dtype, int32_t rows, int64_t row_stride,
@@ -188,6 +223,16 @@ int gs_build_masks(gs_context* ctx, const int32_t* states, int32_t n, uint32_t* 
 int gs_dfa_advance(gs_context* ctx, const int32_t* states_in, const int32_t* tokens, int32_t n,
                    int32_t* states_out);
 
+/* acceptToken(tokenBytes) (src/runtime/constraints.ts:94-103) on one byte
+ * string: *state_out = the state after bytes[0..n) from `state`;
+ * GS_ERR_CONSTRAINT_VIOLATION ("Selected token violates the generation
+ * constraint") if a byte has no edge or leads out of the viable set. An empty
+ * string leaves the state unchanged. */
+int gs_dfa_advance_bytes(gs_context* ctx, int32_t state, const uint8_t* bytes, int64_t n, int32_t* state_out);
+/* legalTokenIds(trie) (src/runtime/constraints.ts:56-92) of one DFA state as
+ * ascending HOST ids: the first min(cap, count) ids go to ids[], the count
+ * to *n_out. Computed by the mask kernel of gs_build_masks. */
+int gs_legal_token_ids(gs_context* ctx, int32_t state, int32_t* ids, int32_t cap, int32_t* n_out);
 /* accepting (src/runtime/constraints.ts:52-54) of a byte-level DFA state. */
 int gs_dfa_accepting(gs_context* ctx, int32_t state, int32_t* out);
 

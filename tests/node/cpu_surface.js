@@ -1,0 +1,137 @@
+"use strict";
+/*
+ * Node host tests that need no GPU: the addon loads and exports every entry
+ * point, the option surface matches the reference's known answers
+ * (tests/sampling.spec.ts:48-84 of the reference), SeededRandom agrees with
+ * the oracle's restatement, the token-byte CSR, constraint compilation
+ * errors, and the loud failure without a device (no CPU fallback).
+ */
+const assert = require("assert");
+const path = require("path");
+const { test, run } = require("./harness");
+
+const g = require(path.join(__dirname, "..", "..", "gemma-webgpu-engine_amd", "node"));
+const oracle = require(path.join(__dirname, "..", "..", "oracle", "sampler_ref.js"));
+
+const ADDON_FUNCTIONS = [
+  "abiVersion", "deviceCount", "seededRandom", "jsExp", "jsLog", "softcap", "layouts", "validateConfigs",
+  "create", "destroy", "synchronize", "deviceAlloc", "deviceFree", "copyToDevice", "copyToHost", "sampleHost",
+  "tokenLogProbHost", "maskLogitsHost", "setVocab", "setDfa", "buildMasks", "legalTokenIds", "dfaAdvance",
+  "dfaAdvanceBytes", "dfaAccepting", "lmhead", "timingBegin", "timingEnd",
+];
+
+test("addon loads and exports every entry point", () => {
+  const a = g.native();
+  for (const name of ADDON_FUNCTIONS) assert.strictEqual(typeof a[name], "function", name);
+  assert.strictEqual(a.abiVersion(), 1);
+  const L = a.layouts();
+  assert.strictEqual(L.rowConfig.size, 112);
+  assert.strictEqual(L.rowResult.size, 16);
+});
+
+test("validates every decoding control (sampling.spec.ts:48-64)", () => {
+  const result = g.validateDecodingConfig({
+    topP: Number.NaN,
+    repetitionWindow: -1,
+    frequencyPenalty: Number.POSITIVE_INFINITY,
+    presencePenalty: -0.1,
+    stopTokenIds: [1, -2],
+  });
+  assert.strictEqual(result.ok, false);
+  assert.deepStrictEqual(result.errors, [
+    "topP must be between 0 and 1",
+    "repetitionWindow must be a non-negative integer",
+    "frequencyPenalty must be finite and non-negative",
+    "presencePenalty must be finite and non-negative",
+    "stopTokenIds must contain non-negative integers",
+  ]);
+  assert.deepStrictEqual(g.validateDecodingConfig({}), { ok: true, errors: [] });
+  assert.deepStrictEqual(g.validateDecodingConfig({ temperature: -1, topK: 1.5, seed: 0.5, maxNewTokens: 0 }).errors, [
+    "temperature must be >= 0",
+    "topK must be a non-negative integer",
+    "maxNewTokens must be a positive integer",
+    "seed must be an integer",
+  ]);
+});
+
+test("generation defaults and greedy routing (sampling.spec.ts:66-84)", () => {
+  const config = g.resolveGemmaGenerationConfig({});
+  assert.strictEqual(config.maxNewTokens, 256);
+  assert.strictEqual(config.temperature, 0);
+  assert.strictEqual(config.repetitionPenalty, 1);
+  assert.strictEqual(config.repetitionWindow, 0);
+  assert.strictEqual(g.usesGemmaGpuGreedy(config), true);
+  assert.strictEqual(g.usesGemmaGpuGreedy(g.resolveGemmaGenerationConfig({ temperature: 0.8 })), false);
+  assert.strictEqual(g.usesGemmaGpuGreedy(g.resolveGemmaGenerationConfig({ repetitionPenalty: 1.1 })), false);
+  assert.strictEqual(g.usesGemmaGpuGreedy(g.resolveGemmaGenerationConfig({ presencePenalty: 0.1 })), false);
+  assert.throws(() => g.resolveGemmaGenerationConfig({ stopTokenIds: [262144] }),
+    /^Error: Gemma stop token IDs must be below 262144$/);
+  assert.throws(() => g.resolveGemmaGenerationConfig({ topK: -1, topP: 3 }),
+    /^Error: Invalid Gemma decoding config: topK must be a non-negative integer; topP must be between 0 and 1$/);
+  const stops = [5];
+  const resolved = g.resolveGemmaGenerationConfig({ stopTokenIds: stops });
+  assert.notStrictEqual(resolved.stopTokenIds, stops);
+});
+
+test("SeededRandom draws agree with the oracle's restatement", () => {
+  for (const seed of [0, 1, 42, 71, -9, 4294967296 + 5, 0x6d2b79f5, 2147483647]) {
+    const a = new g.SeededRandom(seed);
+    const b = new oracle.SeededRandom(seed);
+    for (let i = 0; i < 3000; i += 1) assert.strictEqual(a.next(), b.next(), "seed " + seed + " draw " + i);
+  }
+  const first = new g.SeededRandom(71);
+  const second = new g.SeededRandom(71);
+  const x = Array.from({ length: 20 }, () => first.next());
+  const y = Array.from({ length: 20 }, () => second.next());
+  assert.deepStrictEqual(x, y);
+});
+
+test("engine math exports match the JS engine", () => {
+  const a = g.native();
+  for (const x of [0, -1e-300, -0.5, -3.25, -40.5, -700, 1e-9, 2.5]) {
+    assert.strictEqual(a.jsExp(x), Math.exp(x), "exp " + x);
+    if (x > 0) assert.strictEqual(a.jsLog(x), Math.log(x), "log " + x);
+  }
+});
+
+test("token byte table: null and empty tokens are skipped", () => {
+  const words = [null, "a", "", "ab", "a", "zz"];
+  const trie = new g.TokenByteTrie({
+    vocabularySize: words.length,
+    tokenBytes: (id) => (words[id] === null ? null : Uint8Array.from(Buffer.from(words[id]))),
+  });
+  assert.strictEqual(trie.tokenCount, 4);
+  assert.deepStrictEqual(Array.from(trie.offsets), [0, 0, 1, 1, 3, 4, 6]);
+  assert.strictEqual(trie.tokenBytes(0), null);
+  assert.strictEqual(trie.tokenBytes(2), null);
+  assert.deepStrictEqual(Array.from(trie.tokenBytes(3)), [97, 98]);
+});
+
+test("constraint compilation: byte-level tables only", () => {
+  assert.throws(() => g.compileGenerationConstraint({ type: "regex", pattern: "a+" }),
+    /^Error: Unsupported generation constraint: regex/);
+  assert.throws(() => new g.ByteLevelDfa({ next: [0], finals: [1] }), /stateCount \* 256/);
+  const next = new Array(256).fill(-1);
+  next[97] = 0;
+  const c = g.compileGenerationConstraint({ type: "byte-dfa", next, finals: [1] });
+  assert.strictEqual(c.accepting, true);
+  c.validateFinal("aaa");
+});
+
+test("reference error messages raised before any device work", () => {
+  assert.throws(() => g.sampleToken([], [], g.DEFAULT_DECODING_CONFIG, Math.random), /^Error: Cannot sample empty logits$/);
+  assert.throws(() => g.tokenLogProbability([1, 2, 3], 3), /^Error: Token 3 is outside logits length 3$/);
+  assert.throws(() => g.tokenLogProbability([1, 2, 3], 1.5), /^Error: Token 1.5 is outside logits length 3$/);
+  assert.strictEqual(g.maskConstraintLogits([], [1], [2]).length, 0);
+});
+
+test("without a device every compute call fails loudly", () => {
+  if (g.native().deviceCount() > 0) return "skip";
+  assert.throws(() => new g.Engine({ vocabSize: 8 }), (e) => e.code === "GS_ERR_NO_DEVICE");
+  assert.throws(() => g.sampleToken(new Float32Array([1, 2]), [], g.DEFAULT_DECODING_CONFIG, () => 0.5),
+    (e) => e.code === "GS_ERR_NO_DEVICE");
+  assert.throws(() => g.maskConstraintLogits(new Float32Array([1, 2]), [0], []), (e) => e.code === "GS_ERR_NO_DEVICE");
+  return undefined;
+});
+
+run();

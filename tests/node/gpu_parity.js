@@ -1,0 +1,361 @@
+"use strict";
+/*
+ * GPU parity of the Node host (index.js -> N-API addon -> libgsample) against
+ * the oracle's JavaScript restatement of the reference sampler
+ * (oracle/sampler_ref.js), on the same float32 rows, seeds and histories:
+ * token ids bit-exact, probabilities within PROB_RTOL relative (one-pass rows
+ * take the softmax normaliser from the chunk scan's table-driven exp sum,
+ * relative error at most 4.2e-10 per term; the path's bound is 1e-6).
+ * Also the reference's own known answers (tests/sampling.spec.ts:13-146 of
+ * the reference), the constraint masker against a brute-force DFA walk, and
+ * the bf16 lm_head feeding the sampler.
+ */
+const assert = require("assert");
+const path = require("path");
+const { test, run } = require("./harness");
+
+const g = require(path.join(__dirname, "..", "..", "gemma-webgpu-engine_amd", "node"));
+const oracle = require(path.join(__dirname, "..", "..", "oracle", "sampler_ref.js"));
+
+const PROB_RTOL = 1e-9;
+const D = g.DEFAULT_DECODING_CONFIG;
+
+/* Seeded N(0, sigma^2) float32 rows: Mulberry32 uniforms, Box-Muller. */
+function normalRow(seed, n, sigma) {
+  const rng = new oracle.SeededRandom(seed);
+  const out = new Float32Array(n);
+  for (let i = 0; i < n; i += 2) {
+    const u1 = Math.max(rng.next(), 1e-12);
+    const u2 = rng.next();
+    const r = Math.sqrt(-2 * Math.log(u1)) * sigma;
+    out[i] = r * Math.cos(2 * Math.PI * u2);
+    if (i + 1 < n) out[i + 1] = r * Math.sin(2 * Math.PI * u2);
+  }
+  return out;
+}
+
+function zipfHistory(seed, n, vocab) {
+  const rng = new oracle.SeededRandom(seed);
+  const h = [];
+  for (let i = 0; i < n; i += 1) h.push(Math.min(vocab - 1, Math.floor(Math.pow(vocab, rng.next() * rng.next()))) - 0);
+  return h;
+}
+
+function checkProb(got, want, what) {
+  assert.ok(Math.abs(got - want) <= PROB_RTOL * Math.abs(want), what + ": probability " + got + " vs " + want);
+}
+
+test("reference known answers (sampling.spec.ts:13-146)", () => {
+  assert.strictEqual(g.sampleToken([0.2, 4, 1], [], Object.assign({}, D, { temperature: 0 }), () => 0.5), 1);
+  assert.strictEqual(g.sampleToken([0.2, 4, 1], [], Object.assign({}, D, { topK: 1 }), () => 0.99), 1);
+  const first = new g.SeededRandom(71);
+  const second = new g.SeededRandom(71);
+  const flat = Object.assign({}, D, { topK: 0, topP: 1 });
+  const a = Array.from({ length: 20 }, () => g.sampleToken([1, 1, 1], [], flat, () => first.next()));
+  const b = Array.from({ length: 20 }, () => g.sampleToken([1, 1, 1], [], flat, () => second.next()));
+  assert.deepStrictEqual(a, b);
+  const ref = new oracle.SeededRandom(71);
+  assert.deepStrictEqual(a, Array.from({ length: 20 }, () => oracle.sampleToken([1, 1, 1], [], flat, () => ref.next())));
+  assert.strictEqual(g.sampleToken([2, 1.5], [0], Object.assign({}, D, { temperature: 0, repetitionPenalty: 2 }), () => 0), 1);
+  assert.strictEqual(g.sampleToken([2, 1.5], [0],
+    Object.assign({}, D, { temperature: 0, repetitionPenalty: 2, repetitionWindow: 0 }), () => 0), 0);
+  const pen = Object.assign({}, D, {
+    temperature: 0, repetitionPenalty: 1, repetitionWindow: 2, presencePenalty: 0.1, frequencyPenalty: 0.3,
+  });
+  assert.strictEqual(g.sampleToken([2, 1.5], [0, 0], pen, () => 0), 1);
+  assert.strictEqual(g.sampleToken([2, 2.1], [0, 1],
+    Object.assign({}, pen, { repetitionWindow: 1, presencePenalty: 0.5, frequencyPenalty: 0 }), () => 0), 0);
+  const three = [Math.log(0.6), Math.log(0.3), Math.log(0.1)];
+  assert.strictEqual(g.sampleToken(three, [],
+    Object.assign({}, D, { temperature: 1, topK: 0, topP: 1, typicalP: 1, minP: 0.6 }), () => 0.99), 0);
+  assert.strictEqual(g.sampleToken(three, [],
+    Object.assign({}, D, { temperature: 1, topK: 0, topP: 0.5, minP: 0, typicalP: 1 }), () => 0.99), 0);
+  assert.strictEqual(g.sampleToken([Math.log(0.45), Math.log(0.4), Math.log(0.15)], [],
+    Object.assign({}, D, { temperature: 1, topK: 0, topP: 1, minP: 0, typicalP: 0.3 }), () => 0.5), 1);
+  // toBeCloseTo's default precision: |diff| < 0.005
+  assert.ok(Math.abs(g.tokenLogProbability(three, 0) - Math.log(0.6)) < 0.005);
+  assert.ok(Math.abs(g.tokenLogProbability(three, 2) - Math.log(0.1)) < 0.005);
+  assert.throws(() => g.tokenLogProbability(three, 3), /outside logits length/);
+});
+
+test("sampleToken matches the oracle on random rows", () => {
+  const configs = [
+    { temperature: 0.8, topK: 40, topP: 0.95 },
+    { temperature: 0.7, topK: 50, topP: 0.9, repetitionPenalty: 1.1, presencePenalty: 0.5, frequencyPenalty: 0.3, repetitionWindow: 64 },
+    { temperature: 1.0, topK: 0, topP: 0.9, repetitionWindow: 0 },
+    { temperature: 1.0, topK: 0, topP: 1, minP: 0.05, repetitionWindow: 0 },
+    { temperature: 0.9, topK: 100, topP: 0.95, typicalP: 0.8 },
+    { temperature: 0, repetitionPenalty: 1.3, repetitionWindow: 32 },
+  ];
+  let rowsChecked = 0;
+  for (const V of [3000, 40000, 262144]) {
+    const cs = V === 262144 ? [configs[0], configs[1], configs[2]] : configs;
+    cs.forEach((c, k) => {
+      const cfg = Object.assign({}, D, c);
+      const seed = V + k;
+      const logits = normalRow(seed, V, 3);
+      const history = zipfHistory(seed + 7, 96, V);
+      const rg = new g.SeededRandom(seed);
+      const ro = new oracle.SeededRandom(seed);
+      const got = g.sampleTokenWithProbability(logits, history, cfg, () => rg.next());
+      const want = oracle.sampleWithProbability(logits, history, cfg, () => ro.next());
+      assert.strictEqual(got.token, want.token, "V=" + V + " config " + k);
+      checkProb(got.probability, want.probability, "V=" + V + " config " + k);
+      rowsChecked += 1;
+    });
+  }
+  assert.ok(rowsChecked >= 15);
+});
+
+test("tokenLogProbability matches the f64 log-softmax", () => {
+  const V = 40000;
+  const logits = normalRow(5, V, 4);
+  for (const token of [0, 17, 39999]) {
+    let max = -Infinity;
+    for (let i = 0; i < V; i += 1) max = Math.max(max, logits[i]);
+    let den = 0;
+    for (let i = 0; i < V; i += 1) den += Math.exp(logits[i] - max);
+    const want = logits[token] - max - Math.log(den);
+    const got = g.tokenLogProbability(logits, token);
+    assert.ok(Math.abs(got - want) <= 1e-12 * Math.max(1, Math.abs(want)), token + ": " + got + " vs " + want);
+  }
+});
+
+test("maskConstraintLogits keeps exactly the listed ids", () => {
+  const V = 5000;
+  const raw = normalRow(9, V, 2);
+  const legal = [3, 3, 4999, 5000, -1, 17, 2.5];
+  const term = [1, 50, 106, 17];
+  const got = g.maskConstraintLogits(raw, legal, term);
+  assert.strictEqual(got.length, V);
+  const keep = new Set([3, 4999, 17, 1, 50, 106]);
+  for (let i = 0; i < V; i += 1) {
+    if (keep.has(i)) assert.strictEqual(got[i], raw[i], "id " + i);
+    else assert.strictEqual(got[i], -Infinity, "id " + i);
+  }
+});
+
+/* A small byte-level DFA over 'a'..'d' and a vocab of short strings. */
+function syntheticConstraint(V, seed) {
+  const rng = new oracle.SeededRandom(seed);
+  const words = [];
+  for (let id = 0; id < V; id += 1) {
+    if (id % 97 === 0) { words.push(null); continue; }
+    const len = 1 + Math.floor(rng.next() * 4);
+    const w = [];
+    for (let j = 0; j < len; j += 1) w.push(97 + Math.floor(rng.next() * 4));
+    words.push(Uint8Array.from(w));
+  }
+  const S = 9;
+  const next = new Int32Array(S * 256).fill(-1);
+  for (let s = 0; s < S - 1; s += 1) {
+    for (let c = 97; c < 101; c += 1) if (rng.next() < 0.7) next[s * 256 + c] = Math.floor(rng.next() * (S - 1));
+  }
+  // state S-1 has no edges and is not final: a dead end
+  const finals = new Uint8Array(S);
+  finals[3] = 1;
+  finals[5] = 1;
+  return { words, dfa: new g.ByteLevelDfa({ next, finals }), S };
+}
+
+function viableStates(dfa) {
+  const viable = new Uint8Array(dfa.stateCount);
+  let changed = true;
+  for (let s = 0; s < dfa.stateCount; s += 1) viable[s] = dfa.finals[s];
+  while (changed) {
+    changed = false;
+    for (let s = 0; s < dfa.stateCount; s += 1) {
+      if (viable[s]) continue;
+      for (let c = 0; c < 256; c += 1) {
+        const t = dfa.next[s * 256 + c];
+        if (t >= 0 && viable[t]) { viable[s] = 1; changed = true; break; }
+      }
+    }
+  }
+  return viable;
+}
+
+/* legalTokenIds by definition: every byte step defined and viable. */
+function bruteLegal(words, dfa, viable, state) {
+  const out = [];
+  words.forEach((w, id) => {
+    if (!w || w.length === 0) return;
+    let s = state;
+    for (let i = 0; i < w.length; i += 1) {
+      s = dfa.next[s * 256 + w[i]];
+      if (s < 0 || !viable[s]) return;
+    }
+    out.push(id);
+  });
+  return out;
+}
+
+test("legalTokenIds, acceptToken and accepting follow the DFA", () => {
+  const V = 6000;
+  const { words, dfa, S } = syntheticConstraint(V, 21);
+  const trie = new g.TokenByteTrie({ vocabularySize: V, tokenBytes: (id) => words[id] });
+  const viable = viableStates(dfa);
+  const c = new g.CompiledGenerationConstraint(dfa, () => {});
+  let nonEmpty = 0;
+  for (let s = 0; s < S; s += 1) {
+    c.state = s;
+    const got = c.legalTokenIds(trie);
+    assert.deepStrictEqual(Array.from(got), bruteLegal(words, dfa, viable, s), "state " + s);
+    assert.ok(Object.isFrozen(got));
+    assert.strictEqual(c.legalTokenIds(trie), got);
+    if (got.length) nonEmpty += 1;
+    assert.strictEqual(c.accepting, dfa.finals[s] === 1);
+  }
+  assert.ok(nonEmpty >= 3);
+  c.state = 0;
+  const legal = c.legalTokenIds(trie);
+  const tok = legal[0];
+  let s = 0;
+  for (const byte of words[tok]) s = dfa.next[s * 256 + byte];
+  c.acceptToken(words[tok]);
+  assert.strictEqual(c.state, s);
+  const illegal = words.findIndex((w, id) => w && legal.indexOf(id) < 0);
+  c.state = 0;
+  assert.throws(() => c.acceptToken(words[illegal]), /^Error: Selected token violates the generation constraint$/);
+  assert.strictEqual(c.state, 0);
+  c.state = S - 1;
+  assert.throws(() => c.validateFinal("x"), /^Error: Generated output ended before the constraint accepted it$/);
+});
+
+test("selectConstrainedToken matches the oracle on the masked row", () => {
+  const V = 6000;
+  const { words, dfa, S } = syntheticConstraint(V, 33);
+  const trie = new g.TokenByteTrie({ vocabularySize: V, tokenBytes: (id) => words[id] });
+  const viable = viableStates(dfa);
+  const c = new g.CompiledGenerationConstraint(dfa, () => {});
+  const cfg = Object.assign({}, D, { temperature: 1, topK: 0, topP: 0.95, repetitionWindow: 16, repetitionPenalty: 1.2 });
+  let checked = 0;
+  for (let s = 0; s < S - 1; s += 1) {
+    if (!viable[s]) continue;
+    c.state = s;
+    const logits = normalRow(100 + s, V, 3);
+    const history = zipfHistory(200 + s, 40, V);
+    const got = g.selectConstrainedToken({
+      logits, history, config: cfg, random: new g.SeededRandom(s), constraint: c, trie,
+      customStopTokens: [7], additionalLegalTokens: [100],
+    });
+    const term = new Set([1, 50, 106, 7]);
+    const legal = new Set(bruteLegal(words, dfa, viable, s).concat([100]).filter((id) => !term.has(id)));
+    if (dfa.finals[s]) term.forEach((id) => legal.add(id));
+    const masked = new Float32Array(V).fill(-Infinity);
+    legal.forEach((id) => { masked[id] = logits[id]; });
+    const ro = new oracle.SeededRandom(s);
+    const want = oracle.sampleToken(masked, history, cfg, () => ro.next());
+    assert.strictEqual(got, want, "state " + s);
+    checked += 1;
+  }
+  assert.ok(checked >= 3);
+  c.state = S - 1;
+  assert.throws(() => g.selectConstrainedToken({
+    logits: normalRow(1, V, 1), history: [], config: cfg, random: new g.SeededRandom(1), constraint: c, trie,
+  }), /^Error: Generation constraint reached a tokenization dead end$/);
+});
+
+test("Engine.sampleRows: batched rows with histories and draw indices", () => {
+  const V = 40000;
+  const R = 32;
+  const engine = new g.Engine({ vocabSize: V, maxRows: R });
+  try {
+    const logits = new Float32Array(R * V);
+    const histories = [];
+    const configs = [];
+    for (let r = 0; r < R; r += 1) {
+      logits.set(normalRow(1000 + r, V, 3), r * V);
+      histories.push(zipfHistory(2000 + r, 200, V));
+      configs.push(Object.assign({}, D, {
+        temperature: 0.7, topK: r % 3 === 0 ? 0 : 50, topP: 0.9, repetitionPenalty: 1.1, presencePenalty: 0.5,
+        frequencyPenalty: 0.3, repetitionWindow: 128, seed: r, drawIndex: r % 5,
+      }));
+    }
+    const out = engine.sampleRows({ logits, rows: R, configs, histories });
+    for (let r = 0; r < R; r += 1) {
+      const ro = new oracle.SeededRandom(r);
+      for (let k = 0; k < r % 5; k += 1) ro.next();
+      const want = oracle.sampleWithProbability(logits.subarray(r * V, (r + 1) * V), histories[r], configs[r], () => ro.next());
+      assert.strictEqual(out.tokens[r], want.token, "row " + r);
+      checkProb(out.probabilities[r], want.probability, "row " + r);
+    }
+  } finally {
+    engine.destroy();
+  }
+});
+
+test("Engine.sampleRows: bf16 rows", () => {
+  const V = 40000;
+  const R = 8;
+  const engine = new g.Engine({ vocabSize: V, maxRows: R });
+  try {
+    const bits = new Uint16Array(R * V);
+    const widened = new Float32Array(R * V);
+    const u32 = new Uint32Array(widened.buffer);
+    for (let r = 0; r < R; r += 1) {
+      const row = normalRow(3000 + r, V, 2);
+      const rb = new Uint32Array(row.buffer);
+      for (let i = 0; i < V; i += 1) {
+        bits[r * V + i] = rb[i] >>> 16;
+        u32[r * V + i] = (rb[i] >>> 16) << 16;
+      }
+    }
+    const configs = Array.from({ length: R }, (_, r) => Object.assign({}, D, { temperature: 1, topK: 0, topP: 0.9, seed: r }));
+    const out = engine.sampleRows({ logits: bits, dtype: "bf16", rows: R, configs, histories: null });
+    for (let r = 0; r < R; r += 1) {
+      const ro = new oracle.SeededRandom(r);
+      const want = oracle.sampleWithProbability(widened.subarray(r * V, (r + 1) * V), [], configs[r], () => ro.next());
+      assert.strictEqual(out.tokens[r], want.token, "row " + r);
+      checkProb(out.probabilities[r], want.probability, "row " + r);
+    }
+  } finally {
+    engine.destroy();
+  }
+});
+
+test("lm_head through device buffers feeds the sampler", () => {
+  const M = 4, W = 128, V = 8192;
+  const engine = new g.Engine({ vocabSize: V, maxRows: M });
+  try {
+    const toBf16 = (x) => {
+      const f = new Float32Array(x);
+      const u = new Uint32Array(f.buffer);
+      const out = new Uint16Array(f.length);
+      for (let i = 0; i < f.length; i += 1) out[i] = u[i] >>> 16;
+      return out;
+    };
+    const fromBf16 = (b) => {
+      const u = new Uint32Array(b.length);
+      for (let i = 0; i < b.length; i += 1) u[i] = b[i] << 16;
+      return new Float32Array(u.buffer);
+    };
+    const hb = toBf16(normalRow(41, M * W, 1));
+    const wb = toBf16(normalRow(42, V * W, 0.2));
+    const hidden = engine.allocate(hb.byteLength).write(hb);
+    const weight = engine.allocate(wb.byteLength).write(wb);
+    const scratch = engine.allocate(4 * M * V);
+    const hf = fromBf16(hb);
+    const wf = fromBf16(wb);
+    const configs = Array.from({ length: M }, (_, r) => Object.assign({}, D, { temperature: 1, topK: 64, topP: 0.95, seed: r }));
+    const out = engine.lmheadSample(hidden, weight, W, 30, scratch, { rows: M, configs, histories: null });
+    const logits = scratch.read(new Float32Array(M * V));
+    for (let m = 0; m < M; m += 1) {
+      for (let v = 0; v < V; v += 517) {
+        let dot = 0;
+        for (let k = 0; k < W; k += 1) dot += hf[m * W + k] * wf[v * W + k];
+        const want = 30 * Math.tanh(dot / 30);
+        assert.ok(Math.abs(logits[m * V + v] - want) <= 2e-5 * Math.max(1, Math.abs(want)), m + "," + v);
+      }
+      const ro = new oracle.SeededRandom(m);
+      const want = oracle.sampleWithProbability(logits.subarray(m * V, (m + 1) * V), [], configs[m], () => ro.next());
+      assert.strictEqual(out.tokens[m], want.token, "row " + m);
+    }
+    [hidden, weight, scratch].forEach((b) => b.free());
+  } finally {
+    engine.destroy();
+  }
+});
+
+run();
+g.releaseEngines();
