@@ -208,10 +208,23 @@ class Engine {
     const [foff, fids, fkinds] = this.packForced(request.forced, rows);
     const R = layouts().rowResult;
     const results = new Uint8Array(R.size * rows);
+    if (!Number.isInteger(rows) || rows < 0 || rows > this.maxRows) throw new RangeError("rows must be 0..maxRows");
+    if (!Number.isInteger(stride) || stride < this.vocabSize) throw new RangeError("rowStride must be >= vocabSize");
+    const esize = dtypeCode(request.dtype) === GS_BF16 ? 2 : 4;
+    if (request.logits instanceof DeviceBuffer) {
+      const need = rows > 0 ? ((rows - 1) * stride + this.vocabSize) * esize : 0;
+      if (request.logits.bytes < need) throw new RangeError("logits buffer holds fewer than rows x rowStride elements");
+    } else if (!request.logits || request.logits.length < rows * stride) {
+      throw new RangeError("logits array holds fewer than rows x rowStride elements");
+    }
+    const maskSlots = request.maskSlots || 0;
+    if (request.maskTable && request.maskTable.bytes < maskSlots * 4 * Math.ceil(this.vocabSize / 32)) {
+      throw new RangeError("maskTable holds fewer than maskSlots masks");
+    }
     const logits = request.logits instanceof DeviceBuffer ? request.logits.handle : request.logits;
     const table = request.maskTable ? request.maskTable.handle : null;
     native().sampleHost(this.context(), logits, dtypeCode(request.dtype), rows, stride, packed, hoff, hids,
-      foff, fids, fkinds, table, request.maskSlots || 0, results);
+      foff, fids, fkinds, table, maskSlots, results);
     const dv = new DataView(results.buffer);
     const out = {
       tokens: new Int32Array(rows),
@@ -257,6 +270,7 @@ class Engine {
   buildMasks(states, table) {
     const words = Math.ceil(this.vocabSize / 32);
     const out = table || this.allocate(4 * words * states.length);
+    if (out.bytes < 4 * words * states.length) throw new RangeError("mask table is smaller than states x ceil(V/32) words");
     native().buildMasks(this.context(), Int32Array.from(states), out.handle);
     return out;
   }
@@ -280,6 +294,13 @@ class Engine {
   /* logits[m][v] = softcap * tanh(hidden[m] . weight[v] / softcap) with bf16
    * hidden [mRows][width] and weight [vocabSize][width] DeviceBuffers. */
   lmhead(hidden, weight, mRows, width, softcap, logits) {
+    if (!Number.isInteger(mRows) || mRows <= 0 || !Number.isInteger(width) || width <= 0) {
+      throw new RangeError("mRows and width must be positive integers");
+    }
+    if (hidden.bytes < 2 * mRows * width || weight.bytes < 2 * this.vocabSize * width ||
+        logits.bytes < 4 * mRows * this.vocabSize) {
+      throw new RangeError("lm_head buffers are smaller than [mRows][width], [vocabSize][width] and [mRows][vocabSize]");
+    }
     native().lmhead(this.context(), hidden.handle, weight.handle, mRows, width, softcap, logits.handle);
     return logits;
   }

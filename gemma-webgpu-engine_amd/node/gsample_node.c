@@ -393,7 +393,9 @@ static napi_value js_sample_host(napi_env env, napi_callback_info info) {
     if ((b.dtype == GS_F32 && t != napi_float32_array) || (b.dtype == GS_BF16 && t != napi_uint16_array))
       return throw_error(env, "GS_ERR_INVALID_ARGUMENT", "logits must be a Float32Array (f32) or Uint16Array (bf16 bits)");
     (void)esize;
-    if (b.rows > 0 && (int64_t)len < (int64_t)(b.rows - 1) * stride + 1)
+    /* the library stages rows x rowStride elements' worth (the last row's
+       padding included), so the array must hold all of it */
+    if (stride < 1 || (int64_t)len < (int64_t)b.rows * stride)
       return throw_error(env, "GS_ERR_INVALID_ARGUMENT", "logits array is shorter than rows x rowStride");
   }
   if (!get_typed(env, argv[5], napi_uint8_array, &data, &n) || n != (size_t)b.rows * sizeof(gs_row_config))
