@@ -135,6 +135,53 @@ test("maskConstraintLogits keeps exactly the listed ids", () => {
   }
 });
 
+/* The reference's constraint known answers (tests/constraints.spec.ts:27-70,
+ * 158-161 of the reference), each regex written as the byte-level DFA that
+ * accepts the same byte strings. */
+function byteDfa(n, edges, finals) {
+  const next = new Int32Array(n * 256).fill(-1);
+  edges.forEach((e) => { next[e[0] * 256 + e[1]] = e[2]; });
+  const f = new Uint8Array(n);
+  finals.forEach((s) => { f[s] = 1; });
+  return { type: "byte-dfa", next, finals: f };
+}
+
+function trieOf(words) {
+  return new g.TokenByteTrie({
+    vocabularySize: words.length,
+    tokenBytes: (id) => (words[id] === null ? null : Uint8Array.from(Buffer.from(words[id], "latin1"))),
+  });
+}
+
+test("reference constraint known answers (constraints.spec.ts:27-70,158-161)", () => {
+  const ch = (c) => c.charCodeAt(0);
+  let trie = trieOf([null, "a", "b", "c", "ab", "ac", "x"]);
+  let c = g.compileGenerationConstraint(byteDfa(3, [[0, ch("a"), 1], [1, ch("b"), 2], [1, ch("c"), 2]], [2]));
+  assert.deepStrictEqual(Array.from(c.legalTokenIds(trie)), [1, 4, 5]);
+  c.acceptToken(Buffer.from("a"));
+  assert.strictEqual(c.accepting, false);
+  assert.deepStrictEqual(Array.from(c.legalTokenIds(trie)), [2, 3]);
+  c.acceptToken(Buffer.from("b"));
+  assert.strictEqual(c.accepting, true);
+  c.validateFinal("ab");
+
+  const ar = Buffer.from("\u0623", "utf8");
+  trie = trieOf([null, ar.slice(0, 1).toString("latin1"), ar.slice(1).toString("latin1"), ar.toString("latin1"), "\xff"]);
+  c = g.compileGenerationConstraint(byteDfa(3, [[0, ar[0], 1], [1, ar[1], 2]], [2]));
+  assert.deepStrictEqual(Array.from(c.legalTokenIds(trie)), [1, 3]);
+  c.acceptToken(ar.slice(0, 1));
+  assert.strictEqual(c.accepting, false);
+  assert.deepStrictEqual(Array.from(c.legalTokenIds(trie)), [2]);
+  c.acceptToken(ar.slice(1));
+  assert.strictEqual(c.accepting, true);
+
+  trie = trieOf([null, "\xef", "\xbf", "\xbd", "{"]);
+  c = g.compileGenerationConstraint(byteDfa(2, [[0, ch("{"), 1]], [1]));
+  assert.deepStrictEqual(Array.from(c.legalTokenIds(trie)), [4]);
+
+  assert.deepStrictEqual(Array.from(g.maskConstraintLogits([1, 2, 3, 4], [1, 3], [0])), [1, 2, -Infinity, 4]);
+});
+
 /* A small byte-level DFA over 'a'..'d' and a vocab of short strings. */
 function syntheticConstraint(V, seed) {
   const rng = new oracle.SeededRandom(seed);
