@@ -10,8 +10,10 @@ temperature 0.7, topK 50, topP 0.9, row r drawing SeededRandom(r).next().
 
 The same run reports
   roofline      the dominant kernel's algorithmic bytes per launch over its
-                mean duration, timed with HIP events around every launch of
-                the timed region (gs_timing_begin / gs_timing_end);
+                mean duration, timed with HIP events around every kernel of
+                a second run of the same K steps (gs_timing_begin /
+                gs_timing_end; the events slow a step down, so the step rate
+                comes from the first run, bracketed by two events only);
   traffic       HBM bytes the dominant kernel moves per launch, taken from the
                 PMC summary committed under profiles/ for this workload (a
                 line "bench-traffic: workload=<w> kernel=<k> bytes=<B>" that
@@ -284,7 +286,7 @@ def main():
     torch.cuda.synchronize()
     log(f"warmup {args.warmup} steps done")
 
-    s.timing_begin(args.steps)
+    # the step rate: K steps bracketed by two events on the launch stream
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
     start.record(stream)
@@ -293,9 +295,18 @@ def main():
     end.record(stream)
     torch.cuda.synchronize()
     total_ms = start.elapsed_time(end)
-    stages = s.timing_end()
     ms_per_step = total_ms / args.steps
-    log(f"timed {args.steps} steps: {ms_per_step * 1000:.1f} us/step; stages {stages}")
+    log(f"timed {args.steps} steps: {ms_per_step * 1000:.1f} us/step")
+
+    # kernel durations: K more steps with HIP events around every kernel on
+    # the stream it runs on (the events add ~20 us per step, so the step rate
+    # above is timed without them)
+    s.timing_begin(args.steps)
+    for _ in range(args.steps):
+        launch_step(wl, sp)
+    torch.cuda.synchronize()
+    stages = s.timing_end()
+    log(f"stage timing over {args.steps} more steps: {stages}")
 
     # results of the last step
     res = wl["keep"][-1] if wl["name"] != "lmhead" else wl["keep"][-4]

@@ -455,8 +455,13 @@ __global__ __launch_bounds__(kFinishThreads) void finish_kernel(SampleArgs a) {
   if (tid < a.n_chunks) {
     S.c_sum[tid] = cs.sum;
     S.c_max[tid] = cs.max_key;
-    for (int w = 0; w < kScanWaves; ++w) S.c_nsub[tid * kScanWaves + w] = cs.n_sub[w];
-    atomicOr(&S.flags, cs.flags);
+    uint32_t overflow = 0;
+    for (int w = 0; w < kScanWaves; ++w) {
+      const uint32_t n = cs.n_sub[w];  // above kSubCap: the sub-list overflowed
+      overflow |= n > (uint32_t)kSubCap;
+      S.c_nsub[tid * kScanWaves + w] = n > (uint32_t)kSubCap ? (uint32_t)kSubCap : n;
+    }
+    atomicOr(&S.flags, cs.flags | (overflow ? kChunkOverflow : 0u));
     atomicMax(&S.max_key, cs.max_key);
     if (cs.truncated) { atomicMax(&S.thr_max, cs.threshold); atomicOr(&S.any_truncated, 1u); }
   }

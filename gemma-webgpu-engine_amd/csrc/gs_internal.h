@@ -31,8 +31,9 @@ constexpr int kExactTile = 4096;                  // LDS tile of the exact path'
 // it bounds the reference's own sequential-sum error (V * 2^-53 ~ 3e-11)
 constexpr double kNearTie = 1.0e-10;
 // relative margin of decisions that depend on the softmax normaliser: the
-// scan's exponential (4.2e-10 per term) and summation order, with room
-constexpr double kNormaliserRel = 2.0e-9;
+// scan's exponentials (each term, then the lane and wave rescales, 4.2e-10
+// each, at most 1.3e-9 together) and summation order, with room
+constexpr double kNormaliserRel = 4.0e-9;
 // the north star's reporting tolerance for top-p boundary ties
 constexpr double kTieReport = 1.0e-6;
 
@@ -98,12 +99,14 @@ __host__ __device__ __forceinline__ Plan plan_row(const gs_row_config& c) {
 struct ChunkStat {
   double sum;          // sum of e^((l - lmax)/T) over finite non-special logits of the chunk
   uint32_t max_key;    // key of lmax (kKeyNegInf or below: no finite non-special logit)
-  uint32_t n_list;     // entries written to the chunk's list (all sub-lists)
+  uint32_t n_list;     // unused (0)
   uint32_t n_finite;   // finite non-special logits
   uint32_t threshold;  // the list holds every finite non-special logit with key >= threshold
   uint32_t truncated;  // some finite logit lies below the threshold
-  uint32_t flags;      // kChunkOverflow | kChunkNonFinite
-  uint16_t n_sub[kScanWaves];  // entries of wave w's sub-list, which starts at slot w * kSubCap
+  uint32_t flags;      // kChunkNonFinite
+  // entries of wave w's sub-list, which starts at slot w * kSubCap; a count
+  // above kSubCap means the wave had more and the sub-list is incomplete
+  uint16_t n_sub[kScanWaves];
 };
 
 // A list slot holds the logit's f32 bits (after softcap) high and its id low;

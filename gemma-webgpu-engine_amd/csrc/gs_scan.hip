@@ -9,12 +9,18 @@
 //     of the reference's softmax normaliser (src/runtime/sampling.ts:36-41).
 //     Each thread sums against its own maximum, so no barrier precedes the
 //     sum, and the 256 partial sums are rescaled to the chunk maximum after;
-//   * a candidate list: every finite logit >= tau, where tau comes from a
-//     radix select over the 256 per-thread maxima such that at least `depth`
-//     of them are >= tau. The list therefore holds the chunk's top-`depth` in
+//   * a candidate list: every finite logit >= tau, where tau is the smallest
+//     of the four waves' d-th largest per-thread maxima (d = ceil(depth/4) + 2,
+//     found with ballots inside each wave), so at least `depth` per-thread
+//     maxima are >= tau. The list therefore holds the chunk's top-`depth` in
 //     the reference's (value desc, id asc) order (sampling.ts:33-35) and every
 //     finite logit of the chunk >= tau. Each wave appends to a sub-list of
 //     its own at positions taken from ballots, so no atomics are involved.
+// The chunk's loads are issued first, from kernel arguments alone; the row's
+// options, window ids and mask words follow while they are in flight. After
+// the special-id bitmap the workgroup meets at one barrier (chunk maximum,
+// sums and tau); the statistics are written by thread 0 and each wave's
+// lane 0 (its sub-list length), so no barrier follows the gather.
 // Logits of "special" ids (the row's penalty window and forced ids) are left
 // out here; the finish kernel evaluates them exactly. Masked ids (constraint
 // bitmask) are -inf, as maskConstraintLogits makes them
@@ -22,7 +28,9 @@
 //
 // The normaliser's exponential is 2^(y/256) = 2^(j/256) * 2^k * e^r with a
 // correctly rounded 256-entry table and a quadratic in r, |r| <= ln2/512:
-// relative error below 4.2e-10 per term. Only the normaliser sees it, and only
+// relative error below 4.2e-10 per evaluation; a term, its lane's rescale to
+// the wave maximum and the wave's rescale to the chunk maximum make at most
+// 1.3e-9. Only the normaliser sees it, and only
 // the top-p cut depends on the normaliser (its margin in the finish kernel
 // covers this); every ordering and every probability the filters compare is
 // recomputed exactly later.
@@ -69,86 +77,84 @@ struct VecTraits<uint16_t> {
 
 __device__ __noinline__ float capped(float x, double cap) { return gsm::softcap_f32(x, cap); }
 
-// Threshold t over the u32 keys s_keys[0..kScanThreads): at least k keys are
-// >= t (every key when fewer than k are non-zero) and, once an 8-bit digit
-// narrows the count to k + slack or fewer, at most that many. MSB-first radix
-// select with LDS histograms; every thread returns the same t.
-__device__ uint32_t radix_floor(const uint32_t* s_keys, uint32_t* s_hist, uint32_t* s_sel, uint32_t k,
-                                uint32_t slack) {
-  const int tid = threadIdx.x;
-  uint32_t prefix = 0, above = 0;
-  for (int shift = 24; shift >= 0; shift -= 8) {
-    s_hist[tid] = 0;
-    __syncthreads();
-    const uint32_t hi_mask = shift == 24 ? 0u : (0xFFFFFFFFu << (shift + 8));
-    const uint32_t key = s_keys[tid];
-    if ((key & hi_mask) == prefix) atomicAdd(&s_hist[(key >> shift) & 255u], 1u);
-    __syncthreads();
-    if (tid < 64) {
-      // lane l holds bins 255-4l .. 252-4l, highest first
-      uint32_t h[4], s = 0;
-#pragma unroll
-      for (int q = 0; q < 4; ++q) { h[q] = s_hist[255 - 4 * tid - q]; s += h[q]; }
-      const uint32_t incl = wave_scan_u32(s, tid);
-      const uint64_t hit = __ballot(above + incl >= k);
-      if (hit == 0) {
-        // fewer than k keys share the prefix (first digit only): take them all
-        if (tid == 63) { s_sel[0] = prefix; s_sel[1] = above; s_sel[2] = above + incl; s_sel[3] = 1; }
-      } else if (tid == __ffsll((unsigned long long)hit) - 1) {
-        uint32_t c = above + incl - s;
-        int q = 0;
-        while (q < 3 && c + h[q] < k) { c += h[q]; ++q; }
-        s_sel[0] = prefix | ((uint32_t)(255 - 4 * tid - q) << shift);
-        s_sel[1] = c;
-        s_sel[2] = c + h[q];
-        s_sel[3] = 0;
-      }
-    }
-    __syncthreads();
-    prefix = s_sel[0];
-    above = s_sel[1];
-    const uint32_t total = s_sel[2];
-    const bool all = s_sel[3] != 0;
-    if (all || total <= k + slack) return prefix;
+// The d-th largest of the wave's lane keys (d >= 1): the largest t with at
+// least d keys >= t, found bit by bit from the top with ballots.
+__device__ __forceinline__ uint32_t wave_kth_key(uint32_t key, uint32_t d) {
+  uint32_t t = 0;
+  for (int b = 31; b >= 0; --b) {
+    const uint32_t c = t | (1u << b);
+    if ((uint32_t)__popcll(__ballot(key >= c)) >= d) t = c;
   }
-  return prefix;
+  return t;
 }
 
 struct ScanShared {
   uint32_t special[kChunk / 32];
   double tab[256];
-  uint32_t keys[kScanThreads];
-  uint32_t hist[256];
-  uint32_t sel[4];
-  double wsum[kScanWaves];
-  uint32_t wmax[kScanWaves];
+  double wsum[kScanWaves];     // wave sum of e^((l - wave max)/T)
+  uint32_t wmax[kScanWaves];   // wave maximum key
   uint32_t wbad[kScanWaves];
-  uint32_t wlanes[kScanWaves];
-  uint32_t wgather[kScanWaves];
+  uint32_t wlanes[kScanWaves]; // lanes with a finite maximum
+  uint32_t wtau[kScanWaves];   // the wave's d-th largest lane maximum (0: fewer than d lanes)
   uint64_t wbest[kScanWaves];
 };
+
+// Loads of one chunk's logits (kFull: 16-byte vector loads).
+template <typename In, bool kFull>
+__device__ __forceinline__ void load_chunk(const SampleArgs& a, int64_t row, int64_t gbase, int n_valid,
+                                           uint4 (&raw)[kElemsPerThread / VecTraits<In>::kVec]) {
+  using VT = VecTraits<In>;
+  constexpr int kVec = VT::kVec;
+  constexpr int kLoads = kElemsPerThread / kVec;
+  const int tid = threadIdx.x;
+  const In* rowp = (const In*)a.logits + row * a.row_stride + gbase;
+  if (kFull) {
+#pragma unroll
+    for (int v = 0; v < kLoads; ++v) raw[v] = *(const uint4*)(rowp + (v * kScanThreads + tid) * kVec);
+  } else {
+    // element loads at 32-bit byte offsets from the uniform row base
+    const char* base = (const char*)rowp;
+#pragma unroll
+    for (int v = 0; v < kLoads; ++v) {
+      const int loc = (v * kScanThreads + tid) * kVec;
+      uint32_t w[4] = {0, 0, 0, 0};
+#pragma unroll
+      for (int j = 0; j < kVec; ++j) {
+        const int i = loc + j < n_valid ? loc + j : n_valid - 1;  // bits past n_valid are cleared later
+        const uint32_t b = VT::one((const In*)(base + (uint32_t)i * (uint32_t)sizeof(In)));
+        if (kVec == 4) w[j] = b;
+        else w[j >> 1] |= (j & 1) ? (b & 0xFFFF0000u) : (b >> 16);
+      }
+      raw[v] = make_uint4(w[0], w[1], w[2], w[3]);
+    }
+  }
+}
 
 // One chunk. kFull: all kChunk logits exist and rows are 16-byte aligned;
 // kMasked: the row has a constraint mask. Each combination is straight-line
 // code from the first load to the first barrier, so the only wait before the
 // barrier is for the loads issued ahead of the chunk.
+// The row's penalty window [w0, w1) and forced ids [f0, f1) as offsets into
+// the history and forced id arrays.
+struct RowRanges {
+  int64_t w0, w1, f0, f1;
+};
+
 template <typename In, bool kFull, bool kMasked>
 __device__ __forceinline__ void scan_chunk(const SampleArgs& a, const gs_row_config& cfg, const Plan plan,
-                                           const int64_t row, const int chunk, const int n_valid, ScanShared& S) {
+                                           const RowRanges rr, const int64_t row, const int chunk,
+                                           const int n_valid, ScanShared& S) {
   using VT = VecTraits<In>;
   constexpr int kVec = VT::kVec;
   constexpr int kLoads = kElemsPerThread / kVec;
   constexpr uint32_t kLaneBits = (1u << kVec) - 1u;
   uint32_t* s_special = S.special;
   double* s_tab = S.tab;
-  uint32_t* s_keys = S.keys;
-  uint32_t* s_hist = S.hist;
-  uint32_t* s_sel = S.sel;
   double* s_wsum = S.wsum;
   uint32_t* s_wmax = S.wmax;
   uint32_t* s_wbad = S.wbad;
   uint32_t* s_wlanes = S.wlanes;
-  uint32_t* s_wgather = S.wgather;
+  uint32_t* s_wtau = S.wtau;
   uint64_t* s_wbest = S.wbest;
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -161,42 +167,21 @@ __device__ __forceinline__ void scan_chunk(const SampleArgs& a, const gs_row_con
   // sits under a branch
   const int32_t* dummy = (const int32_t*)a.configs;
 
-  // -- loads the chunk does not wait for go first: the first window and
-  //    forced ids and this thread's exp-table entry
-  int64_t w0, w1;
-  history_window(a, row, cfg, &w0, &w1);
+  // -- the window and forced ids and this thread's exp-table entry
+  const int64_t w0 = rr.w0, w1 = rr.w1;
   const int64_t wn = w1 - w0;
   const int32_t* hp = wn > 0 ? a.history_ids + w0 : dummy;
   const int32_t hid0 = hp[tid < wn ? tid : 0];
   const int32_t hid1 = hp[tid + kScanThreads < wn ? tid + kScanThreads : 0];
-  int64_t f0 = 0, f1 = 0;
-  if (kMasked && a.forced_offsets) { f0 = a.forced_offsets[row]; f1 = a.forced_offsets[row + 1]; }
+  const int64_t f0 = kMasked ? rr.f0 : 0, f1 = kMasked ? rr.f1 : 0;
   const int64_t fn = f1 - f0;
   const int32_t* fp = fn > 0 ? a.forced_ids + f0 : dummy;
   const int32_t fid0 = fp[tid < fn ? tid : 0];
   const double tabv = c_exp2_256[tid];
 
   // -- the chunk: all loads in flight before the first use
-  const In* rowp = (const In*)a.logits + row * a.row_stride + gbase;
   uint4 raw[kLoads];
-  if (kFull) {
-#pragma unroll
-    for (int v = 0; v < kLoads; ++v) raw[v] = *(const uint4*)(rowp + (v * kScanThreads + tid) * kVec);
-  } else {
-#pragma unroll
-    for (int v = 0; v < kLoads; ++v) {
-      const int loc = (v * kScanThreads + tid) * kVec;
-      uint32_t w[4] = {0, 0, 0, 0};
-#pragma unroll
-      for (int j = 0; j < kVec; ++j) {
-        const int i = loc + j < n_valid ? loc + j : n_valid - 1;  // bits past n_valid are cleared below
-        const uint32_t b = VT::one(rowp + i);
-        if (kVec == 4) w[j] = b;
-        else w[j >> 1] |= (j & 1) ? (b & 0xFFFF0000u) : (b >> 16);
-      }
-      raw[v] = make_uint4(w[0], w[1], w[2], w[3]);
-    }
-  }
+  load_chunk<In, kFull>(a, row, gbase, n_valid, raw);
   uint32_t mword[kLoads];
   if (kMasked) {
     const uint32_t* maskp = a.mask_table + (int64_t)slot * a.mask_words + (gbase >> 5);
@@ -343,26 +328,38 @@ __device__ __forceinline__ void scan_chunk(const SampleArgs& a, const gs_row_con
     }
   }
 
-  // chunk maximum, flags and counts
+  // wave statistics: maximum, flags, finite lanes, the sum rescaled to the
+  // wave maximum and the wave's d-th largest lane maximum
   const uint32_t mykey = finite_max ? f32_key(tmax) : 0u;
-  s_keys[tid] = mykey;
+  const uint32_t depth = (uint32_t)plan.depth;
+  const uint32_t dw = (depth + 3u) / 4u + 2u;
   {
     const uint32_t wm = wave_max_u32(mykey);
     const uint64_t wb = __ballot(thread_bad);
-    const uint64_t wl = __ballot(mykey != 0u);
+    const uint32_t wl = (uint32_t)__popcll(__ballot(mykey != 0u));
+    double part = 0.0;
+    if (finite_max && sum > 0.0) {
+      const double y = ((double)tmax - (double)key_f32(wm)) * A;
+      part = y > kSkipY ? sum * exp2_256(y, s_tab) : 0.0;  // the wave maximum's own factor is exactly 1
+    }
+    part = wave_sum_f64(part);
+    const uint32_t wt = wl >= dw ? wave_kth_key(mykey, dw) : 0u;
     if (lane == 0) {
       s_wmax[wave] = wm;
       s_wbad[wave] = wb != 0;
-      s_wlanes[wave] = (uint32_t)__popcll(wl);
+      s_wlanes[wave] = wl;
+      s_wsum[wave] = part;
+      s_wtau[wave] = wt;
     }
   }
   __syncthreads();
-  uint32_t cmax = 0, cbad = 0, lanes = 0;
+  uint32_t cmax = 0, cbad = 0, lanes = 0, tau = 0xFFFFFFFFu, bound = 0;
 #pragma unroll
   for (int w = 0; w < kScanWaves; ++w) {
     cmax = s_wmax[w] > cmax ? s_wmax[w] : cmax;
     cbad |= s_wbad[w];
     lanes += s_wlanes[w];
+    if (s_wtau[w]) { tau = s_wtau[w] < tau ? s_wtau[w] : tau; bound += dw; }
   }
   if (cbad) {
     // NaN or +inf among the live logits: outside the one-pass contract
@@ -375,23 +372,10 @@ __device__ __forceinline__ void scan_chunk(const SampleArgs& a, const gs_row_con
     return;
   }
 
-  // rescale the thread sums to the chunk maximum
-  {
-    double part = 0.0;
-    if (finite_max && sum > 0.0) {
-      const double y = ((double)tmax - (double)key_f32(cmax)) * A;
-      part = y > kSkipY ? sum * exp2_256(y, s_tab) : 0.0;  // the chunk maximum's own factor is exactly 1
-    }
-    part = wave_sum_f64(part);
-    if (lane == 0) s_wsum[wave] = part;
-  }
-
-  // tau: at least `depth` per-thread maxima are >= tau
-  const uint32_t depth = (uint32_t)plan.depth;
-  uint32_t tau = 0;
-  const bool selected = lanes > depth + 32u;
-  if (selected) tau = radix_floor(s_keys, s_hist, s_sel, depth, 32u);
-  const uint32_t thr = tau > kKeyNegInf ? tau : kKeyNegInf + 1u;
+  // tau: at least `depth` per-thread maxima are >= it (dw of each wave that
+  // has dw finite lanes); nearly full chunks are listed whole
+  const bool selected = lanes > depth + 32u && bound >= depth;
+  const uint32_t thr = selected && tau > kKeyNegInf ? tau : kKeyNegInf + 1u;
   const float tf = key_f32(thr);
 
   // gather every finite logit >= tau into this wave's sub-list
@@ -415,30 +399,29 @@ __device__ __forceinline__ void scan_chunk(const SampleArgs& a, const gs_row_con
       }
     }
   }
-  if (lane == 0) s_wgather[wave] = off;
-  __syncthreads();
+  // the sub-list length; a count above kSubCap tells the finish it overflowed
+  if (lane == 0) stat->n_sub[wave] = (uint16_t)(off < 0xFFFFu ? off : 0xFFFFu);
   if (tid == 0) {
-    ChunkStat st;
+    // the chunk sum: each wave's sum rescaled from its maximum to the chunk's
     double csum = 0.0;
-    uint32_t listed = 0, overflow = 0;
+#pragma unroll
     for (int w = 0; w < kScanWaves; ++w) {
-      csum += s_wsum[w];
-      const uint32_t g = s_wgather[w];
-      const uint32_t n = g < (uint32_t)kSubCap ? g : (uint32_t)kSubCap;
-      listed += n;
-      overflow |= g > (uint32_t)kSubCap;
-      st.n_sub[w] = (uint16_t)n;
+      const double ws = s_wsum[w];
+      if (ws > 0.0) {
+        const double y = ((double)key_f32(s_wmax[w]) - (double)key_f32(cmax)) * A;
+        csum += y > kSkipY ? ws * exp2_256(y, s_tab) : 0.0;
+      }
     }
-    st.sum = csum;
-    st.max_key = cmax;
-    st.n_list = listed;
-    st.n_finite = 0;
-    st.threshold = thr;
+    stat->sum = csum;
+    stat->max_key = cmax;
+    stat->n_list = 0;
+    stat->n_finite = 0;
+    stat->threshold = thr;
     // with a tau, lanes whose maximum lies below it left finite logits out
-    st.truncated = selected ? 1u : 0u;
-    st.flags = overflow ? kChunkOverflow : 0u;
-    *stat = st;
+    stat->truncated = selected ? 1u : 0u;
+    stat->flags = 0u;
   }
+
 }
 
 
@@ -447,25 +430,34 @@ __global__ __launch_bounds__(kScanThreads, 5) void scan_kernel(SampleArgs a) {
   __shared__ ScanShared S;
   const int64_t row = blockIdx.y;
   const int chunk = blockIdx.x;
-  if (row == 0 && chunk == 0 && threadIdx.x == 0) {
-    // reset the queue the finish kernel fills for the exact kernel; both run
-    // after this kernel on the same stream
-    a.queue->count = 0;
-    a.queue->next = 0;
-  }
   const gs_row_config cfg = a.configs[row];
   const Plan plan = plan_row(cfg);
-  if (plan.route == kRouteExact) return;
-  const int64_t gbase = (int64_t)chunk * kChunk;
-  const int n_valid = (int)((int64_t)a.vocab - gbase < kChunk ? (int64_t)a.vocab - gbase : kChunk);
-  const bool masked = cfg.mask_slot >= 0 && cfg.mask_slot < a.mask_slots;
-  const bool full = n_valid == kChunk && a.vector_ok;
-  if (full) {
-    if (masked) scan_chunk<In, true, true>(a, cfg, plan, row, chunk, n_valid, S);
-    else scan_chunk<In, true, false>(a, cfg, plan, row, chunk, n_valid, S);
-  } else {
-    if (masked) scan_chunk<In, false, true>(a, cfg, plan, row, chunk, n_valid, S);
-    else scan_chunk<In, false, false>(a, cfg, plan, row, chunk, n_valid, S);
+  // row-uniform offsets read here, ahead of every branch and store, so they
+  // come through the scalar cache and nothing waits on them behind the chunk
+  RowRanges rr;
+  history_window(a, row, cfg, &rr.w0, &rr.w1);
+  rr.f0 = rr.f1 = 0;
+  if (a.forced_offsets) { rr.f0 = a.forced_offsets[row]; rr.f1 = a.forced_offsets[row + 1]; }
+  if (plan.route != kRouteExact) {
+    const int64_t gbase = (int64_t)chunk * kChunk;
+    const int n_valid = (int)((int64_t)a.vocab - gbase < kChunk ? (int64_t)a.vocab - gbase : kChunk);
+    const bool masked = cfg.mask_slot >= 0 && cfg.mask_slot < a.mask_slots;
+    const bool full = n_valid == kChunk && a.vector_ok;
+    if (full) {
+      if (masked) scan_chunk<In, true, true>(a, cfg, plan, rr, row, chunk, n_valid, S);
+      else scan_chunk<In, true, false>(a, cfg, plan, rr, row, chunk, n_valid, S);
+    } else {
+      if (masked) scan_chunk<In, false, true>(a, cfg, plan, rr, row, chunk, n_valid, S);
+      else scan_chunk<In, false, false>(a, cfg, plan, rr, row, chunk, n_valid, S);
+    }
+  }
+  // reset the queue the finish kernel fills for the exact kernel (both run
+  // after this kernel on the same stream). It is the kernel's last store, so
+  // the loads above of the row's options and history offsets may use the
+  // scalar cache.
+  if (row == 0 && chunk == 0 && threadIdx.x == 0) {
+    a.queue->count = 0;
+    a.queue->next = 0;
   }
 }
 

@@ -109,4 +109,4 @@ def test_lmhead_sample_bit_exact_on_gpu_logits(sampler, lm_inputs, oracle):
         masked = oracle.mask_logits(logits[r], legal, [])
         t, tr = oracle.sample_token(masked, hist[r], ocfg, oracle.draw(r, 0))
         assert int(res["token"][r]) == t, (r, int(res["token"][r]), t, int(res["flags"][r]))
-        assert abs(res["probability"][r] - tr.probability) <= 1e-9 * tr.probability
+        assert abs(res["probability"][r] - tr.probability) <= 2e-9 * tr.probability

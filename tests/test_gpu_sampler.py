@@ -4,7 +4,8 @@ exact path resolved and within PROB_RTOL relative on one-pass rows.
 
 One-pass rows take their softmax normaliser from the chunk scan, which sums
 exp through a 256-entry 2^(j/256) table and a quadratic (relative error at
-most 4.2e-10 per term), so one-pass probabilities carry up to that relative
+most 4.2e-10 per evaluation; a term, its lane's rescale and its wave's rescale
+make at most 1.3e-9), so one-pass probabilities carry up to that relative
 error; the path's stated bound is 1e-6 relative."""
 import math
 
@@ -15,7 +16,7 @@ from oracle.oracle import Decoding
 
 pytestmark = pytest.mark.gpu
 
-PROB_RTOL = 1e-9
+PROB_RTOL = 2e-9
 
 
 def _gs():
