@@ -224,6 +224,121 @@ __device__ void top_r(const uint64_t* s, int n, uint64_t* tmp, uint64_t* top) {
   __syncthreads();
 }
 
+// The kTopR largest entries of s[0..n) into top[0..kTopR), descending and
+// zero-padded, found without sorting the region when possible. Keys lie in
+// [lo, hi]. A 256-bin histogram of (key - lo) >> shift finds the bin holding
+// the kTopR-th largest key: every entry of a higher bin outranks it, so the
+// entries of that bin and above (the survivors) hold the top kTopR. A crowded
+// boundary bin gets a second histogram inside it. When at most 128 entries
+// survive, one wave sorts them in registers. Returns false, with top
+// untouched, when more survive (massive ties); the caller then ranks the
+// whole region. hist: 256 counters, zero on entry and on return; sel: 4
+// words; out: 128 entries of scratch. Ends with a barrier.
+__device__ bool top_select(const uint64_t* s, int n, uint32_t lo, uint32_t hi, uint32_t* hist, uint32_t* sel,
+                           uint64_t* out, uint64_t* top) {
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  constexpr int kMaxE = kFinishCap / kFinishThreads;  // entries per thread
+  constexpr int kOut = 128;
+  const uint64_t* src = s;  // the survivors' array
+  int n_src = n;
+  if (n > kOut) {
+    uint64_t e[kMaxE];
+#pragma unroll
+    for (int q = 0; q < kMaxE; ++q) {
+      const int i = tid + q * kFinishThreads;
+      e[q] = i < n ? s[i] : 0ull;
+    }
+    const uint32_t span = hi - lo;
+    int shift = 0;
+    while ((span >> shift) > 255u) ++shift;
+    uint32_t bin_lo = lo;    // start of the range being binned
+    int width = 32;          // the range is [bin_lo, bin_lo + 2^width), 32: unbounded
+    uint32_t above = 0;      // entries above the range (from the first round)
+    uint32_t floor_key = lo;
+    bool ok = false;
+    for (int round = 0; round < 2 && !ok; ++round) {
+#pragma unroll
+      for (int q = 0; q < kMaxE; ++q) {
+        const int i = tid + q * kFinishThreads;
+        if (i < n) {
+          const uint32_t d = entry_key(e[q]) - bin_lo;  // entries below bin_lo wrap to large values
+          const bool in_range = entry_key(e[q]) >= bin_lo && (width >= 32 || (d >> width) == 0u);
+          const uint32_t bin = d >> shift;
+          if (in_range) atomicAdd(&hist[bin < 255u ? bin : 255u], 1u);
+        }
+      }
+      __syncthreads();
+      if (wave == 0) {
+        // lane l holds bins 255-4l .. 252-4l, highest first
+        uint32_t h[4], c = 0;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) { h[q] = hist[255 - 4 * lane - q]; c += h[q]; }
+        const uint32_t incl = wave_scan_u32(c, lane);
+        const uint64_t hit = __ballot(above + incl >= (uint32_t)kTopR);
+        const int first = hit ? __ffsll((unsigned long long)hit) - 1 : 63;
+        if (lane == first) {
+          uint32_t cum = above + incl - c;
+          int q = 0;
+          while (q < 3 && cum + h[q] < (uint32_t)kTopR) { cum += h[q]; ++q; }
+          sel[0] = (uint32_t)(255 - 4 * lane - q);  // boundary bin
+          sel[1] = cum;                              // entries above it
+          sel[2] = cum + h[q];                       // survivors
+        }
+      }
+      __syncthreads();
+      const uint32_t b = sel[0];
+      floor_key = bin_lo + (b << shift);
+      ok = sel[2] <= (uint32_t)kOut;
+      above = sel[1];
+      if (tid < 256) hist[tid] = 0;  // zero again for the next round or the next use
+      __syncthreads();
+      if (!ok) {
+        if (shift == 0) break;  // one key value holds too many entries
+        bin_lo = floor_key;
+        width = shift;
+        shift = shift > 8 ? shift - 8 : 0;
+      }
+    }
+    if (!ok) return false;
+    // compact the survivors (keys >= floor_key) into out[]
+    if (tid == 0) sel[3] = 0;
+    __syncthreads();
+#pragma unroll
+    for (int q = 0; q < kMaxE; ++q) {
+      const int i = tid + q * kFinishThreads;
+      const bool keep = i < n && entry_key(e[q]) >= floor_key;
+      const uint64_t m = __ballot(keep);
+      uint32_t base = 0;
+      if (lane == 0 && m) base = atomicAdd(&sel[3], (uint32_t)__popcll(m));
+      base = (uint32_t)__shfl((int)base, 0, 64);
+      if (keep) {
+        const uint32_t pos =
+            base + __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
+        if (pos < (uint32_t)kOut) out[pos] = e[q];
+      }
+    }
+    __syncthreads();
+    src = out;
+    n_src = (int)(sel[3] < (uint32_t)kOut ? sel[3] : (uint32_t)kOut);
+  }
+  if (wave == 0) {
+    uint64_t v[2];
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+      const int i = lane * 2 + q;
+      v[q] = i < n_src ? src[i] : 0ull;
+    }
+    wave_sort_desc_regs<2>(v);
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+      const int i = lane * 2 + q;
+      if (i < kTopR) top[i] = v[q];
+    }
+  }
+  __syncthreads();
+  return true;
+}
+
 __device__ __forceinline__ int pow2_at_least(int n) {
   int p = 1;
   while (p < n) p <<= 1;
@@ -242,6 +357,8 @@ struct Shared {
   uint32_t c_max[kFinishMaxChunks];
   uint16_t c_nsub[kFinishMaxChunks * kScanWaves];
   uint64_t top[kTopR];                // the fast path's ranked non-specials
+  uint32_t hist[256];                 // top_select's histogram (zero between uses)
+  uint32_t sel[4];
   double wsum[kWaves];
   double wtmp[kWaves];
   double total;
@@ -449,6 +566,7 @@ __global__ __launch_bounds__(kFinishThreads) void finish_kernel(SampleArgs a) {
     S.special_legal = 0; S.best_entry = 0; S.sp_max = 0; S.fast_done = 0;
   }
   for (int h = tid; h < kHashSize; h += kFinishThreads) { S.hash_ids[h] = 0xFFFFFFFFu; S.hash_counts[h] = 0; }
+  if (tid < 256) S.hist[tid] = 0;
   __syncthreads();
 
   // ---- 1. statistics into LDS, distinct special ids into the hash
@@ -738,9 +856,12 @@ __global__ __launch_bounds__(kFinishThreads) void finish_kernel(SampleArgs a) {
   const int n_top_all = n_ns < kTopR ? n_ns : kTopR;
   if (n_sp_in <= 2 * kTopR - n_top_all) {
     uint64_t* tmp = (uint64_t*)S.cand_p;  // kWaves * 64 entries of merge scratch
-    if (n_ns <= kWaves * 64) top_r<1>(S.sorted, n_ns, tmp, S.top);
-    else if (n_ns <= kWaves * 128) top_r<2>(S.sorted, n_ns, tmp, S.top);
-    else top_r<4>(S.sorted, n_ns, tmp, S.top);
+    const uint32_t lo = thr > kKeyNegInf ? thr : kKeyNegInf + 1u;
+    if (!top_select(S.sorted, n_ns, lo, S.max_key > lo ? S.max_key : lo, S.hist, S.sel, tmp, S.top)) {
+      if (n_ns <= kWaves * 64) top_r<1>(S.sorted, n_ns, tmp, S.top);
+      else if (n_ns <= kWaves * 128) top_r<2>(S.sorted, n_ns, tmp, S.top);
+      else top_r<4>(S.sorted, n_ns, tmp, S.top);
+    }
     if (wave == 0) {
       const int n_top = n_ns < kTopR ? n_ns : kTopR;
       double* fp = S.cand_p + kWaves * 64;  // past the merge scratch
