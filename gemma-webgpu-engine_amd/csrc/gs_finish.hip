@@ -637,33 +637,56 @@ __global__ __launch_bounds__(kFinishThreads) void finish_kernel(SampleArgs a) {
     lv[q] = k < cnt0 ? lists[(int64_t)sl0 * kSubCap + k] : 0ull;
   }
 
-  // evaluate every special exactly: mask / termination rules, then penalties
+  // evaluate every special exactly: mask / termination rules, then penalties.
+  // Slots, flags and the maximum are gathered per wave, one LDS atomic each.
+  {
+    uint64_t my_max = 0;
+    bool my_legal = false, my_nonfinite = false;
 #pragma unroll
-  for (int r = 0; r < kSlotsPerThread; ++r) {
-    const uint32_t id = hid[r];
-    if (id == 0xFFFFFFFFu) continue;
-    const uint32_t count = hpk[r] & 0xFFFFFFu, kinds = hpk[r] >> 24;
-    const uint32_t idx = atomicAdd(&S.n_special, 1u);
-    if (idx >= (uint32_t)kSpecialCap) continue;
-    float x32 = raw[r];
-    if (cfg.softcap > 0) x32 = gsm::softcap_f32(x32, cfg.softcap);
-    bool allowed = true;
-    if (constrained) {
-      const bool term = kinds & GS_FORCED_TERMINATION;
-      const bool extra = kinds & GS_FORCED_EXTRA;
-      allowed = term ? cfg.accepting != 0 : (extra || ((mw[r] >> (id & 31)) & 1u));
+    for (int r = 0; r < kSlotsPerThread; ++r) {
+      const uint32_t id = hid[r];
+      const bool used = id != 0xFFFFFFFFu;
+      const uint64_t m = __ballot(used);
+      if (m == 0) continue;
+      uint32_t base = 0;
+      if (lane == 0) base = atomicAdd(&S.n_special, (uint32_t)__popcll(m));
+      base = (uint32_t)__shfl((int)base, 0, 64);
+      if (!used) continue;
+      const uint32_t idx =
+          base + __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
+      if (idx >= (uint32_t)kSpecialCap) continue;
+      const uint32_t count = hpk[r] & 0xFFFFFFu, kinds = hpk[r] >> 24;
+      float x32 = raw[r];
+      if (cfg.softcap > 0) x32 = gsm::softcap_f32(x32, cfg.softcap);
+      bool allowed = true;
+      if (constrained) {
+        const bool term = kinds & GS_FORCED_TERMINATION;
+        const bool extra = kinds & GS_FORCED_EXTRA;
+        allowed = term ? cfg.accepting != 0 : (extra || ((mw[r] >> (id & 31)) & 1u));
+      }
+      my_legal |= allowed;
+      my_nonfinite |= allowed && !(x32 < __builtin_inff());
+      double x = allowed ? (double)x32 : -__builtin_inf();
+      if (count > 0) {
+        x = x < 0 ? x * cfg.repetition_penalty : x / cfg.repetition_penalty;
+        x -= cfg.presence_penalty + (double)count * cfg.frequency_penalty;
+      }
+      const double v = greedy ? x : x / T;
+      const uint64_t key = f64_key(v);
+      S.sp_key[idx] = key;
+      S.sp_id[idx] = id;
+      my_max = key > my_max ? key : my_max;
     }
-    if (allowed) atomicOr(&S.special_legal, 1u);
-    if (allowed && !(x32 < __builtin_inff())) atomicOr(&S.flags, kChunkNonFinite);
-    double x = allowed ? (double)x32 : -__builtin_inf();
-    if (count > 0) {
-      x = x < 0 ? x * cfg.repetition_penalty : x / cfg.repetition_penalty;
-      x -= cfg.presence_penalty + (double)count * cfg.frequency_penalty;
+    const uint64_t legal_w = __ballot(my_legal), bad_w = __ballot(my_nonfinite);
+    for (int m = 32; m > 0; m >>= 1) {
+      const uint64_t o = shfl_xor_u64(my_max, m);
+      my_max = o > my_max ? o : my_max;
     }
-    const double v = greedy ? x : x / T;
-    S.sp_key[idx] = f64_key(v);
-    S.sp_id[idx] = id;
-    atomicMax((unsigned long long*)&S.sp_max, (unsigned long long)f64_key(v));
+    if (lane == 0) {
+      if (legal_w) atomicOr(&S.special_legal, 1u);
+      if (bad_w) atomicOr(&S.flags, kChunkNonFinite);
+      if (my_max) atomicMax((unsigned long long*)&S.sp_max, (unsigned long long)my_max);
+    }
   }
 
   // the complete region: listed entries with key >= thr, appended with one

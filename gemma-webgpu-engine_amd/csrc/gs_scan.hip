@@ -425,8 +425,10 @@ __device__ __forceinline__ void scan_chunk(const SampleArgs& a, const gs_row_con
 }
 
 
-template <typename In>
-__global__ __launch_bounds__(kScanThreads, 5) void scan_kernel(SampleArgs a) {
+// kMaskable: the batch has a mask table (otherwise no row is constrained and
+// the masked variants, which need more registers, are left out).
+template <typename In, bool kMaskable>
+__global__ __launch_bounds__(kScanThreads, kMaskable ? 5 : 6) void scan_kernel(SampleArgs a) {
   __shared__ ScanShared S;
   const int64_t row = blockIdx.y;
   const int chunk = blockIdx.x;
@@ -441,13 +443,13 @@ __global__ __launch_bounds__(kScanThreads, 5) void scan_kernel(SampleArgs a) {
   if (plan.route != kRouteExact) {
     const int64_t gbase = (int64_t)chunk * kChunk;
     const int n_valid = (int)((int64_t)a.vocab - gbase < kChunk ? (int64_t)a.vocab - gbase : kChunk);
-    const bool masked = cfg.mask_slot >= 0 && cfg.mask_slot < a.mask_slots;
+    const bool masked = kMaskable && cfg.mask_slot >= 0 && cfg.mask_slot < a.mask_slots;
     const bool full = n_valid == kChunk && a.vector_ok;
     if (full) {
-      if (masked) scan_chunk<In, true, true>(a, cfg, plan, rr, row, chunk, n_valid, S);
+      if (masked) scan_chunk<In, true, kMaskable>(a, cfg, plan, rr, row, chunk, n_valid, S);
       else scan_chunk<In, true, false>(a, cfg, plan, rr, row, chunk, n_valid, S);
     } else {
-      if (masked) scan_chunk<In, false, true>(a, cfg, plan, rr, row, chunk, n_valid, S);
+      if (masked) scan_chunk<In, false, kMaskable>(a, cfg, plan, rr, row, chunk, n_valid, S);
       else scan_chunk<In, false, false>(a, cfg, plan, rr, row, chunk, n_valid, S);
     }
   }
@@ -465,8 +467,14 @@ __global__ __launch_bounds__(kScanThreads, 5) void scan_kernel(SampleArgs a) {
 
 void launch_scan(const SampleArgs& a, hipStream_t s) {
   dim3 grid(a.n_chunks, a.rows);
-  if (a.dtype == GS_BF16) hipLaunchKernelGGL(scan_kernel<uint16_t>, grid, dim3(kScanThreads), 0, s, a);
-  else hipLaunchKernelGGL(scan_kernel<float>, grid, dim3(kScanThreads), 0, s, a);
+  const bool maskable = a.mask_slots > 0;
+  if (a.dtype == GS_BF16) {
+    if (maskable) hipLaunchKernelGGL((scan_kernel<uint16_t, true>), grid, dim3(kScanThreads), 0, s, a);
+    else hipLaunchKernelGGL((scan_kernel<uint16_t, false>), grid, dim3(kScanThreads), 0, s, a);
+  } else {
+    if (maskable) hipLaunchKernelGGL((scan_kernel<float, true>), grid, dim3(kScanThreads), 0, s, a);
+    else hipLaunchKernelGGL((scan_kernel<float, false>), grid, dim3(kScanThreads), 0, s, a);
+  }
 }
 
 }  // namespace gs
