@@ -470,6 +470,10 @@ __device__ void process_row(const SampleArgs& a, Lds& L, Scratch S, int64_t row)
 __global__ __launch_bounds__(kExactThreads) void exact_kernel(SampleArgs a) {
   __shared__ Lds L;
   const Scratch S = scratch_of(a);
+  // the queue is complete (the finish kernel ran before this one): workgroups
+  // beyond its length leave without touching the shared counter, so an empty
+  // queue costs one plain load per workgroup
+  if (blockIdx.x >= a.queue->count) return;
   for (;;) {
     if (threadIdx.x == 0) {
       const uint32_t q = atomicAdd(&a.queue->next, 1u);

@@ -9,8 +9,9 @@
 //     in slabs of 128 rows (and M in blocks of 64 rows);
 //   * per 64-wide K block a lane loads 64 contiguous bytes of one weight row
 //     (half the block: lanes 0-31 take k 0-31, lanes 32-63 take k 32-63), so
-//     each row's 128-byte line is consumed whole and the next block is
-//     prefetched into registers while the current one is multiplied;
+//     each row's 128-byte line is consumed whole; weight and H loads run
+//     three K blocks ahead of their use in a register ring, so no wait
+//     covers a load issued less than two blocks earlier;
 //   * H's 64x64 block is staged in LDS (double-buffered, rows padded to 144 B)
 //     and shared by the four waves;
 //   * v_mfma_f32_32x32x16_bf16: a K block is 4 steps x 2 M tiles. The K order
@@ -43,47 +44,68 @@ __global__ __launch_bounds__(kLmThreads) void lmhead_kernel(const uint16_t* __re
   const int nrow = n0 + (lane & 31) < V ? n0 + (lane & 31) : V - 1;
   const uint16_t* wrow = W + (size_t)nrow * D + h * 32;
 
+  // H: thread t stages 32 bytes of row t/4 of the 64x64 block (rows past M
+  // read row M-1 and are stored as zeros)
   const int ar = tid >> 2, ac = (tid & 3) * 16;
-  auto load_a = [&](int buf, int kb) {
-    uint4 v0 = make_uint4(0, 0, 0, 0), v1 = make_uint4(0, 0, 0, 0);
-    if (m0 + ar < M) {
-      const uint4* p = (const uint4*)(H + (size_t)(m0 + ar) * D + kb + ac);
-      v0 = p[0];
-      v1 = p[1];
-    }
-    *(uint4*)&sA[buf][ar][ac] = v0;
-    *(uint4*)&sA[buf][ar][ac + 8] = v1;
+  const bool a_live = m0 + ar < M;
+  const uint16_t* hrow = H + (size_t)(a_live ? m0 + ar : M - 1) * D + ac;
+
+  // A ring of kDepth K-blocks in flight per lane: the weight row slice this
+  // lane multiplies (64 bytes) and this thread's share of the H block. The
+  // main loop is unrolled by kDepth and branch-free, so every ring slot is a
+  // fixed register set and each wait covers only loads issued kDepth - 1 or
+  // kDepth blocks earlier (loads complete in issue order). Prefetches past
+  // the last block re-read the last block (cache hits, never used).
+  constexpr int kDepth = 3;
+  const int nk = D / kKBlock;
+  uint4 wr[kDepth][4], hr[kDepth][2];
+  auto issue = [&](int slot, int kb) __attribute__((always_inline)) {
+    kb = kb < nk ? kb : nk - 1;
+    const uint4* pw = (const uint4*)(wrow + (size_t)kb * kKBlock);
+    const uint4* ph = (const uint4*)(hrow + (size_t)kb * kKBlock);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) wr[slot][i] = pw[i];
+    hr[slot][0] = ph[0];
+    hr[slot][1] = ph[1];
+  };
+  const uint32_t a_mask = a_live ? 0xFFFFFFFFu : 0u;  // rows past M stage zeros
+  auto stage_h = [&](int buf, int slot) __attribute__((always_inline)) {
+    const uint4 v0 = hr[slot][0], v1 = hr[slot][1];
+    *(uint4*)&sA[buf][ar][ac] = make_uint4(v0.x & a_mask, v0.y & a_mask, v0.z & a_mask, v0.w & a_mask);
+    *(uint4*)&sA[buf][ar][ac + 8] = make_uint4(v1.x & a_mask, v1.y & a_mask, v1.z & a_mask, v1.w & a_mask);
   };
 
   f32x16 acc0, acc1;
 #pragma unroll
   for (int i = 0; i < 16; ++i) { acc0[i] = 0.0f; acc1[i] = 0.0f; }
-  uint4 b[4], bn[4];
-  load_a(0, 0);
-#pragma unroll
-  for (int i = 0; i < 4; ++i) b[i] = ((const uint4*)wrow)[i];
-  __syncthreads();
-
-  const int nk = D / kKBlock;
-  for (int kbi = 0; kbi < nk; ++kbi) {
+  auto step = [&](int kbi, int p) __attribute__((always_inline)) {
     const int buf = kbi & 1;
-    if (kbi + 1 < nk) {
-      load_a(buf ^ 1, (kbi + 1) * kKBlock);
-      const uint4* p = (const uint4*)(wrow + (size_t)(kbi + 1) * kKBlock);
-#pragma unroll
-      for (int i = 0; i < 4; ++i) bn[i] = p[i];
-    }
+    // the next block's H into the other buffer (its loads left kDepth-1 blocks ago)
+    stage_h(buf ^ 1, (p + 1) % kDepth);
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
-      const bf16x8 bf = as_bf16x8(b[s]);
+      const bf16x8 bf = as_bf16x8(wr[p][s]);
       const bf16x8 a0 = as_bf16x8(*(const uint4*)&sA[buf][lane & 31][h * 32 + s * 8]);
       const bf16x8 a1 = as_bf16x8(*(const uint4*)&sA[buf][32 + (lane & 31)][h * 32 + s * 8]);
       acc0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a0, bf, acc0, 0, 0, 0);
       acc1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a1, bf, acc1, 0, 0, 0);
     }
+    issue(p, kbi + kDepth);  // refill this slot
     __syncthreads();
+  };
 #pragma unroll
-    for (int i = 0; i < 4; ++i) b[i] = bn[i];
+  for (int p = 0; p < kDepth; ++p) issue(p, p);
+  stage_h(0, 0);
+  __syncthreads();
+  const int n_main = nk - nk % kDepth;
+  for (int kb0 = 0; kb0 < n_main; kb0 += kDepth) {
+#pragma unroll
+    for (int p = 0; p < kDepth; ++p) step(kb0 + p, p);
+  }
+  // the last nk % kDepth blocks sit in the first ring slots
+#pragma unroll
+  for (int p = 0; p < kDepth - 1; ++p) {
+    if (n_main + p < nk) step(n_main + p, p);
   }
 
   // D layout of a 32x32 tile: lane l, register r -> column l % 32,
