@@ -234,13 +234,25 @@ __device__ void top_r(const uint64_t* s, int n, uint64_t* tmp, uint64_t* top) {
 // untouched, when more survive (massive ties); the caller then ranks the
 // whole region. hist: 256 counters, zero on entry and on return; sel: 4
 // words; out: 128 entries of scratch. Ends with a barrier.
+__device__ __forceinline__ int top_select_shift(uint32_t lo, uint32_t hi) {
+  const uint32_t span = hi - lo;
+  int shift = 0;
+  while ((span >> shift) > 255u) ++shift;
+  return shift;
+}
+
+// hist_ready: hist already holds the first round's counts of s[0..n)
+// (bins (key - lo) >> top_select_shift(lo, hi), clamped to 255).
 __device__ bool top_select(const uint64_t* s, int n, uint32_t lo, uint32_t hi, uint32_t* hist, uint32_t* sel,
-                           uint64_t* out, uint64_t* top) {
+                           uint64_t* out, uint64_t* top, bool hist_ready) {
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   constexpr int kMaxE = kFinishCap / kFinishThreads;  // entries per thread
   constexpr int kOut = 128;
   const uint64_t* src = s;  // the survivors' array
   int n_src = n;
+  if (n <= kOut && hist_ready) {
+    if (tid < 256) hist[tid] = 0;  // left zero for the next use
+  }
   if (n > kOut) {
     uint64_t e[kMaxE];
 #pragma unroll
@@ -248,9 +260,7 @@ __device__ bool top_select(const uint64_t* s, int n, uint32_t lo, uint32_t hi, u
       const int i = tid + q * kFinishThreads;
       e[q] = i < n ? s[i] : 0ull;
     }
-    const uint32_t span = hi - lo;
-    int shift = 0;
-    while ((span >> shift) > 255u) ++shift;
+    int shift = top_select_shift(lo, hi);
     uint32_t bin_lo = lo;    // start of the range being binned
     int width = 32;          // the range is [bin_lo, bin_lo + 2^width), 32: unbounded
     uint32_t above = 0;      // entries above the range (from the first round)
@@ -259,6 +269,7 @@ __device__ bool top_select(const uint64_t* s, int n, uint32_t lo, uint32_t hi, u
     for (int round = 0; round < 2 && !ok; ++round) {
 #pragma unroll
       for (int q = 0; q < kMaxE; ++q) {
+        if (round == 0 && hist_ready) break;
         const int i = tid + q * kFinishThreads;
         if (i < n) {
           const uint32_t d = entry_key(e[q]) - bin_lo;  // entries below bin_lo wrap to large values
@@ -337,6 +348,24 @@ __device__ bool top_select(const uint64_t* s, int n, uint32_t lo, uint32_t hi, u
   }
   __syncthreads();
   return true;
+}
+
+// special_insert that also reports the id's slot and whether this call put
+// the id there (its "owner" evaluates it once the counts are complete)
+__device__ __forceinline__ bool special_insert_owner(SpecialTable t, uint32_t id, uint32_t kind, int* slot) {
+  uint32_t h = hash_id(id) & (kHashSize - 1);
+  for (int probe = 0; probe < kHashSize; ++probe) {
+    const uint32_t prev = atomicCAS(&t.ids[h], 0xFFFFFFFFu, id);
+    if (prev == 0xFFFFFFFFu || prev == id) {
+      if (kind == 0) atomicAdd(&t.counts[h], 1u);
+      else atomicOr(&t.counts[h], kind << 24);
+      *slot = (int)h;
+      return prev == 0xFFFFFFFFu;
+    }
+    h = (h + 1) & (kHashSize - 1);
+  }
+  *slot = -1;
+  return false;
 }
 
 __device__ __forceinline__ int pow2_at_least(int n) {
@@ -559,6 +588,20 @@ __global__ __launch_bounds__(kFinishThreads) void finish_kernel(SampleArgs a) {
   }
   int64_t f0 = 0, f1 = 0;
   if (constrained && a.forced_offsets) { f0 = a.forced_offsets[row]; f1 = a.forced_offsets[row + 1]; }
+  // specials this thread owns the loads of: its window positions and its
+  // first forced id; rows with longer lists evaluate from the hash slots
+  const bool own_path = w1 - w0 <= (int64_t)kIdsPerThread * kFinishThreads && f1 - f0 <= kFinishThreads;
+  constexpr int kOwn = kIdsPerThread + 1;
+  int32_t oid[kOwn];
+  uint32_t okind[kOwn];
+#pragma unroll
+  for (int r = 0; r < kIdsPerThread; ++r) { oid[r] = wid[r]; okind[r] = 0; }
+  oid[kIdsPerThread] = -1;
+  okind[kIdsPerThread] = 0;
+  if (f0 + tid < f1) {
+    oid[kIdsPerThread] = a.forced_ids[f0 + tid];
+    okind[kIdsPerThread] = (uint32_t)a.forced_kinds[f0 + tid] & 3u;
+  }
 
   if (tid == 0) {
     S.flags = 0; S.max_key = 0; S.thr_max = 0; S.any_truncated = 0; S.n_sorted = 0; S.n_special = 0;
@@ -583,17 +626,31 @@ __global__ __launch_bounds__(kFinishThreads) void finish_kernel(SampleArgs a) {
     atomicMax(&S.max_key, cs.max_key);
     if (cs.truncated) { atomicMax(&S.thr_max, cs.threshold); atomicOr(&S.any_truncated, 1u); }
   }
+  // the owned specials' logits and mask words start loading now, so they
+  // arrive while the hash is built
+  float oraw[kOwn];
+  uint32_t omw[kOwn];
+  int oslot[kOwn];
+  bool ofirst[kOwn];
+#pragma unroll
+  for (int r = 0; r < kOwn; ++r) {
+    const bool ok = own_path && oid[r] >= 0 && oid[r] < a.vocab;
+    oraw[r] = ok ? load_logit(a, row, oid[r]) : 0.0f;
+    omw[r] = ok && constrained ? a.mask_table[(int64_t)slot * a.mask_words + (oid[r] >> 5)] : 0u;
+  }
   {
     SpecialTable tab{S.hash_ids, S.hash_counts};
 #pragma unroll
-    for (int r = 0; r < kIdsPerThread; ++r) {
-      if (wid[r] >= 0 && wid[r] < a.vocab) special_insert(tab, (uint32_t)wid[r], 0u);
+    for (int r = 0; r < kOwn; ++r) {
+      oslot[r] = -1;
+      ofirst[r] = false;
+      if (oid[r] >= 0 && oid[r] < a.vocab) ofirst[r] = special_insert_owner(tab, (uint32_t)oid[r], okind[r], &oslot[r]);
     }
     for (int64_t j = w0 + tid + (int64_t)kIdsPerThread * kFinishThreads; j < w1; j += kFinishThreads) {
       const int32_t id = a.history_ids[j];
       if (id >= 0 && id < a.vocab) special_insert(tab, (uint32_t)id, 0u);
     }
-    for (int64_t j = f0 + tid; j < f1; j += kFinishThreads) {
+    for (int64_t j = f0 + tid + kFinishThreads; j < f1; j += kFinishThreads) {
       const int32_t id = a.forced_ids[j];
       if (id >= 0 && id < a.vocab) special_insert(tab, (uint32_t)id, (uint32_t)a.forced_kinds[j] & 3u);
     }
@@ -613,18 +670,32 @@ __global__ __launch_bounds__(kFinishThreads) void finish_kernel(SampleArgs a) {
   const uint32_t thr = S.thr_max;  // 0 when no chunk was truncated: every finite logit is listed
   const uint64_t* lists = a.lists + row * a.n_chunks * kGatherCap;
   const int n_subs = a.n_chunks * kScanWaves;
-  uint32_t hid[kSlotsPerThread], hpk[kSlotsPerThread], mw[kSlotsPerThread];
-  float raw[kSlotsPerThread];
+  // the specials to evaluate: each owner's (own_path), else every hash slot
+  // with its logit and mask word loaded now
+  constexpr int kEval = kSlotsPerThread > kOwn ? kSlotsPerThread : kOwn;
+  uint32_t hid[kEval], hpk[kEval], mw[kEval];
+  float raw[kEval];
+  if (own_path) {
 #pragma unroll
-  for (int r = 0; r < kSlotsPerThread; ++r) {
-    hid[r] = S.hash_ids[tid + r * kFinishThreads];
-    hpk[r] = S.hash_counts[tid + r * kFinishThreads];
-  }
+    for (int r = 0; r < kEval; ++r) {
+      const bool mine = r < kOwn && ofirst[r];
+      hid[r] = mine ? (uint32_t)oid[r] : 0xFFFFFFFFu;
+      hpk[r] = mine ? S.hash_counts[oslot[r]] : 0u;
+      raw[r] = mine ? oraw[r] : 0.0f;
+      mw[r] = mine ? omw[r] : 0u;
+    }
+  } else {
 #pragma unroll
-  for (int r = 0; r < kSlotsPerThread; ++r) {
-    const bool used = hid[r] != 0xFFFFFFFFu;
-    raw[r] = used ? load_logit(a, row, hid[r]) : 0.0f;
-    mw[r] = used && constrained ? a.mask_table[(int64_t)slot * a.mask_words + (hid[r] >> 5)] : 0u;
+    for (int r = 0; r < kEval; ++r) {
+      hid[r] = r < kSlotsPerThread ? S.hash_ids[tid + r * kFinishThreads] : 0xFFFFFFFFu;
+      hpk[r] = r < kSlotsPerThread ? S.hash_counts[tid + r * kFinishThreads] : 0u;
+    }
+#pragma unroll
+    for (int r = 0; r < kEval; ++r) {
+      const bool used = hid[r] != 0xFFFFFFFFu;
+      raw[r] = used ? load_logit(a, row, hid[r]) : 0.0f;
+      mw[r] = used && constrained ? a.mask_table[(int64_t)slot * a.mask_words + (hid[r] >> 5)] : 0u;
+    }
   }
   // list entries of the first kFinishThreads / kSubThreads sub-lists (every
   // sub-list up to 32 chunks, V <= 262144); wider rows loop below
@@ -643,7 +714,7 @@ __global__ __launch_bounds__(kFinishThreads) void finish_kernel(SampleArgs a) {
     uint64_t my_max = 0;
     bool my_legal = false, my_nonfinite = false;
 #pragma unroll
-    for (int r = 0; r < kSlotsPerThread; ++r) {
+    for (int r = 0; r < kEval; ++r) {
       const uint32_t id = hid[r];
       const bool used = id != 0xFFFFFFFFu;
       const uint64_t m = __ballot(used);
@@ -691,6 +762,8 @@ __global__ __launch_bounds__(kFinishThreads) void finish_kernel(SampleArgs a) {
 
   // the complete region: listed entries with key >= thr, appended with one
   // LDS atomic per wave
+  const uint32_t sel_lo = thr > kKeyNegInf ? thr : kKeyNegInf + 1u;
+  const uint32_t sel_hi = S.max_key > sel_lo ? S.max_key : sel_lo;
   auto append = [&](const uint64_t (&v)[kSubPerThread], int cnt) {
     uint64_t e[kSubPerThread];
     uint32_t keep = 0;
@@ -879,8 +952,7 @@ __global__ __launch_bounds__(kFinishThreads) void finish_kernel(SampleArgs a) {
   const int n_top_all = n_ns < kTopR ? n_ns : kTopR;
   if (n_sp_in <= 2 * kTopR - n_top_all) {
     uint64_t* tmp = (uint64_t*)S.cand_p;  // kWaves * 64 entries of merge scratch
-    const uint32_t lo = thr > kKeyNegInf ? thr : kKeyNegInf + 1u;
-    if (!top_select(S.sorted, n_ns, lo, S.max_key > lo ? S.max_key : lo, S.hist, S.sel, tmp, S.top)) {
+    if (!top_select(S.sorted, n_ns, sel_lo, sel_hi, S.hist, S.sel, tmp, S.top, false)) {
       if (n_ns <= kWaves * 64) top_r<1>(S.sorted, n_ns, tmp, S.top);
       else if (n_ns <= kWaves * 128) top_r<2>(S.sorted, n_ns, tmp, S.top);
       else top_r<4>(S.sorted, n_ns, tmp, S.top);
