@@ -26,6 +26,7 @@ struct gs_context {
   int64_t exact_cap = 0;
   int64_t exact_slot_bytes = 0;
   int32_t exact_slots = 0;
+  int32_t cu_count = 0;  // compute units of the device (the scan's work split)
   // constraint tables
   int64_t* d_vocab_offsets = nullptr;
   uint8_t* d_vocab_bytes = nullptr;
@@ -182,6 +183,9 @@ int gs_create(int device, int32_t vocab_size, int32_t max_rows, gs_context** out
     return status;
   };
   if (hipSetDevice(device) != hipSuccess) return cleanup(GS_ERR_HIP, "hipSetDevice");
+  if (hipDeviceGetAttribute(&ctx->cu_count, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess ||
+      ctx->cu_count <= 0)
+    return cleanup(GS_ERR_HIP, "device attributes");
   if (hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking) != hipSuccess) return cleanup(GS_ERR_HIP, "stream");
   const size_t stats_bytes = (size_t)max_rows * ctx->n_chunks * sizeof(ChunkStat);
   const size_t list_bytes = (size_t)max_rows * ctx->n_chunks * kGatherCap * sizeof(uint64_t);
@@ -296,6 +300,7 @@ int gs_sample(gs_context* ctx, const gs_batch* b, void* stream) {
   a.exact_scratch = ctx->d_exact;
   a.exact_slot_bytes = ctx->exact_slot_bytes;
   a.exact_capacity = ctx->exact_cap;
+  a.cu_count = ctx->cu_count;
   // the exact-path queue is reset by the chunk scan's first workgroup: no
   // memset node, so the call stays capturable and one launch cheaper
   const int32_t slot = timing_slot(ctx);
@@ -527,6 +532,38 @@ int gs_token_log_prob_host(gs_context* ctx, const float* logits, int32_t rows, c
   (void)hipStreamSynchronize(ctx->stream);
   free_dev(d_logits);
   return st;
+}
+
+int gs_check_exp2(gs_context* ctx, float lo, float hi, double* max_rel_err, float* worst_y) {
+  if (!ctx || !max_rel_err || !worst_y || !(lo <= hi)) return fail(ctx, GS_ERR_INVALID_ARGUMENT, "bad arguments");
+  GS_HIP(ctx, hipSetDevice(ctx->device));
+  unsigned long long* d = nullptr;
+  GS_HIP(ctx, hipMalloc(&d, sizeof(unsigned long long)));
+  // every binary32 in [lo, hi]: the negative part by bit patterns from -0
+  // up to lo's, the non-negative part from +0 up to hi's
+  const uint32_t blo = __builtin_bit_cast(uint32_t, lo), bhi = __builtin_bit_cast(uint32_t, hi);
+  int st = GS_OK;
+  if (hipMemsetAsync(d, 0, sizeof(unsigned long long), ctx->stream) != hipSuccess) st = fail(ctx, GS_ERR_HIP, "memset failed");
+  if (st == GS_OK && lo < 0) {
+    const uint32_t neg_hi = hi < 0 ? bhi : 0x80000000u;  // the negative value nearest zero
+    launch_exp2_check(neg_hi, blo - neg_hi + 1, d, ctx->stream);
+  }
+  if (st == GS_OK && hi >= 0) {
+    const uint32_t pos_lo = lo >= 0 ? blo : 0u;
+    launch_exp2_check(pos_lo, bhi - pos_lo + 1, d, ctx->stream);
+  }
+  unsigned long long h = 0;
+  if (st == GS_OK && (hipGetLastError() != hipSuccess ||
+                      hipMemcpyAsync(&h, d, sizeof(h), hipMemcpyDeviceToHost, ctx->stream) != hipSuccess ||
+                      hipStreamSynchronize(ctx->stream) != hipSuccess)) {
+    st = fail(ctx, GS_ERR_HIP, "exp2 check kernel failed");
+  }
+  (void)hipStreamSynchronize(ctx->stream);
+  free_dev(d);
+  if (st != GS_OK) return st;
+  *max_rel_err = (double)__builtin_bit_cast(float, (uint32_t)(h >> 32));
+  *worst_y = __builtin_bit_cast(float, (uint32_t)h);
+  return GS_OK;
 }
 
 int gs_set_vocab(gs_context* ctx, const int64_t* offsets, const uint8_t* bytes, int64_t n_bytes) {

@@ -18,14 +18,18 @@
 //   4. when the filters reach past the top 64 (top-p or min-p cuts deep in
 //      the list), sorts the whole region and repeats step 3 block-wide.
 // The normaliser is summed in a different order from the reference's
-// sequential loop, so every comparison that decides the outcome is checked
-// against a margin that bounds the difference; rows that fail a margin, need
+// sequential loop, from the scan's binary32 terms, so every comparison that
+// decides the outcome is checked against a margin that bounds the
+// difference. A top-p cut within the scan normaliser's bound (3.9e-7
+// relative) is settled again after the row's normaliser is recomputed in
+// binary64 (4.2e-10 per term); rows that still fail a margin, need
 // candidates outside the complete region, or hold non-finite logits are
 // queued for the exact kernel, which replays the reference step by step.
 //
-// Global loads are issued in two rounds (row inputs, then the list entries
+// Global loads are issued in two batches (row inputs, then the list entries
 // and special logits that LDS data locates), so the row's latency is a few
 // memory round trips plus the rank work.
+#include "gs_exp2.h"
 #include "gs_internal.h"
 
 namespace gs {
@@ -380,7 +384,7 @@ struct Shared {
   uint32_t hash_counts[kHashSize];    // specials (keys in hash_ids, ids in hash_counts)
   uint64_t sp_key[kSpecialCap];       // specials: f64 key of their value
   uint32_t sp_id[kSpecialCap];
-  double cand_p[kFinishCap];          // merged candidates: probability (sort scratch before)
+  double cand_p[kFinishCap];          // merged candidates: e^(value - M) (sort scratch before)
   uint32_t cand_id[kFinishCap];
   double c_sum[kFinishMaxChunks];     // chunk statistics
   uint32_t c_max[kFinishMaxChunks];
@@ -391,6 +395,7 @@ struct Shared {
   double wsum[kWaves];
   double wtmp[kWaves];
   double total;
+  double total_sp;                    // the specials' part of total
   uint64_t sp_max;
   uint32_t flags;
   uint32_t max_key;
@@ -425,19 +430,23 @@ __device__ void write_result(const SampleArgs& a, int64_t row, int32_t token, ui
 __device__ __forceinline__ double nonspecial_value(uint64_t e, double T) { return (double)key_f32(entry_key(e)) / T; }
 
 // The filters and the draw over the first n_avail (<= 128) candidates, whose
-// probabilities p[] and ids ids[] sit in LDS in list order, evaluated by the
-// calling wave alone. Returns 0 when the row is settled (result written or
-// queued for the exact path), 1 when the cut lies past the candidates and the
-// caller must widen them. `complete`: the candidates are the row's whole list.
-__device__ int filters_and_draw_wave(const SampleArgs& a, int64_t row, const gs_row_config& cfg, const double* p,
-                                     const uint32_t* ids, int n_avail, bool complete, double margin) {
+// exponentials e[] (probability = e / total, sampling.ts:39,42) and ids ids[]
+// sit in LDS in list order, evaluated by the calling wave alone. Returns 0
+// when the row is settled (result written or queued for the exact path), 1
+// when the cut lies past the candidates and the caller must widen them, 2
+// when the top-p cut lies within `margin` of topP and `refinable` is set: the
+// caller recomputes the normaliser and calls again with the tighter margin.
+// `complete`: the candidates are the row's whole list.
+__device__ int filters_and_draw_wave(const SampleArgs& a, int64_t row, const gs_row_config& cfg, const double* e,
+                                     double total, const uint32_t* ids, int n_avail, bool complete, double margin,
+                                     bool refinable) {
   const int lane = threadIdx.x & 63;
   constexpr int kPerLane = 2;  // list index lane*2 + q
   double pl[kPerLane];
 #pragma unroll
   for (int q = 0; q < kPerLane; ++q) {
     const int i = lane * kPerLane + q;
-    pl[q] = i < n_avail ? p[i] : 0.0;
+    pl[q] = i < n_avail ? e[i] / total : 0.0;
   }
   int n = n_avail;
   bool n_complete = complete;
@@ -510,7 +519,12 @@ __device__ int filters_and_draw_wave(const SampleArgs& a, int64_t row, const gs_
       const int o = __shfl_xor(cut, m, 64);
       cut = o < cut ? o : cut;
     }
-    if (__ballot(near)) exact_why |= 4u;
+    if (__ballot(near)) {
+      // only the normaliser's own error can have put the cut there: settle it
+      // with the recomputed normaliser unless another check already failed
+      if (refinable && !exact_why) return 2;
+      exact_why |= 4u;
+    }
     if (cut == 0x7FFFFFFF) {
       if (!n_complete) return 1;
       cut = n - 1;
@@ -553,10 +567,45 @@ __device__ int filters_and_draw_wave(const SampleArgs& a, int64_t row, const gs_
     if (exact_why || pick == 0x7FFFFFFF) {
       enqueue_exact(a, row, exact_why ? GS_FLAG_NEAR_TIE : 0u);
     } else {
-      write_result(a, row, (int32_t)ids[pick], tie, p[pick]);
+      write_result(a, row, (int32_t)ids[pick], tie, e[pick] / total);
     }
   }
   return 0;
+}
+
+// The normaliser's non-special part from scratch in binary64
+// (sampling.ts:36-41): the sum over the row's allowed logits l (mask bit set,
+// or every id of an unconstrained row) of e^(l/T - M) by the table
+// exponential (4.2e-10 relative per term), minus the same terms of the
+// allowed special ids, which the normaliser counts with their penalised
+// values instead. Identical terms cancel exactly, so the difference keeps the
+// sum's accuracy while the specials hold at most half of it; otherwise, or
+// when a sum overflows, it returns -1. The whole block calls it.
+__device__ double recompute_nonspecial_sum(const SampleArgs& a, int64_t row, const gs_row_config& cfg,
+                                           bool constrained, double M, int n_sp, const uint32_t* sp_id,
+                                           double* s_w) {
+  const int tid = threadIdx.x;
+  const double T = cfg.temperature;
+  const uint32_t* mrow = constrained ? a.mask_table + (int64_t)cfg.mask_slot * a.mask_words : nullptr;
+  auto term = [&](float l) -> double {
+    if (cfg.softcap > 0) l = gsm::softcap_f32(l, cfg.softcap);
+    const double y = ((double)l / T - M) * GS_256_LOG2E;
+    return y > kSkipY ? exp2_256(y, c_exp2_256) : 0.0;
+  };
+  double all = 0.0, sp = 0.0;
+  for (int64_t i = tid; i < a.vocab; i += kFinishThreads) {
+    if (mrow && !((mrow[i >> 5] >> (i & 31)) & 1u)) continue;
+    all += term(load_logit(a, row, i));
+  }
+  for (int i = tid; i < n_sp; i += kFinishThreads) {
+    const uint32_t id = sp_id[i];
+    if (mrow && !((mrow[id >> 5] >> (id & 31)) & 1u)) continue;
+    sp += term(load_logit(a, row, id));
+  }
+  double t_all, t_sp;
+  block_scan_f64(all, s_w, &t_all);
+  block_scan_f64(sp, s_w, &t_sp);
+  return (t_all < __builtin_inf() && t_sp <= 0.5 * t_all) ? t_all - t_sp : -1.0;
 }
 
 __global__ __launch_bounds__(kFinishThreads) void finish_kernel(SampleArgs a) {
@@ -574,7 +623,7 @@ __global__ __launch_bounds__(kFinishThreads) void finish_kernel(SampleArgs a) {
   const bool constrained = slot >= 0 && slot < a.mask_slots;
   const double T = cfg.temperature;
 
-  // ---- round 1 of global loads: chunk statistics, window and forced ids
+  // ---- first batch of global loads: chunk statistics, window and forced ids
   const ChunkStat* st = a.stats + row * a.n_chunks;
   ChunkStat cs{};
   if (tid < a.n_chunks) cs = st[tid];
@@ -614,16 +663,30 @@ __global__ __launch_bounds__(kFinishThreads) void finish_kernel(SampleArgs a) {
 
   // ---- 1. statistics into LDS, distinct special ids into the hash
   if (tid < a.n_chunks) {
-    S.c_sum[tid] = cs.sum;
-    S.c_max[tid] = cs.max_key;
+    // the chunk's maximum and its sum, from its waves' (each rescaled from its
+    // wave maximum to the chunk's by the bit-exact exp)
+    uint32_t cmax = 0, cflags = 0;
+    for (int w = 0; w < kScanWaves; ++w) {
+      cmax = cs.wmax[w] > cmax ? cs.wmax[w] : cmax;
+      cflags |= cs.wflags[w];
+    }
+    double csum = 0.0;
+    if (!greedy && cmax > kKeyNegInf) {
+      for (int w = 0; w < kScanWaves; ++w) {
+        if (cs.wsum[w] > 0.0 && cs.wmax[w] > kKeyNegInf)
+          csum += cs.wsum[w] * gsm::js_exp(((double)key_f32(cs.wmax[w]) - (double)key_f32(cmax)) / T);
+      }
+    }
+    S.c_sum[tid] = csum;
+    S.c_max[tid] = cmax;
     uint32_t overflow = 0;
     for (int w = 0; w < kScanWaves; ++w) {
       const uint32_t n = cs.n_sub[w];  // above kSubCap: the sub-list overflowed
       overflow |= n > (uint32_t)kSubCap;
       S.c_nsub[tid * kScanWaves + w] = n > (uint32_t)kSubCap ? (uint32_t)kSubCap : n;
     }
-    atomicOr(&S.flags, cs.flags | (overflow ? kChunkOverflow : 0u));
-    atomicMax(&S.max_key, cs.max_key);
+    atomicOr(&S.flags, cflags | (overflow ? kChunkOverflow : 0u));
+    atomicMax(&S.max_key, cmax);
     if (cs.truncated) { atomicMax(&S.thr_max, cs.threshold); atomicOr(&S.any_truncated, 1u); }
   }
   // the owned specials' logits and mask words start loading now, so they
@@ -665,7 +728,7 @@ __global__ __launch_bounds__(kFinishThreads) void finish_kernel(SampleArgs a) {
     return;
   }
 
-  // ---- round 2 of global loads: the specials' logits and mask words and
+  // ---- second batch of global loads: the specials' logits and mask words and
   // every list entry, all in flight together
   const uint32_t thr = S.thr_max;  // 0 when no chunk was truncated: every finite logit is listed
   const uint64_t* lists = a.lists + row * a.n_chunks * kGatherCap;
@@ -892,26 +955,30 @@ __global__ __launch_bounds__(kFinishThreads) void finish_kernel(SampleArgs a) {
     if (tid == 0) enqueue_exact(a, row, 0u);
     return;
   }
-  // Margin for the comparisons that depend on the normaliser (the top-p cut).
-  // This total and the reference's differ by: the scan's exponential (4.2e-10
-  // relative per term), summation order (under V 2^-53 < 3e-11), the
-  // reference's rounding of l/T and of l/T - M in every term (2^-52 (2|M| + 60)
-  // for the terms that matter) and the scan's rounding of its exponent
-  // argument (2^-53 |M|, for the threads whose terms matter).
-  const double margin = kNormaliserRel + 0x1p-52 * (3.0 * (M < 0 ? -M : M) + 60.0);
+  // Margins for the comparisons that depend on the normaliser (the top-p
+  // cut). This total and the reference's differ by the scan's normaliser
+  // error (kScanSumRel; kNormaliserRel once recomputed in binary64),
+  // summation order (under V 2^-53 < 3e-11) and the reference's rounding of
+  // l/T and of l/T - M in every term (2^-52 (2|M| + 60) for the terms that
+  // matter) and of the rescale arguments (2^-53 |M|).
+  const double ref_round = 0x1p-52 * (3.0 * (M < 0 ? -M : M) + 60.0);
+  const double margin_fine = kNormaliserRel + ref_round;
+  double margin = kScanSumRel + ref_round;
+  bool refined = false;
 
   // ---- normaliser: chunk partial sums rescaled to M, plus every special
   {
-    double part = 0.0;
+    double part = 0.0, spart = 0.0;
     for (int c = tid; c < a.n_chunks; c += kFinishThreads) {
       const double csum = S.c_sum[c];
       const uint32_t cmax = S.c_max[c];
       if (cmax > kKeyNegInf && csum > 0) part += csum * gsm::js_exp((double)key_f32(cmax) / T - M);
     }
-    for (int i = tid; i < n_sp; i += kFinishThreads) part += gsm::js_exp(key_f64(S.sp_key[i]) - M);
-    double total;
-    block_scan_f64(part, S.wsum, &total);
-    if (tid == 0) S.total = total;
+    for (int i = tid; i < n_sp; i += kFinishThreads) spart += gsm::js_exp(key_f64(S.sp_key[i]) - M);
+    double t_chunks, t_sp;
+    block_scan_f64(part, S.wsum, &t_chunks);
+    block_scan_f64(spart, S.wsum, &t_sp);
+    if (tid == 0) { S.total = t_chunks + t_sp; S.total_sp = t_sp; }
   }
   if (!(S.total < __builtin_inf())) {
     // an exponent argument beyond the double range (|l/T| near 1e18 or more)
@@ -943,8 +1010,18 @@ __global__ __launch_bounds__(kFinishThreads) void finish_kernel(SampleArgs a) {
     if (tid == 0) enqueue_exact(a, row, 0u);
     return;
   }
-  const double total = S.total;
+  double total = S.total;
   const bool region_complete = !S.any_truncated;
+  // after a recomputed normaliser: the new total and the tight margin (the
+  // whole block calls it; false when the row must take the exact path)
+  auto refine = [&]() -> bool {
+    const double part = recompute_nonspecial_sum(a, row, cfg, constrained, M, n_sp, S.sp_id, S.wsum);
+    if (!(part >= 0)) return false;
+    total = part + S.total_sp;
+    margin = margin_fine;
+    refined = true;
+    return true;
+  };
 
   // ---- fast path: the top kTopR non-specials, merged with the region's
   // specials, settle every cut the filters make within them (when the
@@ -957,10 +1034,12 @@ __global__ __launch_bounds__(kFinishThreads) void finish_kernel(SampleArgs a) {
       else if (n_ns <= kWaves * 128) top_r<2>(S.sorted, n_ns, tmp, S.top);
       else top_r<4>(S.sorted, n_ns, tmp, S.top);
     }
+    double* fp = S.cand_p + kWaves * 64;  // past the merge scratch
+    uint32_t* fid = S.cand_id;
+    int n_valid = 0;
+    bool complete = false;
     if (wave == 0) {
       const int n_top = n_ns < kTopR ? n_ns : kTopR;
-      double* fp = S.cand_p + kWaves * 64;  // past the merge scratch
-      uint32_t* fid = S.cand_id;
       const int n_sp_use = n_sp_in;
       for (int i = lane; i < n_top; i += 64) {
         const uint64_t e = S.top[i];
@@ -988,8 +1067,8 @@ __global__ __launch_bounds__(kFinishThreads) void finish_kernel(SampleArgs a) {
       }
       // the merged list equals the row's list up to the last ranked
       // non-special; specials below it may sit under unranked non-specials
-      int n_valid = n_top + n_sp_use;
-      const bool complete = region_complete && n_ns <= kTopR;
+      n_valid = n_top + n_sp_use;
+      complete = region_complete && n_ns <= kTopR;
       if (n_ns > kTopR) {
         const uint64_t e = S.top[kTopR - 1];
         const uint64_t lk = f64_key(nonspecial_value(e, T));
@@ -1001,12 +1080,23 @@ __global__ __launch_bounds__(kFinishThreads) void finish_kernel(SampleArgs a) {
         n_valid -= after;
       }
       __builtin_amdgcn_wave_barrier();
-      for (int i = lane; i < n_valid; i += 64) fp[i] = gsm::js_exp(fp[i] - M) / total;
+      for (int i = lane; i < n_valid; i += 64) fp[i] = gsm::js_exp(fp[i] - M);
       __builtin_amdgcn_wave_barrier();
-      const int r = filters_and_draw_wave(a, row, cfg, fp, fid, n_valid, complete, margin);
-      if (lane == 0) S.fast_done = r == 0 ? 1u : 0u;
+      const int r = filters_and_draw_wave(a, row, cfg, fp, total, fid, n_valid, complete, margin, true);
+      if (lane == 0) S.fast_done = r == 0 ? 1u : (r == 2 ? 2u : 0u);
     }
     __syncthreads();
+    if (S.fast_done == 2) {
+      if (!refine()) {
+        if (tid == 0) enqueue_exact(a, row, GS_FLAG_NEAR_TIE);
+        return;
+      }
+      if (wave == 0) {
+        const int r = filters_and_draw_wave(a, row, cfg, fp, total, fid, n_valid, complete, margin, false);
+        if (lane == 0) S.fast_done = r == 0 ? 1u : 0u;
+      }
+      __syncthreads();
+    }
     if (S.fast_done) return;
   }
 
@@ -1048,7 +1138,8 @@ __global__ __launch_bounds__(kFinishThreads) void finish_kernel(SampleArgs a) {
     S.cand_id[j + lo] = id;
   }
   __syncthreads();
-  for (int i = tid; i < n_cand; i += kFinishThreads) S.cand_p[i] = gsm::js_exp(S.cand_p[i] - M) / total;
+  // exponentials; probability = e / total where the filters read them
+  for (int i = tid; i < n_cand; i += kFinishThreads) S.cand_p[i] = gsm::js_exp(S.cand_p[i] - M);
   __syncthreads();
 
   // ---- top-k (sampling.ts:44)
@@ -1060,10 +1151,10 @@ __global__ __launch_bounds__(kFinishThreads) void finish_kernel(SampleArgs a) {
   }
   // ---- min-p (sampling.ts:45-48): p is non-increasing along the list
   if (cfg.min_p > 0) {
-    const double floor_p = S.cand_p[0] * cfg.min_p;
+    const double floor_p = S.cand_p[0] / total * cfg.min_p;
     for (int i = tid; i < n; i += kFinishThreads) {
-      const double p = S.cand_p[i];
-      if (i + 1 < n && S.cand_p[i + 1] > p) atomicOr(&S.route_exact, 1u);  // not monotone: replay
+      const double p = S.cand_p[i] / total;
+      if (i + 1 < n && S.cand_p[i + 1] / total > p) atomicOr(&S.route_exact, 1u);  // not monotone: replay
       if (!(p >= floor_p)) atomicMin(&S.first_idx, (uint32_t)i);
       const double d = p >= floor_p ? p - floor_p : floor_p - p;
       if (d < kNearTie * floor_p) atomicOr(&S.route_exact, 2u);
@@ -1086,23 +1177,35 @@ __global__ __launch_bounds__(kFinishThreads) void finish_kernel(SampleArgs a) {
   uint32_t tie_report = 0;
   if (cfg.top_p < 1) {
     double local[kPer];
-    double s = 0.0;
-    for (int q = 0; q < kPer; ++q) {
-      const int i = tid * kPer + q;
-      s += i < n ? S.cand_p[i] : 0.0;
-      local[q] = s;
+    double base;
+    for (;;) {
+      double s = 0.0;
+      for (int q = 0; q < kPer; ++q) {
+        const int i = tid * kPer + q;
+        s += i < n ? S.cand_p[i] / total : 0.0;
+        local[q] = s;
+      }
+      double tot;
+      base = block_scan_f64(s, S.wtmp, &tot) - s;
+      for (int q = 0; q < kPer; ++q) {
+        const int i = tid * kPer + q;
+        if (i >= n) break;
+        const double cum = base + local[q];
+        if (cum >= cfg.top_p) atomicMin(&S.first_idx, (uint32_t)i);
+        const double d = cum >= cfg.top_p ? cum - cfg.top_p : cfg.top_p - cum;
+        if (d < margin) atomicOr(&S.route_exact, 4u);
+      }
+      __syncthreads();
+      // a cut within the scan normaliser's margin alone: recompute it, redo
+      if (refined || S.route_exact != 4u) break;
+      __syncthreads();
+      if (tid == 0) { S.route_exact = 0; S.first_idx = 0xFFFFFFFFu; }
+      if (!refine()) {
+        if (tid == 0) enqueue_exact(a, row, GS_FLAG_NEAR_TIE);
+        return;
+      }
+      __syncthreads();
     }
-    double tot;
-    const double base = block_scan_f64(s, S.wtmp, &tot) - s;
-    for (int q = 0; q < kPer; ++q) {
-      const int i = tid * kPer + q;
-      if (i >= n) break;
-      const double cum = base + local[q];
-      if (cum >= cfg.top_p) atomicMin(&S.first_idx, (uint32_t)i);
-      const double d = cum >= cfg.top_p ? cum - cfg.top_p : cfg.top_p - cum;
-      if (d < margin) atomicOr(&S.route_exact, 4u);
-    }
-    __syncthreads();
     int cut = (int)S.first_idx;  // index of the item that reached topP
     if (S.first_idx == 0xFFFFFFFFu) {
       if (!n_complete) {
@@ -1113,7 +1216,7 @@ __global__ __launch_bounds__(kFinishThreads) void finish_kernel(SampleArgs a) {
     } else if (tid == cut / kPer) {
       // 1e-6 boundary ties, as the reference comparison plan reports them
       const double cum = base + local[cut % kPer];
-      const double prev = cum - S.cand_p[cut];
+      const double prev = cum - S.cand_p[cut] / total;
       if (cum - cfg.top_p <= kTieReport * cfg.top_p || (cut > 0 && cfg.top_p - prev <= kTieReport * cfg.top_p)) {
         atomicOr(&S.status_flags, GS_FLAG_TOPP_TIE);
       }
@@ -1134,7 +1237,7 @@ __global__ __launch_bounds__(kFinishThreads) void finish_kernel(SampleArgs a) {
     double s = 0.0;
     for (int q = 0; q < kPer; ++q) {
       const int i = tid * kPer + q;
-      s += i < n ? S.cand_p[i] : 0.0;
+      s += i < n ? S.cand_p[i] / total : 0.0;
       local[q] = s;
     }
     double ctotal;
@@ -1155,7 +1258,7 @@ __global__ __launch_bounds__(kFinishThreads) void finish_kernel(SampleArgs a) {
         enqueue_exact(a, row, S.route_exact ? GS_FLAG_NEAR_TIE : 0u);
       } else {
         const int i = (int)S.first_idx;
-        write_result(a, row, (int32_t)S.cand_id[i], tie_report, S.cand_p[i]);
+        write_result(a, row, (int32_t)S.cand_id[i], tie_report, S.cand_p[i] / total);
       }
     }
   }

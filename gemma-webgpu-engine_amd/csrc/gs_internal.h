@@ -30,11 +30,14 @@ constexpr int kExactTile = 4096;                  // LDS tile of the exact path'
 // relative margin under which a fast-path decision is re-resolved exactly;
 // it bounds the reference's own sequential-sum error (V * 2^-53 ~ 3e-11)
 constexpr double kNearTie = 1.0e-10;
-// relative margin of decisions that depend on the softmax normaliser: the
-// scan's exponentials (each term, then the lane and wave rescales, 4.2e-10
-// each, at most 1.3e-9 together) and summation order, with room
+// relative bound on the chunk scan's normaliser: binary32 terms from the
+// hardware exp2, summed per thread (the derivation is in gs_scan.hip); the
+// finish kernel decides normaliser-dependent cuts with this margin first
+constexpr double kScanSumRel = 3.9e-7;
+// relative margin of those decisions once the finish kernel has recomputed
+// the normaliser in binary64 (4.2e-10 per term, summation order), with room
 constexpr double kNormaliserRel = 4.0e-9;
-// the north star's reporting tolerance for top-p boundary ties
+// reporting tolerance for top-p boundary ties (1e-6 relative)
 constexpr double kTieReport = 1.0e-6;
 
 // ------------------------------------------------------- orderable keys
@@ -97,13 +100,14 @@ __host__ __device__ __forceinline__ Plan plan_row(const gs_row_config& c) {
 
 // ------------------------------------------------------- per-chunk state
 struct ChunkStat {
-  double sum;          // sum of e^((l - lmax)/T) over finite non-special logits of the chunk
-  uint32_t max_key;    // key of lmax (kKeyNegInf or below: no finite non-special logit)
-  uint32_t n_list;     // unused (0)
-  uint32_t n_finite;   // finite non-special logits
+  // wave w of the chunk's workgroup: sum of e^((l - wave max)/T) over its
+  // finite non-special logits, the wave maximum's key (kKeyNegInf or below:
+  // none) and kChunkNonFinite when NaN or +inf was among its live logits
+  double wsum[kScanWaves];
+  uint32_t wmax[kScanWaves];
+  uint32_t wflags[kScanWaves];
   uint32_t threshold;  // the list holds every finite non-special logit with key >= threshold
   uint32_t truncated;  // some finite logit lies below the threshold
-  uint32_t flags;      // kChunkNonFinite
   // entries of wave w's sub-list, which starts at slot w * kSubCap; a count
   // above kSubCap means the wave had more and the sub-list is incomplete
   uint16_t n_sub[kScanWaves];
@@ -152,6 +156,7 @@ struct SampleArgs {
   uint8_t* exact_scratch;
   int64_t exact_slot_bytes;
   int64_t exact_capacity;  // entries per slot (power of two >= vocab)
+  int32_t cu_count;        // compute units of the device
 };
 
 // --------------------------------------------------------- wave helpers
@@ -254,6 +259,7 @@ __device__ __forceinline__ void special_insert(SpecialTable t, uint32_t id, uint
 
 // ---------------------------------------------------- kernel launchers
 void launch_scan(const SampleArgs& a, hipStream_t s);
+void launch_exp2_check(uint32_t first, uint32_t count, unsigned long long* worst, hipStream_t s);
 void launch_finish(const SampleArgs& a, hipStream_t s);
 void launch_exact(const SampleArgs& a, hipStream_t s);
 void launch_logprob(const void* logits, int32_t dtype, int32_t rows, int64_t stride, int32_t vocab,

@@ -1,59 +1,66 @@
 // One-pass chunk scan: the streaming half of the batched sampler.
 //
-// Grid (n_chunks, rows); one 256-thread workgroup reads one 8192-logit chunk
-// of one row exactly once from HBM. Every 16-byte load of a thread is issued
-// before any of them is used, so the whole chunk is in flight at once, and
-// the history-window ids the chunk needs are read while it lands. Per chunk
-// the workgroup emits:
-//   * the chunk maximum and sum_i e^((l_i - lmax)/T) in binary64, the pieces
-//     of the reference's softmax normaliser (src/runtime/sampling.ts:36-41).
-//     Each thread sums against its own maximum, so no barrier precedes the
-//     sum, and the 256 partial sums are rescaled to the chunk maximum after;
-//   * a candidate list: every finite logit >= tau, where tau is the smallest
-//     of the four waves' d-th largest per-thread maxima (d = ceil(depth/4) + 2,
-//     found with ballots inside each wave), so at least `depth` per-thread
-//     maxima are >= tau. The list therefore holds the chunk's top-`depth` in
-//     the reference's (value desc, id asc) order (sampling.ts:33-35) and every
-//     finite logit of the chunk >= tau. Each wave appends to a sub-list of
-//     its own at positions taken from ballots, so no atomics are involved.
-// The chunk's loads are issued first, from kernel arguments alone; the row's
-// options, window ids and mask words follow while they are in flight. After
-// the special-id bitmap the workgroup meets at one barrier (chunk maximum,
-// sums and tau); the statistics are written by thread 0 and each wave's
-// lane 0 (its sub-list length), so no barrier follows the gather.
+// A chunk is 8192 consecutive logits of one row, read exactly once from HBM
+// by one 256-thread workgroup (32 logits per thread, as 16-byte loads). Per
+// chunk the workgroup emits:
+//   * for each of its four waves, the wave maximum and sum_i e^((l_i -
+//     wave max)/T) in binary64, the pieces of the reference's softmax
+//     normaliser (src/runtime/sampling.ts:36-41); each thread sums against
+//     its own maximum and the 64 partial sums are rescaled to the wave's;
+//   * a candidate list: every finite logit >= tau, where tau is a threshold
+//     with at least `depth` logits of the chunk at or above it. The list thus
+//     holds the chunk's top-`depth` in the reference's (value desc, id asc)
+//     order (sampling.ts:33-35) and every finite logit of the chunk >= tau.
+//     Each wave appends to a sub-list of its own at positions taken from
+//     ballots, staged in LDS and written out with one coalesced store.
 // Logits of "special" ids (the row's penalty window and forced ids) are left
 // out here; the finish kernel evaluates them exactly. Masked ids (constraint
 // bitmask) are -inf, as maskConstraintLogits makes them
 // (src/runtime/constraints.ts:159-173).
 //
-// The normaliser's exponential is 2^(y/256) = 2^(j/256) * 2^k * e^r with a
-// correctly rounded 256-entry table and a quadratic in r, |r| <= ln2/512:
-// relative error below 4.2e-10 per evaluation; a term, its lane's rescale to
-// the wave maximum and the wave's rescale to the chunk maximum make at most
-// 1.3e-9. Only the normaliser sees it, and only
-// the top-p cut depends on the normaliser (its margin in the finish kernel
-// covers this); every ordering and every probability the filters compare is
-// recomputed exactly later.
-#include "gs_exp2_table.h"
+// Streaming. A group workgroup scans up to kMaxGroupChunks consecutive full
+// chunks of one row as a two-stage software pipeline: the loads of chunk i+1
+// are in flight while chunk i is reduced. Group loads are raw buffer loads
+// whose extent is one chunk, so the prefetch past the group's last chunk
+// returns zeros without a memory access and no load sits under a branch.
+// The group's first chunk takes its tau from the lane maxima: the smallest of
+// the four waves' d-th largest lane maxima (d = ceil(depth/4) + 2, found with
+// ballots), exchanged at one LDS-only barrier. That tau serves every later
+// chunk of the group as well -- the first chunk alone holds `depth` logits
+// at or above it, so the group's top-`depth` are all >= it -- and the later
+// chunks need no barrier and no exchange at all: each wave reduces, gathers
+// and writes its own statistics. The launch is one generation of workgroups,
+// each row's full chunks split evenly over its groups. The special ids of the
+// group's whole extent are marked once, in an LDS bitmap, before the first
+// chunk. A row's last, partial chunk (vocab not a multiple of 8192) and rows
+// that are not 16-byte aligned are scanned one chunk per workgroup with
+// bounded element loads.
+//
+// Normaliser error. A thread's terms are binary32: 2^(x c - B) by one fma
+// and v_exp_f32 (relative error below 8.5e-8 over its whole binary32 domain
+// [-150, 0], checked exhaustively by a GPU test against 1e-7), whose exponent
+// carries the roundings of c and of the fma, 2u|y| for a term 2^y (u =
+// 2^-24); weighted by the terms, with the thread's maximum among them at
+// y = 0, these average at most 2.64 * 2u ln2 = 2.2e-7. The pair sums round
+// once more (u). A thread's sum is thus within 3.8e-7 relative of the exact
+// one; the lane rescale (2^(y/256) = 2^(j/256) * 2^k * e^r with a correctly
+// rounded 256-entry table and a quadratic in r, 4.2e-10), the finish
+// kernel's rescales (bit-exact exp) and binary64 sums add under 1e-9, so a
+// chunk's sum is within 3.9e-7 relative (kScanSumRel). Only the normaliser sees it, and only the top-p cut depends
+// on the normaliser: the finish kernel decides it with that margin and
+// recomputes the normaliser in binary64 for rows inside it. Every ordering
+// and every probability ratio the filters compare is recomputed exactly.
+#include "gs_exp2.h"
 #include "gs_internal.h"
 
 namespace gs {
 namespace {
 
-__constant__ double c_exp2_256[256] = {GS_EXP2_TABLE_256};
-
-// Terms with (l - lmax)/T < -60 are not summed: each is below e^-60 of the
-// maximum's term, so together they move the normaliser by less than
-// V * e^-60 < 3e-21 relative. In units of y = 256 log2(e) (l - lmax)/T:
-constexpr double kSkipY = -22160.0;
-
-__device__ __forceinline__ double exp2_256(double y, const double* tab) {
-  const double n = __builtin_rint(y);
-  const double s = y - n;  // |s| <= 1/2
-  const double p = __builtin_fma(s, __builtin_fma(s, GS_EXP2_256_C2, GS_EXP2_256_C1), 1.0);
-  const int ni = (int)n;
-  return __builtin_ldexp(tab[ni & 255] * p, ni >> 8);
-}
+constexpr int kChunkWords = kChunk / 32;  // special-bitmap words of one chunk
+constexpr int kMaxGroupChunks = 16;       // chunks one group workgroup streams
+constexpr int kScanWgPerCu = 4;           // resident scan workgroups per CU (launch bound)
+// word 3 of a raw buffer resource on gfx9-family parts (gfx950 included)
+constexpr int32_t kBufferWord3 = 0x00020000;
 
 template <typename In>
 struct VecTraits;
@@ -77,29 +84,99 @@ struct VecTraits<uint16_t> {
 
 __device__ __noinline__ float capped(float x, double cap) { return gsm::softcap_f32(x, cap); }
 
-// The d-th largest of the wave's lane keys (d >= 1): the largest t with at
-// least d keys >= t, found bit by bit from the top with ballots.
-__device__ __forceinline__ uint32_t wave_kth_key(uint32_t key, uint32_t d) {
-  uint32_t t = 0;
-  for (int b = 31; b >= 0; --b) {
+// A lower bound t of the d-th largest of the wave's lane keys (d >= 1), at
+// most 2^14 below it: the largest t whose low 14 bits are zero with at least
+// d keys >= t, found bit by bit with ballots. Bits above the first one where
+// the smallest and largest keys differ are common to every key and to the
+// answer, so the search starts below them. (For binary32 keys 2^14 units are
+// 2^-9 relative: a threshold that low admits a few more list entries.)
+__device__ __forceinline__ uint32_t wave_kth_key(uint32_t key, uint32_t d, uint32_t lo, uint32_t hi) {
+  constexpr int kFloorBit = 14;
+  const uint32_t diff = lo ^ hi;
+  if (diff >> kFloorBit == 0) return lo & ~((1u << kFloorBit) - 1u);
+  const int top = 31 - __builtin_clz(diff);
+  uint32_t t = lo & ~((2u << top) - 1u);  // the common prefix; every key is >= it
+  for (int b = top; b >= kFloorBit; --b) {
     const uint32_t c = t | (1u << b);
     if ((uint32_t)__popcll(__ballot(key >= c)) >= d) t = c;
   }
   return t;
 }
 
-struct ScanShared {
-  uint32_t special[kChunk / 32];
-  double tab[256];
-  double wsum[kScanWaves];     // wave sum of e^((l - wave max)/T)
-  uint32_t wmax[kScanWaves];   // wave maximum key
+// Workgroup barrier for LDS traffic only: LDS stores before it are visible to
+// every wave after it, and global loads in flight are not waited for.
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
+// Wave-wide reductions with DPP row operations (quad_perm, row_ror and the
+// gfx9 row_bcast15/31), which stay in the VALU
+// instead of going through the LDS crossbar: their latency is a few cycles
+// per step, where a cross-lane shuffle costs an LDS round trip.
+constexpr int kDppQuad1032 = 0xB1;  // quad_perm [1,0,3,2]
+constexpr int kDppQuad2301 = 0x4E;  // quad_perm [2,3,0,1]
+constexpr int kDppRowRor4 = 0x124;
+constexpr int kDppRowRor8 = 0x128;
+constexpr int kDppRowBcast15 = 0x142;  // lane 15 of a row to the next row (rows 1 and 3 written)
+constexpr int kDppRowBcast31 = 0x143;  // lane 31 to rows 2 and 3
+
+template <int kCtrl, int kRowMask>
+__device__ __forceinline__ uint32_t dpp_u32(uint32_t identity, uint32_t v) {
+  return (uint32_t)__builtin_amdgcn_update_dpp((int)identity, (int)v, kCtrl, kRowMask, 0xF, false);
+}
+// the maximum and minimum of the wave's values, in every lane
+__device__ __forceinline__ void wave_max_min_u32(uint32_t v, uint32_t* vmax, uint32_t* vmin) {
+  uint32_t a = v, b = v;
+#define GS_MM_STEP(C, M)                                \
+  { const uint32_t x = dpp_u32<C, M>(0u, a);            \
+    const uint32_t y = dpp_u32<C, M>(0xFFFFFFFFu, b);   \
+    a = x > a ? x : a; b = y < b ? y : b; }
+  GS_MM_STEP(kDppQuad1032, 0xF) GS_MM_STEP(kDppQuad2301, 0xF) GS_MM_STEP(kDppRowRor4, 0xF)
+  GS_MM_STEP(kDppRowRor8, 0xF) GS_MM_STEP(kDppRowBcast15, 0xA) GS_MM_STEP(kDppRowBcast31, 0xC)
+#undef GS_MM_STEP
+  *vmax = (uint32_t)__builtin_amdgcn_readlane((int)a, 63);
+  *vmin = (uint32_t)__builtin_amdgcn_readlane((int)b, 63);
+}
+// the sum of the wave's binary64 values (a fixed order), in every lane
+__device__ __forceinline__ double wave_sum_f64_dpp(double v) {
+#define GS_SUM_STEP(C, M)                                                            \
+  { const uint64_t u = __builtin_bit_cast(uint64_t, v);                              \
+    const uint32_t lo = dpp_u32<C, M>(0u, (uint32_t)u);                              \
+    const uint32_t hi = dpp_u32<C, M>(0u, (uint32_t)(u >> 32));                      \
+    v += __builtin_bit_cast(double, ((uint64_t)hi << 32) | lo); }
+  GS_SUM_STEP(kDppQuad1032, 0xF) GS_SUM_STEP(kDppQuad2301, 0xF) GS_SUM_STEP(kDppRowRor4, 0xF)
+  GS_SUM_STEP(kDppRowRor8, 0xF) GS_SUM_STEP(kDppRowBcast15, 0xA) GS_SUM_STEP(kDppRowBcast31, 0xC)
+#undef GS_SUM_STEP
+  const uint64_t u = __builtin_bit_cast(uint64_t, v);
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)u, 63);
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(u >> 32), 63);
+  return __builtin_bit_cast(double, ((uint64_t)hi << 32) | lo);
+}
+// Per-wave results of a group's first chunk, exchanged through LDS.
+struct WaveSlots {
   uint32_t wbad[kScanWaves];
   uint32_t wlanes[kScanWaves]; // lanes with a finite maximum
   uint32_t wtau[kScanWaves];   // the wave's d-th largest lane maximum (0: fewer than d lanes)
   uint64_t wbest[kScanWaves];
 };
 
-// Loads of one chunk's logits (kFull: 16-byte vector loads).
+struct ScanShared {
+  uint32_t special[kMaxGroupChunks * kChunkWords];  // special ids of the workgroup's chunks (thread-major)
+  double tab[256];
+  WaveSlots slots[2];                // consecutive exchanges alternate between the two
+  uint64_t stage[kScanWaves * kSubCap];  // each wave's list entries before they go out
+};
+
+// The row's penalty window [w0, w1) and forced ids [f0, f1) as offsets into
+// the history and forced id arrays.
+struct RowRanges {
+  int64_t w0, w1, f0, f1;
+};
+
+// Loads of one chunk's logits for the single-chunk path (kFull: 16-byte
+// vector loads; otherwise element loads bounded by n_valid).
 template <typename In, bool kFull>
 __device__ __forceinline__ void load_chunk(const SampleArgs& a, int64_t row, int64_t gbase, int n_valid,
                                            uint4 (&raw)[kElemsPerThread / VecTraits<In>::kVec]) {
@@ -130,132 +207,107 @@ __device__ __forceinline__ void load_chunk(const SampleArgs& a, int64_t row, int
   }
 }
 
-// One chunk. kFull: all kChunk logits exist and rows are 16-byte aligned;
-// kMasked: the row has a constraint mask. Each combination is straight-line
-// code from the first load to the first barrier, so the only wait before the
-// barrier is for the loads issued ahead of the chunk.
-// The row's penalty window [w0, w1) and forced ids [f0, f1) as offsets into
-// the history and forced id arrays.
-struct RowRanges {
-  int64_t w0, w1, f0, f1;
-};
+// Loads of chunk lc of a group. Each chunk gets a buffer resource of its own
+// whose extent is the chunk (lc < nc) or empty (lc >= nc): loads of an empty
+// one return zeros without a memory access. Lane offsets are tid * 16 and
+// the load index goes into the scalar offset, so one VGPR addresses them all.
+template <typename In, bool kMasked>
+__device__ __forceinline__ void load_group_chunk(const char* lbase, const char* mbase, int lc, int nc,
+                                                 uint4 (&raw)[kElemsPerThread / VecTraits<In>::kVec],
+                                                 uint32_t (&mword)[kElemsPerThread / VecTraits<In>::kVec]) {
+  using VT = VecTraits<In>;
+  constexpr int kVec = VT::kVec;
+  constexpr int kLoads = kElemsPerThread / kVec;
+  constexpr int32_t kChunkBytes = kChunk * (int32_t)sizeof(In);
+  typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+  const int tid = threadIdx.x;
+  const bool live = lc < nc;
+  const __amdgpu_buffer_rsrc_t lg = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)(lbase + (int64_t)lc * kChunkBytes), (short)0, live ? kChunkBytes : 0, kBufferWord3);
+#pragma unroll
+  for (int v = 0; v < kLoads; ++v) {
+    const u32x4 w = __builtin_amdgcn_raw_buffer_load_b128(lg, tid * 16, v * kScanThreads * 16, 0);
+    raw[v] = make_uint4(w.x, w.y, w.z, w.w);
+  }
+  if (kMasked) {
+    // the chunk's 256 mask words; load v of a thread needs word (v*256 + tid)*kVec/32
+    const __amdgpu_buffer_rsrc_t mk = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)(mbase + (int64_t)lc * (kChunkWords * 4)), (short)0, live ? kChunkWords * 4 : 0, kBufferWord3);
+#pragma unroll
+    for (int v = 0; v < kLoads; ++v) {
+      mword[v] = __builtin_amdgcn_raw_buffer_load_b32(mk, ((tid * kVec) >> 5) * 4, ((v * kScanThreads * kVec) >> 5) * 4, 0);
+    }
+  }
+}
 
+// The statistics and candidate list of one chunk from its loaded logits.
+// kFull: all kChunk logits exist; kMasked: the row has a constraint mask.
+// thr_in > 0 is the group's tau (the stream path: no exchange); with
+// thr_in == 0 the chunk takes its own tau and every path passes exactly one
+// workgroup barrier. special: the chunk's words of the LDS special-id bitmap;
+// W: the LDS slots of an exchange. Returns the threshold the chunk applied
+// when it truncated (0 otherwise).
 template <typename In, bool kFull, bool kMasked>
-__device__ __forceinline__ void scan_chunk(const SampleArgs& a, const gs_row_config& cfg, const Plan plan,
-                                           const RowRanges rr, const int64_t row, const int chunk,
-                                           const int n_valid, ScanShared& S) {
+__device__ __forceinline__ uint32_t chunk_stats(const SampleArgs& a, const gs_row_config& cfg, const Plan plan,
+                                                const int64_t row, const int chunk, const int n_valid,
+                                                const uint4 (&raw)[kElemsPerThread / VecTraits<In>::kVec],
+                                                const uint32_t (&mword)[kElemsPerThread / VecTraits<In>::kVec],
+                                                const uint32_t* s_special, const double* s_tab, WaveSlots& W,
+                                                uint64_t* s_stage, const uint32_t thr_in) {
   using VT = VecTraits<In>;
   constexpr int kVec = VT::kVec;
   constexpr int kLoads = kElemsPerThread / kVec;
   constexpr uint32_t kLaneBits = (1u << kVec) - 1u;
-  uint32_t* s_special = S.special;
-  double* s_tab = S.tab;
-  double* s_wsum = S.wsum;
-  uint32_t* s_wmax = S.wmax;
-  uint32_t* s_wbad = S.wbad;
-  uint32_t* s_wlanes = S.wlanes;
-  uint32_t* s_wtau = S.wtau;
-  uint64_t* s_wbest = S.wbest;
-
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const bool greedy = plan.route == kRouteGreedy;
+  const bool stream = thr_in != 0u;  // uniform over the workgroup
+  const bool greedy = !stream && plan.route == kRouteGreedy;
   const int64_t gbase = (int64_t)chunk * kChunk;
-  const int32_t slot = cfg.mask_slot;
   ChunkStat* stat = a.stats + row * a.n_chunks + chunk;
   uint64_t* list = a.lists + (row * a.n_chunks + chunk) * kGatherCap;
-  // any valid device address, read in place of absent inputs so that no load
-  // sits under a branch
-  const int32_t* dummy = (const int32_t*)a.configs;
-
-  // -- the window and forced ids and this thread's exp-table entry
-  const int64_t w0 = rr.w0, w1 = rr.w1;
-  const int64_t wn = w1 - w0;
-  const int32_t* hp = wn > 0 ? a.history_ids + w0 : dummy;
-  const int32_t hid0 = hp[tid < wn ? tid : 0];
-  const int32_t hid1 = hp[tid + kScanThreads < wn ? tid + kScanThreads : 0];
-  const int64_t f0 = kMasked ? rr.f0 : 0, f1 = kMasked ? rr.f1 : 0;
-  const int64_t fn = f1 - f0;
-  const int32_t* fp = fn > 0 ? a.forced_ids + f0 : dummy;
-  const int32_t fid0 = fp[tid < fn ? tid : 0];
-  const double tabv = c_exp2_256[tid];
-
-  // -- the chunk: all loads in flight before the first use
-  uint4 raw[kLoads];
-  load_chunk<In, kFull>(a, row, gbase, n_valid, raw);
-  uint32_t mword[kLoads];
-  if (kMasked) {
-    const uint32_t* maskp = a.mask_table + (int64_t)slot * a.mask_words + (gbase >> 5);
-#pragma unroll
-    for (int v = 0; v < kLoads; ++v) {
-      const int loc = (v * kScanThreads + tid) * kVec;
-      mword[v] = maskp[(loc < n_valid ? loc : n_valid - 1) >> 5];  // bits past n_valid are cleared below
-    }
-  }
-
-  // -- special ids of this chunk as an LDS bitmap
-  s_special[tid] = 0;  // kChunk / 32 == kScanThreads words
-  s_tab[tid] = tabv;
-  __syncthreads();
-  // ids are below 2^31, so chunk offsets fit in 32 bits
-  const int32_t base32 = (int32_t)gbase;
-  auto mark = [&](int32_t id) {
-    const uint32_t loc = (uint32_t)(id - base32);
-    if (loc < (uint32_t)n_valid) atomicOr(&s_special[loc >> 5], 1u << (loc & 31));
-  };
-  if (tid < wn) mark(hid0);
-  if (tid + kScanThreads < wn) mark(hid1);
-  for (int64_t j = w0 + 2 * kScanThreads + tid; j < w1; j += kScanThreads) mark(a.history_ids[j]);
-  if (tid < fn) mark(fid0);
-  for (int64_t j = f0 + kScanThreads + tid; j < f1; j += kScanThreads) mark(a.forced_ids[j]);
-  __syncthreads();
-
-  // per-load bitmasks: valid = in range and not special; allowed = mask bit
-  auto valid_bits = [&](int v) -> uint32_t {
-    const int loc = (v * kScanThreads + tid) * kVec;
-    uint32_t in_range = kLaneBits;
-    if (!kFull) {
-      const int left = n_valid - loc;
-      in_range = left >= kVec ? kLaneBits : (left > 0 ? (1u << left) - 1u : 0u);
-    }
-    return in_range & ~(s_special[loc >> 5] >> (loc & 31)) & kLaneBits;
-  };
-  auto allowed_bits = [&](int v) -> uint32_t {
-    const int loc = (v * kScanThreads + tid) * kVec;
-    if (kMasked) return (mword[v] >> (loc & 31)) & kLaneBits;
-    return kLaneBits;
-  };
-  const bool use_cap = cfg.softcap > 0;
 
   // values: excluded (special / out of range) and masked ids become -inf,
-  // which neither the normaliser nor the candidate list admits. Most load
-  // groups hold no such id: the per-element masking runs only for groups
-  // where some lane of the wave has one.
+  // which neither the normaliser nor the candidate list admits. The thread's
+  // excluded elements are one bitmap word (bit e = element e of the thread);
+  // the per-element masking runs only when some lane of the wave has one.
   float x[kElemsPerThread];
 #pragma unroll
   for (int v = 0; v < kLoads; ++v) {
-    const uint32_t live = valid_bits(v) & allowed_bits(v);
 #pragma unroll
-    for (int j = 0; j < kVec; ++j) {
-      float y = __builtin_bit_cast(float, VT::bits(raw[v], j));
-      if (use_cap) y = capped(y, cfg.softcap);
-      x[v * kVec + j] = y;
+    for (int j = 0; j < kVec; ++j) x[v * kVec + j] = __builtin_bit_cast(float, VT::bits(raw[v], j));
+  }
+  if (cfg.softcap > 0) {
+#pragma unroll
+    for (int e = 0; e < kElemsPerThread; ++e) x[e] = capped(x[e], cfg.softcap);
+  }
+  uint32_t dead = s_special[tid];
+  if (!kFull) {
+#pragma unroll
+    for (int v = 0; v < kLoads; ++v) {
+      const int left = n_valid - (v * kScanThreads + tid) * kVec;
+      const uint32_t in_range = left >= kVec ? kLaneBits : (left > 0 ? (1u << left) - 1u : 0u);
+      dead |= (~in_range & kLaneBits) << (v * kVec);
     }
-    if (__ballot(live != kLaneBits)) {
+  }
+  if (kMasked) {
 #pragma unroll
-      for (int j = 0; j < kVec; ++j) {
-        if (!((live >> j) & 1u)) x[v * kVec + j] = -__builtin_inff();
-      }
+    for (int v = 0; v < kLoads; ++v) {
+      const int loc = (v * kScanThreads + tid) * kVec;
+      dead |= (~(mword[v] >> (loc & 31)) & kLaneBits) << (v * kVec);
+    }
+  }
+  if (__ballot(dead != 0)) {
+#pragma unroll
+    for (int e = 0; e < kElemsPerThread; ++e) {
+      if ((dead >> e) & 1u) x[e] = -__builtin_inff();
     }
   }
 
-  // pass 1: the thread's maximum (NaN-propagating: NaN or +inf flags the row)
+  // the thread's maximum (NaN-propagating: NaN or +inf flags the row)
   float tmax = -__builtin_inff();
 #pragma unroll
   for (int e = 0; e < kElemsPerThread; ++e) tmax = __builtin_elementwise_maximum(tmax, x[e]);
   const bool finite_max = tmax > -__builtin_inff() && tmax < __builtin_inff();
-  // the normaliser below reads -inf as -FLT_MAX, which adds exactly 0 unless
-  // the thread's maximum is -FLT_MAX itself: such rows take the exact path
-  const bool thread_bad = !(tmax < __builtin_inff()) || tmax == -__FLT_MAX__;
+  const bool thread_bad = !(tmax < __builtin_inff());
 
   // ------------------------------------------------------------ greedy rows
   if (greedy) {
@@ -276,110 +328,105 @@ __device__ __forceinline__ void scan_chunk(const SampleArgs& a, const gs_row_con
       best = o > best ? o : best;
     }
     const uint64_t wb = __ballot(thread_bad);
-    if (lane == 0) { s_wbest[wave] = best; s_wbad[wave] = wb != 0; }
-    __syncthreads();
+    if (lane == 0) { W.wbest[wave] = best; W.wbad[wave] = wb != 0; }
+    lds_barrier();
     if (tid == 0) {
       uint64_t bst = 0;
       uint32_t anybad = 0;
-      for (int w = 0; w < kScanWaves; ++w) { bst = s_wbest[w] > bst ? s_wbest[w] : bst; anybad |= s_wbad[w]; }
+      for (int w = 0; w < kScanWaves; ++w) { bst = W.wbest[w] > bst ? W.wbest[w] : bst; anybad |= W.wbad[w]; }
       if (bst) list[0] = list_slot(__builtin_bit_cast(uint32_t, key_f32(entry_key(bst))), entry_id(bst));
-      ChunkStat st;
-      st.sum = 0.0;
-      st.max_key = entry_key(bst);
-      st.n_list = bst ? 1u : 0u;
-      st.n_finite = 0;
-      st.threshold = entry_key(bst);
-      st.truncated = 0;
-      st.flags = anybad ? kChunkNonFinite : 0u;
-      for (int w = 0; w < kScanWaves; ++w) st.n_sub[w] = 0;
-      st.n_sub[0] = (uint16_t)st.n_list;
-      *stat = st;
-    }
-    return;
-  }
-
-  // pass 2: sum of e^((l - tmax)/T) against the thread's own maximum, with
-  // y = 256 log2(e) (l - tmax) / T formed by one fma; its rounding (of
-  // tmax * A) is of the order of the reference's own rounding of l/T - M,
-  // which the finish kernel's top-p margin already covers.
-  const double A = (1.0 / cfg.temperature) * GS_256_LOG2E;
-  double sum = 0.0;
-  if (finite_max) {
-    const double B = -(double)tmax * A;
-    // logits below lim have (l - tmax)/T < -60 (lim is rounded down)
-    const double lim64 = (double)tmax - 60.0 * cfg.temperature;
-    // 1e-6 relative below lim64 before rounding to binary32 (half an ulp)
-    const float lim = (float)(lim64 - (lim64 < 0 ? -lim64 : lim64) * 1.0e-6 - 1.0e-37);
-    // groups of four terms, so the table reads of a group overlap; a group is
-    // skipped when no lane of the wave has a term above e^-60. -inf enters as
-    // -FLT_MAX (one med3; +inf rows are already flagged): its exponent is
-    // finite and so negative that the term is 0.
-#pragma unroll
-    for (int g = 0; g < kElemsPerThread; g += 4) {
-      const float gmax = __builtin_elementwise_maximum(__builtin_elementwise_maximum(x[g], x[g + 1]),
-                                                       __builtin_elementwise_maximum(x[g + 2], x[g + 3]));
-      if (__ballot(gmax >= lim)) {
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          const float xe = __builtin_amdgcn_fmed3f(x[g + q], -__FLT_MAX__, __FLT_MAX__);
-          sum += exp2_256(__builtin_fma((double)xe, A, B), s_tab);
-        }
-      }
-    }
-  }
-
-  // wave statistics: maximum, flags, finite lanes, the sum rescaled to the
-  // wave maximum and the wave's d-th largest lane maximum
-  const uint32_t mykey = finite_max ? f32_key(tmax) : 0u;
-  const uint32_t depth = (uint32_t)plan.depth;
-  const uint32_t dw = (depth + 3u) / 4u + 2u;
-  {
-    const uint32_t wm = wave_max_u32(mykey);
-    const uint64_t wb = __ballot(thread_bad);
-    const uint32_t wl = (uint32_t)__popcll(__ballot(mykey != 0u));
-    double part = 0.0;
-    if (finite_max && sum > 0.0) {
-      const double y = ((double)tmax - (double)key_f32(wm)) * A;
-      part = y > kSkipY ? sum * exp2_256(y, s_tab) : 0.0;  // the wave maximum's own factor is exactly 1
-    }
-    part = wave_sum_f64(part);
-    const uint32_t wt = wl >= dw ? wave_kth_key(mykey, dw) : 0u;
-    if (lane == 0) {
-      s_wmax[wave] = wm;
-      s_wbad[wave] = wb != 0;
-      s_wlanes[wave] = wl;
-      s_wsum[wave] = part;
-      s_wtau[wave] = wt;
-    }
-  }
-  __syncthreads();
-  uint32_t cmax = 0, cbad = 0, lanes = 0, tau = 0xFFFFFFFFu, bound = 0;
-#pragma unroll
-  for (int w = 0; w < kScanWaves; ++w) {
-    cmax = s_wmax[w] > cmax ? s_wmax[w] : cmax;
-    cbad |= s_wbad[w];
-    lanes += s_wlanes[w];
-    if (s_wtau[w]) { tau = s_wtau[w] < tau ? s_wtau[w] : tau; bound += dw; }
-  }
-  if (cbad) {
-    // NaN or +inf among the live logits: outside the one-pass contract
-    if (tid == 0) {
       ChunkStat st{};
-      st.max_key = cmax;
-      st.flags = kChunkNonFinite;
+      st.wmax[0] = entry_key(bst);
+      st.wflags[0] = anybad ? kChunkNonFinite : 0u;
+      st.threshold = entry_key(bst);
+      st.n_sub[0] = bst ? 1u : 0u;
       *stat = st;
     }
-    return;
+    return 0u;
   }
 
-  // tau: at least `depth` per-thread maxima are >= it (dw of each wave that
-  // has dw finite lanes); nearly full chunks are listed whole
-  const bool selected = lanes > depth + 32u && bound >= depth;
-  const uint32_t thr = selected && tau > kKeyNegInf ? tau : kKeyNegInf + 1u;
+  // the thread's sum of e^((l - tmax)/T) in binary32 terms 2^(x c - B),
+  // c = log2(e)/T and B = tmax c rounded to binary32, each one fma and one
+  // hardware exp2; terms are added in pairs in binary32 and the pairs in
+  // binary64. The rounding of B (berr, exact by fma) is a factor 2^berr
+  // common to the thread's terms, divided out in binary64 by the rescale
+  // below. -inf (excluded, masked) enters as a term of exactly 0.
+  const double A = (1.0 / cfg.temperature) * GS_256_LOG2E;  // 256 log2(e) / T
+  const float c32 = (float)(A * (1.0 / 256.0));
+  double sum = 0.0;
+  float berr = 0.0f;
+  bool scale_bad = false;
+  if (finite_max) {
+    const float B = tmax * c32;
+    berr = __builtin_fmaf(tmax, c32, -B);
+    // an infinite or NaN scale leaves the one-pass contract (exact path)
+    scale_bad = !(__builtin_fabsf(B) < __builtin_inff()) || !(berr == berr);
+#pragma unroll
+    for (int e = 0; e < kElemsPerThread; e += 2) {
+      const float t0 = __builtin_amdgcn_exp2f(__builtin_fmaf(x[e], c32, -B));
+      const float t1 = __builtin_amdgcn_exp2f(__builtin_fmaf(x[e + 1], c32, -B));
+      sum += (double)(t0 + t1);
+    }
+  }
+
+  // wave statistics: the maximum, the flags and the sum rescaled to the wave
+  // maximum (written below); the group's first chunk also takes its tau
+  const uint32_t mykey = finite_max ? f32_key(tmax) : 0u;
+  uint32_t wm, wlo;
+  wave_max_min_u32(mykey, &wm, &wlo);
+  const bool wave_bad = __ballot(thread_bad || scale_bad) != 0;
+  double part = 0.0;
+  if (finite_max && sum > 0.0) {
+    // e^((tmax - wave max)/T) 2^-berr, in units of 2^(1/256)
+    const double y = ((double)tmax - (double)key_f32(wm)) * A - 256.0 * (double)berr;
+    part = y > kSkipY ? sum * exp2_256(y, s_tab) : 0.0;
+  }
+  part = wave_sum_f64_dpp(part);
+
+  uint32_t thr = thr_in;
+  bool selected = true;
+  if (!stream) {
+    const uint32_t depth = (uint32_t)plan.depth;
+    const uint32_t dw = (depth + 3u) / 4u + 2u;
+    const uint32_t wl = (uint32_t)__popcll(__ballot(mykey != 0u));
+    const uint32_t wt = wl >= dw ? wave_kth_key(mykey, dw, wlo, wm) : 0u;
+    if (lane == 0) {
+      W.wbad[wave] = wave_bad;
+      W.wlanes[wave] = wl;
+      W.wtau[wave] = wt;
+    }
+    lds_barrier();
+    uint32_t cbad = 0, lanes = 0, tau = 0xFFFFFFFFu, bound = 0;
+#pragma unroll
+    for (int w = 0; w < kScanWaves; ++w) {
+      cbad |= W.wbad[w];
+      lanes += W.wlanes[w];
+      if (W.wtau[w]) { tau = W.wtau[w] < tau ? W.wtau[w] : tau; bound += dw; }
+    }
+    if (cbad) {
+      // NaN or +inf among the live logits: outside the one-pass contract
+      if (lane == 0) {
+        stat->wmax[wave] = wm;
+        stat->wsum[wave] = 0.0;
+        stat->wflags[wave] = kChunkNonFinite;
+        stat->n_sub[wave] = 0;
+        if (wave == 0) { stat->threshold = 0; stat->truncated = 0; }
+      }
+      return 0u;
+    }
+    // at least `depth` per-thread maxima are >= tau (dw of each wave that
+    // has dw finite lanes); nearly full chunks are listed whole
+    selected = lanes > depth + 32u && bound >= depth;
+    thr = selected && tau > kKeyNegInf ? tau : kKeyNegInf + 1u;
+  }
   const float tf = key_f32(thr);
 
-  // gather every finite logit >= tau into this wave's sub-list
+  // gather every finite logit >= tau into this wave's sub-list, staged in LDS
+  // at positions taken from ballots and written out with one coalesced store
+  // per 64 entries (entries past kSubCap are counted, not kept)
+  uint64_t* stage = s_stage + wave * kSubCap;
   uint64_t* sub = list + wave * kSubCap;
+  const uint32_t id0 = (uint32_t)gbase + (uint32_t)(tid * kVec);
   uint32_t off = 0;
 #pragma unroll
   for (int v = 0; v < kLoads; ++v) {
@@ -392,88 +439,271 @@ __device__ __forceinline__ void scan_chunk(const SampleArgs& a, const gs_row_con
         if (take) {
           const uint32_t pos =
               off + __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
-          const uint32_t id = (uint32_t)(gbase + (v * kScanThreads + tid) * kVec + j);
-          if (pos < (uint32_t)kSubCap) sub[pos] = list_slot(__builtin_bit_cast(uint32_t, y), id);
+          const uint32_t id = id0 + (uint32_t)(v * kScanThreads * kVec + j);
+          if (pos < (uint32_t)kSubCap) stage[pos] = list_slot(__builtin_bit_cast(uint32_t, y), id);
         }
         off += (uint32_t)__popcll(m);
       }
     }
   }
-  // the sub-list length; a count above kSubCap tells the finish it overflowed
-  if (lane == 0) stat->n_sub[wave] = (uint16_t)(off < 0xFFFFu ? off : 0xFFFFu);
-  if (tid == 0) {
-    // the chunk sum: each wave's sum rescaled from its maximum to the chunk's
-    double csum = 0.0;
-#pragma unroll
-    for (int w = 0; w < kScanWaves; ++w) {
-      const double ws = s_wsum[w];
-      if (ws > 0.0) {
-        const double y = ((double)key_f32(s_wmax[w]) - (double)key_f32(cmax)) * A;
-        csum += y > kSkipY ? ws * exp2_256(y, s_tab) : 0.0;
-      }
-    }
-    stat->sum = csum;
-    stat->max_key = cmax;
-    stat->n_list = 0;
-    stat->n_finite = 0;
-    stat->threshold = thr;
-    // with a tau, lanes whose maximum lies below it left finite logits out
-    stat->truncated = selected ? 1u : 0u;
-    stat->flags = 0u;
+  {
+    const uint32_t n = off < (uint32_t)kSubCap ? off : (uint32_t)kSubCap;
+    if ((uint32_t)lane < n) sub[lane] = stage[lane];
+    if ((uint32_t)lane + 64u < n) sub[lane + 64] = stage[lane + 64];
   }
-
+  // the wave's statistics; a sub-list count above kSubCap tells the finish
+  // that it overflowed
+  if (lane == 0) {
+    stat->wsum[wave] = part;
+    stat->wmax[wave] = wm;
+    stat->wflags[wave] = wave_bad ? kChunkNonFinite : 0u;
+    stat->n_sub[wave] = (uint16_t)(off < 0xFFFFu ? off : 0xFFFFu);
+    if (wave == 0) {
+      stat->threshold = thr;
+      // with a tau, lanes whose maximum lies below it left finite logits out
+      stat->truncated = selected ? 1u : 0u;
+    }
+  }
+  return selected ? thr : 0u;
 }
 
+// Marks the row's special ids that fall in [gbase, gbase + span) in the LDS
+// bitmap, thread-major: chunk lc's word t holds thread t's elements, bit
+// e = v * kVec + j for the logit at chunk offset (v * 256 + t) * kVec + j.
+// The first window and forced ids were loaded by the caller ahead of the
+// chunk loads.
+template <typename In, bool kMasked>
+__device__ __forceinline__ void mark_specials(const SampleArgs& a, const RowRanges rr, int64_t gbase, int span,
+                                              int32_t hid0, int32_t hid1, int32_t fid0, uint32_t* s_special) {
+  constexpr int kVec = VecTraits<In>::kVec;
+  const int tid = threadIdx.x;
+  const int64_t wn = rr.w1 - rr.w0;
+  const int64_t f0 = kMasked ? rr.f0 : 0, f1 = kMasked ? rr.f1 : 0;
+  const int64_t fn = f1 - f0;
+  // ids are below 2^31, so offsets from the base fit in 32 bits
+  const int32_t base32 = (int32_t)gbase;
+  auto mark = [&](int32_t id) {
+    const uint32_t loc = (uint32_t)(id - base32);
+    if (loc < (uint32_t)span) {
+      const uint32_t l = loc % (uint32_t)kChunk;
+      const uint32_t t = (l / kVec) % kScanThreads;
+      const uint32_t e = (l / (kVec * kScanThreads)) * kVec + l % kVec;
+      atomicOr(&s_special[(loc / kChunk) * kChunkWords + t], 1u << e);
+    }
+  };
+  if (tid < wn) mark(hid0);
+  if (tid + kScanThreads < wn) mark(hid1);
+  for (int64_t j = rr.w0 + 2 * kScanThreads + tid; j < rr.w1; j += kScanThreads) mark(a.history_ids[j]);
+  if (tid < fn) mark(fid0);
+  for (int64_t j = f0 + kScanThreads + tid; j < f1; j += kScanThreads) mark(a.forced_ids[j]);
+}
+
+// The first window and forced ids of the row (one or two per thread), read
+// from valid addresses only, so that no load sits under a branch.
+template <bool kMasked>
+__device__ __forceinline__ void first_specials(const SampleArgs& a, const RowRanges rr, int32_t* hid0,
+                                               int32_t* hid1, int32_t* fid0) {
+  const int tid = threadIdx.x;
+  const int32_t* dummy = (const int32_t*)a.configs;  // any valid device address
+  const int64_t wn = rr.w1 - rr.w0;
+  const int32_t* hp = wn > 0 ? a.history_ids + rr.w0 : dummy;
+  *hid0 = hp[tid < wn ? tid : 0];
+  *hid1 = hp[tid + kScanThreads < wn ? tid + kScanThreads : 0];
+  const int64_t fn = kMasked ? rr.f1 - rr.f0 : 0;
+  const int32_t* fp = fn > 0 ? a.forced_ids + rr.f0 : dummy;
+  *fid0 = fp[tid < fn ? tid : 0];
+}
+
+// One chunk per workgroup: a row's partial last chunk, or any chunk of a row
+// that is not 16-byte aligned (kFull false), or a full chunk otherwise.
+template <typename In, bool kFull, bool kMasked>
+__device__ __forceinline__ void scan_single(const SampleArgs& a, const gs_row_config& cfg, const Plan plan,
+                                            const RowRanges rr, const int64_t row, const int chunk,
+                                            const int n_valid, ScanShared& S) {
+  using VT = VecTraits<In>;
+  constexpr int kVec = VT::kVec;
+  constexpr int kLoads = kElemsPerThread / kVec;
+  const int tid = threadIdx.x;
+  const int64_t gbase = (int64_t)chunk * kChunk;
+  int32_t hid0, hid1, fid0;
+  first_specials<kMasked>(a, rr, &hid0, &hid1, &fid0);
+  const double tabv = c_exp2_256[tid];
+
+  uint4 raw[kLoads];
+  load_chunk<In, kFull>(a, row, gbase, n_valid, raw);
+  uint32_t mword[kLoads];
+  if (kMasked) {
+    const uint32_t* maskp = a.mask_table + (int64_t)cfg.mask_slot * a.mask_words + (gbase >> 5);
+#pragma unroll
+    for (int v = 0; v < kLoads; ++v) {
+      const int loc = (v * kScanThreads + tid) * kVec;
+      mword[v] = maskp[(loc < n_valid ? loc : n_valid - 1) >> 5];  // bits past n_valid are cleared later
+    }
+  }
+
+  S.special[tid] = 0;  // kChunkWords == kScanThreads
+  S.tab[tid] = tabv;
+  lds_barrier();
+  mark_specials<In, kMasked>(a, rr, gbase, n_valid, hid0, hid1, fid0, S.special);
+  lds_barrier();
+  chunk_stats<In, kFull, kMasked>(a, cfg, plan, row, chunk, n_valid, raw, mword, S.special, S.tab, S.slots[0],
+                                  S.stage, 0u);
+}
+
+// Chunks [c0, c0 + nc) of one row, all full and 16-byte aligned, as a
+// two-stage pipeline over two register buffers.
+template <typename In, bool kMasked>
+__device__ __forceinline__ void scan_group(const SampleArgs& a, const gs_row_config& cfg, const Plan plan,
+                                           const RowRanges rr, const int64_t row, const int c0, const int nc,
+                                           ScanShared& S) {
+  constexpr int kLoads = kElemsPerThread / VecTraits<In>::kVec;
+  const int tid = threadIdx.x;
+  const int64_t gbase = (int64_t)c0 * kChunk;
+  // the window and forced ids go first: after the row's first workgroup they
+  // come from L2, and the marking below waits for them only
+  int32_t hid0, hid1, fid0;
+  first_specials<kMasked>(a, rr, &hid0, &hid1, &fid0);
+  const double tabv = c_exp2_256[tid];
+
+  const char* lg = (const char*)((const In*)a.logits + row * a.row_stride + gbase);
+  const char* mk =
+      (const char*)(kMasked ? a.mask_table + (int64_t)cfg.mask_slot * a.mask_words + (gbase >> 5) : a.mask_table);
+
+  uint4 cur[kLoads], nxt[kLoads];
+  uint32_t mc[kLoads], mn[kLoads];
+  load_group_chunk<In, kMasked>(lg, mk, 0, nc, cur, mc);
+
+  for (int i = tid; i < nc * kChunkWords; i += kScanThreads) S.special[i] = 0;
+  S.tab[tid] = tabv;
+  lds_barrier();
+  mark_specials<In, kMasked>(a, rr, gbase, nc * kChunk, hid0, hid1, fid0, S.special);
+  lds_barrier();
+
+  // One load site and one consumer per iteration (not unrolled): chunk i+1
+  // streams into nxt while chunk i is reduced from cur, then moves over. The
+  // first chunk that truncates fixes the group's tau; the chunks after it
+  // take the stream path.
+  uint32_t thr = 0;
+#pragma unroll 1
+  for (int i = 0; i < nc; ++i) {
+    load_group_chunk<In, kMasked>(lg, mk, i + 1, nc, nxt, mn);
+    const uint32_t t = chunk_stats<In, true, kMasked>(a, cfg, plan, row, c0 + i, kChunk, cur, mc,
+                                                      S.special + i * kChunkWords, S.tab, S.slots[i & 1], S.stage, thr);
+    thr = thr ? thr : t;
+#pragma unroll
+    for (int v = 0; v < kLoads; ++v) {
+      cur[v] = nxt[v];
+      mc[v] = mn[v];
+    }
+  }
+}
+
+// Work split of one launch: blockIdx.x = g < n_groups scans the full chunks
+// [g * n_grouped / n_groups, (g + 1) * n_grouped / n_groups) of row
+// blockIdx.y; the workgroups after them scan the remaining chunks one each,
+// from chunk n_grouped on.
+struct ScanGrid {
+  int32_t n_groups;
+  int32_t n_grouped;
+};
 
 // kMaskable: the batch has a mask table (otherwise no row is constrained and
-// the masked variants, which need more registers, are left out).
+// the masked variants are left out).
 template <typename In, bool kMaskable>
-__global__ __launch_bounds__(kScanThreads, kMaskable ? 5 : 6) void scan_kernel(SampleArgs a) {
+__global__ __launch_bounds__(kScanThreads, kScanWgPerCu) void scan_kernel(SampleArgs a, ScanGrid g) {
   __shared__ ScanShared S;
   const int64_t row = blockIdx.y;
-  const int chunk = blockIdx.x;
   const gs_row_config cfg = a.configs[row];
   const Plan plan = plan_row(cfg);
   // row-uniform offsets read here, ahead of every branch and store, so they
-  // come through the scalar cache and nothing waits on them behind the chunk
+  // come through the scalar cache
   RowRanges rr;
   history_window(a, row, cfg, &rr.w0, &rr.w1);
   rr.f0 = rr.f1 = 0;
   if (a.forced_offsets) { rr.f0 = a.forced_offsets[row]; rr.f1 = a.forced_offsets[row + 1]; }
   if (plan.route != kRouteExact) {
-    const int64_t gbase = (int64_t)chunk * kChunk;
-    const int n_valid = (int)((int64_t)a.vocab - gbase < kChunk ? (int64_t)a.vocab - gbase : kChunk);
     const bool masked = kMaskable && cfg.mask_slot >= 0 && cfg.mask_slot < a.mask_slots;
-    const bool full = n_valid == kChunk && a.vector_ok;
-    if (full) {
-      if (masked) scan_chunk<In, true, kMaskable>(a, cfg, plan, rr, row, chunk, n_valid, S);
-      else scan_chunk<In, true, false>(a, cfg, plan, rr, row, chunk, n_valid, S);
+    if ((int)blockIdx.x < g.n_groups) {
+      const int c0 = (int)(((int64_t)blockIdx.x * g.n_grouped) / g.n_groups);
+      const int nc = (int)(((int64_t)(blockIdx.x + 1) * g.n_grouped) / g.n_groups) - c0;
+      if (masked) scan_group<In, kMaskable>(a, cfg, plan, rr, row, c0, nc, S);
+      else scan_group<In, false>(a, cfg, plan, rr, row, c0, nc, S);
     } else {
-      if (masked) scan_chunk<In, false, kMaskable>(a, cfg, plan, rr, row, chunk, n_valid, S);
-      else scan_chunk<In, false, false>(a, cfg, plan, rr, row, chunk, n_valid, S);
+      const int chunk = g.n_grouped + ((int)blockIdx.x - g.n_groups);
+      const int64_t gbase = (int64_t)chunk * kChunk;
+      const int n_valid = (int)((int64_t)a.vocab - gbase < kChunk ? (int64_t)a.vocab - gbase : kChunk);
+      const bool full = n_valid == kChunk && a.vector_ok;
+      if (full) {
+        if (masked) scan_single<In, true, kMaskable>(a, cfg, plan, rr, row, chunk, n_valid, S);
+        else scan_single<In, true, false>(a, cfg, plan, rr, row, chunk, n_valid, S);
+      } else {
+        if (masked) scan_single<In, false, kMaskable>(a, cfg, plan, rr, row, chunk, n_valid, S);
+        else scan_single<In, false, false>(a, cfg, plan, rr, row, chunk, n_valid, S);
+      }
     }
   }
   // reset the queue the finish kernel fills for the exact kernel (both run
   // after this kernel on the same stream). It is the kernel's last store, so
   // the loads above of the row's options and history offsets may use the
   // scalar cache.
-  if (row == 0 && chunk == 0 && threadIdx.x == 0) {
+  if (row == 0 && blockIdx.x == 0 && threadIdx.x == 0) {
     a.queue->count = 0;
     a.queue->next = 0;
   }
 }
 
+// Relative error of v_exp_f32 at the binary32 values with bit patterns
+// first .. first + count - 1 (one sign), against binary64 exp2; the largest,
+// as (error as binary32 bits) << 32 | y bits, by a 64-bit atomic maximum.
+__global__ void exp2_check_kernel(uint32_t first, uint32_t count, unsigned long long* worst) {
+  const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+  unsigned long long mine = 0;
+  if (i < count) {
+    const uint32_t b = first + i;
+    const float y = __builtin_bit_cast(float, b);
+    const double r = exp2((double)y);
+    if (r >= 0x1p-126 && r <= 0x1.fffffep127) {
+      const double rel = __builtin_fabs((double)__builtin_amdgcn_exp2f(y) - r) / r;
+      // rounded up to binary32, so the reported bound never understates
+      float relf = (float)rel;
+      if ((double)relf < rel) relf = __builtin_bit_cast(float, __builtin_bit_cast(uint32_t, relf) + 1u);
+      mine = ((unsigned long long)__builtin_bit_cast(uint32_t, relf) << 32) | b;
+    }
+  }
+  for (int m = 32; m > 0; m >>= 1) {
+    const unsigned long long o = shfl_xor_u64(mine, m);
+    mine = o > mine ? o : mine;
+  }
+  if ((threadIdx.x & 63) == 0 && mine) atomicMax(worst, mine);
+}
+
 }  // namespace
 
+void launch_exp2_check(uint32_t first, uint32_t count, unsigned long long* worst, hipStream_t s) {
+  if (count == 0) return;
+  hipLaunchKernelGGL(exp2_check_kernel, dim3((count + 255) / 256), dim3(256), 0, s, first, count, worst);
+}
+
 void launch_scan(const SampleArgs& a, hipStream_t s) {
-  dim3 grid(a.n_chunks, a.rows);
+  // group workgroups over the full chunks of 16-byte aligned rows: as many
+  // per row as fills every CU once (kScanWgPerCu each), at least one per
+  // kMaxGroupChunks chunks and at most one per chunk
+  ScanGrid g;
+  const int32_t n_full = a.vector_ok ? a.vocab / kChunk : 0;
+  int64_t per_row = (int64_t)a.cu_count * kScanWgPerCu / a.rows;
+  const int64_t min_groups = (n_full + kMaxGroupChunks - 1) / kMaxGroupChunks;
+  if (per_row < min_groups) per_row = min_groups;
+  if (per_row > n_full) per_row = n_full;
+  g.n_groups = (int32_t)per_row;
+  g.n_grouped = n_full;
+  dim3 grid(g.n_groups + (a.n_chunks - n_full), a.rows);
   const bool maskable = a.mask_slots > 0;
   if (a.dtype == GS_BF16) {
-    if (maskable) hipLaunchKernelGGL((scan_kernel<uint16_t, true>), grid, dim3(kScanThreads), 0, s, a);
-    else hipLaunchKernelGGL((scan_kernel<uint16_t, false>), grid, dim3(kScanThreads), 0, s, a);
+    if (maskable) hipLaunchKernelGGL((scan_kernel<uint16_t, true>), grid, dim3(kScanThreads), 0, s, a, g);
+    else hipLaunchKernelGGL((scan_kernel<uint16_t, false>), grid, dim3(kScanThreads), 0, s, a, g);
   } else {
-    if (maskable) hipLaunchKernelGGL((scan_kernel<float, true>), grid, dim3(kScanThreads), 0, s, a);
-    else hipLaunchKernelGGL((scan_kernel<float, false>), grid, dim3(kScanThreads), 0, s, a);
+    if (maskable) hipLaunchKernelGGL((scan_kernel<float, true>), grid, dim3(kScanThreads), 0, s, a, g);
+    else hipLaunchKernelGGL((scan_kernel<float, false>), grid, dim3(kScanThreads), 0, s, a, g);
   }
 }
 

@@ -106,7 +106,7 @@ EXPORTED_SYMBOLS = (
     "gs_validate_configs", "gs_create", "gs_destroy", "gs_last_error", "gs_synchronize", "gs_stream",
     "gs_sample", "gs_sample_sync", "gs_token_log_prob", "gs_token_log_prob_host", "gs_set_vocab", "gs_set_dfa",
     "gs_build_masks", "gs_dfa_advance", "gs_dfa_accepting", "gs_lmhead", "gs_lmhead_sample", "gs_timing_begin",
-    "gs_timing_end",
+    "gs_timing_end", "gs_check_exp2",
 )
 
 # kernel stages reported by gs_timing_end (include/gsample.h GS_STAGE_*)
@@ -155,6 +155,7 @@ def library():
     L.gs_lmhead_sample.argtypes = [vp, vp, vp, i32, C.c_float, vp, C.POINTER(Batch), vp]
     L.gs_timing_begin.argtypes = [vp, i32]
     L.gs_timing_end.argtypes = [vp, vp, vp]
+    L.gs_check_exp2.argtypes = [vp, C.c_float, C.c_float, C.POINTER(C.c_double), C.POINTER(C.c_float)]
     _lib = L
     return L
 
@@ -370,6 +371,14 @@ class Sampler:
                                                C.c_void_p(out.data_ptr()), None))
         self.synchronize()
         return out.cpu().numpy()
+
+    # -- self-check ----------------------------------------------------
+    def check_exp2(self, lo: float, hi: float):
+        """(largest relative error, where) of the hardware binary32 exp2 over
+        every binary32 in [lo, hi] (gs_check_exp2)."""
+        err, y = C.c_double(), C.c_float()
+        self._check(self.lib.gs_check_exp2(self.ctx, lo, hi, C.byref(err), C.byref(y)))
+        return err.value, y.value
 
     # -- constraints ---------------------------------------------------
     def set_vocab(self, offsets: np.ndarray, data: np.ndarray):

@@ -255,6 +255,15 @@ int gs_lmhead_sample(gs_context* ctx, const void* hidden, const void* weight, in
  * events, writes per stage the summed milliseconds (stage_ms[GS_STAGE_COUNT])
  * and the number of calls that ran that stage (calls[GS_STAGE_COUNT]), and
  * stops timing. The events add a few microseconds per call. */
+/* Self-check of the bound the chunk scan's normaliser rests on; no
+ * counterpart in the reference. Largest relative error of the hardware
+ * binary32 exp2 (v_exp_f32, which the scan evaluates every term with) over
+ * every binary32 y in [lo, hi] whose result is a normal number, against
+ * binary64 exp2, on the context's device; *worst_y is where it occurs. The
+ * scan's normaliser bound assumes at most 1e-7 over [-150, 2^-10].
+ * Synchronous. */
+int gs_check_exp2(gs_context* ctx, float lo, float hi, double* max_rel_err, float* worst_y);
+
 #define GS_STAGE_LMHEAD 0 /* lmhead_kernel */
 #define GS_STAGE_SCAN 1   /* scan_kernel: the one HBM pass over the logits */
 #define GS_STAGE_FINISH 2 /* finish_kernel: per-row merge, filters and draw */

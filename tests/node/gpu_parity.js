@@ -4,8 +4,8 @@
  * the oracle's JavaScript restatement of the reference sampler
  * (oracle/sampler_ref.js), on the same float32 rows, seeds and histories:
  * token ids bit-exact, probabilities within PROB_RTOL relative (one-pass rows
- * take the softmax normaliser from the chunk scan's table-driven exp sum,
- * relative error at most 1.3e-9; the path's bound is 1e-6).
+ * take the softmax normaliser from the chunk scan's binary32 exp2 sums,
+ * relative error at most 3.9e-7; the path's bound is 1e-6).
  * Also the reference's own known answers (tests/sampling.spec.ts:13-146 of
  * the reference), the constraint masker against a brute-force DFA walk, and
  * the bf16 lm_head feeding the sampler.
@@ -17,7 +17,7 @@ const { test, run } = require("./harness");
 const g = require(path.join(__dirname, "..", "..", "gemma-webgpu-engine_amd", "node"));
 const oracle = require(path.join(__dirname, "..", "..", "oracle", "sampler_ref.js"));
 
-const PROB_RTOL = 2e-9;
+const PROB_RTOL = 4e-7;
 const D = g.DEFAULT_DECODING_CONFIG;
 
 /* Seeded N(0, sigma^2) float32 rows: Mulberry32 uniforms, Box-Muller. */

@@ -109,4 +109,5 @@ def test_lmhead_sample_bit_exact_on_gpu_logits(sampler, lm_inputs, oracle):
         masked = oracle.mask_logits(logits[r], legal, [])
         t, tr = oracle.sample_token(masked, hist[r], ocfg, oracle.draw(r, 0))
         assert int(res["token"][r]) == t, (r, int(res["token"][r]), t, int(res["flags"][r]))
-        assert abs(res["probability"][r] - tr.probability) <= 2e-9 * tr.probability
+        # the scan's normaliser bound (3.9e-7 relative) plus binary64 roundings
+        assert abs(res["probability"][r] - tr.probability) <= 4e-7 * tr.probability
