@@ -451,9 +451,10 @@ __device__ int filters_and_draw_wave(const SampleArgs& a, int64_t row, const gs_
   int n = n_avail;
   bool n_complete = complete;
   uint32_t exact_why = 0;
-  // ---- top-k (sampling.ts:44)
-  if (cfg.top_k > 0) {
-    if (cfg.top_k < n) n = cfg.top_k;
+  // ---- top-k (sampling.ts:44): the candidates are the list's first
+  // n_avail, so a cut inside them is the list's own
+  if (cfg.top_k > 0 && cfg.top_k < n) {
+    n = cfg.top_k;
     n_complete = true;
   }
   // ---- min-p (sampling.ts:45-48)
@@ -1145,8 +1146,8 @@ __global__ __launch_bounds__(kFinishThreads) void finish_kernel(SampleArgs a) {
   // ---- top-k (sampling.ts:44)
   int n = n_cand;
   bool n_complete = region_complete;
-  if (cfg.top_k > 0) {
-    if (cfg.top_k < n) n = cfg.top_k;
+  if (cfg.top_k > 0 && cfg.top_k < n) {
+    n = cfg.top_k;
     n_complete = true;  // the first topK of the sorted list are all present
   }
   // ---- min-p (sampling.ts:45-48): p is non-increasing along the list

@@ -18,6 +18,12 @@ constexpr int kSubCap = 128;                      // list entries each wave of a
 constexpr int kGatherCap = kSubCap * kScanWaves;  // 512 list slots per chunk
 constexpr int kMaxFastK = 64;                     // top-k handled by the one-pass path
 constexpr int kTopPListL = 64;                    // rank depth per chunk in top-p mode
+// Rank depth per chunk for top-k rows: min(topK, kTopKChunkDepth). The finish
+// needs the row's top topK; a chunk holding more than 16 of them (about
+// 1e-12 per chunk for topK 50 over 32 chunks of independent logits) leaves
+// fewer than topK candidates above the lists' threshold, which the finish
+// detects and replays exactly.
+constexpr int kTopKChunkDepth = 16;
 constexpr int kFinishThreads = 1024;
 constexpr int kFinishCap = 4096;                  // sorted candidate region in the finish kernel
 constexpr int kFinishMaxChunks = 256;             // chunk statistics the finish keeps in LDS
@@ -93,7 +99,9 @@ __host__ __device__ __forceinline__ Plan plan_row(const gs_row_config& c) {
   // between these bounds l/T keeps the order and the ties of the f32 logits
   if (!(c.temperature >= 1.0e-200 && c.temperature <= 1.0e200)) return Plan{kRouteExact, 0};
   if (c.typical_p < 1) return Plan{kRouteExact, 0};
-  if (c.top_k > 0) return c.top_k <= kMaxFastK ? Plan{kRouteTopK, c.top_k} : Plan{kRouteExact, 0};
+  if (c.top_k > 0)
+    return c.top_k <= kMaxFastK ? Plan{kRouteTopK, c.top_k < kTopKChunkDepth ? c.top_k : kTopKChunkDepth}
+                                : Plan{kRouteExact, 0};
   if (c.top_p < 1 || c.min_p > 0) return Plan{kRouteTopP, kTopPListL};
   return Plan{kRouteExact, 0};
 }

@@ -207,36 +207,38 @@ __device__ __forceinline__ void load_chunk(const SampleArgs& a, int64_t row, int
   }
 }
 
-// Loads of chunk lc of a group. Each chunk gets a buffer resource of its own
-// whose extent is the chunk (lc < nc) or empty (lc >= nc): loads of an empty
-// one return zeros without a memory access. Lane offsets are tid * 16 and
-// the load index goes into the scalar offset, so one VGPR addresses them all.
-template <typename In, bool kMasked>
-__device__ __forceinline__ void load_group_chunk(const char* lbase, const char* mbase, int lc, int nc,
-                                                 uint4 (&raw)[kElemsPerThread / VecTraits<In>::kVec],
-                                                 uint32_t (&mword)[kElemsPerThread / VecTraits<In>::kVec]) {
-  using VT = VecTraits<In>;
-  constexpr int kVec = VT::kVec;
-  constexpr int kLoads = kElemsPerThread / kVec;
+// Loads of chunk lc of a group (logits, and mask words for constrained rows).
+// Each chunk gets a buffer resource of its own whose extent is the chunk
+// (lc < nc) or empty (lc >= nc): loads of an empty one return zeros without
+// a memory access. Lane offsets are tid * 16 and the load index goes into the
+// scalar offset, so one VGPR addresses them all.
+template <typename In>
+__device__ __forceinline__ void load_group_logits(const char* lbase, int lc, int nc,
+                                                  uint4 (&raw)[kElemsPerThread / VecTraits<In>::kVec]) {
+  constexpr int kLoads = kElemsPerThread / VecTraits<In>::kVec;
   constexpr int32_t kChunkBytes = kChunk * (int32_t)sizeof(In);
   typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
   const int tid = threadIdx.x;
-  const bool live = lc < nc;
   const __amdgpu_buffer_rsrc_t lg = __builtin_amdgcn_make_buffer_rsrc(
-      (void*)(lbase + (int64_t)lc * kChunkBytes), (short)0, live ? kChunkBytes : 0, kBufferWord3);
+      (void*)(lbase + (int64_t)lc * kChunkBytes), (short)0, lc < nc ? kChunkBytes : 0, kBufferWord3);
 #pragma unroll
   for (int v = 0; v < kLoads; ++v) {
     const u32x4 w = __builtin_amdgcn_raw_buffer_load_b128(lg, tid * 16, v * kScanThreads * 16, 0);
     raw[v] = make_uint4(w.x, w.y, w.z, w.w);
   }
-  if (kMasked) {
-    // the chunk's 256 mask words; load v of a thread needs word (v*256 + tid)*kVec/32
-    const __amdgpu_buffer_rsrc_t mk = __builtin_amdgcn_make_buffer_rsrc(
-        (void*)(mbase + (int64_t)lc * (kChunkWords * 4)), (short)0, live ? kChunkWords * 4 : 0, kBufferWord3);
+}
+// the chunk's 256 mask words; load v of a thread needs word (v*256 + tid)*kVec/32
+template <typename In>
+__device__ __forceinline__ void load_group_masks(const char* mbase, int lc, int nc,
+                                                 uint32_t (&mword)[kElemsPerThread / VecTraits<In>::kVec]) {
+  constexpr int kVec = VecTraits<In>::kVec;
+  constexpr int kLoads = kElemsPerThread / kVec;
+  const int tid = threadIdx.x;
+  const __amdgpu_buffer_rsrc_t mk = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)(mbase + (int64_t)lc * (kChunkWords * 4)), (short)0, lc < nc ? kChunkWords * 4 : 0, kBufferWord3);
 #pragma unroll
-    for (int v = 0; v < kLoads; ++v) {
-      mword[v] = __builtin_amdgcn_raw_buffer_load_b32(mk, ((tid * kVec) >> 5) * 4, ((v * kScanThreads * kVec) >> 5) * 4, 0);
-    }
+  for (int v = 0; v < kLoads; ++v) {
+    mword[v] = __builtin_amdgcn_raw_buffer_load_b32(mk, ((tid * kVec) >> 5) * 4, ((v * kScanThreads * kVec) >> 5) * 4, 0);
   }
 }
 
@@ -551,27 +553,28 @@ __device__ __forceinline__ void scan_single(const SampleArgs& a, const gs_row_co
 }
 
 // Chunks [c0, c0 + nc) of one row, all full and 16-byte aligned, as a
-// two-stage pipeline over two register buffers.
+// two-stage pipeline over two register buffers; the kernel has already
+// issued the loads of the first chunk's logits into cur.
 template <typename In, bool kMasked>
 __device__ __forceinline__ void scan_group(const SampleArgs& a, const gs_row_config& cfg, const Plan plan,
                                            const RowRanges rr, const int64_t row, const int c0, const int nc,
-                                           ScanShared& S) {
+                                           uint4 (&cur)[kElemsPerThread / VecTraits<In>::kVec], ScanShared& S) {
   constexpr int kLoads = kElemsPerThread / VecTraits<In>::kVec;
   const int tid = threadIdx.x;
   const int64_t gbase = (int64_t)c0 * kChunk;
-  // the window and forced ids go first: after the row's first workgroup they
-  // come from L2, and the marking below waits for them only
+  const char* lg = (const char*)((const In*)a.logits + row * a.row_stride + gbase);
+  uint4 nxt[kLoads];
+  load_group_logits<In>(lg, 1, nc, nxt);
   int32_t hid0, hid1, fid0;
   first_specials<kMasked>(a, rr, &hid0, &hid1, &fid0);
   const double tabv = c_exp2_256[tid];
-
-  const char* lg = (const char*)((const In*)a.logits + row * a.row_stride + gbase);
   const char* mk =
       (const char*)(kMasked ? a.mask_table + (int64_t)cfg.mask_slot * a.mask_words + (gbase >> 5) : a.mask_table);
-
-  uint4 cur[kLoads], nxt[kLoads];
   uint32_t mc[kLoads], mn[kLoads];
-  load_group_chunk<In, kMasked>(lg, mk, 0, nc, cur, mc);
+  if (kMasked) {
+    load_group_masks<In>(mk, 0, nc, mc);
+    load_group_masks<In>(mk, 1, nc, mn);
+  }
 
   for (int i = tid; i < nc * kChunkWords; i += kScanThreads) S.special[i] = 0;
   S.tab[tid] = tabv;
@@ -579,14 +582,12 @@ __device__ __forceinline__ void scan_group(const SampleArgs& a, const gs_row_con
   mark_specials<In, kMasked>(a, rr, gbase, nc * kChunk, hid0, hid1, fid0, S.special);
   lds_barrier();
 
-  // One load site and one consumer per iteration (not unrolled): chunk i+1
-  // streams into nxt while chunk i is reduced from cur, then moves over. The
-  // first chunk that truncates fixes the group's tau; the chunks after it
-  // take the stream path.
+  // Chunk i is reduced from cur while chunk i+1 streams into nxt; then nxt
+  // moves over and chunk i+2 starts loading. The first chunk that truncates
+  // fixes the group's tau; the chunks after it take the stream path.
   uint32_t thr = 0;
 #pragma unroll 1
   for (int i = 0; i < nc; ++i) {
-    load_group_chunk<In, kMasked>(lg, mk, i + 1, nc, nxt, mn);
     const uint32_t t = chunk_stats<In, true, kMasked>(a, cfg, plan, row, c0 + i, kChunk, cur, mc,
                                                       S.special + i * kChunkWords, S.tab, S.slots[i & 1], S.stage, thr);
     thr = thr ? thr : t;
@@ -595,6 +596,8 @@ __device__ __forceinline__ void scan_group(const SampleArgs& a, const gs_row_con
       cur[v] = nxt[v];
       mc[v] = mn[v];
     }
+    load_group_logits<In>(lg, i + 2, nc, nxt);
+    if (kMasked) load_group_masks<In>(mk, i + 2, nc, mn);
   }
 }
 
@@ -612,7 +615,19 @@ struct ScanGrid {
 template <typename In, bool kMaskable>
 __global__ __launch_bounds__(kScanThreads, kScanWgPerCu) void scan_kernel(SampleArgs a, ScanGrid g) {
   __shared__ ScanShared S;
+  constexpr int kLoads = kElemsPerThread / VecTraits<In>::kVec;
   const int64_t row = blockIdx.y;
+  // a group's first chunk starts loading before anything else: its address
+  // comes from the kernel arguments alone
+  const bool group = (int)blockIdx.x < g.n_groups;
+  const uint32_t gx = blockIdx.x, ng = (uint32_t)g.n_groups, nfull = (uint32_t)g.n_grouped;
+  const int c0 = group ? (int)((gx * nfull) / ng) : 0;
+  const int nc = group ? (int)(((gx + 1u) * nfull) / ng) - c0 : 0;
+  uint4 cur[kLoads];
+  if (group) {
+    const char* lg = (const char*)((const In*)a.logits + row * a.row_stride + (int64_t)c0 * kChunk);
+    load_group_logits<In>(lg, 0, nc, cur);
+  }
   const gs_row_config cfg = a.configs[row];
   const Plan plan = plan_row(cfg);
   // row-uniform offsets read here, ahead of every branch and store, so they
@@ -623,11 +638,9 @@ __global__ __launch_bounds__(kScanThreads, kScanWgPerCu) void scan_kernel(Sample
   if (a.forced_offsets) { rr.f0 = a.forced_offsets[row]; rr.f1 = a.forced_offsets[row + 1]; }
   if (plan.route != kRouteExact) {
     const bool masked = kMaskable && cfg.mask_slot >= 0 && cfg.mask_slot < a.mask_slots;
-    if ((int)blockIdx.x < g.n_groups) {
-      const int c0 = (int)(((int64_t)blockIdx.x * g.n_grouped) / g.n_groups);
-      const int nc = (int)(((int64_t)(blockIdx.x + 1) * g.n_grouped) / g.n_groups) - c0;
-      if (masked) scan_group<In, kMaskable>(a, cfg, plan, rr, row, c0, nc, S);
-      else scan_group<In, false>(a, cfg, plan, rr, row, c0, nc, S);
+    if (group) {
+      if (masked) scan_group<In, kMaskable>(a, cfg, plan, rr, row, c0, nc, cur, S);
+      else scan_group<In, false>(a, cfg, plan, rr, row, c0, nc, cur, S);
     } else {
       const int chunk = g.n_grouped + ((int)blockIdx.x - g.n_groups);
       const int64_t gbase = (int64_t)chunk * kChunk;

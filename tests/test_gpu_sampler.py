@@ -150,6 +150,34 @@ def test_random_batches_match_oracle(oracle, V, seed, force_exact):
 # ------------------------------------------------------------- full-size rows
 
 
+def test_topk_deeper_than_chunk_lists(sampler, oracle):
+    """Top-k rows list at most 16 entries' worth of depth per chunk; rows whose
+    top K crowd into one chunk (here the 60 largest logits, one per lane of
+    one chunk) leave fewer than K candidates above the lists' threshold, and
+    must still come out as the oracle's ids (by the block-wide or exact
+    path)."""
+    import torch
+
+    gs = _gs()
+    V = 262144
+    rng = np.random.default_rng(5)
+    rows, cfgs = [], []
+    for k, start in ((50, 0), (64, 8192 * 7), (40, 8192 * 31)):
+        x = rng.normal(0, 1, V).astype(np.float32)
+        ids = start + 4 * np.arange(60)  # thread t's first element, t = 0..59
+        x[ids] = 8.0 + rng.normal(0, 0.3, ids.size).astype(np.float32)
+        rows.append(x)
+        cfgs.append(gs.DecodingConfig(temperature=1.0, topK=k, topP=0.97, repetitionPenalty=1.0, repetitionWindow=0))
+    us = [0.11, 0.5, 0.93]
+    conf = np.stack([gs.runtime.row_config(c, uniform=u) for c, u in zip(cfgs, us)])
+    out = sampler.sample(torch.from_numpy(np.stack(rows)).cuda(), conf)
+    exp = []
+    for x, c, u in zip(rows, cfgs, us):
+        t, tr = oracle.sample_token(x, [], to_oracle_cfg(c), u)
+        exp.append((t, tr.probability))
+    assert_rows_match(out, exp, label="crowded_topk")
+
+
 def test_hardware_exp2_bound(sampler):
     """The chunk scan evaluates every normaliser term with v_exp_f32 and its
     error bound (3.9e-7 per chunk sum) assumes the instruction is within 1e-7
