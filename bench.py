@@ -10,10 +10,11 @@ temperature 0.7, topK 50, topP 0.9, row r drawing SeededRandom(r).next().
 
 The same run reports
   roofline      the dominant kernel's algorithmic bytes per launch over its
-                mean duration, timed with HIP events around every kernel of
-                a second run of the same K steps (gs_timing_begin /
-                gs_timing_end; the events slow a step down, so the step rate
-                comes from the first run, bracketed by two events only);
+                mean duration over a second run of the same K steps, each
+                kernel launched with start/stop HIP events that stamp its own
+                dispatch (gs_timing_begin / gs_timing_end; the events slow a
+                step down, so the step rate comes from the first run,
+                bracketed by two events only);
   traffic       HBM bytes the dominant kernel moves per launch, taken from the
                 PMC summary committed under profiles/ for this workload (a
                 line "bench-traffic: workload=<w> kernel=<k> bytes=<B>" that
@@ -298,9 +299,9 @@ def main():
     ms_per_step = total_ms / args.steps
     log(f"timed {args.steps} steps: {ms_per_step * 1000:.1f} us/step")
 
-    # kernel durations: K more steps with HIP events around every kernel on
-    # the stream it runs on (the events add ~20 us per step, so the step rate
-    # above is timed without them)
+    # kernel durations: K more steps, every kernel launched with start/stop
+    # HIP events on the stream it runs on (the events slow a step down, so
+    # the step rate above is timed without them)
     s.timing_begin(args.steps)
     for _ in range(args.steps):
         launch_step(wl, sp)

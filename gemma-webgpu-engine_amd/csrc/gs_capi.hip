@@ -45,8 +45,8 @@ struct gs_context {
   // device staging for the host-array entry points (grown on demand)
   uint8_t* d_stage = nullptr;
   size_t stage_cap = 0;
-  // kernel timing (gs_timing_begin / gs_timing_end): per timed call, one event
-  // before each stage and one after it
+  // kernel timing (gs_timing_begin / gs_timing_end): per timed call and stage,
+  // the start and stop events of that stage's kernel launch
   std::vector<hipEvent_t> t_events;  // [max_calls][GS_STAGE_COUNT][2]
   std::vector<uint8_t> t_ran;        // [max_calls][GS_STAGE_COUNT]
   int32_t t_cap = 0;
@@ -88,10 +88,16 @@ int32_t timing_slot(gs_context* ctx) {
   return ctx->t_calls;
 }
 
-void stage_mark(gs_context* ctx, int32_t slot, int stage, int edge, hipStream_t s) {
-  if (slot < 0) return;
-  (void)hipEventRecord(ctx->t_events[((size_t)slot * GS_STAGE_COUNT + stage) * 2 + edge], s);
-  if (edge == 0) ctx->t_ran[(size_t)slot * GS_STAGE_COUNT + stage] = 1;
+// The timing events of one stage's launch in timing slot `slot` (none when
+// not timing).
+LaunchEvents stage_events(gs_context* ctx, int32_t slot, int stage) {
+  LaunchEvents ev;
+  if (slot < 0) return ev;
+  const size_t i = (size_t)slot * GS_STAGE_COUNT + stage;
+  ev.start = ctx->t_events[i * 2];
+  ev.stop = ctx->t_events[i * 2 + 1];
+  ctx->t_ran[i] = 1;
+  return ev;
 }
 
 // Grows the context's device staging buffer to at least `bytes`. Waits for
@@ -304,18 +310,12 @@ int gs_sample(gs_context* ctx, const gs_batch* b, void* stream) {
   // the exact-path queue is reset by the chunk scan's first workgroup: no
   // memset node, so the call stays capturable and one launch cheaper
   const int32_t slot = timing_slot(ctx);
-  stage_mark(ctx, slot, GS_STAGE_SCAN, 0, s);
-  launch_scan(a, s);
+  launch_scan(a, s, stage_events(ctx, slot, GS_STAGE_SCAN));
   GS_HIP(ctx, hipGetLastError());
-  stage_mark(ctx, slot, GS_STAGE_SCAN, 1, s);
-  stage_mark(ctx, slot, GS_STAGE_FINISH, 0, s);
-  launch_finish(a, s);
+  launch_finish(a, s, stage_events(ctx, slot, GS_STAGE_FINISH));
   GS_HIP(ctx, hipGetLastError());
-  stage_mark(ctx, slot, GS_STAGE_FINISH, 1, s);
-  stage_mark(ctx, slot, GS_STAGE_EXACT, 0, s);
-  launch_exact(a, s);
+  launch_exact(a, s, stage_events(ctx, slot, GS_STAGE_EXACT));
   GS_HIP(ctx, hipGetLastError());
-  stage_mark(ctx, slot, GS_STAGE_EXACT, 1, s);
   if (slot >= 0) ctx->t_calls++;
   return GS_OK;
 }
@@ -719,10 +719,9 @@ int gs_lmhead(gs_context* ctx, const void* hidden, const void* weight, int32_t m
   GS_HIP(ctx, hipSetDevice(ctx->device));
   hipStream_t s = pick_stream(ctx, stream);
   const int32_t slot = timing_slot(ctx);
-  stage_mark(ctx, slot, GS_STAGE_LMHEAD, 0, s);
-  launch_lmhead((const uint16_t*)hidden, (const uint16_t*)weight, m_rows, width, ctx->vocab, softcap, logits, s);
+  launch_lmhead((const uint16_t*)hidden, (const uint16_t*)weight, m_rows, width, ctx->vocab, softcap, logits, s,
+                stage_events(ctx, slot, GS_STAGE_LMHEAD));
   GS_HIP(ctx, hipGetLastError());
-  stage_mark(ctx, slot, GS_STAGE_LMHEAD, 1, s);
   return GS_OK;
 }
 

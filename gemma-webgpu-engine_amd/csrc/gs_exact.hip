@@ -320,7 +320,7 @@ __device__ void process_row(const SampleArgs& a, Lds& L, Scratch S, int64_t row)
       const uint32_t pos = i < n ? S.order[i] : 0;
       const uint32_t keep = (i < n && S.prob[pos] >= floor_p) ? 1u : 0u;
       const int lane = tid & 63, wave = tid >> 6;
-      const uint32_t incl = wave_scan_u32(keep, lane);
+      const uint32_t incl = wave_scan_u32(keep);
       if (lane == 63) L.wtmp_u[wave] = incl;
       __syncthreads();
       uint32_t off = 0, tot = 0;
@@ -489,8 +489,8 @@ __global__ __launch_bounds__(kExactThreads) void exact_kernel(SampleArgs a) {
 
 }  // namespace
 
-void launch_exact(const SampleArgs& a, hipStream_t s) {
-  hipLaunchKernelGGL(exact_kernel, dim3(a.exact_slots), dim3(kExactThreads), 0, s, a);
+void launch_exact(const SampleArgs& a, hipStream_t s, LaunchEvents ev) {
+  hipExtLaunchKernelGGL(exact_kernel, dim3(a.exact_slots), dim3(kExactThreads), 0, s, ev.start, ev.stop, 0, a);
 }
 
 }  // namespace gs

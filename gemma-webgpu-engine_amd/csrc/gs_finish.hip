@@ -41,10 +41,12 @@ constexpr int kSubThreads = 8;                        // threads that read one w
 constexpr int kSubPerThread = kSubCap / kSubThreads;  // slots each of them reads
 constexpr int kSlotsPerThread = kHashSize / kFinishThreads;
 constexpr int kIdsPerThread = 2;                      // window ids loaded ahead per thread
+constexpr int kSpecQ = 2;  // list slots per thread read with the statistics (16 per sub-list)
+static_assert(kFinishMaxChunks * kScanWaves <= kFinishThreads, "one thread per chunk wave");
 
 __device__ __forceinline__ double block_scan_f64(double v, double* s_w, double* total) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const double incl = wave_scan_f64(v, lane);
+  const double incl = wave_scan_f64(v);
   if (lane == 63) s_w[wave] = incl;
   __syncthreads();
   double off = 0.0, tot = 0.0;
@@ -56,6 +58,20 @@ __device__ __forceinline__ double block_scan_f64(double v, double* s_w, double* 
   __syncthreads();
   *total = tot;
   return incl + off;
+}
+
+// Block-wide sums of two binary64 values in every thread, in a fixed order
+// (per wave, then the waves in order); s_w holds 2 * kWaves values and is
+// used once per kernel, so no barrier follows the reads.
+__device__ __forceinline__ void block_sum2_f64(double x, double y, double* s_w, double* tx, double* ty) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  x = wave_sum_f64_dpp(x);
+  y = wave_sum_f64_dpp(y);
+  if (lane == 0) { s_w[wave] = x; s_w[kWaves + wave] = y; }
+  __syncthreads();
+  // lane l < kWaves holds wave l's totals; the same DPP reduction then sums them
+  *tx = wave_sum_f64_dpp(lane < kWaves ? s_w[lane] : 0.0);
+  *ty = wave_sum_f64_dpp(lane < kWaves ? s_w[kWaves + lane] : 0.0);
 }
 
 // (value key desc, id asc) on parallel arrays
@@ -234,7 +250,7 @@ __device__ void top_r(const uint64_t* s, int n, uint64_t* tmp, uint64_t* top) {
 // the kTopR-th largest key: every entry of a higher bin outranks it, so the
 // entries of that bin and above (the survivors) hold the top kTopR. A crowded
 // boundary bin gets a second histogram inside it. When at most 128 entries
-// survive, one wave sorts them in registers. Returns false, with top
+// survive, each finds its place by counting the survivors above it. Returns false, with top
 // untouched, when more survive (massive ties); the caller then ranks the
 // whole region. hist: 256 counters, zero on entry and on return; sel: 4
 // words; out: 128 entries of scratch. Ends with a barrier.
@@ -288,7 +304,7 @@ __device__ bool top_select(const uint64_t* s, int n, uint32_t lo, uint32_t hi, u
         uint32_t h[4], c = 0;
 #pragma unroll
         for (int q = 0; q < 4; ++q) { h[q] = hist[255 - 4 * lane - q]; c += h[q]; }
-        const uint32_t incl = wave_scan_u32(c, lane);
+        const uint32_t incl = wave_scan_u32(c);
         const uint64_t hit = __ballot(above + incl >= (uint32_t)kTopR);
         const int first = hit ? __ffsll((unsigned long long)hit) - 1 : 63;
         if (lane == first) {
@@ -325,7 +341,7 @@ __device__ bool top_select(const uint64_t* s, int n, uint32_t lo, uint32_t hi, u
       const uint64_t m = __ballot(keep);
       uint32_t base = 0;
       if (lane == 0 && m) base = atomicAdd(&sel[3], (uint32_t)__popcll(m));
-      base = (uint32_t)__shfl((int)base, 0, 64);
+      base = readlane_u32(base, 0);
       if (keep) {
         const uint32_t pos =
             base + __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
@@ -336,19 +352,26 @@ __device__ bool top_select(const uint64_t* s, int n, uint32_t lo, uint32_t hi, u
     src = out;
     n_src = (int)(sel[3] < (uint32_t)kOut ? sel[3] : (uint32_t)kOut);
   }
-  if (wave == 0) {
-    uint64_t v[2];
-#pragma unroll
-    for (int q = 0; q < 2; ++q) {
-      const int i = lane * 2 + q;
-      v[q] = i < n_src ? src[i] : 0ull;
+  // rank the survivors by counting: the entries are distinct, so survivor i's
+  // place is the number of survivors above it; places past the survivors
+  // stay zero
+  if (tid < n_src) {
+    const uint64_t e = src[tid];
+    int rank = 0;
+    // two entries per 16-byte read (src is 16-byte aligned and holds at least
+    // n_src + 1 entries); a read never waits on the previous one
+    const uint4* p = (const uint4*)src;
+    const int n_pair = (n_src + 1) >> 1;
+#pragma unroll 8
+    for (int j = 0; j < n_pair; ++j) {
+      const uint4 w = p[j];
+      const uint64_t x0 = ((uint64_t)w.y << 32) | w.x, x1 = ((uint64_t)w.w << 32) | w.z;
+      rank += x0 > e ? 1 : 0;
+      rank += (2 * j + 1 < n_src && x1 > e) ? 1 : 0;
     }
-    wave_sort_desc_regs<2>(v);
-#pragma unroll
-    for (int q = 0; q < 2; ++q) {
-      const int i = lane * 2 + q;
-      if (i < kTopR) top[i] = v[q];
-    }
+    if (rank < kTopR) top[rank] = e;
+  } else if (tid < kTopR) {
+    top[tid] = 0;
   }
   __syncthreads();
   return true;
@@ -386,14 +409,13 @@ struct Shared {
   uint32_t sp_id[kSpecialCap];
   double cand_p[kFinishCap];          // merged candidates: e^(value - M) (sort scratch before)
   uint32_t cand_id[kFinishCap];
-  double c_sum[kFinishMaxChunks];     // chunk statistics
-  uint32_t c_max[kFinishMaxChunks];
-  uint16_t c_nsub[kFinishMaxChunks * kScanWaves];
+  uint16_t c_nsub[kFinishMaxChunks * kScanWaves];  // sub-list lengths
   uint64_t top[kTopR];                // the fast path's ranked non-specials
   uint32_t hist[256];                 // top_select's histogram (zero between uses)
   uint32_t sel[4];
   double wsum[kWaves];
   double wtmp[kWaves];
+  double wsum2[2 * kWaves];
   double total;
   double total_sp;                    // the specials' part of total
   uint64_t sp_max;
@@ -459,7 +481,7 @@ __device__ int filters_and_draw_wave(const SampleArgs& a, int64_t row, const gs_
   }
   // ---- min-p (sampling.ts:45-48)
   if (cfg.min_p > 0) {
-    const double floor_p = __shfl(pl[0], 0, 64) * cfg.min_p;
+    const double floor_p = readlane_f64(pl[0], 0) * cfg.min_p;
     int first = 0x7FFFFFFF;
     bool bad = false;
 #pragma unroll
@@ -476,10 +498,7 @@ __device__ int filters_and_draw_wave(const SampleArgs& a, int64_t row, const gs_
     if (lane * kPerLane + 1 < n && pl[1] > pl[0]) bad = true;
     if (lane * kPerLane + 2 < n && next > pl[1]) bad = true;
     if (__ballot(bad)) exact_why |= 2u;
-    for (int m = 32; m > 0; m >>= 1) {
-      const int o = __shfl_xor(first, m, 64);
-      first = o < first ? o : first;
-    }
+    first = (int)wave_min_u32((uint32_t)first);
     if (first != 0x7FFFFFFF) {
       n = first;
       n_complete = true;
@@ -498,7 +517,7 @@ __device__ int filters_and_draw_wave(const SampleArgs& a, int64_t row, const gs_
       s += lane * kPerLane + q < n ? pl[q] : 0.0;
       pre[q] = s;
     }
-    const double incl = wave_scan_f64(s, lane);
+    const double incl = wave_scan_f64(s);
 #pragma unroll
     for (int q = 0; q < kPerLane; ++q) pre[q] += incl - s;
   }
@@ -516,10 +535,7 @@ __device__ int filters_and_draw_wave(const SampleArgs& a, int64_t row, const gs_
         if (d < margin) near = true;
       }
     }
-    for (int m = 32; m > 0; m >>= 1) {
-      const int o = __shfl_xor(cut, m, 64);
-      cut = o < cut ? o : cut;
-    }
+    cut = (int)wave_min_u32((uint32_t)cut);
     if (__ballot(near)) {
       // only the normaliser's own error can have put the cut there: settle it
       // with the recomputed normaliser unless another check already failed
@@ -532,8 +548,8 @@ __device__ int filters_and_draw_wave(const SampleArgs& a, int64_t row, const gs_
     } else {
       // 1e-6 boundary ties, as the reference comparison plan reports them
       const int cl = cut / kPerLane, cq = cut % kPerLane;
-      const double cum = __shfl(cq == 0 ? pre[0] : pre[1], cl, 64);
-      const double pc = __shfl(cq == 0 ? pl[0] : pl[1], cl, 64);
+      const double cum = readlane_f64(cq == 0 ? pre[0] : pre[1], cl);
+      const double pc = readlane_f64(cq == 0 ? pl[0] : pl[1], cl);
       const double prev = cum - pc;
       if (cum - cfg.top_p <= kTieReport * cfg.top_p || (cut > 0 && cfg.top_p - prev <= kTieReport * cfg.top_p)) {
         tie = GS_FLAG_TOPP_TIE;
@@ -545,7 +561,7 @@ __device__ int filters_and_draw_wave(const SampleArgs& a, int64_t row, const gs_
   }
   // ---- draw (sampling.ts:58-64): first i with prefix_i >= u * sum_{j<n} p_j
   const int last_lane = (n - 1) / kPerLane, last_q = (n - 1) % kPerLane;
-  const double ctotal = __shfl(last_q == 0 ? pre[0] : pre[1], last_lane, 64);
+  const double ctotal = readlane_f64(last_q == 0 ? pre[0] : pre[1], last_lane);
   const double u = cfg.rng_mode == GS_RNG_EXPLICIT ? cfg.uniform : gsm::mulberry32_draw(cfg.seed, cfg.draw_index);
   const double cursor = u * ctotal;
   int pick = 0x7FFFFFFF;
@@ -559,10 +575,7 @@ __device__ int filters_and_draw_wave(const SampleArgs& a, int64_t row, const gs_
       if (d < kNearTie * ctotal) near = true;
     }
   }
-  for (int m = 32; m > 0; m >>= 1) {
-    const int o = __shfl_xor(pick, m, 64);
-    pick = o < pick ? o : pick;
-  }
+  pick = (int)wave_min_u32((uint32_t)pick);
   if (__ballot(near)) exact_why |= 8u;
   if (lane == 0) {
     if (exact_why || pick == 0x7FFFFFFF) {
@@ -613,6 +626,35 @@ __global__ __launch_bounds__(kFinishThreads) void finish_kernel(SampleArgs a) {
   __shared__ Shared S;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int64_t row = blockIdx.x;
+  // ---- first batch of global loads, all issued before the row's
+  // configuration arrives: the per-wave chunk statistics (thread t holds
+  // chunk t / kScanWaves, wave t % kScanWaves), the first kSpecQ slots of
+  // every sub-list, the history and forced-id offsets. The list slots are
+  // read before the sub-lists' lengths are known: they lie inside the row's
+  // list buffer, and entries past a sub-list's length are dropped once it is.
+  const int n_wstats = a.n_chunks * kScanWaves;  // <= kFinishThreads
+  double w_sum = 0.0;
+  uint32_t w_max = 0, w_flags = 0, w_nsub = 0, w_thr = 0, w_trunc = 0;
+  if (tid < n_wstats) {
+    const ChunkStat* c = a.stats + row * a.n_chunks + tid / kScanWaves;
+    const int w = tid % kScanWaves;
+    w_sum = c->wsum[w];
+    w_max = c->wmax[w];
+    w_flags = c->wflags[w];
+    w_nsub = c->n_sub[w];
+    w_thr = c->threshold;
+    w_trunc = c->truncated;
+  }
+  const uint64_t* lists = a.lists + row * a.n_chunks * kGatherCap;
+  const int n_subs = a.n_chunks * kScanWaves;
+  const int sl0 = tid / kSubThreads, k0 = tid % kSubThreads;
+  uint64_t lv[kSubPerThread];
+#pragma unroll
+  for (int q = 0; q < kSpecQ; ++q) lv[q] = sl0 < n_subs ? lists[(int64_t)sl0 * kSubCap + k0 + q * kSubThreads] : 0ull;
+  int64_t h0 = 0, h1 = 0, f0 = 0, f1 = 0;
+  if (a.history_offsets) { h0 = a.history_offsets[row]; h1 = a.history_offsets[row + 1]; }
+  if (a.forced_offsets) { f0 = a.forced_offsets[row]; f1 = a.forced_offsets[row + 1]; }
+
   const gs_row_config cfg = a.configs[row];
   const Plan plan = plan_row(cfg);
   if (plan.route == kRouteExact) {
@@ -623,21 +665,21 @@ __global__ __launch_bounds__(kFinishThreads) void finish_kernel(SampleArgs a) {
   const int32_t slot = cfg.mask_slot;
   const bool constrained = slot >= 0 && slot < a.mask_slots;
   const double T = cfg.temperature;
+  if (!constrained) f0 = f1 = 0;  // forced ids belong to constrained rows only
 
-  // ---- first batch of global loads: chunk statistics, window and forced ids
-  const ChunkStat* st = a.stats + row * a.n_chunks;
-  ChunkStat cs{};
-  if (tid < a.n_chunks) cs = st[tid];
-  int64_t w0, w1;
-  history_window(a, row, cfg, &w0, &w1);
+  // the penalty window (sampling.ts:22-24)
+  int64_t w0 = 0, w1 = 0;
+  if (a.history_offsets && cfg.repetition_window > 0) {
+    const int64_t s0 = h1 - (int64_t)cfg.repetition_window;
+    w0 = s0 > h0 ? s0 : h0;
+    w1 = h1;
+  }
   int32_t wid[kIdsPerThread];
 #pragma unroll
   for (int r = 0; r < kIdsPerThread; ++r) {
     const int64_t j = w0 + tid + (int64_t)r * kFinishThreads;
     wid[r] = j < w1 ? a.history_ids[j] : -1;
   }
-  int64_t f0 = 0, f1 = 0;
-  if (constrained && a.forced_offsets) { f0 = a.forced_offsets[row]; f1 = a.forced_offsets[row + 1]; }
   // specials this thread owns the loads of: its window positions and its
   // first forced id; rows with longer lists evaluate from the hash slots
   const bool own_path = w1 - w0 <= (int64_t)kIdsPerThread * kFinishThreads && f1 - f0 <= kFinishThreads;
@@ -662,36 +704,23 @@ __global__ __launch_bounds__(kFinishThreads) void finish_kernel(SampleArgs a) {
   if (tid < 256) S.hist[tid] = 0;
   __syncthreads();
 
-  // ---- 1. statistics into LDS, distinct special ids into the hash
-  if (tid < a.n_chunks) {
-    // the chunk's maximum and its sum, from its waves' (each rescaled from its
-    // wave maximum to the chunk's by the bit-exact exp)
-    uint32_t cmax = 0, cflags = 0;
-    for (int w = 0; w < kScanWaves; ++w) {
-      cmax = cs.wmax[w] > cmax ? cs.wmax[w] : cmax;
-      cflags |= cs.wflags[w];
+  // ---- 1. statistics: sub-list lengths into LDS; the flags, the maximum and
+  // the truncation threshold reduced per wave (one LDS atomic each)
+  if (tid < n_wstats) S.c_nsub[tid] = (uint16_t)(w_nsub > (uint32_t)kSubCap ? (uint32_t)kSubCap : w_nsub);
+  {
+    // a sub-list length above kSubCap: the sub-list overflowed
+    const uint32_t fl = wave_or_u32(w_flags | (w_nsub > (uint32_t)kSubCap ? kChunkOverflow : 0u));
+    const uint32_t mk = wave_max_u32(w_max);
+    const uint32_t th = wave_max_u32(w_trunc ? w_thr : 0u);
+    const bool tr = __ballot(w_trunc != 0) != 0;
+    if (lane == 0) {
+      if (fl) atomicOr(&S.flags, fl);
+      if (mk) atomicMax(&S.max_key, mk);
+      if (tr) { atomicMax(&S.thr_max, th); atomicOr(&S.any_truncated, 1u); }
     }
-    double csum = 0.0;
-    if (!greedy && cmax > kKeyNegInf) {
-      for (int w = 0; w < kScanWaves; ++w) {
-        if (cs.wsum[w] > 0.0 && cs.wmax[w] > kKeyNegInf)
-          csum += cs.wsum[w] * gsm::js_exp(((double)key_f32(cs.wmax[w]) - (double)key_f32(cmax)) / T);
-      }
-    }
-    S.c_sum[tid] = csum;
-    S.c_max[tid] = cmax;
-    uint32_t overflow = 0;
-    for (int w = 0; w < kScanWaves; ++w) {
-      const uint32_t n = cs.n_sub[w];  // above kSubCap: the sub-list overflowed
-      overflow |= n > (uint32_t)kSubCap;
-      S.c_nsub[tid * kScanWaves + w] = n > (uint32_t)kSubCap ? (uint32_t)kSubCap : n;
-    }
-    atomicOr(&S.flags, cflags | (overflow ? kChunkOverflow : 0u));
-    atomicMax(&S.max_key, cmax);
-    if (cs.truncated) { atomicMax(&S.thr_max, cs.threshold); atomicOr(&S.any_truncated, 1u); }
   }
-  // the owned specials' logits and mask words start loading now, so they
-  // arrive while the hash is built
+  // the owned specials' logits and mask words start loading now; they are
+  // first used after the region is ranked
   float oraw[kOwn];
   uint32_t omw[kOwn];
   int oslot[kOwn];
@@ -702,6 +731,7 @@ __global__ __launch_bounds__(kFinishThreads) void finish_kernel(SampleArgs a) {
     oraw[r] = ok ? load_logit(a, row, oid[r]) : 0.0f;
     omw[r] = ok && constrained ? a.mask_table[(int64_t)slot * a.mask_words + (oid[r] >> 5)] : 0u;
   }
+  // distinct special ids into the hash
   {
     SpecialTable tab{S.hash_ids, S.hash_counts};
 #pragma unroll
@@ -729,13 +759,11 @@ __global__ __launch_bounds__(kFinishThreads) void finish_kernel(SampleArgs a) {
     return;
   }
 
-  // ---- second batch of global loads: the specials' logits and mask words and
-  // every list entry, all in flight together
+  // ---- second batch of global loads: the hash-slot specials' logits and
+  // mask words (rows whose specials are not owned) and the list slots past
+  // the first kSpecQ
   const uint32_t thr = S.thr_max;  // 0 when no chunk was truncated: every finite logit is listed
-  const uint64_t* lists = a.lists + row * a.n_chunks * kGatherCap;
-  const int n_subs = a.n_chunks * kScanWaves;
   // the specials to evaluate: each owner's (own_path), else every hash slot
-  // with its logit and mask word loaded now
   constexpr int kEval = kSlotsPerThread > kOwn ? kSlotsPerThread : kOwn;
   uint32_t hid[kEval], hpk[kEval], mw[kEval];
   float raw[kEval];
@@ -745,8 +773,8 @@ __global__ __launch_bounds__(kFinishThreads) void finish_kernel(SampleArgs a) {
       const bool mine = r < kOwn && ofirst[r];
       hid[r] = mine ? (uint32_t)oid[r] : 0xFFFFFFFFu;
       hpk[r] = mine ? S.hash_counts[oslot[r]] : 0u;
-      raw[r] = mine ? oraw[r] : 0.0f;
-      mw[r] = mine ? omw[r] : 0u;
+      raw[r] = 0.0f;  // the owned loads are read where the special is evaluated
+      mw[r] = 0u;
     }
   } else {
 #pragma unroll
@@ -761,16 +789,64 @@ __global__ __launch_bounds__(kFinishThreads) void finish_kernel(SampleArgs a) {
       mw[r] = used && constrained ? a.mask_table[(int64_t)slot * a.mask_words + (hid[r] >> 5)] : 0u;
     }
   }
-  // list entries of the first kFinishThreads / kSubThreads sub-lists (every
-  // sub-list up to 32 chunks, V <= 262144); wider rows loop below
-  uint64_t lv[kSubPerThread];
-  const int sl0 = tid / kSubThreads, k0 = tid % kSubThreads;
-  const int cnt0 = (!greedy && sl0 < n_subs) ? (int)S.c_nsub[sl0] : 0;
+
+  // ---- the complete region: listed entries with key >= thr, appended with
+  // one LDS atomic per wave
+  const uint32_t sel_lo = thr > kKeyNegInf ? thr : kKeyNegInf + 1u;
+  const uint32_t sel_hi = S.max_key > sel_lo ? S.max_key : sel_lo;
+  auto append = [&](const uint64_t (&v)[kSubPerThread], int cnt) {
+    uint64_t e[kSubPerThread];
+    uint32_t keep = 0;
 #pragma unroll
-  for (int q = 0; q < kSubPerThread; ++q) {
-    const int k = k0 + q * kSubThreads;
-    lv[q] = k < cnt0 ? lists[(int64_t)sl0 * kSubCap + k] : 0ull;
+    for (int q = 0; q < kSubPerThread; ++q) {
+      e[q] = 0;
+      if (k0 + q * kSubThreads < cnt) {
+        e[q] = list_rank(v[q]);
+        if (entry_key(e[q]) >= thr) keep |= 1u << q;
+      }
+    }
+    const uint32_t mine = (uint32_t)__popc(keep);
+    const uint32_t incl = wave_scan_u32(mine);
+    uint32_t base = 0;
+    if (lane == 63) base = atomicAdd(&S.n_sorted, incl);
+    base = readlane_u32(base, 63);
+    uint32_t pos = base + incl - mine;
+#pragma unroll
+    for (int q = 0; q < kSubPerThread; ++q) {
+      if ((keep >> q) & 1u) {
+        if (pos < (uint32_t)kFinishCap) S.sorted[pos] = e[q];
+        ++pos;
+      }
+    }
+  };
+  if (!greedy) {
+    const int cnt0 = sl0 < n_subs ? (int)S.c_nsub[sl0] : 0;
+#pragma unroll
+    for (int q = kSpecQ; q < kSubPerThread; ++q) {
+      const int k = k0 + q * kSubThreads;
+      lv[q] = k < cnt0 ? lists[(int64_t)sl0 * kSubCap + k] : 0ull;
+    }
+    append(lv, cnt0);
+    // sub-lists past the first kFinishThreads / kSubThreads (more than 32 chunks)
+    for (int s0 = kFinishThreads / kSubThreads; s0 < n_subs; s0 += kFinishThreads / kSubThreads) {
+      const int sl = s0 + tid / kSubThreads;
+      const int cnt = sl < n_subs ? (int)S.c_nsub[sl] : 0;
+      uint64_t v[kSubPerThread];
+#pragma unroll
+      for (int q = 0; q < kSubPerThread; ++q) {
+        const int k = k0 + q * kSubThreads;
+        v[q] = k < cnt ? lists[(int64_t)sl * kSubCap + k] : 0ull;
+      }
+      append(v, cnt);
+    }
   }
+  __syncthreads();
+  const int n_region = (int)S.n_sorted;
+  // the region's top kTopR non-specials, ranked while the specials' loads are
+  // still in flight (false: too many ties, the fast path merges instead)
+  bool top_ok = false;
+  if (!greedy && n_region <= kFinishCap)
+    top_ok = top_select(S.sorted, n_region, sel_lo, sel_hi, S.hist, S.sel, (uint64_t*)S.cand_p, S.top, false);
 
   // evaluate every special exactly: mask / termination rules, then penalties.
   // Slots, flags and the maximum are gathered per wave, one LDS atomic each.
@@ -785,19 +861,24 @@ __global__ __launch_bounds__(kFinishThreads) void finish_kernel(SampleArgs a) {
       if (m == 0) continue;
       uint32_t base = 0;
       if (lane == 0) base = atomicAdd(&S.n_special, (uint32_t)__popcll(m));
-      base = (uint32_t)__shfl((int)base, 0, 64);
+      base = readlane_u32(base, 0);
       if (!used) continue;
       const uint32_t idx =
           base + __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
       if (idx >= (uint32_t)kSpecialCap) continue;
       const uint32_t count = hpk[r] & 0xFFFFFFu, kinds = hpk[r] >> 24;
       float x32 = raw[r];
+      uint32_t mword = mw[r];
+      if (own_path && r < kOwn) {
+        x32 = oraw[r < kOwn ? r : 0];
+        mword = omw[r < kOwn ? r : 0];
+      }
       if (cfg.softcap > 0) x32 = gsm::softcap_f32(x32, cfg.softcap);
       bool allowed = true;
       if (constrained) {
         const bool term = kinds & GS_FORCED_TERMINATION;
         const bool extra = kinds & GS_FORCED_EXTRA;
-        allowed = term ? cfg.accepting != 0 : (extra || ((mw[r] >> (id & 31)) & 1u));
+        allowed = term ? cfg.accepting != 0 : (extra || ((mword >> (id & 31)) & 1u));
       }
       my_legal |= allowed;
       my_nonfinite |= allowed && !(x32 < __builtin_inff());
@@ -813,58 +894,11 @@ __global__ __launch_bounds__(kFinishThreads) void finish_kernel(SampleArgs a) {
       my_max = key > my_max ? key : my_max;
     }
     const uint64_t legal_w = __ballot(my_legal), bad_w = __ballot(my_nonfinite);
-    for (int m = 32; m > 0; m >>= 1) {
-      const uint64_t o = shfl_xor_u64(my_max, m);
-      my_max = o > my_max ? o : my_max;
-    }
+    my_max = wave_max_u64(my_max);
     if (lane == 0) {
       if (legal_w) atomicOr(&S.special_legal, 1u);
       if (bad_w) atomicOr(&S.flags, kChunkNonFinite);
       if (my_max) atomicMax((unsigned long long*)&S.sp_max, (unsigned long long)my_max);
-    }
-  }
-
-  // the complete region: listed entries with key >= thr, appended with one
-  // LDS atomic per wave
-  const uint32_t sel_lo = thr > kKeyNegInf ? thr : kKeyNegInf + 1u;
-  const uint32_t sel_hi = S.max_key > sel_lo ? S.max_key : sel_lo;
-  auto append = [&](const uint64_t (&v)[kSubPerThread], int cnt) {
-    uint64_t e[kSubPerThread];
-    uint32_t keep = 0;
-#pragma unroll
-    for (int q = 0; q < kSubPerThread; ++q) {
-      e[q] = 0;
-      if (k0 + q * kSubThreads < cnt) {
-        e[q] = list_rank(v[q]);
-        if (entry_key(e[q]) >= thr) keep |= 1u << q;
-      }
-    }
-    const uint32_t mine = (uint32_t)__popc(keep);
-    const uint32_t incl = wave_scan_u32(mine, lane);
-    uint32_t base = 0;
-    if (lane == 63) base = atomicAdd(&S.n_sorted, incl);
-    base = (uint32_t)__shfl((int)base, 63, 64);
-    uint32_t pos = base + incl - mine;
-#pragma unroll
-    for (int q = 0; q < kSubPerThread; ++q) {
-      if ((keep >> q) & 1u) {
-        if (pos < (uint32_t)kFinishCap) S.sorted[pos] = e[q];
-        ++pos;
-      }
-    }
-  };
-  if (!greedy) {
-    append(lv, cnt0);
-    for (int s0 = kFinishThreads / kSubThreads; s0 < n_subs; s0 += kFinishThreads / kSubThreads) {
-      const int sl = s0 + tid / kSubThreads;
-      const int cnt = sl < n_subs ? (int)S.c_nsub[sl] : 0;
-      uint64_t v[kSubPerThread];
-#pragma unroll
-      for (int q = 0; q < kSubPerThread; ++q) {
-        const int k = k0 + q * kSubThreads;
-        v[q] = k < cnt ? lists[(int64_t)sl * kSubCap + k] : 0ull;
-      }
-      append(v, cnt);
     }
   }
   __syncthreads();
@@ -937,11 +971,11 @@ __global__ __launch_bounds__(kFinishThreads) void finish_kernel(SampleArgs a) {
     return;
   }
 
-  if (S.n_sorted > (uint32_t)kFinishCap) {
+  if (n_region > kFinishCap) {
     if (tid == 0) enqueue_exact(a, row, 0u);
     return;
   }
-  const int n_ns = (int)S.n_sorted;
+  const int n_ns = n_region;
 
   // ---- the maximum value M = scaled[0].logit (sampling.ts:36): the best
   // finite non-special logit / T, or the best special value
@@ -967,21 +1001,19 @@ __global__ __launch_bounds__(kFinishThreads) void finish_kernel(SampleArgs a) {
   double margin = kScanSumRel + ref_round;
   bool refined = false;
 
-  // ---- normaliser: chunk partial sums rescaled to M, plus every special
+  // ---- normaliser: the scan's per-wave partial sums rescaled from their wave
+  // maximum to M (the rescale argument computed as the reference computes
+  // l/T - M for that logit), plus every special (threads from the top down,
+  // so that they are not the ones holding wave sums)
+  double t_chunks, t_sp;
   {
     double part = 0.0, spart = 0.0;
-    for (int c = tid; c < a.n_chunks; c += kFinishThreads) {
-      const double csum = S.c_sum[c];
-      const uint32_t cmax = S.c_max[c];
-      if (cmax > kKeyNegInf && csum > 0) part += csum * gsm::js_exp((double)key_f32(cmax) / T - M);
-    }
-    for (int i = tid; i < n_sp; i += kFinishThreads) spart += gsm::js_exp(key_f64(S.sp_key[i]) - M);
-    double t_chunks, t_sp;
-    block_scan_f64(part, S.wsum, &t_chunks);
-    block_scan_f64(spart, S.wsum, &t_sp);
+    if (w_sum > 0.0 && w_max > kKeyNegInf) part = w_sum * gsm::js_exp((double)key_f32(w_max) / T - M);
+    for (int i = kFinishThreads - 1 - tid; i < n_sp; i += kFinishThreads) spart += gsm::js_exp(key_f64(S.sp_key[i]) - M);
+    block_sum2_f64(part, spart, S.wsum2, &t_chunks, &t_sp);
     if (tid == 0) { S.total = t_chunks + t_sp; S.total_sp = t_sp; }
   }
-  if (!(S.total < __builtin_inf())) {
+  if (!(t_chunks + t_sp < __builtin_inf())) {
     // an exponent argument beyond the double range (|l/T| near 1e18 or more)
     if (tid == 0) enqueue_exact(a, row, 0u);
     return;
@@ -1030,7 +1062,7 @@ __global__ __launch_bounds__(kFinishThreads) void finish_kernel(SampleArgs a) {
   const int n_top_all = n_ns < kTopR ? n_ns : kTopR;
   if (n_sp_in <= 2 * kTopR - n_top_all) {
     uint64_t* tmp = (uint64_t*)S.cand_p;  // kWaves * 64 entries of merge scratch
-    if (!top_select(S.sorted, n_ns, sel_lo, sel_hi, S.hist, S.sel, tmp, S.top, false)) {
+    if (!top_ok) {
       if (n_ns <= kWaves * 64) top_r<1>(S.sorted, n_ns, tmp, S.top);
       else if (n_ns <= kWaves * 128) top_r<2>(S.sorted, n_ns, tmp, S.top);
       else top_r<4>(S.sorted, n_ns, tmp, S.top);
@@ -1077,8 +1109,14 @@ __global__ __launch_bounds__(kFinishThreads) void finish_kernel(SampleArgs a) {
         for (int j = lane; j < n_sp_use; j += 64) {
           if (!ranks_before(in_key[j], in_id[j], lk, entry_id(e))) ++after;
         }
-        for (int m = 32; m > 0; m >>= 1) after += __shfl_xor(after, m, 64);
+        after = (int)wave_sum_u32((uint32_t)after);
         n_valid -= after;
+      }
+      // a top-k cut inside the candidates is the list's own (sampling.ts:44):
+      // only the first topK exponentials are needed
+      if (cfg.top_k > 0 && cfg.top_k < n_valid) {
+        n_valid = cfg.top_k;
+        complete = true;
       }
       __builtin_amdgcn_wave_barrier();
       for (int i = lane; i < n_valid; i += 64) fp[i] = gsm::js_exp(fp[i] - M);
@@ -1267,8 +1305,8 @@ __global__ __launch_bounds__(kFinishThreads) void finish_kernel(SampleArgs a) {
 
 }  // namespace
 
-void launch_finish(const SampleArgs& a, hipStream_t s) {
-  hipLaunchKernelGGL(finish_kernel, dim3(a.rows), dim3(kFinishThreads), 0, s, a);
+void launch_finish(const SampleArgs& a, hipStream_t s, LaunchEvents ev) {
+  hipExtLaunchKernelGGL(finish_kernel, dim3(a.rows), dim3(kFinishThreads), 0, s, ev.start, ev.stop, 0, a);
 }
 
 }  // namespace gs

@@ -1,6 +1,7 @@
 // Internal declarations shared by libgsample's kernels and host code.
 #pragma once
 
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -168,6 +169,134 @@ struct SampleArgs {
 };
 
 // --------------------------------------------------------- wave helpers
+// Workgroup barrier for LDS traffic only: LDS stores before it are visible to
+// every wave after it, and global loads in flight are not waited for.
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
+// Wave-wide reductions and scans with DPP row operations (quad_perm,
+// row_shr, row_ror and the gfx9 row_bcast15/31), which stay in the VALU:
+// their latency is a few cycles per step, where a cross-lane shuffle
+// (ds_bpermute) costs an LDS round trip. Same-address LDS atomics from many
+// lanes serialise (about 30 ns per lane), so values are reduced per wave first.
+constexpr int kDppQuad1032 = 0xB1;  // quad_perm [1,0,3,2]
+constexpr int kDppQuad2301 = 0x4E;  // quad_perm [2,3,0,1]
+constexpr int kDppRowShr1 = 0x111;
+constexpr int kDppRowShr2 = 0x112;
+constexpr int kDppRowShr4 = 0x114;
+constexpr int kDppRowShr8 = 0x118;
+constexpr int kDppRowRor4 = 0x124;
+constexpr int kDppRowRor8 = 0x128;
+constexpr int kDppRowBcast15 = 0x142;  // lane 15 of a row to the next row (rows 1 and 3 written)
+constexpr int kDppRowBcast31 = 0x143;  // lane 31 to rows 2 and 3
+
+// v moved by the DPP control kCtrl; lanes without a source (or in rows that
+// kRowMask disables) receive `identity`
+template <int kCtrl, int kRowMask>
+__device__ __forceinline__ uint32_t dpp_u32(uint32_t identity, uint32_t v) {
+  return (uint32_t)__builtin_amdgcn_update_dpp((int)identity, (int)v, kCtrl, kRowMask, 0xF, false);
+}
+template <int kCtrl, int kRowMask>
+__device__ __forceinline__ uint64_t dpp_u64(uint64_t identity, uint64_t v) {
+  const uint32_t lo = dpp_u32<kCtrl, kRowMask>((uint32_t)identity, (uint32_t)v);
+  const uint32_t hi = dpp_u32<kCtrl, kRowMask>((uint32_t)(identity >> 32), (uint32_t)(v >> 32));
+  return ((uint64_t)hi << 32) | lo;
+}
+__device__ __forceinline__ uint32_t readlane_u32(uint32_t v, int lane) {
+  return (uint32_t)__builtin_amdgcn_readlane((int)v, lane);
+}
+__device__ __forceinline__ uint64_t readlane_u64(uint64_t v, int lane) {
+  return ((uint64_t)readlane_u32((uint32_t)(v >> 32), lane) << 32) | readlane_u32((uint32_t)v, lane);
+}
+__device__ __forceinline__ double readlane_f64(double v, int lane) {
+  return __builtin_bit_cast(double, readlane_u64(__builtin_bit_cast(uint64_t, v), lane));
+}
+
+// All-reduce of the wave: within rows by quad_perm and row_ror, across rows
+// by the two broadcasts; lane 63 ends with the whole wave's result, which
+// every lane then reads. OP(a, b) combines, ID is its identity.
+#define GS_WAVE_REDUCE(T, DPP, v, ID, OP)                                          \
+  do {                                                                             \
+    v = OP(v, DPP<kDppQuad1032, 0xF>(ID, v));                                      \
+    v = OP(v, DPP<kDppQuad2301, 0xF>(ID, v));                                      \
+    v = OP(v, DPP<kDppRowRor4, 0xF>(ID, v));                                       \
+    v = OP(v, DPP<kDppRowRor8, 0xF>(ID, v));                                       \
+    v = OP(v, DPP<kDppRowBcast15, 0xA>(ID, v));                                    \
+    v = OP(v, DPP<kDppRowBcast31, 0xC>(ID, v));                                    \
+  } while (0)
+
+__device__ __forceinline__ uint32_t op_max_u32(uint32_t a, uint32_t b) { return a > b ? a : b; }
+__device__ __forceinline__ uint32_t op_min_u32(uint32_t a, uint32_t b) { return a < b ? a : b; }
+__device__ __forceinline__ uint32_t op_or_u32(uint32_t a, uint32_t b) { return a | b; }
+__device__ __forceinline__ uint32_t op_add_u32(uint32_t a, uint32_t b) { return a + b; }
+__device__ __forceinline__ uint64_t op_max_u64(uint64_t a, uint64_t b) { return a > b ? a : b; }
+
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
+  GS_WAVE_REDUCE(uint32_t, dpp_u32, v, 0u, op_max_u32);
+  return readlane_u32(v, 63);
+}
+__device__ __forceinline__ uint32_t wave_min_u32(uint32_t v) {
+  GS_WAVE_REDUCE(uint32_t, dpp_u32, v, 0xFFFFFFFFu, op_min_u32);
+  return readlane_u32(v, 63);
+}
+__device__ __forceinline__ uint32_t wave_or_u32(uint32_t v) {
+  GS_WAVE_REDUCE(uint32_t, dpp_u32, v, 0u, op_or_u32);
+  return readlane_u32(v, 63);
+}
+__device__ __forceinline__ uint32_t wave_sum_u32(uint32_t v) {
+  GS_WAVE_REDUCE(uint32_t, dpp_u32, v, 0u, op_add_u32);
+  return readlane_u32(v, 63);
+}
+__device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
+  GS_WAVE_REDUCE(uint64_t, dpp_u64, v, 0ull, op_max_u64);
+  return readlane_u64(v, 63);
+}
+// the maximum and minimum of the wave's values, in every lane
+__device__ __forceinline__ void wave_max_min_u32(uint32_t v, uint32_t* vmax, uint32_t* vmin) {
+  uint32_t a = v, b = v;
+  GS_WAVE_REDUCE(uint32_t, dpp_u32, a, 0u, op_max_u32);
+  GS_WAVE_REDUCE(uint32_t, dpp_u32, b, 0xFFFFFFFFu, op_min_u32);
+  *vmax = readlane_u32(a, 63);
+  *vmin = readlane_u32(b, 63);
+}
+// the sum of the wave's binary64 values (a fixed order), in every lane
+__device__ __forceinline__ double wave_sum_f64_dpp(double v) {
+  uint64_t u = __builtin_bit_cast(uint64_t, v);
+#define GS_SUM_STEP(C, M)                                                                \
+  {                                                                                      \
+    const double o = __builtin_bit_cast(double, dpp_u64<C, M>(0ull, u));                 \
+    u = __builtin_bit_cast(uint64_t, __builtin_bit_cast(double, u) + o);                 \
+  }
+  GS_SUM_STEP(kDppQuad1032, 0xF) GS_SUM_STEP(kDppQuad2301, 0xF) GS_SUM_STEP(kDppRowRor4, 0xF)
+  GS_SUM_STEP(kDppRowRor8, 0xF) GS_SUM_STEP(kDppRowBcast15, 0xA) GS_SUM_STEP(kDppRowBcast31, 0xC)
+#undef GS_SUM_STEP
+  return __builtin_bit_cast(double, readlane_u64(u, 63));
+}
+// Inclusive prefix sums across the wave: within each row of 16 lanes by
+// row_shr 1, 2, 4, 8 (lanes without a source add zero), then the last lane
+// of row 0 into rows 1 and 3 and the last lane of row 1 into rows 2 and 3.
+__device__ __forceinline__ uint32_t wave_scan_u32(uint32_t v) {
+  v += dpp_u32<kDppRowShr1, 0xF>(0u, v);
+  v += dpp_u32<kDppRowShr2, 0xF>(0u, v);
+  v += dpp_u32<kDppRowShr4, 0xF>(0u, v);
+  v += dpp_u32<kDppRowShr8, 0xF>(0u, v);
+  v += dpp_u32<kDppRowBcast15, 0xA>(0u, v);
+  v += dpp_u32<kDppRowBcast31, 0xC>(0u, v);
+  return v;
+}
+__device__ __forceinline__ double wave_scan_f64(double v) {
+#define GS_SCAN_STEP(C, M) \
+  v += __builtin_bit_cast(double, dpp_u64<C, M>(0ull, __builtin_bit_cast(uint64_t, v)));
+  GS_SCAN_STEP(kDppRowShr1, 0xF) GS_SCAN_STEP(kDppRowShr2, 0xF) GS_SCAN_STEP(kDppRowShr4, 0xF)
+  GS_SCAN_STEP(kDppRowShr8, 0xF) GS_SCAN_STEP(kDppRowBcast15, 0xA) GS_SCAN_STEP(kDppRowBcast31, 0xC)
+#undef GS_SCAN_STEP
+  return v;
+}
+
+// cross-lane shuffles for the bitonic networks (partner lane = lane ^ m)
 __device__ __forceinline__ uint32_t shfl_xor_u32(uint32_t v, int m) { return (uint32_t)__shfl_xor((int)v, m, 64); }
 __device__ __forceinline__ uint64_t shfl_xor_u64(uint64_t v, int m) {
   const uint32_t lo = shfl_xor_u32((uint32_t)v, m), hi = shfl_xor_u32((uint32_t)(v >> 32), m);
@@ -176,31 +305,9 @@ __device__ __forceinline__ uint64_t shfl_xor_u64(uint64_t v, int m) {
 __device__ __forceinline__ double shfl_xor_f64(double v, int m) {
   return __builtin_bit_cast(double, shfl_xor_u64(__builtin_bit_cast(uint64_t, v), m));
 }
-__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
-  for (int m = 32; m > 0; m >>= 1) { const uint32_t o = shfl_xor_u32(v, m); v = o > v ? o : v; }
-  return v;
-}
-__device__ __forceinline__ uint32_t wave_sum_u32(uint32_t v) {
-  for (int m = 32; m > 0; m >>= 1) v += shfl_xor_u32(v, m);
-  return v;
-}
+// butterfly sum of the wave's binary64 values, in every lane
 __device__ __forceinline__ double wave_sum_f64(double v) {
   for (int m = 32; m > 0; m >>= 1) v += shfl_xor_f64(v, m);
-  return v;
-}
-// inclusive prefix sum of u32 across the wave
-__device__ __forceinline__ uint32_t wave_scan_u32(uint32_t v, int lane) {
-  for (int d = 1; d < 64; d <<= 1) {
-    const uint32_t o = (uint32_t)__shfl_up((int)v, d, 64);
-    if (lane >= d) v += o;
-  }
-  return v;
-}
-__device__ __forceinline__ double wave_scan_f64(double v, int lane) {
-  for (int d = 1; d < 64; d <<= 1) {
-    const double o = __shfl_up(v, d, 64);
-    if (lane >= d) v += o;
-  }
   return v;
 }
 // bitonic sort of one u64 per lane, descending across the wave
@@ -266,10 +373,18 @@ __device__ __forceinline__ void special_insert(SpecialTable t, uint32_t id, uint
 }
 
 // ---------------------------------------------------- kernel launchers
-void launch_scan(const SampleArgs& a, hipStream_t s);
+// Optional timing events of one launch: hipExtLaunchKernel stamps `start`
+// when the dispatch begins and `stop` when its last wave ends, so their
+// elapsed time is the kernel alone (no event packets or launch gaps).
+struct LaunchEvents {
+  hipEvent_t start = nullptr;
+  hipEvent_t stop = nullptr;
+};
+
+void launch_scan(const SampleArgs& a, hipStream_t s, LaunchEvents ev = {});
 void launch_exp2_check(uint32_t first, uint32_t count, unsigned long long* worst, hipStream_t s);
-void launch_finish(const SampleArgs& a, hipStream_t s);
-void launch_exact(const SampleArgs& a, hipStream_t s);
+void launch_finish(const SampleArgs& a, hipStream_t s, LaunchEvents ev = {});
+void launch_exact(const SampleArgs& a, hipStream_t s, LaunchEvents ev = {});
 void launch_logprob(const void* logits, int32_t dtype, int32_t rows, int64_t stride, int32_t vocab,
                     const int32_t* tokens, double* out, hipStream_t s);
 void launch_mask_logits(const float* raw, int64_t n, const int32_t* ids, int64_t n_ids, float* out, hipStream_t s);
@@ -277,6 +392,6 @@ void launch_masks(const int64_t* offsets, const uint8_t* bytes, int32_t vocab, c
                   const int32_t* states, int32_t n, uint32_t* masks, int32_t mask_words, int32_t n_states,
                   hipStream_t s);
 void launch_lmhead(const uint16_t* hidden, const uint16_t* weight, int32_t m, int32_t width, int32_t vocab,
-                   float softcap, float* out, hipStream_t s);
+                   float softcap, float* out, hipStream_t s, LaunchEvents ev = {});
 
 }  // namespace gs

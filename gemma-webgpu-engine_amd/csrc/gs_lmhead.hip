@@ -128,9 +128,10 @@ __global__ __launch_bounds__(kLmThreads) void lmhead_kernel(const uint16_t* __re
 }  // namespace
 
 void launch_lmhead(const uint16_t* hidden, const uint16_t* weight, int32_t m, int32_t width, int32_t vocab,
-                   float softcap, float* out, hipStream_t s) {
+                   float softcap, float* out, hipStream_t s, LaunchEvents ev) {
   dim3 grid((vocab + kLmRows - 1) / kLmRows, (m + kLmM - 1) / kLmM);
-  hipLaunchKernelGGL(lmhead_kernel, grid, dim3(kLmThreads), 0, s, hidden, weight, m, width, vocab, softcap, out);
+  hipExtLaunchKernelGGL(lmhead_kernel, grid, dim3(kLmThreads), 0, s, ev.start, ev.stop, 0, hidden, weight, m, width,
+                        vocab, softcap, out);
 }
 
 }  // namespace gs

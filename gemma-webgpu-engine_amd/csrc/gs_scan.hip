@@ -103,57 +103,6 @@ __device__ __forceinline__ uint32_t wave_kth_key(uint32_t key, uint32_t d, uint3
   return t;
 }
 
-// Workgroup barrier for LDS traffic only: LDS stores before it are visible to
-// every wave after it, and global loads in flight are not waited for.
-__device__ __forceinline__ void lds_barrier() {
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
-  __builtin_amdgcn_s_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
-}
-
-// Wave-wide reductions with DPP row operations (quad_perm, row_ror and the
-// gfx9 row_bcast15/31), which stay in the VALU
-// instead of going through the LDS crossbar: their latency is a few cycles
-// per step, where a cross-lane shuffle costs an LDS round trip.
-constexpr int kDppQuad1032 = 0xB1;  // quad_perm [1,0,3,2]
-constexpr int kDppQuad2301 = 0x4E;  // quad_perm [2,3,0,1]
-constexpr int kDppRowRor4 = 0x124;
-constexpr int kDppRowRor8 = 0x128;
-constexpr int kDppRowBcast15 = 0x142;  // lane 15 of a row to the next row (rows 1 and 3 written)
-constexpr int kDppRowBcast31 = 0x143;  // lane 31 to rows 2 and 3
-
-template <int kCtrl, int kRowMask>
-__device__ __forceinline__ uint32_t dpp_u32(uint32_t identity, uint32_t v) {
-  return (uint32_t)__builtin_amdgcn_update_dpp((int)identity, (int)v, kCtrl, kRowMask, 0xF, false);
-}
-// the maximum and minimum of the wave's values, in every lane
-__device__ __forceinline__ void wave_max_min_u32(uint32_t v, uint32_t* vmax, uint32_t* vmin) {
-  uint32_t a = v, b = v;
-#define GS_MM_STEP(C, M)                                \
-  { const uint32_t x = dpp_u32<C, M>(0u, a);            \
-    const uint32_t y = dpp_u32<C, M>(0xFFFFFFFFu, b);   \
-    a = x > a ? x : a; b = y < b ? y : b; }
-  GS_MM_STEP(kDppQuad1032, 0xF) GS_MM_STEP(kDppQuad2301, 0xF) GS_MM_STEP(kDppRowRor4, 0xF)
-  GS_MM_STEP(kDppRowRor8, 0xF) GS_MM_STEP(kDppRowBcast15, 0xA) GS_MM_STEP(kDppRowBcast31, 0xC)
-#undef GS_MM_STEP
-  *vmax = (uint32_t)__builtin_amdgcn_readlane((int)a, 63);
-  *vmin = (uint32_t)__builtin_amdgcn_readlane((int)b, 63);
-}
-// the sum of the wave's binary64 values (a fixed order), in every lane
-__device__ __forceinline__ double wave_sum_f64_dpp(double v) {
-#define GS_SUM_STEP(C, M)                                                            \
-  { const uint64_t u = __builtin_bit_cast(uint64_t, v);                              \
-    const uint32_t lo = dpp_u32<C, M>(0u, (uint32_t)u);                              \
-    const uint32_t hi = dpp_u32<C, M>(0u, (uint32_t)(u >> 32));                      \
-    v += __builtin_bit_cast(double, ((uint64_t)hi << 32) | lo); }
-  GS_SUM_STEP(kDppQuad1032, 0xF) GS_SUM_STEP(kDppQuad2301, 0xF) GS_SUM_STEP(kDppRowRor4, 0xF)
-  GS_SUM_STEP(kDppRowRor8, 0xF) GS_SUM_STEP(kDppRowBcast15, 0xA) GS_SUM_STEP(kDppRowBcast31, 0xC)
-#undef GS_SUM_STEP
-  const uint64_t u = __builtin_bit_cast(uint64_t, v);
-  const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)u, 63);
-  const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(u >> 32), 63);
-  return __builtin_bit_cast(double, ((uint64_t)hi << 32) | lo);
-}
 // Per-wave results of a group's first chunk, exchanged through LDS.
 struct WaveSlots {
   uint32_t wbad[kScanWaves];
@@ -697,7 +646,7 @@ void launch_exp2_check(uint32_t first, uint32_t count, unsigned long long* worst
   hipLaunchKernelGGL(exp2_check_kernel, dim3((count + 255) / 256), dim3(256), 0, s, first, count, worst);
 }
 
-void launch_scan(const SampleArgs& a, hipStream_t s) {
+void launch_scan(const SampleArgs& a, hipStream_t s, LaunchEvents ev) {
   // group workgroups over the full chunks of 16-byte aligned rows: as many
   // per row as fills every CU once (kScanWgPerCu each), at least one per
   // kMaxGroupChunks chunks and at most one per chunk
@@ -712,11 +661,11 @@ void launch_scan(const SampleArgs& a, hipStream_t s) {
   dim3 grid(g.n_groups + (a.n_chunks - n_full), a.rows);
   const bool maskable = a.mask_slots > 0;
   if (a.dtype == GS_BF16) {
-    if (maskable) hipLaunchKernelGGL((scan_kernel<uint16_t, true>), grid, dim3(kScanThreads), 0, s, a, g);
-    else hipLaunchKernelGGL((scan_kernel<uint16_t, false>), grid, dim3(kScanThreads), 0, s, a, g);
+    if (maskable) hipExtLaunchKernelGGL((scan_kernel<uint16_t, true>), grid, dim3(kScanThreads), 0, s, ev.start, ev.stop, 0, a, g);
+    else hipExtLaunchKernelGGL((scan_kernel<uint16_t, false>), grid, dim3(kScanThreads), 0, s, ev.start, ev.stop, 0, a, g);
   } else {
-    if (maskable) hipLaunchKernelGGL((scan_kernel<float, true>), grid, dim3(kScanThreads), 0, s, a, g);
-    else hipLaunchKernelGGL((scan_kernel<float, false>), grid, dim3(kScanThreads), 0, s, a, g);
+    if (maskable) hipExtLaunchKernelGGL((scan_kernel<float, true>), grid, dim3(kScanThreads), 0, s, ev.start, ev.stop, 0, a, g);
+    else hipExtLaunchKernelGGL((scan_kernel<float, false>), grid, dim3(kScanThreads), 0, s, ev.start, ev.stop, 0, a, g);
   }
 }
 

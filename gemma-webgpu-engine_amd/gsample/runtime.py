@@ -413,7 +413,7 @@ class Sampler:
 
     # -- kernel timing ---------------------------------------------------
     def timing_begin(self, max_calls: int):
-        """Record HIP events around every kernel of the next `max_calls` calls."""
+        """Launch every kernel of the next `max_calls` calls with start/stop HIP events."""
         self._check(self.lib.gs_timing_begin(self.ctx, int(max_calls)))
 
     def timing_end(self) -> dict:

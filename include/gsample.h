@@ -247,14 +247,6 @@ int gs_lmhead(gs_context* ctx, const void* hidden, const void* weight, int32_t m
 int gs_lmhead_sample(gs_context* ctx, const void* hidden, const void* weight, int32_t width, float softcap,
                      float* logits_scratch, const gs_batch* batch, void* stream);
 
-/* Kernel timing with HIP events: replaces the WebGPU timestamp queries of
- * measureGpuDispatches (src/webgpu/gpu-timestamp.ts:1-56). After
- * gs_timing_begin(ctx, max_calls), the next max_calls gs_sample /
- * gs_lmhead_sample calls record an event before and after each of their
- * kernels, on the stream they launch on. gs_timing_end waits for those
- * events, writes per stage the summed milliseconds (stage_ms[GS_STAGE_COUNT])
- * and the number of calls that ran that stage (calls[GS_STAGE_COUNT]), and
- * stops timing. The events add a few microseconds per call. */
 /* Self-check of the bound the chunk scan's normaliser rests on; no
  * counterpart in the reference. Largest relative error of the hardware
  * binary32 exp2 (v_exp_f32, which the scan evaluates every term with) over
@@ -264,6 +256,15 @@ int gs_lmhead_sample(gs_context* ctx, const void* hidden, const void* weight, in
  * Synchronous. */
 int gs_check_exp2(gs_context* ctx, float lo, float hi, double* max_rel_err, float* worst_y);
 
+/* Kernel timing with HIP events: replaces the WebGPU timestamp queries of
+ * measureGpuDispatches (src/webgpu/gpu-timestamp.ts:1-56). After
+ * gs_timing_begin(ctx, max_calls), the next max_calls gs_sample /
+ * gs_lmhead_sample calls launch each of their kernels with a start and a stop
+ * event (hipExtLaunchKernel), stamped when the dispatch begins and when its
+ * last wave ends, so each figure is the kernel alone. gs_timing_end waits for
+ * those events, writes per stage the summed milliseconds
+ * (stage_ms[GS_STAGE_COUNT]) and the number of calls that ran that stage
+ * (calls[GS_STAGE_COUNT]), and stops timing. */
 #define GS_STAGE_LMHEAD 0 /* lmhead_kernel */
 #define GS_STAGE_SCAN 1   /* scan_kernel: the one HBM pass over the logits */
 #define GS_STAGE_FINISH 2 /* finish_kernel: per-row merge, filters and draw */
