@@ -182,7 +182,13 @@ int gs_create(int device, int32_t vocab_size, int32_t max_rows, gs_context** out
   ctx->exact_cap = 1;
   while (ctx->exact_cap < vocab_size) ctx->exact_cap <<= 1;
   ctx->exact_slot_bytes = 36 * ctx->exact_cap;
-  ctx->exact_slots = std::min<int32_t>(max_rows, 64);
+  // exact-path scratch slots: one per row up to kExactScratchBudget bytes (at
+  // least 64), so that a row of a batch within the slots is replayed by its
+  // own finish workgroup and the exact kernel runs only for larger batches
+  {
+    const int64_t by_budget = std::max<int64_t>(64, kExactScratchBudget / ctx->exact_slot_bytes);
+    ctx->exact_slots = (int32_t)std::min<int64_t>(max_rows, by_budget);
+  }
   auto cleanup = [&](int status, const char* what) {
     gs_destroy(ctx);
     (void)what;
@@ -314,8 +320,11 @@ int gs_sample(gs_context* ctx, const gs_batch* b, void* stream) {
   GS_HIP(ctx, hipGetLastError());
   launch_finish(a, s, stage_events(ctx, slot, GS_STAGE_FINISH));
   GS_HIP(ctx, hipGetLastError());
-  launch_exact(a, s, stage_events(ctx, slot, GS_STAGE_EXACT));
-  GS_HIP(ctx, hipGetLastError());
+  if (b->rows > ctx->exact_slots) {
+    // rows past the slots were queued by the finish kernel
+    launch_exact(a, s, stage_events(ctx, slot, GS_STAGE_EXACT));
+    GS_HIP(ctx, hipGetLastError());
+  }
   if (slot >= 0) ctx->t_calls++;
   return GS_OK;
 }

@@ -29,6 +29,7 @@
 // Global loads are issued in two batches (row inputs, then the list entries
 // and special logits that LDS data locates), so the row's latency is a few
 // memory round trips plus the rank work.
+#include "gs_exact_row.h"
 #include "gs_exp2.h"
 #include "gs_internal.h"
 
@@ -42,6 +43,8 @@ constexpr int kSubPerThread = kSubCap / kSubThreads;  // slots each of them read
 constexpr int kSlotsPerThread = kHashSize / kFinishThreads;
 constexpr int kIdsPerThread = 2;                      // window ids loaded ahead per thread
 constexpr int kSpecQ = 2;  // list slots per thread read with the statistics (16 per sub-list)
+constexpr uint32_t kDeepLists = 1u << 30;  // row flag: some sub-list holds more than 16 entries
+constexpr uint32_t kExactRequest = 1u << 31;  // finish_row's answer: the row goes to the exact path
 static_assert(kFinishMaxChunks * kScanWaves <= kFinishThreads, "one thread per chunk wave");
 
 __device__ __forceinline__ double block_scan_f64(double v, double* s_w, double* total) {
@@ -352,26 +355,32 @@ __device__ bool top_select(const uint64_t* s, int n, uint32_t lo, uint32_t hi, u
     src = out;
     n_src = (int)(sel[3] < (uint32_t)kOut ? sel[3] : (uint32_t)kOut);
   }
-  // rank the survivors by counting: the entries are distinct, so survivor i's
-  // place is the number of survivors above it; places past the survivors
-  // stay zero
-  if (tid < n_src) {
-    const uint64_t e = src[tid];
-    int rank = 0;
-    // two entries per 16-byte read (src is 16-byte aligned and holds at least
-    // n_src + 1 entries); a read never waits on the previous one
-    const uint4* p = (const uint4*)src;
-    const int n_pair = (n_src + 1) >> 1;
-#pragma unroll 8
-    for (int j = 0; j < n_pair; ++j) {
-      const uint4 w = p[j];
-      const uint64_t x0 = ((uint64_t)w.y << 32) | w.x, x1 = ((uint64_t)w.w << 32) | w.z;
-      rank += x0 > e ? 1 : 0;
-      rank += (2 * j + 1 < n_src && x1 > e) ? 1 : 0;
+  // rank the survivors (at most 128) by counting: the entries are distinct,
+  // so survivor i's place is the number of survivors above it. Eight threads
+  // share survivor tid / 8, each counting over 16 of the survivors (src holds
+  // at least 128 entries), and the eight counts meet by DPP; places past the
+  // survivors stay zero.
+  {
+    const int i = tid >> 3, part = tid & 7;
+    uint64_t e = 0;
+    uint32_t cnt = 0;
+    if (i < n_src) {
+      e = src[i];
+      const uint4* p = (const uint4*)(src + part * 16);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const uint4 w = p[j];
+        const int k = part * 16 + 2 * j;
+        const uint64_t x0 = ((uint64_t)w.y << 32) | w.x, x1 = ((uint64_t)w.w << 32) | w.z;
+        cnt += (k < n_src && x0 > e) ? 1u : 0u;
+        cnt += (k + 1 < n_src && x1 > e) ? 1u : 0u;
+      }
     }
-    if (rank < kTopR) top[rank] = e;
-  } else if (tid < kTopR) {
-    top[tid] = 0;
+    cnt += dpp_u32<kDppQuad1032, 0xF>(0u, cnt);
+    cnt += dpp_u32<kDppQuad2301, 0xF>(0u, cnt);
+    cnt += dpp_u32<kDppRowHalfMirror, 0xF>(0u, cnt);  // lane l of 8 meets lane 7 - l: the other quad
+    if (part == 0 && i < n_src && cnt < (uint32_t)kTopR) top[cnt] = e;
+    if (tid >= n_src && tid < kTopR) top[tid] = 0;
   }
   __syncthreads();
   return true;
@@ -432,6 +441,7 @@ struct Shared {
   uint32_t legal_bits;
   uint32_t special_legal;
   uint32_t fast_done;
+  uint32_t exact_flags;
   uint64_t best_entry;
 };
 
@@ -439,6 +449,27 @@ __device__ void enqueue_exact(const SampleArgs& a, int64_t row, uint32_t flags) 
   const uint32_t q = atomicAdd(&a.queue->count, 1u);
   a.queue->rows[q] = (uint32_t)row;
   a.results[row].flags = flags;
+}
+
+// The finish's LDS and, for a row it replays in place, the exact path's
+union FinishLds {
+  Shared fin;
+  exact::Lds ex;
+};
+
+// Sends the row to the exact path: replayed here by the whole workgroup when
+// it has a scratch slot of its own (row < slots), else queued for the exact
+// kernel. Every thread of the workgroup calls it.
+__device__ __forceinline__ void to_exact(const SampleArgs& a, FinishLds& U, int64_t row, uint32_t flags) {
+  if (row < a.exact_slots) {
+    __syncthreads();  // every wave is done with the finish's LDS
+    // the replay is a call of its own; it reads the arguments where the
+    // kernel received them, so the kernel's copy never goes to the stack
+    const SampleArgs& ka = *(const SampleArgs*)__builtin_amdgcn_kernarg_segment_ptr();
+    exact::process_row(ka, U.ex, exact::scratch_at(a, row), row, flags);
+  } else if (threadIdx.x == 0) {
+    enqueue_exact(a, row, flags);
+  }
 }
 
 __device__ void write_result(const SampleArgs& a, int64_t row, int32_t token, uint32_t flags, double p) {
@@ -454,14 +485,15 @@ __device__ __forceinline__ double nonspecial_value(uint64_t e, double T) { retur
 // The filters and the draw over the first n_avail (<= 128) candidates, whose
 // exponentials e[] (probability = e / total, sampling.ts:39,42) and ids ids[]
 // sit in LDS in list order, evaluated by the calling wave alone. Returns 0
-// when the row is settled (result written or queued for the exact path), 1
-// when the cut lies past the candidates and the caller must widen them, 2
-// when the top-p cut lies within `margin` of topP and `refinable` is set: the
-// caller recomputes the normaliser and calls again with the tighter margin.
+// when the row is settled (result written), 1 when the cut lies past the
+// candidates and the caller must widen them, 2 when the top-p cut lies within
+// `margin` of topP and `refinable` is set: the caller recomputes the
+// normaliser and calls again with the tighter margin; 3 when the row needs
+// the exact path, with its result flags in *exact_flags.
 // `complete`: the candidates are the row's whole list.
-__device__ int filters_and_draw_wave(const SampleArgs& a, int64_t row, const gs_row_config& cfg, const double* e,
+__device__ __forceinline__ int filters_and_draw_wave(const SampleArgs& a, int64_t row, const gs_row_config& cfg, const double* e,
                                      double total, const uint32_t* ids, int n_avail, bool complete, double margin,
-                                     bool refinable) {
+                                     bool refinable, uint32_t* exact_flags) {
   const int lane = threadIdx.x & 63;
   constexpr int kPerLane = 2;  // list index lane*2 + q
   double pl[kPerLane];
@@ -577,13 +609,11 @@ __device__ int filters_and_draw_wave(const SampleArgs& a, int64_t row, const gs_
   }
   pick = (int)wave_min_u32((uint32_t)pick);
   if (__ballot(near)) exact_why |= 8u;
-  if (lane == 0) {
-    if (exact_why || pick == 0x7FFFFFFF) {
-      enqueue_exact(a, row, exact_why ? GS_FLAG_NEAR_TIE : 0u);
-    } else {
-      write_result(a, row, (int32_t)ids[pick], tie, e[pick] / total);
-    }
+  if (exact_why || pick == 0x7FFFFFFF) {
+    *exact_flags = exact_why ? GS_FLAG_NEAR_TIE : 0u;
+    return 3;
   }
+  if (lane == 0) write_result(a, row, (int32_t)ids[pick], tie, e[pick] / total);
   return 0;
 }
 
@@ -622,8 +652,10 @@ __device__ double recompute_nonspecial_sum(const SampleArgs& a, int64_t row, con
   return (t_all < __builtin_inf() && t_sp <= 0.5 * t_all) ? t_all - t_sp : -1.0;
 }
 
-__global__ __launch_bounds__(kFinishThreads) void finish_kernel(SampleArgs a) {
-  __shared__ Shared S;
+// The finish of row blockIdx.x. Returns 0 when the row's result is written,
+// else kExactRequest | the result flags the exact path keeps.
+__device__ __forceinline__ uint32_t finish_row(const SampleArgs& a, FinishLds& U) {
+  Shared& S = U.fin;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int64_t row = blockIdx.x;
   // ---- first batch of global loads, all issued before the row's
@@ -632,25 +664,25 @@ __global__ __launch_bounds__(kFinishThreads) void finish_kernel(SampleArgs a) {
   // every sub-list, the history and forced-id offsets. The list slots are
   // read before the sub-lists' lengths are known: they lie inside the row's
   // list buffer, and entries past a sub-list's length are dropped once it is.
+  // Every load here is unconditional (threads past the last chunk wave or
+  // sub-list read the first one and drop it where the value is used), so no
+  // branch merge makes a thread wait for its load before the next is issued.
   const int n_wstats = a.n_chunks * kScanWaves;  // <= kFinishThreads
-  double w_sum = 0.0;
-  uint32_t w_max = 0, w_flags = 0, w_nsub = 0, w_thr = 0, w_trunc = 0;
-  if (tid < n_wstats) {
-    const ChunkStat* c = a.stats + row * a.n_chunks + tid / kScanWaves;
-    const int w = tid % kScanWaves;
-    w_sum = c->wsum[w];
-    w_max = c->wmax[w];
-    w_flags = c->wflags[w];
-    w_nsub = c->n_sub[w];
-    w_thr = c->threshold;
-    w_trunc = c->truncated;
-  }
+  const bool has_w = tid < n_wstats;
+  const int tw = has_w ? tid : 0;
+  const ChunkStat* wc = a.stats + row * a.n_chunks + tw / kScanWaves;
+  const double w_sum = wc->wsum[tw % kScanWaves];
+  const uint32_t w_max = wc->wmax[tw % kScanWaves];
+  const uint32_t w_flags = wc->wflags[tw % kScanWaves];
+  const uint32_t w_nsub = wc->n_sub[tw % kScanWaves];
+  const uint32_t w_thr = wc->threshold;
+  const uint32_t w_trunc = wc->truncated;
   const uint64_t* lists = a.lists + row * a.n_chunks * kGatherCap;
   const int n_subs = a.n_chunks * kScanWaves;
   const int sl0 = tid / kSubThreads, k0 = tid % kSubThreads;
   uint64_t lv[kSubPerThread];
 #pragma unroll
-  for (int q = 0; q < kSpecQ; ++q) lv[q] = sl0 < n_subs ? lists[(int64_t)sl0 * kSubCap + k0 + q * kSubThreads] : 0ull;
+  for (int q = 0; q < kSpecQ; ++q) lv[q] = lists[(int64_t)(sl0 < n_subs ? sl0 : 0) * kSubCap + k0 + q * kSubThreads];
   int64_t h0 = 0, h1 = 0, f0 = 0, f1 = 0;
   if (a.history_offsets) { h0 = a.history_offsets[row]; h1 = a.history_offsets[row + 1]; }
   if (a.forced_offsets) { f0 = a.forced_offsets[row]; f1 = a.forced_offsets[row + 1]; }
@@ -658,8 +690,7 @@ __global__ __launch_bounds__(kFinishThreads) void finish_kernel(SampleArgs a) {
   const gs_row_config cfg = a.configs[row];
   const Plan plan = plan_row(cfg);
   if (plan.route == kRouteExact) {
-    if (tid == 0) enqueue_exact(a, row, 0u);
-    return;
+    return kExactRequest | 0u;
   }
   const bool greedy = plan.route == kRouteGreedy;
   const int32_t slot = cfg.mask_slot;
@@ -706,13 +737,15 @@ __global__ __launch_bounds__(kFinishThreads) void finish_kernel(SampleArgs a) {
 
   // ---- 1. statistics: sub-list lengths into LDS; the flags, the maximum and
   // the truncation threshold reduced per wave (one LDS atomic each)
-  if (tid < n_wstats) S.c_nsub[tid] = (uint16_t)(w_nsub > (uint32_t)kSubCap ? (uint32_t)kSubCap : w_nsub);
+  if (has_w) S.c_nsub[tid] = (uint16_t)(w_nsub > (uint32_t)kSubCap ? (uint32_t)kSubCap : w_nsub);
   {
     // a sub-list length above kSubCap: the sub-list overflowed
-    const uint32_t fl = wave_or_u32(w_flags | (w_nsub > (uint32_t)kSubCap ? kChunkOverflow : 0u));
-    const uint32_t mk = wave_max_u32(w_max);
-    const uint32_t th = wave_max_u32(w_trunc ? w_thr : 0u);
-    const bool tr = __ballot(w_trunc != 0) != 0;
+    const uint32_t fl = wave_or_u32(has_w ? w_flags | (w_nsub > (uint32_t)kSubCap ? kChunkOverflow : 0u) |
+                                                (w_nsub > (uint32_t)(kSpecQ * kSubThreads) ? kDeepLists : 0u)
+                                          : 0u);
+    const uint32_t mk = wave_max_u32(has_w ? w_max : 0u);
+    const uint32_t th = wave_max_u32(has_w && w_trunc ? w_thr : 0u);
+    const bool tr = __ballot(has_w && w_trunc != 0) != 0;
     if (lane == 0) {
       if (fl) atomicOr(&S.flags, fl);
       if (mk) atomicMax(&S.max_key, mk);
@@ -721,15 +754,26 @@ __global__ __launch_bounds__(kFinishThreads) void finish_kernel(SampleArgs a) {
   }
   // the owned specials' logits and mask words start loading now; they are
   // first used after the region is ranked
-  float oraw[kOwn];
+  uint32_t oraw[kOwn];  // logit bits as loaded (bf16: the 16 bits, widened at use)
   uint32_t omw[kOwn];
   int oslot[kOwn];
   bool ofirst[kOwn];
+  {
+    bool ok[kOwn];
 #pragma unroll
-  for (int r = 0; r < kOwn; ++r) {
-    const bool ok = own_path && oid[r] >= 0 && oid[r] < a.vocab;
-    oraw[r] = ok ? load_logit(a, row, oid[r]) : 0.0f;
-    omw[r] = ok && constrained ? a.mask_table[(int64_t)slot * a.mask_words + (oid[r] >> 5)] : 0u;
+    for (int r = 0; r < kOwn; ++r) ok[r] = own_path && oid[r] >= 0 && oid[r] < a.vocab;
+    if (a.dtype == GS_BF16) {
+      const uint16_t* lp = (const uint16_t*)a.logits + row * a.row_stride;
+#pragma unroll
+      for (int r = 0; r < kOwn; ++r) oraw[r] = ok[r] ? (uint32_t)lp[oid[r]] : 0u;
+    } else {
+      const uint32_t* lp = (const uint32_t*)a.logits + row * a.row_stride;
+#pragma unroll
+      for (int r = 0; r < kOwn; ++r) oraw[r] = ok[r] ? lp[oid[r]] : 0u;
+    }
+#pragma unroll
+    for (int r = 0; r < kOwn; ++r)
+      omw[r] = ok[r] && constrained ? a.mask_table[(int64_t)slot * a.mask_words + (oid[r] >> 5)] : 0u;
   }
   // distinct special ids into the hash
   {
@@ -751,12 +795,10 @@ __global__ __launch_bounds__(kFinishThreads) void finish_kernel(SampleArgs a) {
   }
   __syncthreads();
   if (S.flags & kChunkNonFinite) {
-    if (tid == 0) enqueue_exact(a, row, GS_FLAG_NONFINITE);
-    return;
+    return kExactRequest | GS_FLAG_NONFINITE;
   }
   if (!greedy && (S.flags & kChunkOverflow)) {
-    if (tid == 0) enqueue_exact(a, row, 0u);
-    return;
+    return kExactRequest | 0u;
   }
 
   // ---- second batch of global loads: the hash-slot specials' logits and
@@ -794,13 +836,15 @@ __global__ __launch_bounds__(kFinishThreads) void finish_kernel(SampleArgs a) {
   // one LDS atomic per wave
   const uint32_t sel_lo = thr > kKeyNegInf ? thr : kKeyNegInf + 1u;
   const uint32_t sel_hi = S.max_key > sel_lo ? S.max_key : sel_lo;
-  auto append = [&](const uint64_t (&v)[kSubPerThread], int cnt) {
+  // slots [lo, cnt) of the thread's sub-list slots k0 + q * kSubThreads
+  auto append = [&](const uint64_t (&v)[kSubPerThread], int lo, int cnt) {
     uint64_t e[kSubPerThread];
     uint32_t keep = 0;
 #pragma unroll
     for (int q = 0; q < kSubPerThread; ++q) {
       e[q] = 0;
-      if (k0 + q * kSubThreads < cnt) {
+      const int k = k0 + q * kSubThreads;
+      if (k >= lo && k < cnt) {
         e[q] = list_rank(v[q]);
         if (entry_key(e[q]) >= thr) keep |= 1u << q;
       }
@@ -820,13 +864,24 @@ __global__ __launch_bounds__(kFinishThreads) void finish_kernel(SampleArgs a) {
     }
   };
   if (!greedy) {
+    // the first kSpecQ * kSubThreads slots of every sub-list came with the
+    // statistics; deeper slots (rows with some longer sub-list) are read in a
+    // pass of their own, so that the common path never waits for loads
+    // issued after the special gathers
+    constexpr int kHead = kSpecQ * kSubThreads;
     const int cnt0 = sl0 < n_subs ? (int)S.c_nsub[sl0] : 0;
 #pragma unroll
-    for (int q = kSpecQ; q < kSubPerThread; ++q) {
-      const int k = k0 + q * kSubThreads;
-      lv[q] = k < cnt0 ? lists[(int64_t)sl0 * kSubCap + k] : 0ull;
+    for (int q = kSpecQ; q < kSubPerThread; ++q) lv[q] = 0;
+    append(lv, 0, cnt0 < kHead ? cnt0 : kHead);
+    if (S.flags & kDeepLists) {
+      uint64_t v[kSubPerThread];
+#pragma unroll
+      for (int q = 0; q < kSubPerThread; ++q) {
+        const int k = k0 + q * kSubThreads;
+        v[q] = (k >= kHead && k < cnt0) ? lists[(int64_t)sl0 * kSubCap + k] : 0ull;
+      }
+      append(v, kHead, cnt0);
     }
-    append(lv, cnt0);
     // sub-lists past the first kFinishThreads / kSubThreads (more than 32 chunks)
     for (int s0 = kFinishThreads / kSubThreads; s0 < n_subs; s0 += kFinishThreads / kSubThreads) {
       const int sl = s0 + tid / kSubThreads;
@@ -837,7 +892,7 @@ __global__ __launch_bounds__(kFinishThreads) void finish_kernel(SampleArgs a) {
         const int k = k0 + q * kSubThreads;
         v[q] = k < cnt ? lists[(int64_t)sl * kSubCap + k] : 0ull;
       }
-      append(v, cnt);
+      append(v, 0, cnt);
     }
   }
   __syncthreads();
@@ -870,7 +925,8 @@ __global__ __launch_bounds__(kFinishThreads) void finish_kernel(SampleArgs a) {
       float x32 = raw[r];
       uint32_t mword = mw[r];
       if (own_path && r < kOwn) {
-        x32 = oraw[r < kOwn ? r : 0];
+        const uint32_t b = oraw[r < kOwn ? r : 0];
+        x32 = __builtin_bit_cast(float, a.dtype == GS_BF16 ? b << 16 : b);
         mword = omw[r < kOwn ? r : 0];
       }
       if (cfg.softcap > 0) x32 = gsm::softcap_f32(x32, cfg.softcap);
@@ -904,11 +960,10 @@ __global__ __launch_bounds__(kFinishThreads) void finish_kernel(SampleArgs a) {
   __syncthreads();
   if (S.n_special > (uint32_t)kSpecialCap) {
     if (tid == 0) write_result(a, row, -1, GS_FLAG_UNSUPPORTED, 0.0);
-    return;
+    return 0;
   }
   if (S.flags & kChunkNonFinite) {
-    if (tid == 0) enqueue_exact(a, row, GS_FLAG_NONFINITE);
-    return;
+    return kExactRequest | GS_FLAG_NONFINITE;
   }
   const int n_sp = (int)S.n_special;
 
@@ -939,7 +994,7 @@ __global__ __launch_bounds__(kFinishThreads) void finish_kernel(SampleArgs a) {
     }
     if (!S.legal_bits) {
       if (tid == 0) write_result(a, row, -1, GS_FLAG_DEAD_END, 0.0);
-      return;
+      return 0;
     }
   }
 
@@ -968,12 +1023,11 @@ __global__ __launch_bounds__(kFinishThreads) void finish_kernel(SampleArgs a) {
       }
       write_result(a, row, token, GS_FLAG_GREEDY, 1.0);
     }
-    return;
+    return 0;
   }
 
   if (n_region > kFinishCap) {
-    if (tid == 0) enqueue_exact(a, row, 0u);
-    return;
+    return kExactRequest | 0u;
   }
   const int n_ns = n_region;
 
@@ -987,8 +1041,7 @@ __global__ __launch_bounds__(kFinishThreads) void finish_kernel(SampleArgs a) {
   }
   if (!(M > -__builtin_inf())) {
     // every logit is -inf: the reference's arithmetic turns NaN; replay it exactly
-    if (tid == 0) enqueue_exact(a, row, 0u);
-    return;
+    return kExactRequest | 0u;
   }
   // Margins for the comparisons that depend on the normaliser (the top-p
   // cut). This total and the reference's differ by the scan's normaliser
@@ -1008,40 +1061,58 @@ __global__ __launch_bounds__(kFinishThreads) void finish_kernel(SampleArgs a) {
   double t_chunks, t_sp;
   {
     double part = 0.0, spart = 0.0;
-    if (w_sum > 0.0 && w_max > kKeyNegInf) part = w_sum * gsm::js_exp((double)key_f32(w_max) / T - M);
+    if (has_w && w_sum > 0.0 && w_max > kKeyNegInf) part = w_sum * gsm::js_exp((double)key_f32(w_max) / T - M);
     for (int i = kFinishThreads - 1 - tid; i < n_sp; i += kFinishThreads) spart += gsm::js_exp(key_f64(S.sp_key[i]) - M);
     block_sum2_f64(part, spart, S.wsum2, &t_chunks, &t_sp);
     if (tid == 0) { S.total = t_chunks + t_sp; S.total_sp = t_sp; }
   }
   if (!(t_chunks + t_sp < __builtin_inf())) {
     // an exponent argument beyond the double range (|l/T| near 1e18 or more)
-    if (tid == 0) enqueue_exact(a, row, 0u);
-    return;
+    return kExactRequest | 0u;
   }
 
   // specials inside the complete region (value >= the threshold's value),
-  // moved into the dead hash table and sorted there; usually none or a few
+  // compacted into the dead hash table (one LDS atomic per wave) and ordered
+  // there: up to 64 by one wave counting each one's rank, more by a
+  // block-wide bitonic sort; usually there are none or a few
   uint64_t* in_key = (uint64_t*)S.hash_ids;
   uint32_t* in_id = S.hash_counts;
   const uint64_t region_floor = thr ? f64_key((double)key_f32(thr) / T) : 0;
-  for (int i = tid; i < n_sp; i += kFinishThreads) {
-    if (S.sp_key[i] >= region_floor) {
-      const uint32_t p = atomicAdd(&S.n_sp_in, 1u);
+  for (int i0 = 0; i0 < n_sp; i0 += kFinishThreads) {
+    const int i = i0 + tid;
+    const bool in = i < n_sp && S.sp_key[i] >= region_floor;
+    const uint64_t m = __ballot(in);
+    uint32_t base = 0;
+    if (lane == 0 && m) base = atomicAdd(&S.n_sp_in, (uint32_t)__popcll(m));
+    base = readlane_u32(base, 0);
+    if (in) {
+      const uint32_t p = base + __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
       in_key[p] = S.sp_key[i];
       in_id[p] = S.sp_id[i];
     }
   }
   __syncthreads();
   const int n_sp_in = (int)S.n_sp_in;
-  {
+  if (n_sp_in <= 64) {
+    if (n_sp_in > 1 && wave == 0) {
+      const uint64_t k = lane < n_sp_in ? in_key[lane] : 0ull;
+      const uint32_t id = lane < n_sp_in ? in_id[lane] : 0xFFFFFFFFu;
+      int rank = 0;  // the ids are distinct, so the ranks are too
+      for (int j = 0; j < n_sp_in; ++j) rank += ranks_before(readlane_u64(k, j), readlane_u32(id, j), k, id) ? 1 : 0;
+      if (lane < n_sp_in) {
+        in_key[rank] = k;
+        in_id[rank] = id;
+      }
+    }
+    __syncthreads();
+  } else {
     const int m2 = pow2_at_least(n_sp_in);
     for (int i = n_sp_in + tid; i < m2; i += kFinishThreads) { in_key[i] = 0; in_id[i] = 0xFFFFFFFFu; }
     __syncthreads();
-    if (m2 > 1) block_sort_pairs_desc(in_key, in_id, m2);
+    block_sort_pairs_desc(in_key, in_id, m2);
   }
   if (n_ns + n_sp_in == 0) {
-    if (tid == 0) enqueue_exact(a, row, 0u);
-    return;
+    return kExactRequest | 0u;
   }
   double total = S.total;
   const bool region_complete = !S.any_truncated;
@@ -1121,22 +1192,32 @@ __global__ __launch_bounds__(kFinishThreads) void finish_kernel(SampleArgs a) {
       __builtin_amdgcn_wave_barrier();
       for (int i = lane; i < n_valid; i += 64) fp[i] = gsm::js_exp(fp[i] - M);
       __builtin_amdgcn_wave_barrier();
-      const int r = filters_and_draw_wave(a, row, cfg, fp, total, fid, n_valid, complete, margin, true);
-      if (lane == 0) S.fast_done = r == 0 ? 1u : (r == 2 ? 2u : 0u);
+      uint32_t xf = 0;
+      const int r = filters_and_draw_wave(a, row, cfg, fp, total, fid, n_valid, complete, margin, true, &xf);
+      if (lane == 0) {
+        S.fast_done = r == 0 ? 1u : (r == 2 ? 2u : (r == 3 ? 3u : 0u));
+        S.exact_flags = xf;
+      }
     }
     __syncthreads();
     if (S.fast_done == 2) {
       if (!refine()) {
-        if (tid == 0) enqueue_exact(a, row, GS_FLAG_NEAR_TIE);
-        return;
+        return kExactRequest | GS_FLAG_NEAR_TIE;
       }
       if (wave == 0) {
-        const int r = filters_and_draw_wave(a, row, cfg, fp, total, fid, n_valid, complete, margin, false);
-        if (lane == 0) S.fast_done = r == 0 ? 1u : 0u;
+        uint32_t xf = 0;
+        const int r = filters_and_draw_wave(a, row, cfg, fp, total, fid, n_valid, complete, margin, false, &xf);
+        if (lane == 0) {
+          S.fast_done = r == 0 ? 1u : (r == 3 ? 3u : 0u);
+          S.exact_flags = xf;
+        }
       }
       __syncthreads();
     }
-    if (S.fast_done) return;
+    if (S.fast_done == 3) {
+      return kExactRequest | S.exact_flags;
+    }
+    if (S.fast_done) return 0;
   }
 
   // ---- slow path: the whole region sorted, then the filters block-wide
@@ -1148,8 +1229,7 @@ __global__ __launch_bounds__(kFinishThreads) void finish_kernel(SampleArgs a) {
   }
   const int n_cand = n_ns + n_sp_in;
   if (n_cand > kFinishCap) {
-    if (tid == 0) enqueue_exact(a, row, 0u);
-    return;
+    return kExactRequest | 0u;
   }
   // merge by rank into (value, id), then probabilities (sampling.ts:39,42)
   for (int i = tid; i < n_ns; i += kFinishThreads) {
@@ -1191,12 +1271,20 @@ __global__ __launch_bounds__(kFinishThreads) void finish_kernel(SampleArgs a) {
   // ---- min-p (sampling.ts:45-48): p is non-increasing along the list
   if (cfg.min_p > 0) {
     const double floor_p = S.cand_p[0] / total * cfg.min_p;
+    uint32_t my_first = 0xFFFFFFFFu, my_route = 0;
     for (int i = tid; i < n; i += kFinishThreads) {
       const double p = S.cand_p[i] / total;
-      if (i + 1 < n && S.cand_p[i + 1] / total > p) atomicOr(&S.route_exact, 1u);  // not monotone: replay
-      if (!(p >= floor_p)) atomicMin(&S.first_idx, (uint32_t)i);
+      if (i + 1 < n && S.cand_p[i + 1] / total > p) my_route |= 1u;  // not monotone: replay
+      if (!(p >= floor_p) && (uint32_t)i < my_first) my_first = (uint32_t)i;
       const double d = p >= floor_p ? p - floor_p : floor_p - p;
-      if (d < kNearTie * floor_p) atomicOr(&S.route_exact, 2u);
+      if (d < kNearTie * floor_p) my_route |= 2u;
+    }
+    // one LDS atomic per wave
+    my_first = wave_min_u32(my_first);
+    my_route = wave_or_u32(my_route);
+    if (lane == 0) {
+      if (my_first != 0xFFFFFFFFu) atomicMin(&S.first_idx, my_first);
+      if (my_route) atomicOr(&S.route_exact, my_route);
     }
     __syncthreads();
     if (S.first_idx != 0xFFFFFFFFu) {
@@ -1208,7 +1296,7 @@ __global__ __launch_bounds__(kFinishThreads) void finish_kernel(SampleArgs a) {
     __syncthreads();
     if (n == 0) {
       if (tid == 0) write_result(a, row, -1, GS_FLAG_EMPTY_CANDIDATES, 0.0);
-      return;
+      return 0;
     }
   }
   // ---- top-p (sampling.ts:56,82-90) on inclusive prefix sums
@@ -1226,13 +1314,22 @@ __global__ __launch_bounds__(kFinishThreads) void finish_kernel(SampleArgs a) {
       }
       double tot;
       base = block_scan_f64(s, S.wtmp, &tot) - s;
-      for (int q = 0; q < kPer; ++q) {
+      uint32_t my_first = 0xFFFFFFFFu;
+      bool my_near = false;
+      for (int q = kPer - 1; q >= 0; --q) {
         const int i = tid * kPer + q;
-        if (i >= n) break;
+        if (i >= n) continue;
         const double cum = base + local[q];
-        if (cum >= cfg.top_p) atomicMin(&S.first_idx, (uint32_t)i);
+        if (cum >= cfg.top_p) my_first = (uint32_t)i;
         const double d = cum >= cfg.top_p ? cum - cfg.top_p : cfg.top_p - cum;
-        if (d < margin) atomicOr(&S.route_exact, 4u);
+        if (d < margin) my_near = true;
+      }
+      // one LDS atomic per wave
+      my_first = wave_min_u32(my_first);
+      const bool wave_near = __ballot(my_near) != 0;
+      if (lane == 0) {
+        if (my_first != 0xFFFFFFFFu) atomicMin(&S.first_idx, my_first);
+        if (wave_near) atomicOr(&S.route_exact, 4u);
       }
       __syncthreads();
       // a cut within the scan normaliser's margin alone: recompute it, redo
@@ -1240,16 +1337,14 @@ __global__ __launch_bounds__(kFinishThreads) void finish_kernel(SampleArgs a) {
       __syncthreads();
       if (tid == 0) { S.route_exact = 0; S.first_idx = 0xFFFFFFFFu; }
       if (!refine()) {
-        if (tid == 0) enqueue_exact(a, row, GS_FLAG_NEAR_TIE);
-        return;
+        return kExactRequest | GS_FLAG_NEAR_TIE;
       }
       __syncthreads();
     }
     int cut = (int)S.first_idx;  // index of the item that reached topP
     if (S.first_idx == 0xFFFFFFFFu) {
       if (!n_complete) {
-        if (tid == 0) enqueue_exact(a, row, 0u);
-        return;
+        return kExactRequest | 0u;
       }
       cut = n - 1;
     } else if (tid == cut / kPer) {
@@ -1265,8 +1360,7 @@ __global__ __launch_bounds__(kFinishThreads) void finish_kernel(SampleArgs a) {
     if (tid == 0) S.first_idx = 0xFFFFFFFFu;
     __syncthreads();
   } else if (!n_complete) {
-    if (tid == 0) enqueue_exact(a, row, 0u);
-    return;
+    return kExactRequest | 0u;
   }
   tie_report = S.status_flags;
 
@@ -1283,24 +1377,39 @@ __global__ __launch_bounds__(kFinishThreads) void finish_kernel(SampleArgs a) {
     const double base = block_scan_f64(s, S.wtmp, &ctotal) - s;
     const double u = cfg.rng_mode == GS_RNG_EXPLICIT ? cfg.uniform : gsm::mulberry32_draw(cfg.seed, cfg.draw_index);
     const double cursor = u * ctotal;
-    for (int q = 0; q < kPer; ++q) {
+    uint32_t my_first = 0xFFFFFFFFu;
+    bool my_near = false;
+    for (int q = kPer - 1; q >= 0; --q) {
       const int i = tid * kPer + q;
-      if (i >= n) break;
+      if (i >= n) continue;
       const double pre = base + local[q];
-      if (pre >= cursor) atomicMin(&S.first_idx, (uint32_t)i);
+      if (pre >= cursor) my_first = (uint32_t)i;
       const double d = pre >= cursor ? pre - cursor : cursor - pre;
-      if (d < kNearTie * ctotal) atomicOr(&S.route_exact, 8u);
+      if (d < kNearTie * ctotal) my_near = true;
+    }
+    my_first = wave_min_u32(my_first);
+    const bool wave_near = __ballot(my_near) != 0;
+    if (lane == 0) {
+      if (my_first != 0xFFFFFFFFu) atomicMin(&S.first_idx, my_first);
+      if (wave_near) atomicOr(&S.route_exact, 8u);
     }
     __syncthreads();
+    if (S.route_exact || S.first_idx == 0xFFFFFFFFu) {
+      return kExactRequest | (S.route_exact ? GS_FLAG_NEAR_TIE : 0u);
+    }
     if (tid == 0) {
-      if (S.route_exact || S.first_idx == 0xFFFFFFFFu) {
-        enqueue_exact(a, row, S.route_exact ? GS_FLAG_NEAR_TIE : 0u);
-      } else {
-        const int i = (int)S.first_idx;
-        write_result(a, row, (int32_t)S.cand_id[i], tie_report, S.cand_p[i] / total);
-      }
+      const int i = (int)S.first_idx;
+      write_result(a, row, (int32_t)S.cand_id[i], tie_report, S.cand_p[i] / total);
     }
   }
+  return 0;
+}
+
+__global__ __launch_bounds__(kFinishThreads) void finish_kernel(SampleArgs a) {
+  __shared__ FinishLds U;
+  const uint32_t r = finish_row(a, U);
+  // the exact path is entered from here only, where nothing else is live
+  if (r & kExactRequest) to_exact(a, U, blockIdx.x, r & ~kExactRequest);
 }
 
 }  // namespace

@@ -33,6 +33,7 @@ constexpr int kSpecialCap = 2048;                 // distinct (history window + 
 constexpr int kHashSize = 4096;                   // open-addressing table for those ids
 constexpr int kExactThreads = 1024;
 constexpr int kExactTile = 4096;                  // LDS tile of the exact path's bitonic sort
+constexpr int64_t kExactScratchBudget = 2560ll << 20;  // bytes of exact-path row scratch per context
 
 // relative margin under which a fast-path decision is re-resolved exactly;
 // it bounds the reference's own sequential-sum error (V * 2^-53 ~ 3e-11)
@@ -94,17 +95,22 @@ struct Plan {
   int32_t depth;  // per-chunk rank depth of the one-pass path
 };
 
+// Every field is read whatever the route (selects, not branches), so that a
+// kernel fetches the whole configuration at once instead of one field after
+// another behind branches.
 __host__ __device__ __forceinline__ Plan plan_row(const gs_row_config& c) {
-  if (c.temperature == 0) return Plan{kRouteGreedy, 1};
-  if (c.options & GS_ROW_FORCE_EXACT) return Plan{kRouteExact, 0};
+  const bool greedy = c.temperature == 0;
+  const bool forced = (c.options & GS_ROW_FORCE_EXACT) != 0;
   // between these bounds l/T keeps the order and the ties of the f32 logits
-  if (!(c.temperature >= 1.0e-200 && c.temperature <= 1.0e200)) return Plan{kRouteExact, 0};
-  if (c.typical_p < 1) return Plan{kRouteExact, 0};
-  if (c.top_k > 0)
-    return c.top_k <= kMaxFastK ? Plan{kRouteTopK, c.top_k < kTopKChunkDepth ? c.top_k : kTopKChunkDepth}
-                                : Plan{kRouteExact, 0};
-  if (c.top_p < 1 || c.min_p > 0) return Plan{kRouteTopP, kTopPListL};
-  return Plan{kRouteExact, 0};
+  const bool t_out = !(c.temperature >= 1.0e-200 && c.temperature <= 1.0e200);
+  const bool typical = c.typical_p < 1;
+  const bool topk = c.top_k > 0, topk_fast = c.top_k <= kMaxFastK;
+  const bool topp = c.top_p < 1 || c.min_p > 0;
+  const int depth_k = c.top_k < kTopKChunkDepth ? c.top_k : kTopKChunkDepth;
+  const bool exact = forced || t_out || typical || (topk ? !topk_fast : !topp);
+  const int route = greedy ? kRouteGreedy : (exact ? kRouteExact : (topk ? kRouteTopK : kRouteTopP));
+  const int depth = greedy ? 1 : (exact ? 0 : (topk ? depth_k : kTopPListL));
+  return Plan{route, depth};
 }
 
 // ------------------------------------------------------- per-chunk state
@@ -190,6 +196,7 @@ constexpr int kDppRowShr4 = 0x114;
 constexpr int kDppRowShr8 = 0x118;
 constexpr int kDppRowRor4 = 0x124;
 constexpr int kDppRowRor8 = 0x128;
+constexpr int kDppRowHalfMirror = 0x141;  // lane l of each 8 to lane 7 - l
 constexpr int kDppRowBcast15 = 0x142;  // lane 15 of a row to the next row (rows 1 and 3 written)
 constexpr int kDppRowBcast31 = 0x143;  // lane 31 to rows 2 and 3
 

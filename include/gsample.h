@@ -137,7 +137,11 @@ int gs_validate_configs(gs_context* ctx, const gs_row_config* configs, int32_t n
 
 /* Context: device ordinal, vocab size V (1 .. 2097152; larger returns
  * GS_ERR_UNSUPPORTED), the largest batch it will see. Calls on one context
- * share its scratch memory, so they must be ordered on one stream.
+ * share its scratch memory, so they must be ordered on one stream. Device
+ * memory: per row about V / 2 bytes of chunk statistics and lists, plus
+ * 36 * 2^ceil(log2 V) bytes of exact-path scratch for each of
+ * min(max_rows, max(64, 2.5 GiB / that)) rows -- rows beyond those, in
+ * larger batches, share the slots through a second kernel.
  * (no reference counterpart: the reference keeps its WebGPU device in a
  *  module singleton, src/webgpu/device.ts:4-40) */
 int gs_create(int device, int32_t vocab_size, int32_t max_rows, gs_context** out);
@@ -268,7 +272,7 @@ int gs_check_exp2(gs_context* ctx, float lo, float hi, double* max_rel_err, floa
 #define GS_STAGE_LMHEAD 0 /* lmhead_kernel */
 #define GS_STAGE_SCAN 1   /* scan_kernel: the one HBM pass over the logits */
 #define GS_STAGE_FINISH 2 /* finish_kernel: per-row merge, filters and draw */
-#define GS_STAGE_EXACT 3  /* exact_kernel: sequential replay of queued rows */
+#define GS_STAGE_EXACT 3  /* exact_kernel: replay of rows beyond the context's exact slots */
 #define GS_STAGE_COUNT 4
 int gs_timing_begin(gs_context* ctx, int32_t max_calls);
 int gs_timing_end(gs_context* ctx, double* stage_ms, int32_t* calls);
