@@ -252,11 +252,12 @@ __device__ void top_r(const uint64_t* s, int n, uint64_t* tmp, uint64_t* top) {
 // [lo, hi]. A 256-bin histogram of (key - lo) >> shift finds the bin holding
 // the kTopR-th largest key: every entry of a higher bin outranks it, so the
 // entries of that bin and above (the survivors) hold the top kTopR. A crowded
-// boundary bin gets a second histogram inside it. When at most 128 entries
-// survive, each finds its place by counting the survivors above it. Returns false, with top
-// untouched, when more survive (massive ties); the caller then ranks the
-// whole region. hist: 256 counters, zero on entry and on return; sel: 4
-// words; out: 128 entries of scratch. Ends with a barrier.
+// boundary bin gets a second histogram inside it. The survivors (at most
+// 128) are compacted and each finds its place by counting the survivors
+// above it. Returns false, with top untouched, when more survive (massive
+// ties); the caller then ranks the whole region. hist: 256 counters, zero on
+// entry and on return; sel: 4 words; out: 128 entries of scratch (16-byte
+// aligned, at least 129 entries). Ends with a barrier.
 __device__ __forceinline__ int top_select_shift(uint32_t lo, uint32_t hi) {
   const uint32_t span = hi - lo;
   int shift = 0;
@@ -264,37 +265,33 @@ __device__ __forceinline__ int top_select_shift(uint32_t lo, uint32_t hi) {
   return shift;
 }
 
-// hist_ready: hist already holds the first round's counts of s[0..n)
-// (bins (key - lo) >> top_select_shift(lo, hi), clamped to 255).
-__device__ bool top_select(const uint64_t* s, int n, uint32_t lo, uint32_t hi, uint32_t* hist, uint32_t* sel,
-                           uint64_t* out, uint64_t* top, bool hist_ready) {
+// The selection over entries the threads hold in registers: thread t's e[q]
+// is an entry when bit q of `valid` is set. n (block-uniform) counts them, or
+// is -1: then the first histogram pass also counts them into *n_out (zero on
+// entry; one LDS atomic per wave). The histogram settles any count, so the
+// pass runs whenever the count is unknown or above 128.
+template <int kE>
+__device__ __forceinline__ bool top_select_regs(const uint64_t (&e)[kE], uint32_t valid, int n, uint32_t lo,
+                                                uint32_t hi, uint32_t* hist, uint32_t* sel, uint64_t* out,
+                                                uint64_t* top, uint32_t* n_out) {
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  constexpr int kMaxE = kFinishCap / kFinishThreads;  // entries per thread
   constexpr int kOut = 128;
-  const uint64_t* src = s;  // the survivors' array
-  int n_src = n;
-  if (n <= kOut && hist_ready) {
-    if (tid < 256) hist[tid] = 0;  // left zero for the next use
+  uint32_t floor_key = 0;  // survivors: valid entries with key >= floor_key
+  if (n < 0) {
+    const uint32_t w = wave_sum_u32((uint32_t)__popc(valid));
+    if (lane == 0 && w) atomicAdd(n_out, w);
   }
-  if (n > kOut) {
-    uint64_t e[kMaxE];
-#pragma unroll
-    for (int q = 0; q < kMaxE; ++q) {
-      const int i = tid + q * kFinishThreads;
-      e[q] = i < n ? s[i] : 0ull;
-    }
+  if (n > kOut || n < 0) {
     int shift = top_select_shift(lo, hi);
     uint32_t bin_lo = lo;    // start of the range being binned
     int width = 32;          // the range is [bin_lo, bin_lo + 2^width), 32: unbounded
     uint32_t above = 0;      // entries above the range (from the first round)
-    uint32_t floor_key = lo;
+    floor_key = lo;
     bool ok = false;
     for (int round = 0; round < 2 && !ok; ++round) {
 #pragma unroll
-      for (int q = 0; q < kMaxE; ++q) {
-        if (round == 0 && hist_ready) break;
-        const int i = tid + q * kFinishThreads;
-        if (i < n) {
+      for (int q = 0; q < kE; ++q) {
+        if ((valid >> q) & 1u) {
           const uint32_t d = entry_key(e[q]) - bin_lo;  // entries below bin_lo wrap to large values
           const bool in_range = entry_key(e[q]) >= bin_lo && (width >= 32 || (d >> width) == 0u);
           const uint32_t bin = d >> shift;
@@ -334,56 +331,70 @@ __device__ bool top_select(const uint64_t* s, int n, uint32_t lo, uint32_t hi, u
       }
     }
     if (!ok) return false;
-    // compact the survivors (keys >= floor_key) into out[]
-    if (tid == 0) sel[3] = 0;
-    __syncthreads();
-#pragma unroll
-    for (int q = 0; q < kMaxE; ++q) {
-      const int i = tid + q * kFinishThreads;
-      const bool keep = i < n && entry_key(e[q]) >= floor_key;
-      const uint64_t m = __ballot(keep);
-      uint32_t base = 0;
-      if (lane == 0 && m) base = atomicAdd(&sel[3], (uint32_t)__popcll(m));
-      base = readlane_u32(base, 0);
-      if (keep) {
-        const uint32_t pos =
-            base + __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
-        if (pos < (uint32_t)kOut) out[pos] = e[q];
-      }
-    }
-    __syncthreads();
-    src = out;
-    n_src = (int)(sel[3] < (uint32_t)kOut ? sel[3] : (uint32_t)kOut);
   }
+  // compact the survivors into out[] (one LDS atomic per wave)
+  if (tid == 0) sel[3] = 0;
+  __syncthreads();
+#pragma unroll
+  for (int q = 0; q < kE; ++q) {
+    const bool keep = ((valid >> q) & 1u) && entry_key(e[q]) >= floor_key;
+    const uint64_t m = __ballot(keep);
+    uint32_t base = 0;
+    if (lane == 0 && m) base = atomicAdd(&sel[3], (uint32_t)__popcll(m));
+    base = readlane_u32(base, 0);
+    if (keep) {
+      const uint32_t pos =
+          base + __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
+      if (pos < (uint32_t)kOut) out[pos] = e[q];
+    }
+  }
+  __syncthreads();
+  const uint64_t* src = out;
+  const int n_src = (int)(sel[3] < (uint32_t)kOut ? sel[3] : (uint32_t)kOut);
   // rank the survivors (at most 128) by counting: the entries are distinct,
   // so survivor i's place is the number of survivors above it. Eight threads
-  // share survivor tid / 8, each counting over 16 of the survivors (src holds
+  // share survivor tid / 8, each counting over 16 of the survivors (out holds
   // at least 128 entries), and the eight counts meet by DPP; places past the
   // survivors stay zero.
   {
     const int i = tid >> 3, part = tid & 7;
-    uint64_t e = 0;
+    uint64_t ei = 0;
     uint32_t cnt = 0;
     if (i < n_src) {
-      e = src[i];
+      ei = src[i];
       const uint4* p = (const uint4*)(src + part * 16);
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
         const uint4 w = p[j];
         const int k = part * 16 + 2 * j;
         const uint64_t x0 = ((uint64_t)w.y << 32) | w.x, x1 = ((uint64_t)w.w << 32) | w.z;
-        cnt += (k < n_src && x0 > e) ? 1u : 0u;
-        cnt += (k + 1 < n_src && x1 > e) ? 1u : 0u;
+        cnt += (k < n_src && x0 > ei) ? 1u : 0u;
+        cnt += (k + 1 < n_src && x1 > ei) ? 1u : 0u;
       }
     }
     cnt += dpp_u32<kDppQuad1032, 0xF>(0u, cnt);
     cnt += dpp_u32<kDppQuad2301, 0xF>(0u, cnt);
     cnt += dpp_u32<kDppRowHalfMirror, 0xF>(0u, cnt);  // lane l of 8 meets lane 7 - l: the other quad
-    if (part == 0 && i < n_src && cnt < (uint32_t)kTopR) top[cnt] = e;
+    if (part == 0 && i < n_src && cnt < (uint32_t)kTopR) top[cnt] = ei;
     if (tid >= n_src && tid < kTopR) top[tid] = 0;
   }
   __syncthreads();
   return true;
+}
+
+// The selection over the region s[0..n) in LDS (n <= kFinishCap).
+__device__ __forceinline__ bool top_select(const uint64_t* s, int n, uint32_t lo, uint32_t hi, uint32_t* hist,
+                                           uint32_t* sel, uint64_t* out, uint64_t* top) {
+  constexpr int kMaxE = kFinishCap / kFinishThreads;  // entries per thread
+  uint64_t e[kMaxE];
+  uint32_t valid = 0;
+#pragma unroll
+  for (int q = 0; q < kMaxE; ++q) {
+    const int i = threadIdx.x + q * kFinishThreads;
+    e[q] = i < n ? s[i] : 0ull;
+    valid |= (i < n ? 1u : 0u) << q;
+  }
+  return top_select_regs<kMaxE>(e, valid, n, lo, hi, hist, sel, out, top, nullptr);
 }
 
 // special_insert that also reports the id's slot and whether this call put
@@ -683,9 +694,10 @@ __device__ __forceinline__ uint32_t finish_row(const SampleArgs& a, FinishLds& U
   uint64_t lv[kSubPerThread];
 #pragma unroll
   for (int q = 0; q < kSpecQ; ++q) lv[q] = lists[(int64_t)(sl0 < n_subs ? sl0 : 0) * kSubCap + k0 + q * kSubThreads];
-  int64_t h0 = 0, h1 = 0, f0 = 0, f1 = 0;
-  if (a.history_offsets) { h0 = a.history_offsets[row]; h1 = a.history_offsets[row + 1]; }
-  if (a.forced_offsets) { f0 = a.forced_offsets[row]; f1 = a.forced_offsets[row + 1]; }
+  // absent arrays are read at a valid address (the configs) and dropped
+  const int64_t* hoff = a.history_offsets ? a.history_offsets : (const int64_t*)a.configs;
+  const int64_t* foff = a.forced_offsets ? a.forced_offsets : (const int64_t*)a.configs;
+  const int64_t h0r = hoff[row], h1r = hoff[row + 1], f0r = foff[row], f1r = foff[row + 1];
 
   const gs_row_config cfg = a.configs[row];
   const Plan plan = plan_row(cfg);
@@ -696,7 +708,9 @@ __device__ __forceinline__ uint32_t finish_row(const SampleArgs& a, FinishLds& U
   const int32_t slot = cfg.mask_slot;
   const bool constrained = slot >= 0 && slot < a.mask_slots;
   const double T = cfg.temperature;
-  if (!constrained) f0 = f1 = 0;  // forced ids belong to constrained rows only
+  const int64_t h0 = a.history_offsets ? h0r : 0, h1 = a.history_offsets ? h1r : 0;
+  // forced ids belong to constrained rows only
+  const int64_t f0 = constrained && a.forced_offsets ? f0r : 0, f1 = constrained && a.forced_offsets ? f1r : 0;
 
   // the penalty window (sampling.ts:22-24)
   int64_t w0 = 0, w1 = 0;
@@ -705,26 +719,32 @@ __device__ __forceinline__ uint32_t finish_row(const SampleArgs& a, FinishLds& U
     w0 = s0 > h0 ? s0 : h0;
     w1 = h1;
   }
-  int32_t wid[kIdsPerThread];
+  // The window and forced ids this thread owns, loaded unconditionally (a
+  // position past the list reads its last entry, an empty list a valid dummy
+  // address) and dropped where used: a load under a branch that may be
+  // skipped would make every later wait for an earlier load a full wait.
+  constexpr int kOwn = kIdsPerThread + 1;
+  int32_t oraw_id[kOwn];
+  bool oid_ok[kOwn];
+  uint8_t fkind_raw;
+  {
+    const bool has_win = w1 > w0;
+    const int32_t* wb = has_win ? a.history_ids : (const int32_t*)a.configs;
 #pragma unroll
-  for (int r = 0; r < kIdsPerThread; ++r) {
-    const int64_t j = w0 + tid + (int64_t)r * kFinishThreads;
-    wid[r] = j < w1 ? a.history_ids[j] : -1;
+    for (int r = 0; r < kIdsPerThread; ++r) {
+      const int64_t j = w0 + tid + (int64_t)r * kFinishThreads;
+      oid_ok[r] = j < w1;
+      oraw_id[r] = wb[has_win ? (j < w1 ? j : w1 - 1) : 0];
+    }
+    const bool has_forced = f1 > f0;
+    const int64_t jf = has_forced ? (f0 + tid < f1 ? f0 + tid : f1 - 1) : 0;
+    oid_ok[kIdsPerThread] = f0 + tid < f1;
+    oraw_id[kIdsPerThread] = (has_forced ? a.forced_ids : (const int32_t*)a.configs)[jf];
+    fkind_raw = (has_forced ? a.forced_kinds : (const uint8_t*)a.configs)[jf];
   }
   // specials this thread owns the loads of: its window positions and its
   // first forced id; rows with longer lists evaluate from the hash slots
   const bool own_path = w1 - w0 <= (int64_t)kIdsPerThread * kFinishThreads && f1 - f0 <= kFinishThreads;
-  constexpr int kOwn = kIdsPerThread + 1;
-  int32_t oid[kOwn];
-  uint32_t okind[kOwn];
-#pragma unroll
-  for (int r = 0; r < kIdsPerThread; ++r) { oid[r] = wid[r]; okind[r] = 0; }
-  oid[kIdsPerThread] = -1;
-  okind[kIdsPerThread] = 0;
-  if (f0 + tid < f1) {
-    oid[kIdsPerThread] = a.forced_ids[f0 + tid];
-    okind[kIdsPerThread] = (uint32_t)a.forced_kinds[f0 + tid] & 3u;
-  }
 
   if (tid == 0) {
     S.flags = 0; S.max_key = 0; S.thr_max = 0; S.any_truncated = 0; S.n_sorted = 0; S.n_special = 0;
@@ -754,26 +774,44 @@ __device__ __forceinline__ uint32_t finish_row(const SampleArgs& a, FinishLds& U
   }
   // the owned specials' logits and mask words start loading now; they are
   // first used after the region is ranked
+  int32_t oid[kOwn];
+  uint32_t okind[kOwn];
+#pragma unroll
+  for (int r = 0; r < kOwn; ++r) {
+    oid[r] = oid_ok[r] ? oraw_id[r] : -1;
+    okind[r] = r == kIdsPerThread ? (uint32_t)fkind_raw & 3u : 0u;
+  }
   uint32_t oraw[kOwn];  // logit bits as loaded (bf16: the 16 bits, widened at use)
   uint32_t omw[kOwn];
   int oslot[kOwn];
   bool ofirst[kOwn];
+  // Every load issued so far has arrived by now (they went out before the
+  // row's configuration came back); wait for them here, before the first
+  // loads that only some rows issue. A later wait for one of them (or a reuse
+  // of its register) would otherwise count those too and wait for the gathers.
+  asm volatile("" ::"v"(lv[0]), "v"(lv[1]), "v"((uint32_t)fkind_raw));
   {
-    bool ok[kOwn];
+    // unconditional loads again: ids that are not owned read index 0
+    int64_t gi[kOwn];
 #pragma unroll
-    for (int r = 0; r < kOwn; ++r) ok[r] = own_path && oid[r] >= 0 && oid[r] < a.vocab;
+    for (int r = 0; r < kOwn; ++r) gi[r] = own_path && oid[r] >= 0 && oid[r] < a.vocab ? oid[r] : 0;
     if (a.dtype == GS_BF16) {
       const uint16_t* lp = (const uint16_t*)a.logits + row * a.row_stride;
 #pragma unroll
-      for (int r = 0; r < kOwn; ++r) oraw[r] = ok[r] ? (uint32_t)lp[oid[r]] : 0u;
+      for (int r = 0; r < kOwn; ++r) oraw[r] = lp[gi[r]];
     } else {
       const uint32_t* lp = (const uint32_t*)a.logits + row * a.row_stride;
 #pragma unroll
-      for (int r = 0; r < kOwn; ++r) oraw[r] = ok[r] ? lp[oid[r]] : 0u;
+      for (int r = 0; r < kOwn; ++r) oraw[r] = lp[gi[r]];
     }
+    // mask words for constrained rows only (a branch the whole workgroup takes)
 #pragma unroll
-    for (int r = 0; r < kOwn; ++r)
-      omw[r] = ok[r] && constrained ? a.mask_table[(int64_t)slot * a.mask_words + (oid[r] >> 5)] : 0u;
+    for (int r = 0; r < kOwn; ++r) omw[r] = 0u;
+    if (constrained) {
+      const uint32_t* mrow = a.mask_table + (int64_t)slot * a.mask_words;
+#pragma unroll
+      for (int r = 0; r < kOwn; ++r) omw[r] = mrow[gi[r] >> 5];
+    }
   }
   // distinct special ids into the hash
   {
@@ -863,13 +901,18 @@ __device__ __forceinline__ uint32_t finish_row(const SampleArgs& a, FinishLds& U
       }
     }
   };
-  if (!greedy) {
-    // the first kSpecQ * kSubThreads slots of every sub-list came with the
-    // statistics; deeper slots (rows with some longer sub-list) are read in a
-    // pass of their own, so that the common path never waits for loads
-    // issued after the special gathers
-    constexpr int kHead = kSpecQ * kSubThreads;
-    const int cnt0 = sl0 < n_subs ? (int)S.c_nsub[sl0] : 0;
+  // The fast selection works on the list entries the threads already hold:
+  // the first kSpecQ * kSubThreads slots of every sub-list came with the
+  // statistics (rows with no longer sub-list and at most
+  // kFinishThreads / kSubThreads sub-lists). Other rows, and the paths that
+  // need the whole region, append it to LDS; deeper slots are read there in a
+  // pass of their own, so that the common path never waits for loads issued
+  // after the special gathers.
+  constexpr int kHead = kSpecQ * kSubThreads;
+  const int cnt0 = sl0 < n_subs ? (int)S.c_nsub[sl0] : 0;
+  bool region_in_lds = false;
+  int n_region = 0;
+  auto fill_region = [&]() {  // block-wide, ends with a barrier
 #pragma unroll
     for (int q = kSpecQ; q < kSubPerThread; ++q) lv[q] = 0;
     append(lv, 0, cnt0 < kHead ? cnt0 : kHead);
@@ -894,14 +937,42 @@ __device__ __forceinline__ uint32_t finish_row(const SampleArgs& a, FinishLds& U
       }
       append(v, 0, cnt);
     }
-  }
-  __syncthreads();
-  const int n_region = (int)S.n_sorted;
+    __syncthreads();
+    n_region = (int)S.n_sorted;
+    region_in_lds = true;
+  };
   // the region's top kTopR non-specials, ranked while the specials' loads are
   // still in flight (false: too many ties, the fast path merges instead)
   bool top_ok = false;
-  if (!greedy && n_region <= kFinishCap)
-    top_ok = top_select(S.sorted, n_region, sel_lo, sel_hi, S.hist, S.sel, (uint64_t*)S.cand_p, S.top, false);
+  if (!greedy) {
+    if (!(S.flags & kDeepLists) && n_subs <= kFinishThreads / kSubThreads) {
+      uint64_t e[kSpecQ];
+      uint32_t valid = 0;
+#pragma unroll
+      for (int q = 0; q < kSpecQ; ++q) {
+        e[q] = 0;
+        if (k0 + q * kSubThreads < cnt0) {
+          e[q] = list_rank(lv[q]);
+          if (entry_key(e[q]) >= thr) valid |= 1u << q;
+        }
+      }
+      top_ok = top_select_regs<kSpecQ>(e, valid, -1, sel_lo, sel_hi, S.hist, S.sel, (uint64_t*)S.cand_p, S.top,
+                                       &S.n_sorted);
+      n_region = (int)S.n_sorted;
+    } else {
+      fill_region();
+      if (n_region <= kFinishCap)
+        top_ok = top_select(S.sorted, n_region, sel_lo, sel_hi, S.hist, S.sel, (uint64_t*)S.cand_p, S.top);
+    }
+  }
+  // the whole region in LDS, for the paths that rank or sort it
+  auto need_region = [&]() {
+    if (region_in_lds) return;
+    __syncthreads();
+    if (tid == 0) S.n_sorted = 0;
+    __syncthreads();
+    fill_region();
+  };
 
   // evaluate every special exactly: mask / termination rules, then penalties.
   // Slots, flags and the maximum are gathered per wave, one LDS atomic each.
@@ -1134,6 +1205,7 @@ __device__ __forceinline__ uint32_t finish_row(const SampleArgs& a, FinishLds& U
   if (n_sp_in <= 2 * kTopR - n_top_all) {
     uint64_t* tmp = (uint64_t*)S.cand_p;  // kWaves * 64 entries of merge scratch
     if (!top_ok) {
+      need_region();
       if (n_ns <= kWaves * 64) top_r<1>(S.sorted, n_ns, tmp, S.top);
       else if (n_ns <= kWaves * 128) top_r<2>(S.sorted, n_ns, tmp, S.top);
       else top_r<4>(S.sorted, n_ns, tmp, S.top);
@@ -1223,6 +1295,7 @@ __device__ __forceinline__ uint32_t finish_row(const SampleArgs& a, FinishLds& U
   // ---- slow path: the whole region sorted, then the filters block-wide
   {
     uint64_t* scratch = (uint64_t*)S.cand_p;
+    need_region();
     if (n_ns <= kFinishThreads) sort_region<1>(S.sorted, n_ns, scratch);
     else if (n_ns <= 2 * kFinishThreads) sort_region<2>(S.sorted, n_ns, scratch);
     else sort_region<4>(S.sorted, n_ns, scratch);
