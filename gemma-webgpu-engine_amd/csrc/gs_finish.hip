@@ -700,7 +700,7 @@ __device__ __forceinline__ uint32_t finish_row(const SampleArgs& a, FinishLds& U
   const int64_t h0r = hoff[row], h1r = hoff[row + 1], f0r = foff[row], f1r = foff[row + 1];
 
   const gs_row_config cfg = a.configs[row];
-  const Plan plan = plan_row(cfg);
+  const Plan plan = plan_row_flat(cfg);
   if (plan.route == kRouteExact) {
     return kExactRequest | 0u;
   }

@@ -95,13 +95,24 @@ struct Plan {
   int32_t depth;  // per-chunk rank depth of the one-pass path
 };
 
-// Every field is read whatever the route (selects, not branches), so that a
-// kernel fetches the whole configuration at once instead of one field after
-// another behind branches.
 __host__ __device__ __forceinline__ Plan plan_row(const gs_row_config& c) {
+  if (c.temperature == 0) return Plan{kRouteGreedy, 1};
+  if (c.options & GS_ROW_FORCE_EXACT) return Plan{kRouteExact, 0};
+  // between these bounds l/T keeps the order and the ties of the f32 logits
+  if (!(c.temperature >= 1.0e-200 && c.temperature <= 1.0e200)) return Plan{kRouteExact, 0};
+  if (c.typical_p < 1) return Plan{kRouteExact, 0};
+  if (c.top_k > 0)
+    return c.top_k <= kMaxFastK ? Plan{kRouteTopK, c.top_k < kTopKChunkDepth ? c.top_k : kTopKChunkDepth}
+                                : Plan{kRouteExact, 0};
+  if (c.top_p < 1 || c.min_p > 0) return Plan{kRouteTopP, kTopPListL};
+  return Plan{kRouteExact, 0};
+}
+// plan_row with every field read whatever the route (selects, not branches),
+// so that a kernel fetches the whole configuration at once instead of one
+// field after another behind branches
+__device__ __forceinline__ Plan plan_row_flat(const gs_row_config& c) {
   const bool greedy = c.temperature == 0;
   const bool forced = (c.options & GS_ROW_FORCE_EXACT) != 0;
-  // between these bounds l/T keeps the order and the ties of the f32 logits
   const bool t_out = !(c.temperature >= 1.0e-200 && c.temperature <= 1.0e200);
   const bool typical = c.typical_p < 1;
   const bool topk = c.top_k > 0, topk_fast = c.top_k <= kMaxFastK;
@@ -261,26 +272,31 @@ __device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
   GS_WAVE_REDUCE(uint64_t, dpp_u64, v, 0ull, op_max_u64);
   return readlane_u64(v, 63);
 }
-// the maximum and minimum of the wave's values, in every lane
+// the maximum and minimum of the wave's values, in every lane (the two
+// chains interleaved step by step)
 __device__ __forceinline__ void wave_max_min_u32(uint32_t v, uint32_t* vmax, uint32_t* vmin) {
   uint32_t a = v, b = v;
-  GS_WAVE_REDUCE(uint32_t, dpp_u32, a, 0u, op_max_u32);
-  GS_WAVE_REDUCE(uint32_t, dpp_u32, b, 0xFFFFFFFFu, op_min_u32);
+#define GS_MM_STEP(C, M)                                \
+  { const uint32_t x = dpp_u32<C, M>(0u, a);            \
+    const uint32_t y = dpp_u32<C, M>(0xFFFFFFFFu, b);   \
+    a = x > a ? x : a; b = y < b ? y : b; }
+  GS_MM_STEP(kDppQuad1032, 0xF) GS_MM_STEP(kDppQuad2301, 0xF) GS_MM_STEP(kDppRowRor4, 0xF)
+  GS_MM_STEP(kDppRowRor8, 0xF) GS_MM_STEP(kDppRowBcast15, 0xA) GS_MM_STEP(kDppRowBcast31, 0xC)
+#undef GS_MM_STEP
   *vmax = readlane_u32(a, 63);
   *vmin = readlane_u32(b, 63);
 }
 // the sum of the wave's binary64 values (a fixed order), in every lane
 __device__ __forceinline__ double wave_sum_f64_dpp(double v) {
-  uint64_t u = __builtin_bit_cast(uint64_t, v);
-#define GS_SUM_STEP(C, M)                                                                \
-  {                                                                                      \
-    const double o = __builtin_bit_cast(double, dpp_u64<C, M>(0ull, u));                 \
-    u = __builtin_bit_cast(uint64_t, __builtin_bit_cast(double, u) + o);                 \
-  }
+#define GS_SUM_STEP(C, M)                                                            \
+  { const uint64_t u = __builtin_bit_cast(uint64_t, v);                              \
+    const uint32_t lo = dpp_u32<C, M>(0u, (uint32_t)u);                              \
+    const uint32_t hi = dpp_u32<C, M>(0u, (uint32_t)(u >> 32));                      \
+    v += __builtin_bit_cast(double, ((uint64_t)hi << 32) | lo); }
   GS_SUM_STEP(kDppQuad1032, 0xF) GS_SUM_STEP(kDppQuad2301, 0xF) GS_SUM_STEP(kDppRowRor4, 0xF)
   GS_SUM_STEP(kDppRowRor8, 0xF) GS_SUM_STEP(kDppRowBcast15, 0xA) GS_SUM_STEP(kDppRowBcast31, 0xC)
 #undef GS_SUM_STEP
-  return __builtin_bit_cast(double, readlane_u64(u, 63));
+  return readlane_f64(v, 63);
 }
 // Inclusive prefix sums across the wave: within each row of 16 lanes by
 // row_shr 1, 2, 4, 8 (lanes without a source add zero), then the last lane
