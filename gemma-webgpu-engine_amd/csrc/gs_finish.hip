@@ -42,8 +42,8 @@ constexpr int kSubThreads = 8;                        // threads that read one w
 constexpr int kSubPerThread = kSubCap / kSubThreads;  // slots each of them reads
 constexpr int kSlotsPerThread = kHashSize / kFinishThreads;
 constexpr int kIdsPerThread = 2;                      // window ids loaded ahead per thread
-constexpr int kSpecQ = 2;  // list slots per thread read with the statistics (16 per sub-list)
-constexpr uint32_t kDeepLists = 1u << 30;  // row flag: some sub-list holds more than 16 entries
+constexpr int kSpecQ = 4;  // list slots per thread read with the statistics (32 per sub-list)
+constexpr uint32_t kDeepLists = 1u << 30;  // row flag: some sub-list holds more than 32 entries
 constexpr uint32_t kExactRequest = 1u << 31;  // finish_row's answer: the row goes to the exact path
 static_assert(kFinishMaxChunks * kScanWaves <= kFinishThreads, "one thread per chunk wave");
 
@@ -690,16 +690,18 @@ __device__ __forceinline__ uint32_t finish_row(const SampleArgs& a, FinishLds& U
   const uint32_t w_trunc = wc->truncated;
   const uint64_t* lists = a.lists + row * a.n_chunks * kGatherCap;
   const int n_subs = a.n_chunks * kScanWaves;
-  const int sl0 = tid / kSubThreads, k0 = tid % kSubThreads;
-  uint64_t lv[kSubPerThread];
-#pragma unroll
-  for (int q = 0; q < kSpecQ; ++q) lv[q] = lists[(int64_t)(sl0 < n_subs ? sl0 : 0) * kSubCap + k0 + q * kSubThreads];
   // absent arrays are read at a valid address (the configs) and dropped
   const int64_t* hoff = a.history_offsets ? a.history_offsets : (const int64_t*)a.configs;
   const int64_t* foff = a.forced_offsets ? a.forced_offsets : (const int64_t*)a.configs;
   const int64_t h0r = hoff[row], h1r = hoff[row + 1], f0r = foff[row], f1r = foff[row + 1];
 
   const gs_row_config cfg = a.configs[row];
+  // the list slots go out after the configuration: the first wait (for the
+  // configuration) does not wait for them
+  const int sl0 = tid / kSubThreads, k0 = tid % kSubThreads;
+  uint64_t lv[kSubPerThread];
+#pragma unroll
+  for (int q = 0; q < kSpecQ; ++q) lv[q] = lists[(int64_t)(sl0 < n_subs ? sl0 : 0) * kSubCap + k0 + q * kSubThreads];
   const Plan plan = plan_row_flat(cfg);
   if (plan.route == kRouteExact) {
     return kExactRequest | 0u;
@@ -789,7 +791,8 @@ __device__ __forceinline__ uint32_t finish_row(const SampleArgs& a, FinishLds& U
   // row's configuration came back); wait for them here, before the first
   // loads that only some rows issue. A later wait for one of them (or a reuse
   // of its register) would otherwise count those too and wait for the gathers.
-  asm volatile("" ::"v"(lv[0]), "v"(lv[1]), "v"((uint32_t)fkind_raw));
+  static_assert(kSpecQ == 4, "the list slots read with the statistics, waited for here");
+  asm volatile("" ::"v"(lv[0]), "v"(lv[1]), "v"(lv[2]), "v"(lv[3]), "v"((uint32_t)fkind_raw));
   {
     // unconditional loads again: ids that are not owned read index 0
     int64_t gi[kOwn];
