@@ -845,7 +845,7 @@ __device__ __forceinline__ uint32_t finish_row(const SampleArgs& a, FinishLds& U
   // ---- second batch of global loads: the hash-slot specials' logits and
   // mask words (rows whose specials are not owned) and the list slots past
   // the first kSpecQ
-  const uint32_t thr = S.thr_max;  // 0 when no chunk was truncated: every finite logit is listed
+  uint32_t thr = S.thr_max;  // 0 when no chunk was truncated: every finite logit is listed
   // the specials to evaluate: each owner's (own_path), else every hash slot
   constexpr int kEval = kSlotsPerThread > kOwn ? kSlotsPerThread : kOwn;
   uint32_t hid[kEval], hpk[kEval], mw[kEval];
@@ -964,8 +964,53 @@ __device__ __forceinline__ uint32_t finish_row(const SampleArgs& a, FinishLds& U
       n_region = (int)S.n_sorted;
     } else {
       fill_region();
+      if (n_region > kFinishCap) {
+        // More entries than the LDS region holds. Any floor above the current
+        // one leaves a complete region: a histogram of the listed keys (read
+        // again from the lists) finds the lowest bin boundary with at most
+        // kFinishCap entries above it, and the region is filled again above it.
+        const int shift = top_select_shift(sel_lo, sel_hi);
+        for (int s0 = 0; s0 < n_subs; s0 += kFinishThreads / kSubThreads) {
+          const int sl = s0 + tid / kSubThreads;
+          const int cnt = sl < n_subs ? (int)S.c_nsub[sl] : 0;
+#pragma unroll 1
+          for (int k = k0; k < cnt; k += kSubThreads) {
+            const uint32_t key = entry_key(list_rank(lists[(int64_t)sl * kSubCap + k]));
+            if (key >= thr) {
+              const uint32_t bin = (key - sel_lo) >> shift;
+              atomicAdd(&S.hist[bin < 255u ? bin : 255u], 1u);
+            }
+          }
+        }
+        __syncthreads();
+        if (wave == 0) {
+          // lane l holds bins 255-4l .. 252-4l, highest first
+          uint32_t h[4], c = 0;
+#pragma unroll
+          for (int q = 0; q < 4; ++q) { h[q] = S.hist[255 - 4 * lane - q]; c += h[q]; }
+          const uint32_t incl = wave_scan_u32(c);
+          const uint64_t hit = __ballot(incl > (uint32_t)kFinishCap);
+          const int first = hit ? __ffsll((unsigned long long)hit) - 1 : 64;
+          if (lane == first) {
+            uint32_t cum = incl - c;
+            int q = 0;
+            while (cum + h[q] <= (uint32_t)kFinishCap) { cum += h[q]; ++q; }
+            S.sel[0] = (uint32_t)(255 - 4 * lane - q) + 1u;  // the lowest bin kept (256: none)
+          }
+          if (first == 64 && lane == 0) S.sel[0] = 0u;
+        }
+        __syncthreads();
+        const uint32_t b = S.sel[0];
+        if (tid < 256) S.hist[tid] = 0;
+        if (b == 0u || b > 255u) return kExactRequest | 0u;  // all of it fits, or no boundary fits
+        thr = sel_lo + (b << shift);
+        if (tid == 0) { S.n_sorted = 0; S.any_truncated = 1u; }
+        __syncthreads();
+        fill_region();
+      }
       if (n_region <= kFinishCap)
-        top_ok = top_select(S.sorted, n_region, sel_lo, sel_hi, S.hist, S.sel, (uint64_t*)S.cand_p, S.top);
+        top_ok = top_select(S.sorted, n_region, thr > sel_lo ? thr : sel_lo, sel_hi, S.hist, S.sel,
+                            (uint64_t*)S.cand_p, S.top);
     }
   }
   // the whole region in LDS, for the paths that rank or sort it
