@@ -645,12 +645,32 @@ __device__ double recompute_nonspecial_sum(const SampleArgs& a, int64_t row, con
   auto term = [&](float l) -> double {
     if (cfg.softcap > 0) l = gsm::softcap_f32(l, cfg.softcap);
     const double y = ((double)l / T - M) * GS_256_LOG2E;
-    return y > kSkipY ? exp2_256(y, c_exp2_256) : 0.0;
+    // evaluated for every y (no branch), so that independent terms overlap;
+    // exp2_256 reads its table at an index masked to 0..255 for any y
+    const double e = exp2_256(y, c_exp2_256);
+    return y > kSkipY ? e : 0.0;
   };
   double all = 0.0, sp = 0.0;
-  for (int64_t i = tid; i < a.vocab; i += kFinishThreads) {
-    if (mrow && !((mrow[i >> 5] >> (i & 31)) & 1u)) continue;
-    all += term(load_logit(a, row, i));
+  // the loads of kBatch elements go out together (one memory round trip per
+  // batch, not per element) and their terms overlap; the sum keeps each
+  // thread's order
+  constexpr int kBatch = 4;
+  const int64_t V = a.vocab;
+  for (int64_t i0 = tid; i0 < V; i0 += (int64_t)kBatch * kFinishThreads) {
+    float l[kBatch];
+    bool ok[kBatch];
+#pragma unroll
+    for (int k = 0; k < kBatch; ++k) {
+      const int64_t i = i0 + (int64_t)k * kFinishThreads;
+      const int64_t ic = i < V ? i : V - 1;  // in bounds; dropped below
+      l[k] = load_logit(a, row, ic);
+      ok[k] = i < V && (!mrow || ((mrow[ic >> 5] >> (ic & 31)) & 1u));
+    }
+    double t[kBatch];
+#pragma unroll
+    for (int k = 0; k < kBatch; ++k) t[k] = term(l[k]);
+#pragma unroll
+    for (int k = 0; k < kBatch; ++k) all += ok[k] ? t[k] : 0.0;
   }
   for (int i = tid; i < n_sp; i += kFinishThreads) {
     const uint32_t id = sp_id[i];
