@@ -58,7 +58,12 @@ namespace {
 
 constexpr int kChunkWords = kChunk / 32;  // special-bitmap words of one chunk
 constexpr int kMaxGroupChunks = 16;       // chunks one group workgroup streams
-constexpr int kScanWgPerCu = 4;           // resident scan workgroups per CU (launch bound)
+// Resident scan workgroups per CU (the launch bound). The constrained
+// variants carry the masked and the unmasked group scan in one kernel and
+// need more registers: bound at 4 they spill (f32: 117 VGPRs), so they trade
+// occupancy for a spill-free loop (f32 189 VGPRs, bf16 143).
+template <typename In, bool kMaskable>
+constexpr int scan_wg_per_cu() { return !kMaskable ? 4 : sizeof(In) == 4 ? 2 : 3; }
 // word 3 of a raw buffer resource on gfx9-family parts (gfx950 included)
 constexpr int32_t kBufferWord3 = 0x00020000;
 
@@ -562,7 +567,7 @@ struct ScanGrid {
 // kMaskable: the batch has a mask table (otherwise no row is constrained and
 // the masked variants are left out).
 template <typename In, bool kMaskable>
-__global__ __launch_bounds__(kScanThreads, kScanWgPerCu) void scan_kernel(SampleArgs a, ScanGrid g) {
+__global__ __launch_bounds__(kScanThreads, (scan_wg_per_cu<In, kMaskable>())) void scan_kernel(SampleArgs a, ScanGrid g) {
   __shared__ ScanShared S;
   constexpr int kLoads = kElemsPerThread / VecTraits<In>::kVec;
   const int64_t row = blockIdx.y;
@@ -646,26 +651,35 @@ void launch_exp2_check(uint32_t first, uint32_t count, unsigned long long* worst
   hipLaunchKernelGGL(exp2_check_kernel, dim3((count + 255) / 256), dim3(256), 0, s, first, count, worst);
 }
 
-void launch_scan(const SampleArgs& a, hipStream_t s, LaunchEvents ev) {
+namespace {
+
+template <typename In, bool kMaskable>
+void launch_scan_as(const SampleArgs& a, hipStream_t s, LaunchEvents ev) {
   // group workgroups over the full chunks of 16-byte aligned rows: as many
-  // per row as fills every CU once (kScanWgPerCu each), at least one per
+  // per row as fills every CU once (scan_wg_per_cu each), at least one per
   // kMaxGroupChunks chunks and at most one per chunk
   ScanGrid g;
   const int32_t n_full = a.vector_ok ? a.vocab / kChunk : 0;
-  int64_t per_row = (int64_t)a.cu_count * kScanWgPerCu / a.rows;
+  int64_t per_row = (int64_t)a.cu_count * scan_wg_per_cu<In, kMaskable>() / a.rows;
   const int64_t min_groups = (n_full + kMaxGroupChunks - 1) / kMaxGroupChunks;
   if (per_row < min_groups) per_row = min_groups;
   if (per_row > n_full) per_row = n_full;
   g.n_groups = (int32_t)per_row;
   g.n_grouped = n_full;
   dim3 grid(g.n_groups + (a.n_chunks - n_full), a.rows);
+  hipExtLaunchKernelGGL((scan_kernel<In, kMaskable>), grid, dim3(kScanThreads), 0, s, ev.start, ev.stop, 0, a, g);
+}
+
+}  // namespace
+
+void launch_scan(const SampleArgs& a, hipStream_t s, LaunchEvents ev) {
   const bool maskable = a.mask_slots > 0;
   if (a.dtype == GS_BF16) {
-    if (maskable) hipExtLaunchKernelGGL((scan_kernel<uint16_t, true>), grid, dim3(kScanThreads), 0, s, ev.start, ev.stop, 0, a, g);
-    else hipExtLaunchKernelGGL((scan_kernel<uint16_t, false>), grid, dim3(kScanThreads), 0, s, ev.start, ev.stop, 0, a, g);
+    if (maskable) launch_scan_as<uint16_t, true>(a, s, ev);
+    else launch_scan_as<uint16_t, false>(a, s, ev);
   } else {
-    if (maskable) hipExtLaunchKernelGGL((scan_kernel<float, true>), grid, dim3(kScanThreads), 0, s, ev.start, ev.stop, 0, a, g);
-    else hipExtLaunchKernelGGL((scan_kernel<float, false>), grid, dim3(kScanThreads), 0, s, ev.start, ev.stop, 0, a, g);
+    if (maskable) launch_scan_as<float, true>(a, s, ev);
+    else launch_scan_as<float, false>(a, s, ev);
   }
 }
 
