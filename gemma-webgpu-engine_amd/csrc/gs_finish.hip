@@ -651,12 +651,48 @@ __device__ double recompute_nonspecial_sum(const SampleArgs& a, int64_t row, con
     return y > kSkipY ? e : 0.0;
   };
   double all = 0.0, sp = 0.0;
-  // the loads of kBatch elements go out together (one memory round trip per
-  // batch, not per element) and their terms overlap; the sum keeps each
-  // thread's order
-  constexpr int kBatch = 4;
   const int64_t V = a.vocab;
-  for (int64_t i0 = tid; i0 < V; i0 += (int64_t)kBatch * kFinishThreads) {
+  if (mrow) {
+    // constrained rows: only legal ids contribute (masked logits are -inf).
+    // A thread holds kWords mask words and takes, per pass, the lowest set
+    // bit of each: kWords independent loads per memory round trip, as many
+    // passes as the wave's fullest word has bits, masked ids never evaluated
+    constexpr int kWords = 4;
+    const int32_t n_words = a.mask_words;
+    for (int32_t w0 = tid; w0 < n_words; w0 += kWords * kFinishThreads) {
+      uint32_t m[kWords];
+#pragma unroll
+      for (int k = 0; k < kWords; ++k) {
+        const int32_t w = w0 + k * kFinishThreads;
+        m[k] = w < n_words ? mrow[w] : 0u;
+      }
+      for (;;) {
+        uint32_t any = 0;
+#pragma unroll
+        for (int k = 0; k < kWords; ++k) any |= m[k];
+        if (!any) break;
+        float l[kWords];
+        bool ok[kWords];
+#pragma unroll
+        for (int k = 0; k < kWords; ++k) {
+          const int64_t id = (int64_t)(w0 + k * kFinishThreads) * 32 + (m[k] ? __builtin_ctz(m[k]) : 0);
+          ok[k] = m[k] != 0u && id < V;
+          l[k] = load_logit(a, row, ok[k] ? id : 0);
+          m[k] &= m[k] - 1u;
+        }
+        double t[kWords];
+#pragma unroll
+        for (int k = 0; k < kWords; ++k) t[k] = term(l[k]);
+#pragma unroll
+        for (int k = 0; k < kWords; ++k) all += ok[k] ? t[k] : 0.0;
+      }
+    }
+  }
+  // unconstrained rows: every id. The loads of kBatch elements go out
+  // together (one memory round trip per batch, not per element) and their
+  // terms overlap; the sum keeps each thread's order
+  constexpr int kBatch = 4;
+  for (int64_t i0 = mrow ? V : tid; i0 < V; i0 += (int64_t)kBatch * kFinishThreads) {
     float l[kBatch];
     bool ok[kBatch];
 #pragma unroll
@@ -664,7 +700,7 @@ __device__ double recompute_nonspecial_sum(const SampleArgs& a, int64_t row, con
       const int64_t i = i0 + (int64_t)k * kFinishThreads;
       const int64_t ic = i < V ? i : V - 1;  // in bounds; dropped below
       l[k] = load_logit(a, row, ic);
-      ok[k] = i < V && (!mrow || ((mrow[ic >> 5] >> (ic & 31)) & 1u));
+      ok[k] = i < V;
     }
     double t[kBatch];
 #pragma unroll

@@ -270,6 +270,43 @@ def test_topp_cut_inside_scan_normaliser_bound(sampler, oracle):
 
 
 
+def test_constrained_topp_cut_inside_scan_normaliser_bound(sampler, oracle):
+    """Constrained rows (about 3% of ids legal, the first and last ids among
+    them) whose top-p cut lies within the scan normaliser's bound: the
+    binary64 recomputation visits only the legal ids, by the mask words' set
+    bits. Ids and probabilities are the oracle's; the cuts beyond 4e-9 stay
+    on the one-pass path, the one inside it takes the exact replay."""
+    import torch
+
+    gs = _gs()
+    V = 262144
+    rng = np.random.default_rng(23)
+    x = rng.normal(0, 3, V).astype(np.float32)
+    legal = np.union1d(rng.choice(V, V // 32, replace=False), [0, V - 2, V - 1])
+    words = np.zeros(V // 32, np.uint32)
+    np.bitwise_or.at(words, legal >> 5, np.left_shift(np.uint32(1), (legal & 31).astype(np.uint32)))
+    assert np.array_equal(oracle.mask_bits_to_ids(words, V), legal)
+    masked = oracle.mask_logits(x, legal, [])
+    probe = gs.DecodingConfig(temperature=1.0, topK=0, topP=0.95, repetitionPenalty=1.0, repetitionWindow=0)
+    _, tr = oracle.sample_token(masked, [], to_oracle_cfg(probe), 0.5)
+    cum = tr.cumulative_at_cut
+    assert 0.95 <= cum < 1.0, cum
+    rels = ((-1e-8, False), (1e-8, False), (-3e-7, False), (2e-7, False), (-1e-11, True))
+    cfgs = [probe.merged(topP=cum * (1.0 + rel)) for rel, _ in rels]
+    us = [0.41 + 0.1 * i for i in range(len(rels))]
+    conf = np.stack([gs.runtime.row_config(c, uniform=u, mask_slot=0) for c, u in zip(cfgs, us)])
+    masks = torch.from_numpy(words.view(np.int32)[None].copy()).cuda()
+    out = sampler.sample(torch.from_numpy(np.stack([x] * len(rels))).cuda(), conf, mask_table=masks)
+    expected = []
+    for c, u in zip(cfgs, us):
+        t, trc = oracle.sample_token(masked, [], to_oracle_cfg(c), u)
+        expected.append((t, trc.probability))
+    assert_rows_match(out, expected, label="constrained topp_near")
+    for r, (_, want_exact) in enumerate(rels):
+        assert bool(out.flags[r] & gs.GS_FLAG_EXACT_PATH) == want_exact, (r, int(out.flags[r]))
+        assert out.flags[r] & gs.GS_FLAG_TOPP_TIE, (r, int(out.flags[r]))
+
+
 def test_single_row_config(sampler, oracle):
     import torch
 
