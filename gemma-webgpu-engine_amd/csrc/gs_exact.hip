@@ -1,6 +1,6 @@
 // Exact-path kernel: the rows queued by the finish kernel that have no
 // scratch slot of their own (batches with more rows than slots). One
-// 1024-thread workgroup per slot walks the device queue; every workgroup
+// 1024-thread workgroup per slot, at most one per CU, walks the device queue; every workgroup
 // leaves once the queue is drained. The replay itself is in gs_exact_row.h.
 #include "gs_exact_row.h"
 
@@ -30,7 +30,10 @@ __global__ __launch_bounds__(kExactThreads) void exact_kernel(SampleArgs a) {
 }  // namespace
 
 void launch_exact(const SampleArgs& a, hipStream_t s, LaunchEvents ev) {
-  hipExtLaunchKernelGGL(exact_kernel, dim3(a.exact_slots), dim3(kExactThreads), 0, s, ev.start, ev.stop, 0, a);
+  // one resident workgroup per CU at most: the workgroups walk the queue, so
+  // more of them only add a second round of launches to an empty queue
+  const int n = a.exact_slots < a.cu_count ? a.exact_slots : a.cu_count;
+  hipExtLaunchKernelGGL(exact_kernel, dim3(n > 0 ? n : 1), dim3(kExactThreads), 0, s, ev.start, ev.stop, 0, a);
 }
 
 }  // namespace gs
