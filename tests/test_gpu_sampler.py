@@ -353,6 +353,41 @@ def test_heavy_tail_bf16(sampler, oracle):
     assert_rows_match(out, exp, label="heavy_tail")
 
 
+def test_constrained_bf16_mixed_batch(sampler, oracle):
+    """bf16 logits with a mask table: constrained rows (about 3% of ids
+    legal) and unconstrained rows (no mask slot) in one batch run the bf16
+    constrained scan variant through both its masked and its unmasked group
+    scan. Ids and probabilities are the oracle's on the same bf16 values."""
+    import torch
+
+    gs = _gs()
+    V = 262144
+    rng = np.random.default_rng(31)
+    x32 = rng.normal(0, 3, (6, V)).astype(np.float32)
+    u32 = x32.view(np.uint32)
+    bits = ((u32 + np.uint32(0x7FFF) + ((u32 >> 16) & np.uint32(1))) >> 16).astype(np.uint16)
+    legal = np.union1d(rng.choice(V, V // 32, replace=False), [0, V - 1])
+    words = np.zeros(V // 32, np.uint32)
+    np.bitwise_or.at(words, legal >> 5, np.left_shift(np.uint32(1), (legal & 31).astype(np.uint32)))
+    slots = [0, -1, 0, -1, 0, -1]
+    base = gs.DecodingConfig(temperature=1.0, topK=0, topP=0.9, repetitionPenalty=1.0, repetitionWindow=0)
+    cfgs = [base, base.merged(topK=40, temperature=0.8), base.merged(topP=0.95), base.merged(topK=64),
+            base.merged(temperature=0.0), base.merged(temperature=0.0)]
+    us = [0.13 + 0.14 * i for i in range(6)]
+    conf = np.stack([gs.runtime.row_config(c, uniform=u, mask_slot=m) for c, u, m in zip(cfgs, us, slots)])
+    masks = torch.from_numpy(words.view(np.int32)[None].copy()).cuda()
+    x = torch.from_numpy(bits.view(np.int16)).cuda().view(torch.bfloat16)
+    out = sampler.sample(x, conf, mask_table=masks)
+    expected = []
+    for i in range(6):
+        f = gs.workloads.bf16_bits_to_f32(bits[i])
+        if slots[i] >= 0:
+            f = oracle.mask_logits(f, legal, [])
+        t, tr = oracle.sample_token(f, [], to_oracle_cfg(cfgs[i]), us[i])
+        expected.append((t, tr.probability))
+    assert_rows_match(out, expected, label="constrained bf16 mixed")
+
+
 def test_constrained_masks_and_samples(sampler, oracle):
     import torch
 
