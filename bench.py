@@ -3,7 +3,9 @@
 
 A step is one gs_sample call (chunk scan -> row finish -> exact replay) over a
 batch of synthetic logits already resident in HBM; `value` is sampled rows per
-second over the timed steps. The default workload is the batched penalties +
+second over the timed steps. The steps rotate over copies of the logits whose
+total size is three times the 256 MB Infinity Cache, so no step finds its
+logits left in that cache by the step before. The default workload is the batched penalties +
 top-k/top-p case: 256 rows x 262144 f32 logits ~ N(0, 3^2), 512-id Zipf(1.1)
 histories, repetition 1.1 / presence 0.5 / frequency 0.3 over a 512-id window,
 temperature 0.7, topK 50, topP 0.9, row r drawing SeededRandom(r).next().
@@ -21,10 +23,12 @@ The same run reports
                 scales rocprofv3's FETCH_SIZE + WRITE_SIZE per dispatch by
                 what those counters read for a copy of known size); null when
                 no such summary exists;
-  cpu_baseline  the JavaScript restatement of the reference sampler run by
-                Node on one host core over a bounded sample of the same rows
-                (falls back to the C restatement when node is absent), and a
-                bit-exact comparison of those rows' token ids.
+  cpu_baseline  the JavaScript restatement of the reference sampler (and of
+                its constraint masking for constrained rows) run by Node over
+                bounded samples of the same rows: (i) on one thread, as the
+                reference runs; (ii) split over worker_threads, one per host
+                core up to --cpu-threads; and a bit-exact comparison of those
+                rows' token ids with the GPU's.
 
 usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload NAME]
 """
@@ -82,8 +86,12 @@ def parse_args():
     ap.add_argument("--steps", type=int, default=100)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--workload", default="penalties",
-                    choices=["penalties", "single_row", "heavy_tail", "constrained", "lmhead"])
-    ap.add_argument("--cpu-rows", type=int, default=128, help="rows of the CPU baseline sample (about 14 s on one core)")
+                    choices=["penalties", "single_row", "heavy_tail", "constrained", "lmhead", "multinomial",
+                             "topk_deep", "typical"])
+    ap.add_argument("--cpu-rows", type=int, default=128,
+                    help="rows of the one-thread CPU baseline sample (about 13 s on one core)")
+    ap.add_argument("--cpu-threads", type=int, default=16,
+                    help="worker threads of the all-cores CPU baseline leg (one per host core, at most this)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--copy-probe", action="store_true",
                     help="also time a plain device copy of the logits' byte count (achievable HBM bandwidth; "
@@ -93,41 +101,62 @@ def parse_args():
 
 # ----------------------------------------------------------------- workloads
 
+# Bytes of logits the timed steps rotate through, so that no step reads its
+# logits from the 256 MB Infinity Cache a previous step left them in.
+ROTATE_BYTES = 3 * (256 << 20)
+PLAIN = {"multinomial": "T 0.8, topK 0, topP 1 (a full-vocabulary draw, the generate() defaults with a temperature)",
+         "topk_deep": "T 0.8, topK 200, topP 0.95", "typical": "T 0.8, topK 40, typicalP 0.9"}
+
+
+def rotated(torch, device, host, dtype_in):
+    """n >= 1 device copies of the [rows][V] logits whose total size is at
+    least ROTATE_BYTES, as one tensor [n][rows][V]."""
+    if dtype_in == "bf16":
+        t = torch.from_numpy(host.view(np.int16)).to(device).view(torch.bfloat16)
+    else:
+        t = torch.from_numpy(host).to(device)
+    nbytes = t.numel() * t.element_size()
+    n = max(2, -(-ROTATE_BYTES // nbytes))
+    out = torch.empty((n,) + tuple(t.shape), dtype=t.dtype, device=device)
+    out[:] = t
+    return out
+
 
 def build_workload(name, gs, torch, device):
-    """Device-resident inputs + the gs_batch for one workload.
+    """Device-resident inputs + one gs_batch per rotated logits copy.
 
-    Returns dict(rows, batch, keep, sampler, desc, scan_bytes_per_row, step_bytes, rows_cpu, ...)."""
+    Returns dict(rows, batches=[(batch, keep)], sampler, desc, scan_bytes_per_row, step_bytes, cpu=..., ...)."""
     W = gs.workloads
     rt = gs.runtime
     out = {"name": name}
-    if name in ("penalties", "single_row"):
-        w = W.penalties() if name == "penalties" else W.single_row()
-        window = w.configs[0].repetitionWindow
+    if name in ("penalties", "single_row", "heavy_tail") or name in PLAIN:
+        if name == "penalties":
+            w = W.penalties()
+        elif name == "single_row":
+            w = W.single_row()
+        elif name == "heavy_tail":
+            w = W.heavy_tail()
+        else:
+            w = getattr(W, name)()
+        window = w.configs[0].repetitionWindow if w.histories is not None else 0
         conf = np.stack([rt.row_config(c, seed=s) for c, s in zip(w.configs, w.seeds)])
         s = gs.Sampler(vocab_size=V, max_rows=w.rows)
-        logits = torch.from_numpy(w.logits).to(device)
-        batch, keep = s.prepare(logits, conf, histories=w.histories)
-        per_row = 4 * V + 4 * window  # logits + window ids, read once by the scan
-        out.update(rows=w.rows, sampler=s, batch=batch, keep=keep, workload=w, dtype_in="f32",
-                   scan_bytes_per_row=per_row, step_bytes=w.rows * (per_row + 8),
-                   dominant="scan",
-                   desc=(f"{name}: {w.rows} x {V} f32 logits ~ N(0, 3^2); "
-                         + ("512-id Zipf(1.1) histories, repetition 1.1, presence 0.5, frequency 0.3, window 512; "
-                            "T 0.7, topK 50, topP 0.9; row r seeds SeededRandom(r)"
-                            if name == "penalties" else "T 0.8, topK 40, topP 0.95, seed 42")))
-        return out
-    if name == "heavy_tail":
-        w = W.heavy_tail()
-        conf = np.stack([rt.row_config(c, seed=s) for c, s in zip(w.configs, w.seeds)])
-        s = gs.Sampler(vocab_size=V, max_rows=w.rows)
-        logits = torch.from_numpy(w.logits.view(np.int16)).to(device).view(torch.bfloat16)
-        batch, keep = s.prepare(logits, conf)
-        per_row = 2 * V
-        out.update(rows=w.rows, sampler=s, batch=batch, keep=keep, workload=w, dtype_in="bf16",
-                   scan_bytes_per_row=per_row, step_bytes=w.rows * (per_row + 8), dominant="scan",
-                   desc=f"heavy_tail: {w.rows} x {V} bf16 logits 8 ln(rank^-1.1) + N(0, 0.5^2), permuted per row; "
-                        "topP 0.9, T 1, seed = row")
+        copies = rotated(torch, device, w.logits, w.dtype)
+        batches = [s.prepare(copies[i], conf, histories=w.histories) for i in range(copies.shape[0])]
+        esize = 2 if w.dtype == "bf16" else 4
+        per_row = esize * V + 4 * window  # logits + window ids, read once by the scan
+        if name == "penalties":
+            desc = ("penalties: 256 x 262144 f32 logits ~ N(0, 3^2); 512-id Zipf(1.1) histories, repetition 1.1, "
+                    "presence 0.5, frequency 0.3, window 512; T 0.7, topK 50, topP 0.9; row r seeds SeededRandom(r)")
+        elif name == "single_row":
+            desc = "single_row: 1 x 262144 f32 logits ~ N(0, 3^2); T 0.8, topK 40, topP 0.95, seed 42"
+        elif name == "heavy_tail":
+            desc = (f"heavy_tail: {w.rows} x {V} bf16 logits 8 ln(rank^-1.1) + N(0, 0.5^2), permuted per row; "
+                    "topP 0.9, T 1, seed = row")
+        else:
+            desc = f"{name}: {w.rows} x {V} f32 logits ~ N(0, 3^2); {PLAIN[name]}; seed = row"
+        out.update(rows=w.rows, sampler=s, batches=batches, copies=copies, workload=w, dtype_in=w.dtype,
+                   scan_bytes_per_row=per_row, step_bytes=w.rows * (per_row + 8), dominant="scan", desc=desc)
         return out
     if name == "constrained":
         w = W.constrained()
@@ -139,12 +168,12 @@ def build_workload(name, gs, torch, device):
         table = s.build_masks(list(range(64)))
         conf = np.stack([rt.row_config(c, seed=sd, mask_slot=int(st))
                          for c, sd, st in zip(w.configs, w.seeds, w.states)])
-        logits = torch.from_numpy(w.logits).to(device)
-        batch, keep = s.prepare(logits, conf, mask_table=table)
+        copies = rotated(torch, device, w.logits, "f32")
+        batches = [s.prepare(copies[i], conf, mask_table=table) for i in range(copies.shape[0])]
         per_row = 4 * V + (V // 8)  # logits + the row's legal-token bitmask
-        out.update(rows=w.rows, sampler=s, batch=batch, keep=keep, workload=w, dtype_in="f32",
+        out.update(rows=w.rows, sampler=s, batches=batches, copies=copies, workload=w, dtype_in="f32",
                    scan_bytes_per_row=per_row, step_bytes=w.rows * (per_row + 8), dominant="scan",
-                   masks=table, vocab_tables=(offsets, data, nxt, finals),
+                   masks=table, dfa=(offsets, data, nxt, finals),
                    desc=f"constrained: {w.rows} x {V} f32 logits ~ N(0, 3^2); synthetic 1-12-byte vocab, 64-state "
                         "byte DFA (~3% legal), per-row start state; topP 0.95, T 1 (masks built once per state)")
         return out
@@ -164,9 +193,9 @@ def build_workload(name, gs, torch, device):
         scratch = torch.empty((M, V), dtype=torch.float32, device=device)
         batch, keep = s.prepare(scratch, conf, histories=hist, mask_table=table)
         keep += [hidden, weight, scratch]
-        out.update(rows=M, sampler=s, batch=batch, keep=keep, dtype_in="bf16", hidden=hidden, weight=weight,
-                   scratch=scratch, histories=hist, states=states, masks=table,
-                   lm_bytes=2 * V * D + 2 * M * D + 4 * M * V, lm_flops=2 * M * D * V,
+        out.update(rows=M, sampler=s, batches=[(batch, keep)], dtype_in="bf16", hidden=hidden, weight=weight,
+                   scratch=scratch, histories=hist, states=states, masks=table, dfa=(offsets, data, nxt, finals),
+                   lm_bytes=2 * V * D + 2 * M * D, lm_logits_bytes=4 * M * V, lm_flops=2 * M * D * V,
                    step_bytes=2 * V * D + 2 * M * D + 4 * 256 * M + 8 * M, dominant="lmhead",
                    desc=f"lmhead: H {M} x {D} bf16 ~ N(0,1), W {V} x {D} bf16 ~ N(0, 0.02^2), softcap 30, "
                         "256-id histories (window 256), DFA masks, topK 64, topP 0.95, T 1, seed = row")
@@ -174,82 +203,116 @@ def build_workload(name, gs, torch, device):
     raise SystemExit(f"unknown workload {name}")
 
 
-def launch_step(wl, stream):
+def launch_step(wl, i, stream):
     s = wl["sampler"]
+    batch = wl["batches"][i % len(wl["batches"])][0]
     if wl["name"] == "lmhead":
-        s.lmhead_sample_launch(wl["hidden"], wl["weight"], 30.0, wl["scratch"], wl["batch"], stream)
+        s.lmhead_sample_launch(wl["hidden"], wl["weight"], 30.0, wl["scratch"], batch, stream)
     else:
-        s.launch(wl["batch"], stream)
+        s.launch(batch, stream)
 
 
 # -------------------------------------------------------------- CPU baseline
 
 
-def cpu_baseline(wl, gs, tokens, probs, n_rows):
-    """Times the reference sampler's restatement on a bounded row sample and
-    compares its ids with the GPU's on those rows."""
-    if wl["name"] not in ("penalties", "single_row", "heavy_tail"):
-        return None, None
-    w = wl["workload"]
-    step = max(1, w.rows // n_rows)
-    pick = list(range(0, w.rows, step))[:n_rows]
-    node = shutil.which("node")
-    if node:
-        tmp = tempfile.mkdtemp(prefix="gs_cpu_")
-        try:
-            sub = np.ascontiguousarray(w.logits[pick])
-            sub.tofile(os.path.join(tmp, "logits.bin"))
-            spec = {"logits": os.path.join(tmp, "logits.bin"), "dtype": wl["dtype_in"], "rows": len(pick),
-                    "vocab": V, "pick": list(range(len(pick))), "seeds": [w.seeds[r] for r in pick],
-                    "warmup": 1, "out": os.path.join(tmp, "out.json"),
-                    "configs": [{k: getattr(w.configs[r], k) for k in (
-                        "temperature", "topK", "topP", "minP", "typicalP", "repetitionPenalty", "repetitionWindow",
-                        "frequencyPenalty", "presencePenalty")} for r in pick]}
-            if w.histories is not None:
-                hist = [np.asarray(w.histories[r], np.int32) for r in pick]
-                off = np.zeros(len(pick) + 1, np.float64)
-                off[1:] = np.cumsum([h.size for h in hist])
-                off.tofile(os.path.join(tmp, "hoff.bin"))
-                np.concatenate(hist).astype(np.int32).tofile(os.path.join(tmp, "hids.bin"))
-                spec["history_offsets"] = os.path.join(tmp, "hoff.bin")
-                spec["history_ids"] = os.path.join(tmp, "hids.bin")
-            with open(os.path.join(tmp, "spec.json"), "w") as f:
-                json.dump(spec, f)
-            runner = os.path.join(ROOT, "oracle", "node_runner.js")
-            log(f"cpu baseline: node on {len(pick)} rows")
-            subprocess.run([node, runner, os.path.join(tmp, "spec.json")], check=True, timeout=600)
-            with open(os.path.join(tmp, "out.json")) as f:
-                res = json.load(f)
-        finally:
-            shutil.rmtree(tmp, ignore_errors=True)
-        seconds = res["seconds"]
-        ref_tokens, ref_probs = res["tokens"], res["probabilities"]
-        kind_note = f"JavaScript restatement on Node {res['node']}, 1 thread, {res['cpu_model']} ({res['host_cpus']} host cpus)"
-    else:
-        from oracle import oracle as orc  # the checker's C restatement
+def _cfg_dict(c):
+    return {k: getattr(c, k) for k in ("temperature", "topK", "topP", "minP", "typicalP", "repetitionPenalty",
+                                        "repetitionWindow", "frequencyPenalty", "presencePenalty")}
 
-        log(f"cpu baseline: C restatement on {len(pick)} rows")
-        ref_tokens, ref_probs = [], []
-        seconds = 0.0
-        for r in pick:
-            c = w.configs[r]
-            x = w.logits[r] if wl["dtype_in"] == "f32" else gs.workloads.bf16_bits_to_f32(w.logits[r])
-            cfg = orc.Decoding(temperature=c.temperature, topK=c.topK, topP=c.topP, minP=c.minP, typicalP=c.typicalP,
-                               repetitionPenalty=c.repetitionPenalty, repetitionWindow=c.repetitionWindow,
-                               frequencyPenalty=c.frequencyPenalty, presencePenalty=c.presencePenalty)
-            hist = w.histories[r] if w.histories is not None else []
-            t0 = time.perf_counter()
-            t, tr = orc.sample_token(x, hist, cfg, orc.draw(w.seeds[r], 0))
-            seconds += time.perf_counter() - t0
-            ref_tokens.append(t)
-            ref_probs.append(tr.probability)
-        kind_note = "C restatement (oracle/sampler_ref.c), 1 thread"
-    mism = [r for k, r in enumerate(pick) if int(tokens[r]) != int(ref_tokens[k])]
-    rel = max((abs(probs[r] - ref_probs[k]) / abs(ref_probs[k]) if ref_probs[k] else 0.0)
-              for k, r in enumerate(pick))
-    base = {"value": len(pick) / seconds, "unit": "rows/s", "cores": 1, "kind": "port",
-            "sample": f"{len(pick)} of the {w.rows} rows (one row in {step}), {seconds:.2f} s; {kind_note}"}
-    parity = {"rows_checked": len(pick), "token_mismatches": len(mism), "max_prob_rel_diff": rel}
+
+def cpu_inputs(wl):
+    """(logits [rows][V] as stored, dtype, configs, seeds, histories, constraint) of the workload
+    for the CPU restatement; the lm_head workload's logits are the ones the GPU produced."""
+    if wl["name"] == "lmhead":
+        logits = wl["scratch"].cpu().numpy()
+        import gsample
+
+        cfgs = [gsample.workloads.LMHEAD_CONFIG] * wl["rows"]
+        return logits, "f32", cfgs, list(range(wl["rows"])), wl["histories"], wl["states"]
+    w = wl["workload"]
+    return w.logits, wl["dtype_in"], w.configs, w.seeds, w.histories, (w.states if wl["name"] == "constrained"
+                                                                       else None)
+
+
+def run_node_leg(wl, node, pick, threads, tmp):
+    """The JavaScript restatement over rows `pick` on `threads` Node threads."""
+    logits, dtype, cfgs, seeds, hists, states = cpu_inputs(wl)
+    sub = np.ascontiguousarray(logits[pick])
+    sub.tofile(os.path.join(tmp, "logits.bin"))
+    spec = {"logits": os.path.join(tmp, "logits.bin"), "dtype": dtype, "rows": len(pick), "vocab": V,
+            "pick": list(range(len(pick))), "seeds": [int(seeds[r]) for r in pick], "warmup": 1,
+            "threads": threads, "out": os.path.join(tmp, "out.json"),
+            "configs": [_cfg_dict(cfgs[r]) for r in pick]}
+    if hists is not None:
+        hist = [np.asarray(hists[r], np.int32) for r in pick]
+        off = np.zeros(len(pick) + 1, np.float64)
+        off[1:] = np.cumsum([h.size for h in hist])
+        off.tofile(os.path.join(tmp, "hoff.bin"))
+        np.concatenate(hist).astype(np.int32).tofile(os.path.join(tmp, "hids.bin"))
+        spec["history_offsets"] = os.path.join(tmp, "hoff.bin")
+        spec["history_ids"] = os.path.join(tmp, "hids.bin")
+    if states is not None:
+        offsets, data, nxt, finals = wl["dfa"]
+        np.asarray(offsets, np.float64).tofile(os.path.join(tmp, "voff.bin"))
+        np.asarray(data, np.uint8).tofile(os.path.join(tmp, "vbytes.bin"))
+        np.asarray(nxt, np.int32).tofile(os.path.join(tmp, "next.bin"))
+        np.asarray(finals, np.uint8).tofile(os.path.join(tmp, "finals.bin"))
+        spec["constraint"] = {"next": os.path.join(tmp, "next.bin"), "finals": os.path.join(tmp, "finals.bin"),
+                              "states": int(nxt.shape[0]), "vocab_offsets": os.path.join(tmp, "voff.bin"),
+                              "vocab_bytes": os.path.join(tmp, "vbytes.bin"),
+                              "row_states": [int(states[r]) for r in pick], "termination": []}
+    with open(os.path.join(tmp, "spec.json"), "w") as f:
+        json.dump(spec, f)
+    runner = os.path.join(ROOT, "oracle", "node_runner.js")
+    subprocess.run([node, runner, os.path.join(tmp, "spec.json")], check=True, timeout=900)
+    with open(os.path.join(tmp, "out.json")) as f:
+        return json.load(f)
+
+
+def cpu_baseline(wl, tokens, probs, n_rows, threads_cap):
+    """Times the reference sampler's JavaScript restatement (with the masking
+    restatement for constrained rows) on Node on bounded row samples: (i) one
+    thread, as the reference runs; (ii) the rows split over worker threads,
+    one per host core up to `threads_cap`. Compares both legs' ids with the
+    GPU's on those rows."""
+    node = shutil.which("node")
+    if not node:
+        log("cpu baseline: node is not installed; skipped")
+        return None, None
+    rows = wl["rows"]
+    step = max(1, rows // n_rows)
+    pick1 = list(range(0, rows, step))[:n_rows]
+    host_cpus = os.cpu_count() or 1
+    threads = max(1, min(threads_cap, host_cpus))
+    pickn = list(range(min(rows, 256)))
+    tmp = tempfile.mkdtemp(prefix="gs_cpu_")
+    try:
+        log(f"cpu baseline (i): node, 1 thread, {len(pick1)} rows")
+        r1 = run_node_leg(wl, node, pick1, 1, tmp)
+        log(f"cpu baseline (ii): node, {threads} threads, {len(pickn)} rows")
+        rn = run_node_leg(wl, node, pickn, threads, tmp)
+    finally:
+        shutil.rmtree(tmp, ignore_errors=True)
+    checked, mism, rel = 0, 0, 0.0
+    for res, pick in ((r1, pick1), (rn, pickn)):
+        for k, r in enumerate(pick):
+            checked += 1
+            if int(tokens[r]) != int(res["tokens"][k]):
+                mism += 1
+            p = res["probabilities"][k]
+            if p:
+                rel = max(rel, abs(probs[r] - p) / abs(p))
+    what = "the sampler" if wl["name"] not in ("constrained", "lmhead") else (
+        "legal-id walk (cached per state) + maskConstraintLogits + the sampler")
+    if wl["name"] == "lmhead":
+        what += " on the GPU-produced logits (no CPU bf16 GEMM exists in the reference)"
+    base = {"value": round(len(pick1) / r1["seconds"], 2), "unit": "rows/s", "cores": 1, "kind": "port",
+            "sample": (f"{len(pick1)} of the {rows} rows (one in {step}), {r1['seconds']:.2f} s; JavaScript "
+                       f"restatement of {what} on Node {r1['node']}, {r1['cpu_model']} ({r1['host_cpus']} host cpus)"),
+            "all_cores": {"value": round(len(pickn) / rn["seconds"], 2), "unit": "rows/s", "cores": rn["threads"],
+                          "sample": (f"{len(pickn)} rows split over {rn['threads']} worker_threads "
+                                     f"(one per host core, at most {threads_cap}), {rn['seconds']:.2f} s")}}
+    parity = {"rows_checked": checked, "token_mismatches": mism, "max_prob_rel_diff": rel}
     return base, parity
 
 
@@ -274,7 +337,8 @@ def main():
     t0 = time.time()
     wl = build_workload(args.workload, gs, torch, device)
     torch.cuda.synchronize()
-    log(f"workload ready in {time.time() - t0:.1f} s")
+    n_rot = len(wl["batches"])
+    log(f"workload ready in {time.time() - t0:.1f} s ({n_rot} rotated logits buffers)")
     s = wl["sampler"]
     # a dedicated stream at the default priority: torch's default stream has a
     # null handle, which the library would read as "use the context's stream"
@@ -282,17 +346,18 @@ def main():
     sp = stream.cuda_stream
     torch.cuda.synchronize()
 
-    for _ in range(args.warmup):
-        launch_step(wl, sp)
+    for i in range(args.warmup):
+        launch_step(wl, i, sp)
     torch.cuda.synchronize()
     log(f"warmup {args.warmup} steps done")
 
-    # the step rate: K steps bracketed by two events on the launch stream
+    # the step rate: K steps bracketed by two events on the launch stream,
+    # step i reading logits copy i mod n
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
     start.record(stream)
-    for _ in range(args.steps):
-        launch_step(wl, sp)
+    for i in range(args.steps):
+        launch_step(wl, i, sp)
     end.record(stream)
     torch.cuda.synchronize()
     total_ms = start.elapsed_time(end)
@@ -303,14 +368,15 @@ def main():
     # HIP events on the stream it runs on (the events slow a step down, so
     # the step rate above is timed without them)
     s.timing_begin(args.steps)
-    for _ in range(args.steps):
-        launch_step(wl, sp)
+    for i in range(args.steps):
+        launch_step(wl, i, sp)
     torch.cuda.synchronize()
     stages = s.timing_end()
     log(f"stage timing over {args.steps} more steps: {stages}")
 
     # results of the last step
-    res = wl["keep"][-1] if wl["name"] != "lmhead" else wl["keep"][-4]
+    last = (2 * args.steps - 1) % n_rot
+    res = wl["batches"][last][1][-1] if wl["name"] != "lmhead" else wl["batches"][0][1][-4]
     raw = res.cpu().numpy().view(np.uint8).reshape(-1)[: wl["rows"] * 16]
     rr = raw.view(gs.runtime.RESULT_DTYPE)
     tokens, probs, flags = rr["token"], rr["probability"], rr["flags"]
@@ -324,21 +390,25 @@ def main():
     dom_ms, dom_calls = stages[dom]
     dom_avg_ms = dom_ms / max(1, dom_calls)
     if dom == "lmhead":
-        achieved = wl["lm_bytes"] / (dom_avg_ms * 1e6)
+        algo = wl["lm_bytes"]
         mfma_tflops = wl["lm_flops"] / (dom_avg_ms * 1e9)
     else:
-        achieved = rows * wl["scan_bytes_per_row"] / (dom_avg_ms * 1e6)
+        algo = rows * wl["scan_bytes_per_row"]
         mfma_tflops = None
+    achieved = algo / (dom_avg_ms * 1e6)
     kname = {"scan": "scan_kernel", "lmhead": "lmhead_kernel"}[dom]
     roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                 "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": profiled_traffic(wl["name"], kname),
-                "kernel": kname, "algorithmic_bytes_per_launch": int(
-                    wl["lm_bytes"] if dom == "lmhead" else rows * wl["scan_bytes_per_row"]),
+                "kernel": kname, "algorithmic_bytes_per_launch": int(algo),
                 "kernel_avg_us": round(dom_avg_ms * 1000, 2),
-                "stage_avg_us": {k: round(v[0] / v[1] * 1000, 2) for k, v in stages.items() if v[1]}}
+                "stage_avg_us": {k: round(v[0] / v[1] * 1000, 2) for k, v in stages.items() if v[1]},
+                "rotated_logits_buffers": n_rot}
     if mfma_tflops is not None:
         roofline["mfma_tflops"] = round(mfma_tflops, 1)
         roofline["mfma_frac_bf16_dense"] = round(mfma_tflops / BF16_PEAK_TFLOPS, 4)
+        # the unfused logits write, reported beside the weight-streaming figure
+        roofline["logits_write_bytes"] = wl["lm_logits_bytes"]
+        roofline["achieved_with_logits_write"] = round((algo + wl["lm_logits_bytes"]) / (dom_avg_ms * 1e6), 1)
 
     if args.copy_probe:
         # a plain 256 MiB device-to-device copy: reads and writes each byte once
@@ -361,12 +431,15 @@ def main():
 
     base, parity = (None, None)
     if not args.no_cpu:
-        base, parity = cpu_baseline(wl, gs, tokens, probs, args.cpu_rows)
+        base, parity = cpu_baseline(wl, tokens, probs, args.cpu_rows, args.cpu_threads)
 
     line = {
         "metric": METRIC, "value": round(value, 1), "unit": "rows/s", "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "ms_per_step": round(ms_per_step, 5), "higher_is_better": True, "scaling": "weak",
-        "vs_baseline": None, "dtype": "f64", "data": "synthetic",
+        "vs_baseline": None, "dtype": "f32/f64",
+        "precision": ("logits f32 (bf16 widened exactly); normaliser terms binary32 hardware exp2 summed in "
+                      "binary64; every ranking, cut and draw decided in binary64 as the reference does"),
+        "data": "synthetic",
         "config": {"workload": wl["desc"], "rows": rows, "vocab": V, "logits_dtype": wl["dtype_in"]},
         "step_hbm_gbps": round(wl["step_bytes"] / (ms_per_step * 1e6), 1),
         "step_hbm_frac": round(wl["step_bytes"] / (ms_per_step * 1e6) / HBM_PEAK_GBPS, 4),

@@ -39,9 +39,6 @@ struct gs_context {
   std::vector<uint8_t> viable;
   int32_t* d_states = nullptr;
   int32_t states_cap = 0;
-  int32_t* d_tokens = nullptr;
-  double* d_logprob = nullptr;
-  int32_t tokens_cap = 0;
   // device staging for the host-array entry points (grown on demand)
   uint8_t* d_stage = nullptr;
   size_t stage_cap = 0;
@@ -123,8 +120,10 @@ int map_row_failures(gs_context* ctx, const gs_row_result* res, int32_t rows) {
     if (f & GS_FLAG_DEAD_END) return fail(ctx, GS_ERR_DEAD_END, "Generation constraint reached a tokenization dead end");
     if (f & GS_FLAG_EMPTY_CANDIDATES)
       return fail(ctx, GS_ERR_EMPTY_CANDIDATES, "min-p left no candidate token (row " + std::to_string(r) + ")");
+    if (f & GS_FLAG_INVALID_SLOT)
+      return fail(ctx, GS_ERR_INVALID_ARGUMENT, "row " + std::to_string(r) + ": mask_slot outside the mask table");
     if (f & GS_FLAG_UNSUPPORTED)
-      return fail(ctx, GS_ERR_UNSUPPORTED, "row " + std::to_string(r) + ": more than 2048 distinct penalty-window and forced ids");
+      return fail(ctx, GS_ERR_UNSUPPORTED, "row " + std::to_string(r) + ": beyond a documented size limit");
   }
   return GS_OK;
 }
@@ -223,8 +222,6 @@ int gs_destroy(gs_context* ctx) {
   free_dev(ctx->d_vocab_bytes);
   free_dev(ctx->d_next);
   free_dev(ctx->d_states);
-  free_dev(ctx->d_tokens);
-  free_dev(ctx->d_logprob);
   free_dev(ctx->d_stage);
   destroy_timing(ctx);
   if (ctx->stream) (void)hipStreamDestroy(ctx->stream);
@@ -513,34 +510,22 @@ int gs_token_log_prob_host(gs_context* ctx, const float* logits, int32_t rows, c
     }
   }
   if (rows == 0) return GS_OK;
+  // staged in the context's reusable device buffer: logits, tokens, results
+  const size_t logit_bytes = sizeof(float) * (size_t)rows * ctx->vocab;
+  const size_t o_tok = align256(logit_bytes);
+  const size_t o_out = o_tok + align256(sizeof(int32_t) * rows);
   GS_HIP(ctx, hipSetDevice(ctx->device));
-  float* d_logits = nullptr;
-  GS_HIP(ctx, hipMalloc(&d_logits, sizeof(float) * (size_t)rows * ctx->vocab));
-  if (rows > ctx->tokens_cap) {
-    free_dev(ctx->d_tokens);
-    free_dev(ctx->d_logprob);
-    ctx->d_tokens = nullptr;
-    ctx->d_logprob = nullptr;
-    GS_HIP(ctx, hipMalloc(&ctx->d_tokens, sizeof(int32_t) * rows));
-    GS_HIP(ctx, hipMalloc(&ctx->d_logprob, sizeof(double) * rows));
-    ctx->tokens_cap = rows;
-  }
-  int st = GS_OK;
-  if (hipMemcpyAsync(d_logits, logits, sizeof(float) * (size_t)rows * ctx->vocab, hipMemcpyHostToDevice, ctx->stream) !=
-          hipSuccess ||
-      hipMemcpyAsync(ctx->d_tokens, tokens, sizeof(int32_t) * rows, hipMemcpyHostToDevice, ctx->stream) != hipSuccess) {
-    st = fail(ctx, GS_ERR_HIP, "copy to device failed");
-  } else {
-    launch_logprob(d_logits, GS_F32, rows, ctx->vocab, ctx->vocab, ctx->d_tokens, ctx->d_logprob, ctx->stream);
-    if (hipGetLastError() != hipSuccess ||
-        hipMemcpyAsync(out, ctx->d_logprob, sizeof(double) * rows, hipMemcpyDeviceToHost, ctx->stream) != hipSuccess ||
-        hipStreamSynchronize(ctx->stream) != hipSuccess) {
-      st = fail(ctx, GS_ERR_HIP, "log-probability kernel failed");
-    }
-  }
-  (void)hipStreamSynchronize(ctx->stream);
-  free_dev(d_logits);
-  return st;
+  int st = ensure_stage(ctx, o_out + sizeof(double) * rows);
+  if (st != GS_OK) return st;
+  uint8_t* d = ctx->d_stage;
+  hipStream_t s = ctx->stream;
+  GS_HIP(ctx, hipMemcpyAsync(d, logits, logit_bytes, hipMemcpyHostToDevice, s));
+  GS_HIP(ctx, hipMemcpyAsync(d + o_tok, tokens, sizeof(int32_t) * rows, hipMemcpyHostToDevice, s));
+  launch_logprob(d, GS_F32, rows, ctx->vocab, ctx->vocab, (const int32_t*)(d + o_tok), (double*)(d + o_out), s);
+  GS_HIP(ctx, hipGetLastError());
+  GS_HIP(ctx, hipMemcpyAsync(out, d + o_out, sizeof(double) * rows, hipMemcpyDeviceToHost, s));
+  GS_HIP(ctx, hipStreamSynchronize(s));
+  return GS_OK;
 }
 
 int gs_check_exp2(gs_context* ctx, float lo, float hi, double* max_rel_err, float* worst_y) {

@@ -46,17 +46,14 @@ __device__ inline Scratch scratch_at(const SampleArgs& a, int64_t slot) {
 struct Lds {  // the replay's LDS (a finish workgroup reuses its own for it)
   uint64_t tkey[kExactTile];
   uint32_t tid_[kExactTile];
-  uint32_t hash_ids[kHashSize];
-  uint32_t hash_counts[kHashSize];
   double stage[kExactTile];
   double wtmp[kWaves];
   uint32_t wtmp_u[kWaves];
   uint64_t wtmp_k[kWaves];
   uint32_t row;
-  uint32_t n_special;
   uint32_t flag;
   uint32_t count;
-  int32_t legal;   // legal ids of a constrained row (mask bits adjusted for specials)
+  int32_t legal;   // legal ids of a constrained row
   double result_p;
   int32_t result_token;
   uint32_t result_flags;
@@ -193,66 +190,64 @@ __device__ __noinline__ void process_row(const SampleArgs& a, Lds& L, Scratch S,
   const int64_t N = pow2_ge(V);
   const double T = cfg.temperature;
 
-  // ---- values of every logit (masking, then penalties on the distinct window ids)
-  for (int h = tid; h < kHashSize; h += kExactThreads) { L.hash_ids[h] = 0xFFFFFFFFu; L.hash_counts[h] = 0; }
-  if (tid == 0) { L.n_special = 0; L.legal = 0; }
+  // ---- values of every logit (masking, then penalties on the distinct window
+  // ids). Window counts and forced kinds are kept per vocabulary id in the
+  // slot's scratch (sidx and order are free until the candidate reorderings
+  // below), so a window of any length and any number of distinct ids is
+  // counted exactly (sampling.ts:22-30).
+  uint32_t* counts = S.sidx;
+  uint32_t* kinds = S.order;
+  for (int64_t i = tid; i < V; i += kExactThreads) { counts[i] = 0; kinds[i] = 0; }
+  if (tid == 0) L.legal = 0;
   __syncthreads();
-  if (constrained) {
-    const uint32_t* m = a.mask_table + (int64_t)slot * a.mask_words;
-    int32_t bits = 0;
-    for (int w = tid; w < a.mask_words; w += kExactThreads) bits += __popc(m[w]);
-    atomicAdd(&L.legal, bits);
-  }
   {
     int64_t w0, w1;
     history_window(a, row, cfg, &w0, &w1);
-    SpecialTable tab{L.hash_ids, L.hash_counts};
     for (int64_t j = w0 + tid; j < w1; j += kExactThreads) {
       const int32_t id = a.history_ids[j];
-      if (id >= 0 && id < a.vocab) special_insert(tab, (uint32_t)id, 0u);
+      if (id >= 0 && id < a.vocab) atomicAdd(&counts[id], 1u);
     }
     if (constrained && a.forced_offsets) {
       const int64_t f0 = a.forced_offsets[row], f1 = a.forced_offsets[row + 1];
       for (int64_t j = f0 + tid; j < f1; j += kExactThreads) {
         const int32_t id = a.forced_ids[j];
-        if (id >= 0 && id < a.vocab) special_insert(tab, (uint32_t)id, (uint32_t)a.forced_kinds[j] & 3u);
+        if (id >= 0 && id < a.vocab) atomicOr(&kinds[id], (uint32_t)a.forced_kinds[j] & 3u);
       }
     }
   }
-  for (int64_t i = tid; i < N; i += kExactThreads) {
-    if (i < V) {
-      float x = load_logit(a, row, i);
-      if (cfg.softcap > 0) x = gsm::softcap_f32(x, cfg.softcap);
-      const bool allowed = !constrained || mask_allows(a, slot, i);
-      const double l = allowed ? (double)x : -__builtin_inf();
-      S.key[i] = f64_key(greedy ? l : l / T);
-      S.id[i] = (uint32_t)i;
-    } else {
-      S.key[i] = 0;
-      S.id[i] = 0xFFFFFFFFu;
-    }
-  }
   __syncthreads();
-  for (int h = tid; h < kHashSize; h += kExactThreads) {
-    const uint32_t id = L.hash_ids[h];
-    if (id == 0xFFFFFFFFu) continue;
-    const uint32_t packed = L.hash_counts[h];
-    const uint32_t count = packed & 0xFFFFFFu, kinds = packed >> 24;
-    float raw = load_logit(a, row, id);
-    if (cfg.softcap > 0) raw = gsm::softcap_f32(raw, cfg.softcap);
-    bool allowed = true;
+  {
+    int32_t legal = 0;  // legal ids this thread saw (constrained rows)
+    for (int64_t i = tid; i < N; i += kExactThreads) {
+      if (i < V) {
+        float x = load_logit(a, row, i);
+        if (cfg.softcap > 0) x = gsm::softcap_f32(x, cfg.softcap);
+        const uint32_t count = counts[i], kd = kinds[i];
+        bool allowed = true;
+        if (constrained) {
+          // selectConstrainedToken's legal set (gemma-session.ts:1305-1329):
+          // termination ids only when accepting, extra ids always, the rest by
+          // the mask
+          allowed = (kd & GS_FORCED_TERMINATION) ? cfg.accepting != 0
+                                                  : ((kd & GS_FORCED_EXTRA) != 0 || mask_allows(a, slot, i));
+          legal += allowed ? 1 : 0;
+        }
+        double l = allowed ? (double)x : -__builtin_inf();
+        if (count > 0) {
+          l = l < 0 ? l * cfg.repetition_penalty : l / cfg.repetition_penalty;
+          l -= cfg.presence_penalty + (double)count * cfg.frequency_penalty;
+        }
+        S.key[i] = f64_key(greedy ? l : l / T);
+        S.id[i] = (uint32_t)i;
+      } else {
+        S.key[i] = 0;
+        S.id[i] = 0xFFFFFFFFu;
+      }
+    }
     if (constrained) {
-      const bool term = kinds & GS_FORCED_TERMINATION;
-      const bool extra = kinds & GS_FORCED_EXTRA;
-      allowed = term ? cfg.accepting != 0 : (extra || mask_allows(a, slot, id));
-      atomicAdd(&L.legal, (allowed ? 1 : 0) - (mask_allows(a, slot, id) ? 1 : 0));
+      legal = (int32_t)wave_sum_u32((uint32_t)legal);
+      if ((tid & 63) == 0 && legal) atomicAdd(&L.legal, legal);
     }
-    double x = allowed ? (double)raw : -__builtin_inf();
-    if (count > 0) {
-      x = x < 0 ? x * cfg.repetition_penalty : x / cfg.repetition_penalty;
-      x -= cfg.presence_penalty + (double)count * cfg.frequency_penalty;
-    }
-    S.key[id] = f64_key(greedy ? x : x / T);
   }
   __syncthreads();
   if (constrained && L.legal <= 0) {

@@ -44,6 +44,7 @@ constexpr int kSlotsPerThread = kHashSize / kFinishThreads;
 constexpr int kIdsPerThread = 2;                      // window ids loaded ahead per thread
 constexpr int kSpecQ = 4;  // list slots per thread read with the statistics (32 per sub-list)
 constexpr uint32_t kDeepLists = 1u << 30;  // row flag: some sub-list holds more than 32 entries
+constexpr uint32_t kSpecialOverflow = 1u << 29;  // row flag: an id found no hash slot (exact path)
 constexpr uint32_t kExactRequest = 1u << 31;  // finish_row's answer: the row goes to the exact path
 static_assert(kFinishMaxChunks * kScanWaves <= kFinishThreads, "one thread per chunk wave");
 
@@ -401,7 +402,7 @@ __device__ __forceinline__ bool top_select(const uint64_t* s, int n, uint32_t lo
 // the id there (its "owner" evaluates it once the counts are complete)
 __device__ __forceinline__ bool special_insert_owner(SpecialTable t, uint32_t id, uint32_t kind, int* slot) {
   uint32_t h = hash_id(id) & (kHashSize - 1);
-  for (int probe = 0; probe < kHashSize; ++probe) {
+  for (int probe = 0; probe < kMaxProbe; ++probe) {
     const uint32_t prev = atomicCAS(&t.ids[h], 0xFFFFFFFFu, id);
     if (prev == 0xFFFFFFFFu || prev == id) {
       if (kind == 0) atomicAdd(&t.counts[h], 1u);
@@ -759,6 +760,11 @@ __device__ __forceinline__ uint32_t finish_row(const SampleArgs& a, FinishLds& U
 #pragma unroll
   for (int q = 0; q < kSpecQ; ++q) lv[q] = lists[(int64_t)(sl0 < n_subs ? sl0 : 0) * kSubCap + k0 + q * kSubThreads];
   const Plan plan = plan_row_flat(cfg);
+  if (cfg.mask_slot >= a.mask_slots) {
+    // a constrained row whose mask is not in the table: never sampled unmasked
+    if (tid == 0) write_result(a, row, -1, GS_FLAG_INVALID_SLOT, 0.0);
+    return 0;
+  }
   if (plan.route == kRouteExact) {
     return kExactRequest | 0u;
   }
@@ -875,24 +881,34 @@ __device__ __forceinline__ uint32_t finish_row(const SampleArgs& a, FinishLds& U
   // distinct special ids into the hash
   {
     SpecialTable tab{S.hash_ids, S.hash_counts};
+    bool lost = false;  // an id that found no slot: the table is too crowded
 #pragma unroll
     for (int r = 0; r < kOwn; ++r) {
       oslot[r] = -1;
       ofirst[r] = false;
-      if (oid[r] >= 0 && oid[r] < a.vocab) ofirst[r] = special_insert_owner(tab, (uint32_t)oid[r], okind[r], &oslot[r]);
+      if (oid[r] >= 0 && oid[r] < a.vocab) {
+        ofirst[r] = special_insert_owner(tab, (uint32_t)oid[r], okind[r], &oslot[r]);
+        lost |= oslot[r] < 0;
+      }
     }
-    for (int64_t j = w0 + tid + (int64_t)kIdsPerThread * kFinishThreads; j < w1; j += kFinishThreads) {
+    for (int64_t j = w0 + tid + (int64_t)kIdsPerThread * kFinishThreads; j < w1 && !lost; j += kFinishThreads) {
       const int32_t id = a.history_ids[j];
-      if (id >= 0 && id < a.vocab) special_insert(tab, (uint32_t)id, 0u);
+      if (id >= 0 && id < a.vocab) lost |= !special_insert(tab, (uint32_t)id, 0u);
     }
-    for (int64_t j = f0 + tid + kFinishThreads; j < f1; j += kFinishThreads) {
+    for (int64_t j = f0 + tid + kFinishThreads; j < f1 && !lost; j += kFinishThreads) {
       const int32_t id = a.forced_ids[j];
-      if (id >= 0 && id < a.vocab) special_insert(tab, (uint32_t)id, (uint32_t)a.forced_kinds[j] & 3u);
+      if (id >= 0 && id < a.vocab) lost |= !special_insert(tab, (uint32_t)id, (uint32_t)a.forced_kinds[j] & 3u);
     }
+    if (__ballot(lost) && lane == 0) atomicOr(&S.flags, kSpecialOverflow);
   }
   __syncthreads();
   if (S.flags & kChunkNonFinite) {
     return kExactRequest | GS_FLAG_NONFINITE;
+  }
+  if (S.flags & kSpecialOverflow) {
+    // more distinct window and forced ids than the table holds: the exact
+    // path counts them per vocabulary id
+    return kExactRequest | 0u;
   }
   if (!greedy && (S.flags & kChunkOverflow)) {
     return kExactRequest | 0u;
@@ -1134,8 +1150,8 @@ __device__ __forceinline__ uint32_t finish_row(const SampleArgs& a, FinishLds& U
   }
   __syncthreads();
   if (S.n_special > (uint32_t)kSpecialCap) {
-    if (tid == 0) write_result(a, row, -1, GS_FLAG_UNSUPPORTED, 0.0);
-    return 0;
+    // more specials than the finish evaluates: the exact path takes any number
+    return kExactRequest | 0u;
   }
   if (S.flags & kChunkNonFinite) {
     return kExactRequest | GS_FLAG_NONFINITE;

@@ -29,7 +29,7 @@ constexpr int kFinishThreads = 1024;
 constexpr int kFinishCap = 4096;                  // sorted candidate region in the finish kernel
 constexpr int kFinishMaxChunks = 256;             // chunk statistics the finish keeps in LDS
 constexpr int64_t kMaxVocab = (int64_t)kFinishMaxChunks * kChunk;  // 2097152 ids
-constexpr int kSpecialCap = 2048;                 // distinct (history window + forced) ids per row
+constexpr int kSpecialCap = 2048;                 // distinct (window + forced) ids the one-pass finish evaluates
 constexpr int kHashSize = 4096;                   // open-addressing table for those ids
 constexpr int kExactThreads = 1024;
 constexpr int kExactTile = 4096;                  // LDS tile of the exact path's bitonic sort
@@ -381,18 +381,26 @@ struct SpecialTable {
 
 __device__ __forceinline__ uint32_t hash_id(uint32_t id) { return (id * 2654435761u) >> 20; }
 
-// window ids add 1 to the low 24 bits; forced ids OR their kind into the top 8
-__device__ __forceinline__ void special_insert(SpecialTable t, uint32_t id, uint32_t kind) {
+// Probes an insert may take before the table counts as too crowded: a row
+// with more than kSpecialCap distinct ids fills more than half the table,
+// and a row that crowded (or whose ids cluster) is replayed on the exact
+// path, which counts window ids per vocabulary id instead.
+constexpr int kMaxProbe = 64;
+
+// window ids add 1 to the low 24 bits; forced ids OR their kind into the top
+// 8. Returns false when the id found no slot within kMaxProbe probes.
+__device__ __forceinline__ bool special_insert(SpecialTable t, uint32_t id, uint32_t kind) {
   uint32_t h = hash_id(id) & (kHashSize - 1);
-  for (int probe = 0; probe < kHashSize; ++probe) {
+  for (int probe = 0; probe < kMaxProbe; ++probe) {
     const uint32_t prev = atomicCAS(&t.ids[h], 0xFFFFFFFFu, id);
     if (prev == 0xFFFFFFFFu || prev == id) {
       if (kind == 0) atomicAdd(&t.counts[h], 1u);
       else atomicOr(&t.counts[h], kind << 24);
-      return;
+      return true;
     }
     h = (h + 1) & (kHashSize - 1);
   }
+  return false;
 }
 
 // ---------------------------------------------------- kernel launchers

@@ -11,6 +11,18 @@
 //
 // mulberry32_draw is SeededRandom.next() (src/runtime/sampling.ts:3-16) as a
 // counter-based function of (seed, draw number).
+//
+// The exp and log routines restate fdlibm's published method and carry its
+// notice:
+//   ====================================================
+//   Copyright (C) 1993 by Sun Microsystems, Inc. All rights reserved.
+//   (e_exp.c: Copyright (C) 2004 by Sun Microsystems, Inc.)
+//
+//   Developed at SunSoft, a Sun Microsystems, Inc. business.
+//   Permission to use, copy, modify, and distribute this
+//   software is freely granted, provided that this notice
+//   is preserved.
+//   ====================================================
 
 #pragma once
 

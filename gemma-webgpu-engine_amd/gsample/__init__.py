@@ -28,6 +28,7 @@ from .runtime import (  # noqa: F401
     GS_FLAG_NONFINITE,
     GS_FLAG_TOPP_TIE,
     GS_FLAG_UNSUPPORTED,
+    GS_FLAG_INVALID_SLOT,
     GSampleError,
     LIB_PATH,
     RowConfig,

@@ -12,7 +12,7 @@ from typing import Optional, Sequence
 
 import numpy as np
 
-from .config import DecodingConfig
+from .config import DecodingConfig, validate_decoding_config
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 PKG = os.path.dirname(HERE)
@@ -30,6 +30,7 @@ GS_FLAG_NONFINITE = 16
 GS_FLAG_EMPTY_CANDIDATES = 32
 GS_FLAG_GREEDY = 64
 GS_FLAG_UNSUPPORTED = 128
+GS_FLAG_INVALID_SLOT = 256
 
 GS_OK = 0
 GS_ERR_DEAD_END = 4
@@ -472,6 +473,13 @@ def sample_token(raw_logits, history: Sequence[int], config: DecodingConfig, ran
     x = np.asarray(raw_logits, dtype=np.float32).reshape(-1)
     if x.size == 0:
         raise GSampleError(3, "Cannot sample empty logits")
+    # the session validates before any sampleToken call
+    # (src/runtime/generation-config.ts:62-70); so does this entry point
+    check = validate_decoding_config({f: getattr(config, f) for f in (
+        "temperature", "topK", "topP", "minP", "typicalP", "repetitionPenalty", "repetitionWindow",
+        "frequencyPenalty", "presencePenalty")})
+    if not check["ok"]:
+        raise GSampleError(2, "Invalid Gemma decoding config: " + "; ".join(check["errors"]))
     s = _sampler_for(int(x.size))
     u = None if config.temperature == 0 else float(random())
     cfg = row_config(config, uniform=u if u is not None else 0.0)

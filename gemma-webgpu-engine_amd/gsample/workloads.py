@@ -16,6 +16,10 @@ the batch, and buffers are identical on every machine.
   lmhead         H 64 x 2048 bf16 ~ N(0,1), W 262144 x 2048 bf16 ~ N(0, 0.02^2),
                  softcap 30, 256-id histories (window 256), the constrained
                  workload's DFA, topK 64, topP 0.95, T 1, seed = row
+  multinomial    256 x 262144 f32 ~ N(0, 3^2); T 0.8 with topK 0, topP 1: the
+                 generate() defaults with a temperature (a full-vocabulary draw)
+  topk_deep      256 x 262144 f32 ~ N(0, 3^2); T 0.8, topK 200, topP 0.95
+  typical        256 x 262144 f32 ~ N(0, 3^2); T 0.8, topK 40, typicalP 0.9
 """
 from __future__ import annotations
 
@@ -171,3 +175,27 @@ def lmhead_inputs(n_rows: int = 64, width: int = 2048, vocab: int = V, device=No
 
 def lmhead_histories(n_rows: int = 64, vocab: int = V) -> List[np.ndarray]:
     return [zipf_ids(rng(11, r), 256, vocab=vocab) for r in range(n_rows)]
+
+
+MULTINOMIAL_CONFIG = DecodingConfig(temperature=0.8, topK=0, topP=1.0, minP=0.0, typicalP=1.0, repetitionPenalty=1.0,
+                                    repetitionWindow=0, frequencyPenalty=0.0, presencePenalty=0.0)
+TOPK_DEEP_CONFIG = MULTINOMIAL_CONFIG.merged(topK=200, topP=0.95)
+TYPICAL_CONFIG = MULTINOMIAL_CONFIG.merged(topK=40, typicalP=0.9)
+
+
+def _plain(name: str, cfg: DecodingConfig, seed: int, rows: Optional[List[int]], n_rows: int, vocab: int) -> Workload:
+    rows = list(range(n_rows)) if rows is None else rows
+    logits = normal_logits(seed, rows, vocab=vocab)
+    return Workload(name, len(rows), logits, "f32", [cfg.merged(seed=r) for r in rows], list(rows))
+
+
+def multinomial(rows: Optional[List[int]] = None, n_rows: int = 256, vocab: int = V) -> Workload:
+    return _plain("multinomial", MULTINOMIAL_CONFIG, 12, rows, n_rows, vocab)
+
+
+def topk_deep(rows: Optional[List[int]] = None, n_rows: int = 256, vocab: int = V) -> Workload:
+    return _plain("topk_deep", TOPK_DEEP_CONFIG, 13, rows, n_rows, vocab)
+
+
+def typical(rows: Optional[List[int]] = None, n_rows: int = 256, vocab: int = V) -> Workload:
+    return _plain("typical", TYPICAL_CONFIG, 14, rows, n_rows, vocab)

@@ -31,6 +31,7 @@ const FLAGS = Object.freeze({
   EMPTY_CANDIDATES: 32,
   GREEDY: 64,
   UNSUPPORTED: 128,
+  INVALID_SLOT: 256,
 });
 
 const STAGES = Object.freeze(["lmhead", "scan", "finish", "exact"]);

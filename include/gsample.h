@@ -84,7 +84,8 @@ typedef struct gs_row_config {
 #define GS_FLAG_NONFINITE 16u     /* NaN or +Inf logits: outside the reference's contract */
 #define GS_FLAG_EMPTY_CANDIDATES 32u
 #define GS_FLAG_GREEDY 64u
-#define GS_FLAG_UNSUPPORTED 128u  /* beyond a documented size limit (e.g. > 2048 distinct window ids) */
+#define GS_FLAG_UNSUPPORTED 128u  /* beyond a documented size limit */
+#define GS_FLAG_INVALID_SLOT 256u /* mask_slot >= 0 but not below the batch's mask_slots (row not sampled) */
 
 typedef struct gs_row_result {
   int32_t token;         /* sampled id; -1 when the row failed (see flags) */

@@ -11,8 +11,8 @@
  *    restatement of those published methods (Sun Microsystems fdlibm 5.3:
  *    argument reduction x = k*ln2 + r, Remez rational approximation of
  *    r*(e^r+1)/(e^r-1) for exp; x = 2^k*(1+f), s = f/(2+f) series for log).
- *    Pinned by tests/test_oracle_jsmath.py against Node's own Math.exp /
- *    Math.log on millions of inputs.
+ *    Pinned by tests/test_oracle_vs_node.py against Node's own Math.exp /
+ *    Math.log.
  *
  *  - mulberry32_draw: SeededRandom (src/runtime/sampling.ts:3-16). The state is
  *    an unbounded JS double advanced by 0x6d2b79f5 per draw, so the n-th draw
@@ -20,7 +20,18 @@
  *    s0 = (seed >>> 0) || 0x6d2b79f5. Exact while s0 + (n+1)*C <= 2^53.
  *
  * All arithmetic here uses IEEE-754 binary64 basic operations only; compile
- * with -ffp-contract=off so no fused multiply-add changes a rounding.
+ * with -ffp-contract=off so no fused multiply-add changes a rounding. *
+ * The exp and log routines restate fdlibm's published method and carry its
+ * notice:
+ *   ====================================================
+ *   Copyright (C) 1993 by Sun Microsystems, Inc. All rights reserved.
+ *   (e_exp.c: Copyright (C) 2004 by Sun Microsystems, Inc.)
+ *
+ *   Developed at SunSoft, a Sun Microsystems, Inc. business.
+ *   Permission to use, copy, modify, and distribute this
+ *   software is freely granted, provided that this notice
+ *   is preserved.
+ *   ====================================================
  */
 #ifndef ORACLE_JSMATH_H
 #define ORACLE_JSMATH_H

@@ -76,6 +76,8 @@ def lib():
         L.or_log.argtypes = [C.c_double]
         L.or_draw.restype = C.c_double
         L.or_draw.argtypes = [C.c_int64, C.c_uint64]
+        L.or_softcap_row.restype = None
+        L.or_softcap_row.argtypes = [fp, C.c_int64, C.c_double, fp]
         L.or_draws.restype = None
         L.or_draws.argtypes = [C.c_int64, C.c_uint64, C.c_int64, dp]
         u8p = C.POINTER(C.c_uint8)
@@ -153,6 +155,15 @@ def draw(seed: int, index: int) -> float:
 def draws(seed: int, first: int, count: int) -> np.ndarray:
     out = np.empty(count, dtype=np.float64)
     lib().or_draws(int(seed), int(first), int(count), _ptr(out, C.c_double))
+    return out
+
+
+def softcap(x, cap: float) -> np.ndarray:
+    """cap * tanh(x / cap) per element, binary32 in and out (the engine's
+    final-logit softcap; closed form only, the reference never applies one)."""
+    a = np.ascontiguousarray(np.asarray(x, dtype=np.float32))
+    out = np.empty_like(a)
+    lib().or_softcap_row(_ptr(a, C.c_float), a.size, float(cap), _ptr(out, C.c_float))
     return out
 
 

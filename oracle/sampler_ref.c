@@ -14,6 +14,10 @@
  *                          reached along its bytes exists and is viable
  *   or_viable_states       src/runtime/constraints.ts:300-322 (findViableStates)
  *   or_mask_logits         src/runtime/constraints.ts:159-173 (maskConstraintLogits)
+ *   or_softcap_row         the engine's optional final-logit softcap
+ *                          cap*tanh(x/cap) (jsmath.h softcap_f32); the
+ *                          reference declares the cap but never applies it,
+ *                          so it is pinned by closed-form tests only
  *
  * The steps kept alike (and why): the sampler's order of operations is the
  * reference's because the token ids must be bit-exact — widening to f64
@@ -304,6 +308,10 @@ double or_exp(double x) { return js_exp(x); }
 double or_log(double x) { return js_log(x); }
 
 double or_draw(int64_t seed, uint64_t index) { return mulberry32_draw(seed, index); }
+
+void or_softcap_row(const float* x, int64_t n, double cap, float* out) {
+  for (int64_t i = 0; i < n; ++i) out[i] = softcap_f32(x[i], cap);
+}
 
 void or_draws(int64_t seed, uint64_t first, int64_t count, double* out) {
   for (int64_t i = 0; i < count; ++i) out[i] = mulberry32_draw(seed, first + (uint64_t)i);

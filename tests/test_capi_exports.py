@@ -50,6 +50,14 @@ def test_host_math_exports_match_the_oracle(oracle):
     for seed in (0, 42, -9, 2 ** 35):
         for i in (0, 1, 2, 1000, 4_000_000):
             assert lib.gs_seeded_random(seed, i) == oracle.draw(seed, i)
+    # the final-logit softcap: bit for bit with the oracle's, over the normal,
+    # tiny (series branch), saturated and special inputs
+    xs32 = np.concatenate([rng.normal(0, 25, 20000), rng.normal(0, 1e-3, 2000), [0.0, -0.0, 1e-30, 3000.0, -3000.0,
+                                                                                  np.inf, -np.inf]]).astype(np.float32)
+    for cap in (30.0, 50.0, 7.5):
+        ref = oracle.softcap(xs32, cap)
+        got = np.array([lib.gs_softcap(float(x), cap) for x in xs32], dtype=np.float32)
+        assert np.array_equal(got.view(np.uint32), ref.view(np.uint32)), cap
 
 
 def test_config_validation_messages_through_the_abi():

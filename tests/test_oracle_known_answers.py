@@ -145,3 +145,24 @@ def test_out_of_range_history_ids_are_skipped(oracle):
     x = np.array([1.0, 0.9], dtype=np.float32)
     cfg = d(temperature=0, repetitionPenalty=5, repetitionWindow=4)
     assert oracle.sample_token(x, [-1, 7, 262144, 99], cfg, 0)[0] == 0
+
+
+def test_softcap_closed_form(oracle):
+    """The final-logit softcap cap*tanh(x/cap) (no reference vectors: the
+    reference declares the cap but never applies it) against the binary64
+    closed form: within one binary32 ulp of the correctly rounded value, odd,
+    saturating at +-cap, the identity to first order near 0, NaN kept."""
+    rng = np.random.default_rng(21)
+    x = np.concatenate([rng.normal(0, 25, 200000), rng.normal(0, 1e-3, 20000), rng.uniform(-400, 400, 20000)])
+    x = x.astype(np.float32)
+    for cap in (30.0, 50.0):
+        got = oracle.softcap(x, cap).astype(np.float64)
+        ref = cap * np.tanh(x.astype(np.float64) / cap)
+        ulp = np.spacing(np.abs(ref).astype(np.float32)).astype(np.float64)
+        assert np.all(np.abs(got - ref) <= ulp), cap
+        assert np.array_equal(oracle.softcap(-x, cap), -oracle.softcap(x, cap))
+    big = np.array([1e6, -1e6, np.inf, -np.inf], np.float32)
+    assert oracle.softcap(big, 30.0).tolist() == [30.0, -30.0, 30.0, -30.0]
+    tiny = np.array([1e-20, -3e-10], np.float32)
+    assert np.array_equal(oracle.softcap(tiny, 30.0), tiny)
+    assert np.isnan(oracle.softcap(np.array([np.nan], np.float32), 30.0)[0])
