@@ -5,6 +5,7 @@
 #include <cmath>
 #include <cstdio>
 #include <cstring>
+#include <mutex>
 #include <string>
 #include <vector>
 
@@ -54,12 +55,21 @@ struct gs_context {
 
 namespace {
 
-// message of the last failure of a call made without a context
-thread_local std::string g_no_context_error = "no context";
+// message of the last failure of a call made without a context, in a fixed
+// buffer: a context-free call allocates nothing, not even for its message
+thread_local char g_no_context_error[256] = "no context";
+
+int fail_static(int status, const char* msg) {
+  size_t n = strlen(msg);
+  if (n > sizeof(g_no_context_error) - 1) n = sizeof(g_no_context_error) - 1;
+  memcpy(g_no_context_error, msg, n);
+  g_no_context_error[n] = 0;
+  return status;
+}
 
 int fail(gs_context* ctx, int status, const std::string& msg) {
   if (ctx) ctx->error = msg;
-  else g_no_context_error = msg;
+  else fail_static(status, msg.c_str());
   return status;
 }
 
@@ -136,6 +146,74 @@ bool csr_ok(const int64_t* off, int32_t rows) {
   return true;
 }
 
+// The first thing wrong with a batch's pointers and sizes (NULL: nothing).
+const char* batch_error(const gs_batch* b, int32_t vocab) {
+  if (!b->logits || !b->configs || !b->results) return "logits, configs and results are required";
+  if (b->dtype != GS_F32 && b->dtype != GS_BF16) return "dtype must be f32 or bf16";
+  if (b->row_stride < vocab) return "row_stride is smaller than the vocab";
+  if (b->history_offsets && !b->history_ids) return "history_ids missing";
+  if (b->forced_offsets && (!b->forced_ids || !b->forced_kinds)) return "forced ids missing";
+  if (b->mask_slots > 0 && !b->mask_table) return "mask_table missing";
+  return nullptr;
+}
+
+// Device memory one sampling launch works in: a context's, or the
+// no-allocation entry point's fixed array.
+struct Workspace {
+  int32_t vocab = 0, n_chunks = 0, mask_words = 0, exact_slots = 0, cu_count = 0;
+  ChunkStat* stats = nullptr;
+  uint64_t* lists = nullptr;
+  ExactQueue* queue = nullptr;
+  uint8_t* exact = nullptr;
+  int64_t exact_slot_bytes = 0, exact_cap = 0;
+};
+
+// Enqueues the sampling kernels of one checked batch on stream s (ev: the
+// timing events of each stage, none when not timing). The exact-path queue is
+// reset by the chunk scan's first workgroup: no memset node, so the launch
+// stays capturable and allocates nothing.
+hipError_t launch_sample(const Workspace& w, const gs_batch* b, hipStream_t s, const LaunchEvents* ev) {
+  const size_t esize = b->dtype == GS_BF16 ? 2 : 4;
+  SampleArgs a{};
+  a.logits = b->logits;
+  a.row_stride = b->row_stride;
+  a.dtype = b->dtype;
+  a.rows = b->rows;
+  a.vocab = w.vocab;
+  a.n_chunks = w.n_chunks;
+  a.vector_ok = aligned16(b->logits) && ((b->row_stride * esize) % 16 == 0);
+  a.mask_words = w.mask_words;
+  a.configs = b->configs;
+  a.history_offsets = b->history_offsets;
+  a.history_ids = b->history_ids;
+  a.forced_offsets = b->forced_offsets;
+  a.forced_ids = b->forced_ids;
+  a.forced_kinds = b->forced_kinds;
+  a.mask_table = b->mask_table;
+  a.mask_slots = b->mask_table ? b->mask_slots : 0;
+  a.exact_slots = w.exact_slots;
+  a.results = b->results;
+  a.stats = w.stats;
+  a.lists = w.lists;
+  a.queue = w.queue;
+  a.exact_scratch = w.exact;
+  a.exact_slot_bytes = w.exact_slot_bytes;
+  a.exact_capacity = w.exact_cap;
+  a.cu_count = w.cu_count;
+  launch_scan(a, s, ev[GS_STAGE_SCAN]);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  launch_finish(a, s, ev[GS_STAGE_FINISH]);
+  e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  if (b->rows > w.exact_slots) {
+    // rows past the slots were queued by the finish kernel
+    launch_exact(a, s, ev[GS_STAGE_EXACT]);
+    e = hipGetLastError();
+  }
+  return e;
+}
+
 void destroy_timing(gs_context* ctx) {
   for (hipEvent_t e : ctx->t_events) (void)hipEventDestroy(e);
   ctx->t_events.clear();
@@ -144,9 +222,100 @@ void destroy_timing(gs_context* ctx) {
   ctx->t_on = false;
 }
 
+// ------------------------------------------------ no-allocation sampling
+// gs_sample_noalloc works in one fixed device array instead of a context's
+// memory: chunk statistics and lists for up to kNoAllocMaxRows rows of up to
+// kNoAllocMaxVocab logits, the exact-path queue, and kNoAllocExactSlots
+// exact-path row slots (rows past them are replayed by the exact kernel,
+// which walks the queue with one workgroup per slot).
+constexpr int32_t kNoAllocMaxRows = 64;
+constexpr int32_t kNoAllocMaxVocab = 262144;
+constexpr int32_t kNoAllocExactSlots = 2;
+constexpr int kMaxDevices = 64;
+constexpr size_t kNaChunks = (kNoAllocMaxVocab + kChunk - 1) / kChunk;
+constexpr size_t align256c(size_t x) { return (x + 255) & ~(size_t)255; }
+constexpr size_t kNaStatsBytes = align256c(kNoAllocMaxRows * kNaChunks * sizeof(ChunkStat));
+constexpr size_t kNaListBytes = align256c(kNoAllocMaxRows * kNaChunks * kGatherCap * sizeof(uint64_t));
+constexpr size_t kNaQueueBytes = align256c(sizeof(ExactQueue) + kNoAllocMaxRows * sizeof(uint32_t));
+constexpr size_t kNaSlotBytes = 36 * (size_t)kNoAllocMaxVocab;  // 36 B per entry of a 2^18-entry slot
+constexpr size_t kNoAllocScratchBytes =
+    kNaStatsBytes + kNaListBytes + kNaQueueBytes + kNoAllocExactSlots * kNaSlotBytes;  // 27,427,328 B
+
+}  // namespace
+
+// The no-allocation entry point's device memory (27.4 MB): each GPU the
+// library runs on holds its own copy until the process ends. Host code never
+// passes this name to a kernel (on the host it is a stand-in, not a device
+// address); it uses the per-device address hipGetSymbolAddress returns.
+static __device__ __align__(256) uint8_t scratch[kNoAllocScratchBytes];
+
+namespace {
+
+struct NoAllocDevice {
+  uint8_t* ptr = nullptr;  // device address of `scratch` on this device
+  int32_t cu_count = 0;
+};
+NoAllocDevice g_noalloc[kMaxDevices];
+std::mutex g_noalloc_mu;
+
+// The array's address and the CU count of device `dev` (the current device),
+// looked up once per device on its first call.
+int noalloc_device(int dev, NoAllocDevice* out) {
+  std::lock_guard<std::mutex> lock(g_noalloc_mu);
+  NoAllocDevice& d = g_noalloc[dev];
+  if (!d.ptr) {
+    void* p = nullptr;
+    if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess || !p)
+      return fail_static(GS_ERR_HIP, "gs_sample_noalloc: hipGetSymbolAddress of the scratch array failed");
+    int cu = 0;
+    if (hipDeviceGetAttribute(&cu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cu <= 0)
+      return fail_static(GS_ERR_HIP, "gs_sample_noalloc: reading the device's compute-unit count failed");
+    d.cu_count = cu;
+    d.ptr = (uint8_t*)p;
+  }
+  *out = d;
+  return GS_OK;
+}
+
 }  // namespace
 
 extern "C" {
+
+int gs_sample_noalloc(const gs_batch* b, int32_t vocab_size, void* stream) {
+  if (!b) return fail_static(GS_ERR_INVALID_ARGUMENT, "null batch");
+  if (vocab_size <= 0 || vocab_size > kNoAllocMaxVocab)
+    return fail_static(GS_ERR_UNSUPPORTED,
+                       "gs_sample_noalloc: vocab_size must be 1..262144 (the size of its fixed device scratch)");
+  if (b->rows < 0 || b->rows > kNoAllocMaxRows)
+    return fail_static(GS_ERR_UNSUPPORTED,
+                       "gs_sample_noalloc: rows must be 0..64 (the size of its fixed device scratch)");
+  if (b->rows == 0) return GS_OK;
+  const char* bad = batch_error(b, vocab_size);
+  if (bad) return fail_static(GS_ERR_INVALID_ARGUMENT, bad);
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices)
+    return fail_static(GS_ERR_NO_DEVICE, "gs_sample_noalloc: no current HIP device");
+  NoAllocDevice d;
+  const int st = noalloc_device(dev, &d);
+  if (st != GS_OK) return st;
+  Workspace w;
+  w.vocab = vocab_size;
+  w.n_chunks = (vocab_size + kChunk - 1) / kChunk;
+  w.mask_words = (vocab_size + 31) / 32;
+  w.exact_slots = kNoAllocExactSlots;
+  w.cu_count = d.cu_count;
+  w.stats = (ChunkStat*)d.ptr;
+  w.lists = (uint64_t*)(d.ptr + kNaStatsBytes);
+  w.queue = (ExactQueue*)(d.ptr + kNaStatsBytes + kNaListBytes);
+  w.exact = d.ptr + kNaStatsBytes + kNaListBytes + kNaQueueBytes;
+  w.exact_cap = 1;
+  while (w.exact_cap < vocab_size) w.exact_cap <<= 1;
+  w.exact_slot_bytes = 36 * w.exact_cap;
+  const LaunchEvents ev[GS_STAGE_COUNT] = {};
+  const hipError_t e = launch_sample(w, b, (hipStream_t)stream, ev);
+  if (e != hipSuccess) return fail_static(GS_ERR_HIP, hipGetErrorString(e));
+  return GS_OK;
+}
 
 int gs_abi_version(void) { return GSAMPLE_ABI_VERSION; }
 
@@ -229,7 +398,7 @@ int gs_destroy(gs_context* ctx) {
   return GS_OK;
 }
 
-const char* gs_last_error(const gs_context* ctx) { return ctx ? ctx->error.c_str() : g_no_context_error.c_str(); }
+const char* gs_last_error(const gs_context* ctx) { return ctx ? ctx->error.c_str() : g_no_context_error; }
 
 int gs_synchronize(gs_context* ctx) {
   if (!ctx) return GS_ERR_INVALID_ARGUMENT;
@@ -275,53 +444,27 @@ int gs_sample(gs_context* ctx, const gs_batch* b, void* stream) {
   if (!ctx || !b) return fail(ctx, GS_ERR_INVALID_ARGUMENT, "null context or batch");
   if (b->rows == 0) return GS_OK;
   if (b->rows < 0 || b->rows > ctx->max_rows) return fail(ctx, GS_ERR_INVALID_ARGUMENT, "rows outside [0, max_rows]");
-  if (!b->logits || !b->configs || !b->results) return fail(ctx, GS_ERR_INVALID_ARGUMENT, "logits, configs and results are required");
-  if (b->dtype != GS_F32 && b->dtype != GS_BF16) return fail(ctx, GS_ERR_INVALID_ARGUMENT, "dtype must be f32 or bf16");
-  if (b->row_stride < ctx->vocab) return fail(ctx, GS_ERR_INVALID_ARGUMENT, "row_stride is smaller than the vocab");
-  if (b->history_offsets && !b->history_ids) return fail(ctx, GS_ERR_INVALID_ARGUMENT, "history_ids missing");
-  if (b->forced_offsets && (!b->forced_ids || !b->forced_kinds)) return fail(ctx, GS_ERR_INVALID_ARGUMENT, "forced ids missing");
-  if (b->mask_slots > 0 && !b->mask_table) return fail(ctx, GS_ERR_INVALID_ARGUMENT, "mask_table missing");
+  const char* bad = batch_error(b, ctx->vocab);
+  if (bad) return fail(ctx, GS_ERR_INVALID_ARGUMENT, bad);
   GS_HIP(ctx, hipSetDevice(ctx->device));
-  hipStream_t s = pick_stream(ctx, stream);
-  const size_t esize = b->dtype == GS_BF16 ? 2 : 4;
-  SampleArgs a{};
-  a.logits = b->logits;
-  a.row_stride = b->row_stride;
-  a.dtype = b->dtype;
-  a.rows = b->rows;
-  a.vocab = ctx->vocab;
-  a.n_chunks = ctx->n_chunks;
-  a.vector_ok = aligned16(b->logits) && ((b->row_stride * esize) % 16 == 0);
-  a.mask_words = ctx->mask_words;
-  a.configs = b->configs;
-  a.history_offsets = b->history_offsets;
-  a.history_ids = b->history_ids;
-  a.forced_offsets = b->forced_offsets;
-  a.forced_ids = b->forced_ids;
-  a.forced_kinds = b->forced_kinds;
-  a.mask_table = b->mask_table;
-  a.mask_slots = b->mask_table ? b->mask_slots : 0;
-  a.exact_slots = ctx->exact_slots;
-  a.results = b->results;
-  a.stats = ctx->d_stats;
-  a.lists = ctx->d_lists;
-  a.queue = ctx->d_queue;
-  a.exact_scratch = ctx->d_exact;
-  a.exact_slot_bytes = ctx->exact_slot_bytes;
-  a.exact_capacity = ctx->exact_cap;
-  a.cu_count = ctx->cu_count;
-  // the exact-path queue is reset by the chunk scan's first workgroup: no
-  // memset node, so the call stays capturable and one launch cheaper
+  Workspace w;
+  w.vocab = ctx->vocab;
+  w.n_chunks = ctx->n_chunks;
+  w.mask_words = ctx->mask_words;
+  w.exact_slots = ctx->exact_slots;
+  w.cu_count = ctx->cu_count;
+  w.stats = ctx->d_stats;
+  w.lists = ctx->d_lists;
+  w.queue = ctx->d_queue;
+  w.exact = ctx->d_exact;
+  w.exact_slot_bytes = ctx->exact_slot_bytes;
+  w.exact_cap = ctx->exact_cap;
   const int32_t slot = timing_slot(ctx);
-  launch_scan(a, s, stage_events(ctx, slot, GS_STAGE_SCAN));
-  GS_HIP(ctx, hipGetLastError());
-  launch_finish(a, s, stage_events(ctx, slot, GS_STAGE_FINISH));
-  GS_HIP(ctx, hipGetLastError());
-  if (b->rows > ctx->exact_slots) {
-    // rows past the slots were queued by the finish kernel
-    launch_exact(a, s, stage_events(ctx, slot, GS_STAGE_EXACT));
-    GS_HIP(ctx, hipGetLastError());
-  }
+  LaunchEvents ev[GS_STAGE_COUNT];
+  for (int k = GS_STAGE_SCAN; k <= GS_STAGE_FINISH; ++k) ev[k] = stage_events(ctx, slot, k);
+  if (b->rows > ctx->exact_slots) ev[GS_STAGE_EXACT] = stage_events(ctx, slot, GS_STAGE_EXACT);
+  const hipError_t e = launch_sample(w, b, pick_stream(ctx, stream), ev);
+  if (e != hipSuccess) return fail(ctx, GS_ERR_HIP, std::string("kernel launch: ") + hipGetErrorString(e));
   if (slot >= 0) ctx->t_calls++;
   return GS_OK;
 }

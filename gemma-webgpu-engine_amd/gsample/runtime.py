@@ -105,7 +105,7 @@ assert RESULT_DTYPE.itemsize == C.sizeof(RowResult)
 EXPORTED_SYMBOLS = (
     "gs_abi_version", "gs_device_count", "gs_seeded_random", "gs_js_exp", "gs_js_log", "gs_softcap",
     "gs_validate_configs", "gs_create", "gs_destroy", "gs_last_error", "gs_synchronize", "gs_stream",
-    "gs_sample", "gs_sample_sync", "gs_token_log_prob", "gs_token_log_prob_host", "gs_set_vocab", "gs_set_dfa",
+    "gs_sample", "gs_sample_noalloc", "gs_sample_sync", "gs_token_log_prob", "gs_token_log_prob_host", "gs_set_vocab", "gs_set_dfa",
     "gs_build_masks", "gs_dfa_advance", "gs_dfa_accepting", "gs_lmhead", "gs_lmhead_sample", "gs_timing_begin",
     "gs_timing_end", "gs_check_exp2",
 )
@@ -145,6 +145,7 @@ def library():
     L.gs_stream.argtypes = [vp]
     L.gs_sample.argtypes = [vp, C.POINTER(Batch), vp]
     L.gs_sample_sync.argtypes = [vp, C.POINTER(Batch), vp]
+    L.gs_sample_noalloc.argtypes = [C.POINTER(Batch), i32, vp]
     L.gs_token_log_prob.argtypes = [vp, vp, i32, i32, i64, vp, vp, vp]
     L.gs_token_log_prob_host.argtypes = [vp, vp, i32, vp, vp]
     L.gs_set_vocab.argtypes = [vp, vp, vp, i64]

@@ -159,6 +159,20 @@ void* gs_stream(gs_context* ctx);
  * batch->results; per-row failures are flagged there. */
 int gs_sample(gs_context* ctx, const gs_batch* batch, void* stream);
 
+/* gs_sample with no allocation at all, for callers that cannot allocate
+ * device memory: code under HIP graph capture, tight serving loops, hosts
+ * that forbid hipMalloc. No counterpart in the reference (its sampler
+ * allocates a fresh JS array per call, src/runtime/sampling.ts:20,33-35).
+ * The same kernels as gs_sample work in one fixed 27.4 MB device array that
+ * each GPU holds from its first call until the process ends: no context,
+ * no hipMalloc/hipFree. Limits: rows <= 64 and vocab_size <= 262144
+ * (GS_ERR_UNSUPPORTED beyond them, nothing launched). Every pointer of
+ * `batch` is device memory of the CURRENT device; `stream` is a hipStream_t
+ * of that device (NULL: the null stream). Calls on one GPU share its array,
+ * so calls whose kernels overlap on that GPU (concurrent streams or host
+ * threads) race: order them on one stream. Failures set gs_last_error(NULL). */
+int gs_sample_noalloc(const gs_batch* batch, int32_t vocab_size, void* stream);
+
 /* As gs_sample, then waits and maps the first failing row to its reference
  * error (status + gs_last_error text). Host copy of the results in `host_out`
  * (may be NULL). */
