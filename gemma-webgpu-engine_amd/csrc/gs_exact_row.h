@@ -119,6 +119,25 @@ __device__ __forceinline__ int64_t pow2_ge(int64_t n) {
   return p;
 }
 
+// The one-lane walks below read their LDS values kSeqBatch at a time, ahead
+// of the additions that consume them in order, so a walk runs at the
+// latency of its binary64 additions instead of one LDS round trip per value.
+constexpr int kSeqBatch = 32;
+
+// acc + st[0] + ... + st[m-1], left to right, on the calling lane.
+__device__ __forceinline__ double seq_sum_lds(const double* st, int64_t m, double acc) {
+  int64_t i = 0;
+  for (; i + kSeqBatch <= m; i += kSeqBatch) {
+    double v[kSeqBatch];
+#pragma unroll
+    for (int k = 0; k < kSeqBatch; ++k) v[k] = st[i + k];
+#pragma unroll
+    for (int k = 0; k < kSeqBatch; ++k) acc = acc + v[k];
+  }
+  for (; i < m; ++i) acc = acc + st[i];
+  return acc;
+}
+
 // Sequential left-to-right sum of prob[order[i]] for i < n, on one lane.
 __device__ double sequential_sum(Lds& L, const double* prob, const uint32_t* order, int64_t n, bool identity) {
   double acc = 0.0;
@@ -127,7 +146,7 @@ __device__ double sequential_sum(Lds& L, const double* prob, const uint32_t* ord
     for (int64_t i = threadIdx.x; i < m; i += kExactThreads) L.stage[i] = prob[identity ? b + i : order[b + i]];
     __syncthreads();
     if (threadIdx.x == 0) {
-      for (int64_t i = 0; i < m; ++i) acc = acc + L.stage[i];
+      acc = seq_sum_lds(L.stage, m, acc);
       L.dtmp = acc;
     }
     __syncthreads();
@@ -153,12 +172,23 @@ __device__ int64_t cumulative_cut(Lds& L, const double* prob, const uint32_t* or
     if (threadIdx.x == 0) {
       int64_t i = 0;
       bool stop = false;
-      while (i < m) {
-        prev = cum;
-        cum += L.stage[i];
-        ++end;
-        ++i;
-        if (!(end < n && cum < threshold)) { stop = true; break; }
+      while (i < m && !stop) {
+        // the next kSeqBatch values (reads past m stay inside the stage and
+        // are not used)
+        double v[kSeqBatch];
+#pragma unroll
+        for (int k = 0; k < kSeqBatch; ++k) v[k] = L.stage[(i + k) & (kExactTile - 1)];
+        const int64_t cnt = m - i < kSeqBatch ? m - i : kSeqBatch;
+#pragma unroll
+        for (int k = 0; k < kSeqBatch; ++k) {
+          if (k < cnt && !stop) {
+            prev = cum;
+            cum += v[k];
+            ++end;
+            if (!(end < n && cum < threshold)) stop = true;
+          }
+        }
+        i += cnt;
       }
       L.flag = stop ? 1u : 0u;
       L.bcast_d[0] = cum;
@@ -350,10 +380,24 @@ __device__ __noinline__ void process_row(const SampleArgs& a, Lds& L, Scratch S,
     double entropy = 0.0;
     for (int64_t b = 0; b < n; b += kExactTile) {
       const int64_t m = n - b < kExactTile ? n - b : kExactTile;
-      for (int64_t i = tid; i < m; i += kExactThreads) L.stage[i] = S.prob[S.order[b + i]];
+      // the terms p * log(p) in parallel (each rounded as the reference
+      // rounds it), then subtracted left to right on one lane
+      double* terms = (double*)L.tkey;
+      for (int64_t i = tid; i < m; i += kExactThreads) {
+        const double pi = S.prob[S.order[b + i]];
+        terms[i] = pi * gsm::js_log(pi);
+      }
       __syncthreads();
       if (tid == 0) {
-        for (int64_t i = 0; i < m; ++i) entropy = entropy - L.stage[i] * gsm::js_log(L.stage[i]);
+        int64_t i = 0;
+        for (; i + kSeqBatch <= m; i += kSeqBatch) {
+          double v[kSeqBatch];
+#pragma unroll
+          for (int k = 0; k < kSeqBatch; ++k) v[k] = terms[i + k];
+#pragma unroll
+          for (int k = 0; k < kSeqBatch; ++k) entropy = entropy - v[k];
+        }
+        for (; i < m; ++i) entropy = entropy - terms[i];
         L.dtmp = entropy;
       }
       __syncthreads();
@@ -438,13 +482,23 @@ __device__ __noinline__ void process_row(const SampleArgs& a, Lds& L, Scratch S,
     for (int64_t i = tid; i < m; i += kExactThreads) L.stage[i] = S.prob[S.order[b + i]];
     __syncthreads();
     if (tid == 0 && L.result_token < 0) {
-      for (int64_t i = 0; i < m; ++i) {
-        cursor -= L.stage[i];
-        if (cursor <= 0) {
-          L.result_token = (int32_t)S.id[S.order[b + i]];
-          L.result_p = L.stage[i];
-          break;
+      int64_t hit = -1;
+      for (int64_t i = 0; i < m && hit < 0; i += kSeqBatch) {
+        double v[kSeqBatch];
+#pragma unroll
+        for (int k = 0; k < kSeqBatch; ++k) v[k] = L.stage[(i + k) & (kExactTile - 1)];
+        const int64_t cnt = m - i < kSeqBatch ? m - i : kSeqBatch;
+#pragma unroll
+        for (int k = 0; k < kSeqBatch; ++k) {
+          if (k < cnt && hit < 0) {
+            cursor -= v[k];
+            if (cursor <= 0) hit = i + k;
+          }
         }
+      }
+      if (hit >= 0) {
+        L.result_token = (int32_t)S.id[S.order[b + hit]];
+        L.result_p = L.stage[hit];
       }
       L.dtmp = cursor;
     }

@@ -46,6 +46,9 @@ constexpr int kSpecQ = 4;  // list slots per thread read with the statistics (32
 constexpr uint32_t kDeepLists = 1u << 30;  // row flag: some sub-list holds more than 32 entries
 constexpr uint32_t kSpecialOverflow = 1u << 29;  // row flag: an id found no hash slot (exact path)
 constexpr uint32_t kExactRequest = 1u << 31;  // finish_row's answer: the row goes to the exact path
+constexpr uint32_t kDeepRequest = 1u << 30;   // finish_row's answer: a full-vocabulary draw for deep_draw
+constexpr int kDeepBins = 4096;                // value bins of the deep draw's tail histogram
+constexpr double kDeepSpan = 40.0;             // natural-log span of those bins below the region floor
 static_assert(kFinishMaxChunks * kScanWaves <= kFinishThreads, "one thread per chunk wave");
 
 __device__ __forceinline__ double block_scan_f64(double v, double* s_w, double* total) {
@@ -433,6 +436,10 @@ struct Shared {
   uint16_t c_nsub[kFinishMaxChunks * kScanWaves];  // sub-list lengths
   uint64_t top[kTopR];                // the fast path's ranked non-specials
   uint32_t hist[256];                 // top_select's histogram (zero between uses)
+  double tab[256];                    // the table exponential's table (deep draw)
+  double deep_m, deep_u, deep_margin; // a deep draw's inputs, left by finish_row
+  uint64_t deep_floor;
+  uint32_t deep_thr, deep_n, deep_count;
   uint32_t sel[4];
   double wsum[kWaves];
   double wtmp[kWaves];
@@ -497,15 +504,20 @@ __device__ __forceinline__ double nonspecial_value(uint64_t e, double T) { retur
 // The filters and the draw over the first n_avail (<= 128) candidates, whose
 // exponentials e[] (probability = e / total, sampling.ts:39,42) and ids ids[]
 // sit in LDS in list order, evaluated by the calling wave alone. Returns 0
-// when the row is settled (result written), 1 when the cut lies past the
-// candidates and the caller must widen them, 2 when the top-p cut lies within
-// `margin` of topP and `refinable` is set: the caller recomputes the
-// normaliser and calls again with the tighter margin; 3 when the row needs
-// the exact path, with its result flags in *exact_flags.
-// `complete`: the candidates are the row's whole list.
-__device__ __forceinline__ int filters_and_draw_wave(const SampleArgs& a, int64_t row, const gs_row_config& cfg, const double* e,
-                                     double total, const uint32_t* ids, int n_avail, bool complete, double margin,
-                                     bool refinable, uint32_t* exact_flags) {
+// when the row is settled (result written), 1 when a cut or the draw lies past
+// the candidates and the caller must widen them, 2 when a decision that
+// depends on the normaliser (a top-p or typical-p cut, the typical set's
+// order, a draw over the whole row's mass) lies within `margin` and
+// `refinable` is set: the caller recomputes the normaliser and calls again
+// with the tighter margin; 3 when the row needs the exact path, with its
+// result flags in *exact_flags.
+// `complete`: the candidates are the row's whole list. aux: 256 doubles of
+// LDS scratch for typical-p. full_mass_rel: the bound on how far the
+// reference's sum of all the row's probabilities lies from 1.
+__device__ __forceinline__ int filters_and_draw_wave(const SampleArgs& a, int64_t row, const gs_row_config& cfg,
+                                                     const double* e, double total, const uint32_t* ids, int n_avail,
+                                                     bool complete, double margin, bool refinable, double full_mass_rel,
+                                                     double* aux, uint32_t* exact_flags) {
   const int lane = threadIdx.x & 63;
   constexpr int kPerLane = 2;  // list index lane*2 + q
   double pl[kPerLane];
@@ -517,6 +529,7 @@ __device__ __forceinline__ int filters_and_draw_wave(const SampleArgs& a, int64_
   int n = n_avail;
   bool n_complete = complete;
   uint32_t exact_why = 0;
+  bool near_normaliser = false;  // a decision within `margin` that only the normaliser's error can move
   // ---- top-k (sampling.ts:44): the candidates are the list's first
   // n_avail, so a cut inside them is the list's own
   if (cfg.top_k > 0 && cfg.top_k < n) {
@@ -552,13 +565,99 @@ __device__ __forceinline__ int filters_and_draw_wave(const SampleArgs& a, int64_
       return 0;
     }
   }
-  // inclusive prefix sums of the first n probabilities
+  // pool membership of list positions below n (typical-p drops some)
+  bool kept[kPerLane];
+#pragma unroll
+  for (int q = 0; q < kPerLane; ++q) kept[q] = lane * kPerLane + q < n;
+  // ---- typical-p (sampling.ts:49-55) over the whole pool: entropy in list
+  // order, a stable ascending order of surprise |-ln p - H|, the leading
+  // mass of that order up to typicalP, and the kept items back in list order
+  // (sorted by probability desc, stable: the list's own order)
+  if (cfg.typical_p < 1) {
+    if (!n_complete) return 1;
+    double t = 0.0;
+#pragma unroll
+    for (int q = 0; q < kPerLane; ++q) t += kept[q] ? pl[q] * gsm::js_log(pl[q]) : 0.0;
+    const double H = -wave_sum_f64_dpp(t);
+    if (!(H == H)) {  // a probability of 0: the reference's arithmetic turns NaN
+      *exact_flags = 0u;
+      return 3;
+    }
+    double sp[kPerLane];
+#pragma unroll
+    for (int q = 0; q < kPerLane; ++q) {
+      const int i = lane * kPerLane + q;
+      sp[q] = kept[q] ? __builtin_fabs(-gsm::js_log(pl[q]) - H) : __builtin_inf();
+      if (i < 128) aux[i] = sp[q];
+    }
+    __builtin_amdgcn_wave_barrier();
+    // The surprises carry the normaliser's error twice (through ln p and
+    // through H): |ds| <= margin (H + 2). Two items of different value
+    // whose surprises lie within twice that may be ordered either way.
+    const double ms = 2.0 * margin * (H + 2.0) + 1e-13 * (H + 1.0);
+    int rank[kPerLane];
+    bool amb = false;
+#pragma unroll
+    for (int q = 0; q < kPerLane; ++q) {
+      const int i = lane * kPerLane + q;
+      int r = 0;
+      for (int j = 0; j < n; ++j) {
+        const double sj = aux[j];
+        r += (sj < sp[q] || (sj == sp[q] && j < i)) ? 1 : 0;
+        const double d = sj >= sp[q] ? sj - sp[q] : sp[q] - sj;
+        if (kept[q] && j != i && sj != sp[q] && d <= ms) amb = true;
+      }
+      rank[q] = r;
+    }
+    __builtin_amdgcn_wave_barrier();
+    // probabilities in surprise order; their leading mass up to typicalP
+#pragma unroll
+    for (int q = 0; q < kPerLane; ++q) {
+      if (kept[q]) aux[128 + rank[q]] = pl[q];
+    }
+    __builtin_amdgcn_wave_barrier();
+    double ps[kPerLane], cs[kPerLane];
+    {
+      double run = 0.0;
+#pragma unroll
+      for (int q = 0; q < kPerLane; ++q) {
+        const int r = lane * kPerLane + q;
+        ps[q] = r < n ? aux[128 + r] : 0.0;
+        run += ps[q];
+        cs[q] = run;
+      }
+      const double incl = wave_scan_f64(run);
+#pragma unroll
+      for (int q = 0; q < kPerLane; ++q) cs[q] += incl - run;
+    }
+    int cut = 0x7FFFFFFF;
+    bool near = false;
+#pragma unroll
+    for (int q = kPerLane - 1; q >= 0; --q) {
+      const int r = lane * kPerLane + q;
+      if (r < n) {
+        if (cs[q] >= cfg.typical_p) cut = r;
+        const double d = cs[q] >= cfg.typical_p ? cs[q] - cfg.typical_p : cfg.typical_p - cs[q];
+        if (d < margin) near = true;
+      }
+    }
+    cut = (int)wave_min_u32((uint32_t)cut);
+    if (cut == 0x7FFFFFFF) cut = n - 1;  // keepLeadingMass keeps the whole list
+    if (__ballot(amb || near)) near_normaliser = true;
+#pragma unroll
+    for (int q = 0; q < kPerLane; ++q) kept[q] = kept[q] && rank[q] <= cut;
+  }
+  if (near_normaliser) {
+    if (refinable && !exact_why) return 2;
+    exact_why |= 4u;
+  }
+  // inclusive prefix sums of the pool's probabilities in list order
   double pre[kPerLane];
   {
     double s = 0.0;
 #pragma unroll
     for (int q = 0; q < kPerLane; ++q) {
-      s += lane * kPerLane + q < n ? pl[q] : 0.0;
+      s += kept[q] ? pl[q] : 0.0;
       pre[q] = s;
     }
     const double incl = wave_scan_f64(s);
@@ -566,6 +665,7 @@ __device__ __forceinline__ int filters_and_draw_wave(const SampleArgs& a, int64_
     for (int q = 0; q < kPerLane; ++q) pre[q] += incl - s;
   }
   uint32_t tie = 0;
+  bool full_mass = false;  // the pool is the whole row and reaches past the candidates
   // ---- top-p (sampling.ts:56,82-90)
   if (cfg.top_p < 1) {
     int cut = 0x7FFFFFFF;
@@ -573,7 +673,7 @@ __device__ __forceinline__ int filters_and_draw_wave(const SampleArgs& a, int64_
 #pragma unroll
     for (int q = kPerLane - 1; q >= 0; --q) {
       const int i = lane * kPerLane + q;
-      if (i < n) {
+      if (kept[q]) {
         if (pre[q] >= cfg.top_p) cut = i;
         const double d = pre[q] >= cfg.top_p ? pre[q] - cfg.top_p : cfg.top_p - pre[q];
         if (d < margin) near = true;
@@ -588,7 +688,11 @@ __device__ __forceinline__ int filters_and_draw_wave(const SampleArgs& a, int64_
     }
     if (cut == 0x7FFFFFFF) {
       if (!n_complete) return 1;
-      cut = n - 1;
+      // the whole pool: its last member
+      int last = -1;
+#pragma unroll
+      for (int q = 0; q < kPerLane; ++q) last = kept[q] ? lane * kPerLane + q : last;
+      cut = (int)wave_max_u32((uint32_t)(last + 1)) - 1;
     } else {
       // 1e-6 boundary ties, as the reference comparison plan reports them
       const int cl = cut / kPerLane, cq = cut % kPerLane;
@@ -601,11 +705,31 @@ __device__ __forceinline__ int filters_and_draw_wave(const SampleArgs& a, int64_
     }
     n = cut + 1;  // prefix sums below the cut are unchanged
   } else if (!n_complete) {
-    return 1;
+    // no cut inside the candidates: with no top-k bound and no min-p floor
+    // the pool is the whole row (a full-vocabulary draw), whose candidate
+    // total is the row's whole probability mass; otherwise its end lies past
+    // the candidates
+    if (!(cfg.top_k <= 0 && !(cfg.min_p > 0))) return 1;
+    full_mass = true;
   }
-  // ---- draw (sampling.ts:58-64): first i with prefix_i >= u * sum_{j<n} p_j
-  const int last_lane = (n - 1) / kPerLane, last_q = (n - 1) % kPerLane;
-  const double ctotal = readlane_f64(last_q == 0 ? pre[0] : pre[1], last_lane);
+  // ---- draw (sampling.ts:58-64): first pool member i with prefix_i >= u *
+  // sum of the pool's probabilities
+  int last = -1;
+#pragma unroll
+  for (int q = 0; q < kPerLane; ++q) {
+    if (kept[q] && lane * kPerLane + q < n) last = lane * kPerLane + q;
+  }
+  last = (int)wave_max_u32((uint32_t)(last + 1)) - 1;
+  double ctotal, dmargin;
+  if (full_mass) {
+    // the reference's sum of all V probabilities lies within full_mass_rel of
+    // 1; the candidates' prefix sums carry the normaliser's error (margin)
+    ctotal = 1.0;
+    dmargin = margin + full_mass_rel + kNearTie;
+  } else {
+    ctotal = readlane_f64((last % kPerLane) == 0 ? pre[0] : pre[1], last / kPerLane);
+    dmargin = kNearTie * ctotal;
+  }
   const double u = cfg.rng_mode == GS_RNG_EXPLICIT ? cfg.uniform : gsm::mulberry32_draw(cfg.seed, cfg.draw_index);
   const double cursor = u * ctotal;
   int pick = 0x7FFFFFFF;
@@ -613,16 +737,26 @@ __device__ __forceinline__ int filters_and_draw_wave(const SampleArgs& a, int64_
 #pragma unroll
   for (int q = kPerLane - 1; q >= 0; --q) {
     const int i = lane * kPerLane + q;
-    if (i < n) {
+    if (kept[q] && i < n) {
       if (pre[q] >= cursor) pick = i;
       const double d = pre[q] >= cursor ? pre[q] - cursor : cursor - pre[q];
-      if (d < kNearTie * ctotal) near = true;
+      if (d < dmargin) near = true;
     }
   }
   pick = (int)wave_min_u32((uint32_t)pick);
-  if (__ballot(near)) exact_why |= 8u;
-  if (exact_why || pick == 0x7FFFFFFF) {
-    *exact_flags = exact_why ? GS_FLAG_NEAR_TIE : 0u;
+  if (__ballot(near)) {
+    // a full-vocabulary draw within the normaliser's margin: the block-wide
+    // path hands it to the deep draw, which recomputes the normaliser
+    if (full_mass && !exact_why) return 1;
+    exact_why |= 8u;
+  }
+  if (exact_why) {
+    *exact_flags = GS_FLAG_NEAR_TIE;
+    return 3;
+  }
+  if (pick == 0x7FFFFFFF) {
+    if (full_mass) return 1;  // the draw lies past the candidates
+    *exact_flags = 0u;
     return 3;
   }
   if (lane == 0) write_result(a, row, (int32_t)ids[pick], tie, e[pick] / total);
@@ -1242,6 +1376,9 @@ __device__ __forceinline__ uint32_t finish_row(const SampleArgs& a, FinishLds& U
   // matter) and of the rescale arguments (2^-53 |M|).
   const double ref_round = 0x1p-52 * (3.0 * (M < 0 ? -M : M) + 60.0);
   const double margin_fine = kNormaliserRel + ref_round;
+  // how far the reference's sum of all V probabilities (each rounded, summed
+  // in list order) lies from 1 at most
+  const double full_mass_rel = (2.0 * (double)a.vocab + 2.0) * 0x1p-53;
   double margin = kScanSumRel + ref_round;
   bool refined = false;
 
@@ -1385,7 +1522,8 @@ __device__ __forceinline__ uint32_t finish_row(const SampleArgs& a, FinishLds& U
       for (int i = lane; i < n_valid; i += 64) fp[i] = gsm::js_exp(fp[i] - M);
       __builtin_amdgcn_wave_barrier();
       uint32_t xf = 0;
-      const int r = filters_and_draw_wave(a, row, cfg, fp, total, fid, n_valid, complete, margin, true, &xf);
+      const int r = filters_and_draw_wave(a, row, cfg, fp, total, fid, n_valid, complete, margin, true, full_mass_rel,
+                                          fp + 2 * kTopR, &xf);
       if (lane == 0) {
         S.fast_done = r == 0 ? 1u : (r == 2 ? 2u : (r == 3 ? 3u : 0u));
         S.exact_flags = xf;
@@ -1398,7 +1536,8 @@ __device__ __forceinline__ uint32_t finish_row(const SampleArgs& a, FinishLds& U
       }
       if (wave == 0) {
         uint32_t xf = 0;
-        const int r = filters_and_draw_wave(a, row, cfg, fp, total, fid, n_valid, complete, margin, false, &xf);
+        const int r = filters_and_draw_wave(a, row, cfg, fp, total, fid, n_valid, complete, margin, false,
+                                            full_mass_rel, fp + 2 * kTopR, &xf);
         if (lane == 0) {
           S.fast_done = r == 0 ? 1u : (r == 3 ? 3u : 0u);
           S.exact_flags = xf;
@@ -1413,6 +1552,10 @@ __device__ __forceinline__ uint32_t finish_row(const SampleArgs& a, FinishLds& U
   }
 
   // ---- slow path: the whole region sorted, then the filters block-wide
+  // (typical-p needs its whole pool among the fast path's candidates)
+  if (cfg.typical_p < 1) {
+    return kExactRequest | 0u;
+  }
   {
     uint64_t* scratch = (uint64_t*)S.cand_p;
     need_region();
@@ -1552,12 +1695,20 @@ __device__ __forceinline__ uint32_t finish_row(const SampleArgs& a, FinishLds& U
     __syncthreads();
     if (tid == 0) S.first_idx = 0xFFFFFFFFu;
     __syncthreads();
-  } else if (!n_complete) {
+  }
+  // no cut reached past the region: the pool is the whole row (a
+  // full-vocabulary draw), whose candidate total is the row's whole mass
+  const bool full_mass = cfg.top_p >= 1 && !n_complete;
+  if (full_mass && !(cfg.top_k <= 0 && !(cfg.min_p > 0))) {
+    // a top-k or min-p pool that ends past the region
     return kExactRequest | 0u;
   }
   tie_report = S.status_flags;
 
   // ---- draw (sampling.ts:58-64): first i with prefix_i >= u * sum_{j<n} p_j
+  // (with a full pool: u * 1, the prefix sums carrying the normaliser's error,
+  // settled again with the recomputed normaliser when within that margin)
+  const double u = cfg.rng_mode == GS_RNG_EXPLICIT ? cfg.uniform : gsm::mulberry32_draw(cfg.seed, cfg.draw_index);
   {
     double local[kPer];
     double s = 0.0;
@@ -1568,7 +1719,11 @@ __device__ __forceinline__ uint32_t finish_row(const SampleArgs& a, FinishLds& U
     }
     double ctotal;
     const double base = block_scan_f64(s, S.wtmp, &ctotal) - s;
-    const double u = cfg.rng_mode == GS_RNG_EXPLICIT ? cfg.uniform : gsm::mulberry32_draw(cfg.seed, cfg.draw_index);
+    double dmargin = kNearTie * ctotal;
+    if (full_mass) {
+      ctotal = 1.0;
+      dmargin = margin + full_mass_rel + kNearTie;
+    }
     const double cursor = u * ctotal;
     uint32_t my_first = 0xFFFFFFFFu;
     bool my_near = false;
@@ -1578,7 +1733,7 @@ __device__ __forceinline__ uint32_t finish_row(const SampleArgs& a, FinishLds& U
       const double pre = base + local[q];
       if (pre >= cursor) my_first = (uint32_t)i;
       const double d = pre >= cursor ? pre - cursor : cursor - pre;
-      if (d < kNearTie * ctotal) my_near = true;
+      if (d < dmargin) my_near = true;
     }
     my_first = wave_min_u32(my_first);
     const bool wave_near = __ballot(my_near) != 0;
@@ -1587,20 +1742,478 @@ __device__ __forceinline__ uint32_t finish_row(const SampleArgs& a, FinishLds& U
       if (wave_near) atomicOr(&S.route_exact, 8u);
     }
     __syncthreads();
+    if (full_mass && !constrained && (S.route_exact == 8u || S.first_idx == 0xFFFFFFFFu)) {
+      // a full-vocabulary draw within the scan normaliser's margin or past
+      // the region: the deep draw takes it from the region's candidates
+      if (tid == 0) {
+        S.deep_m = M;
+        S.deep_u = u;
+        S.deep_thr = thr;
+        S.deep_floor = region_floor;
+        S.deep_n = (uint32_t)n;
+        S.deep_margin = margin_fine + full_mass_rel + kNearTie;
+      }
+      return kDeepRequest;
+    }
     if (S.route_exact || S.first_idx == 0xFFFFFFFFu) {
+      // a near tie, or a full-vocabulary draw past the region
       return kExactRequest | (S.route_exact ? GS_FLAG_NEAR_TIE : 0u);
     }
     if (tid == 0) {
       const int i = (int)S.first_idx;
       write_result(a, row, (int32_t)S.cand_id[i], tie_report, S.cand_p[i] / total);
     }
+    return 0;
   }
+}
+
+// Bin of a value v (l/T, or a special's penalised value) in the deep draw's
+// tail histogram: kDeepBins bins of kDeepSpan / kDeepBins below vf, the
+// region floor's value, bin 0 the highest, values further down in the last.
+// A non-increasing function of v, so the bins are contiguous runs of the
+// reference's sorted list.
+__device__ __forceinline__ int deep_bin(double v, double vf) {
+  const double z = (vf - v) * ((double)kDeepBins / kDeepSpan);
+  return z < (double)(kDeepBins - 1) ? (int)z : kDeepBins - 1;
+}
+
+// Exact sums of exponentials in 128-bit fixed point (units of 2^-100): a
+// term e in (0, 1] is its 53-bit mantissa shifted to that scale, truncated
+// below 2^-100 (at most V 2^-100 over a row); integer addition is exact and
+// associative, so any summation order gives the same sum.
+struct Fix128 {
+  uint64_t lo, hi;
+};
+__device__ __forceinline__ Fix128 fix_add(Fix128 a, Fix128 b) {
+  Fix128 r;
+  r.lo = a.lo + b.lo;
+  r.hi = a.hi + b.hi + (r.lo < a.lo ? 1ull : 0ull);
+  return r;
+}
+__device__ __forceinline__ Fix128 fix_neg(Fix128 a) {
+  Fix128 r;
+  r.lo = ~a.lo + 1ull;
+  r.hi = ~a.hi + (r.lo == 0 ? 1ull : 0ull);
+  return r;
+}
+__device__ __forceinline__ Fix128 fix_of(double e) {
+  Fix128 r{0ull, 0ull};
+  if (!(e > 0)) return r;
+  int ex;
+  const double m = __builtin_frexp(e, &ex);            // e = m 2^ex, m in [0.5, 1)
+  const uint64_t mi = (uint64_t)__builtin_ldexp(m, 53);  // 53-bit integer mantissa
+  const int sh = ex - 53 + 100;                        // e 2^100 = mi 2^sh
+  if (sh <= -64) return r;
+  if (sh < 0) { r.lo = mi >> (-sh); return r; }
+  if (sh < 64) { r.lo = mi << sh; r.hi = sh ? mi >> (64 - sh) : 0ull; return r; }
+  r.hi = mi << (sh - 64);
+  return r;
+}
+__device__ __forceinline__ double fix_to_double(Fix128 a) {
+  return __builtin_ldexp((double)a.hi, -36) + __builtin_ldexp((double)a.lo, -100);
+}
+// the block-wide sum of one Fix128 per thread, in every thread; s_w holds
+// 2 * kWaves u64 of LDS
+__device__ __forceinline__ Fix128 block_fix_sum(Fix128 v, uint64_t* s_w) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  for (int m = 32; m > 0; m >>= 1) {
+    Fix128 o;
+    o.lo = shfl_xor_u64(v.lo, m);
+    o.hi = shfl_xor_u64(v.hi, m);
+    v = fix_add(v, o);
+  }
+  __syncthreads();
+  if (lane == 0) { s_w[2 * wave] = v.lo; s_w[2 * wave + 1] = v.hi; }
+  __syncthreads();
+  Fix128 t{0ull, 0ull};
+  for (int w = 0; w < kWaves; ++w) t = fix_add(t, Fix128{s_w[2 * w], s_w[2 * w + 1]});
+  __syncthreads();
+  return t;
+}
+
+// Slot of id in the LDS hash set of the row's special ids (-1: absent).
+__device__ __forceinline__ bool deep_is_special(const uint32_t* set, uint32_t id) {
+  uint32_t h = hash_id(id) & (kHashSize - 1);
+  for (int probe = 0; probe < kHashSize; ++probe) {
+    const uint32_t x = set[h];
+    if (x == id) return true;
+    if (x == 0xFFFFFFFFu) return false;
+    h = (h + 1) & (kHashSize - 1);
+  }
+  return false;
+}
+
+// A full-vocabulary draw (topK 0, topP 1, no min-p or typical-p) whose cursor
+// lies past the complete region of the chunk lists, or within the scan
+// normaliser's margin of one of its prefix sums (sampling.ts:58-64 over the
+// whole sorted list). finish_row left the region's candidates in list order
+// with their exact exponentials (cand_p / cand_id, deep_n of them), the row's
+// specials (sp_key / sp_id) and M, u, the region floor and the decision
+// margin. One pass over the row's logits below the floor builds a binary64
+// mass histogram over value bins (the table exponential, 4.2e-10 per term),
+// which also gives the normaliser to that accuracy; the region is walked
+// again with it; failing that, the bins the cursor falls in are gathered,
+// sorted by (value desc, id asc), given their exact exponentials and walked.
+// Returns 0 with the result written, or kExactRequest | flags. Unconstrained
+// rows only; the whole block calls it.
+__device__ __noinline__ uint32_t deep_draw(const SampleArgs& a, FinishLds& U) {
+  Shared& S = U.fin;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int64_t row = blockIdx.x;
+  const gs_row_config cfg = a.configs[row];
+  const double T = cfg.temperature;
+  const double M = S.deep_m, u = S.deep_u, margin = S.deep_margin;
+  const uint32_t thr = S.deep_thr;
+  const int n_reg = (int)S.deep_n;
+  const int n_sp = (int)(S.n_special < (uint32_t)kSpecialCap ? S.n_special : (uint32_t)kSpecialCap);
+  const double vf = (double)key_f32(thr) / T;  // the region floor's value
+  const int64_t V = a.vocab;
+  double* mass = (double*)S.sorted;   // [kDeepBins]
+  uint32_t* count = S.hash_ids;       // [kDeepBins]
+  uint32_t* spset = S.hash_counts;    // hash set of the special ids
+  for (int b = tid; b < kDeepBins; b += kFinishThreads) { mass[b] = 0.0; count[b] = 0; spset[b] = 0xFFFFFFFFu; }
+  if (tid < 256) S.tab[tid] = c_exp2_256[tid];
+  if (tid == 0) S.deep_count = 0;
+  __syncthreads();
+  for (int i = tid; i < n_sp; i += kFinishThreads) special_insert(SpecialTable{spset, S.hist}, S.sp_id[i], 1u);
+  // the term e^(v - M) of a value v, by the table exponential
+  auto term = [&](double v) -> double {
+    const double y = (v - M) * GS_256_LOG2E;
+    const double e = exp2_256(y, S.tab);
+    return y > kSkipY ? e : 0.0;
+  };
+  // ---- pass 1: the tail's mass and count per bin. Every finite logit below
+  // the floor counts with its own value (specials too; corrected below)
+  auto visit = [&](float l) {
+    if (cfg.softcap > 0) l = gsm::softcap_f32(l, cfg.softcap);
+    if (!(l > -__builtin_inff()) || f32_key(l) >= thr) return;
+    const double v = (double)l / T;
+    const int b = deep_bin(v, vf);
+    atomicAdd(&mass[b], term(v));
+    atomicAdd(&count[b], 1u);
+  };
+  int64_t from = 0;
+  if (a.vector_ok) {
+    const bool bf16 = a.dtype == GS_BF16;
+    const int per = bf16 ? 8 : 4;
+    const int64_t n_vec = V / per;
+    const uint4* base = (const uint4*)((const char*)a.logits + row * a.row_stride * (bf16 ? 2 : 4));
+#pragma unroll 2
+    for (int64_t vi = tid; vi < n_vec; vi += kFinishThreads) {
+      const uint4 w = base[vi];
+      const uint32_t q[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        if (bf16) {
+          visit(__builtin_bit_cast(float, q[j] << 16));
+          visit(__builtin_bit_cast(float, q[j] & 0xFFFF0000u));
+        } else {
+          visit(__builtin_bit_cast(float, q[j]));
+        }
+      }
+    }
+    from = n_vec * per;
+  }
+  for (int64_t i = from + tid; i < V; i += kFinishThreads) visit(load_logit(a, row, i));
+  __syncthreads();
+  // specials: out with their raw values (where the pass counted them), in with
+  // their penalised ones when those lie below the floor
+  for (int i = tid; i < n_sp; i += kFinishThreads) {
+    const uint32_t id = S.sp_id[i];
+    float l = load_logit(a, row, id);
+    if (cfg.softcap > 0) l = gsm::softcap_f32(l, cfg.softcap);
+    if (l > -__builtin_inff() && f32_key(l) < thr) {
+      const double v = (double)l / T;
+      const int b = deep_bin(v, vf);
+      atomicAdd(&mass[b], -term(v));
+      atomicSub(&count[b], 1u);
+    }
+    const double vs = key_f64(S.sp_key[i]);
+    if (S.sp_key[i] < S.deep_floor && vs > -__builtin_inf()) {
+      const int b = deep_bin(vs, vf);
+      atomicAdd(&mass[b], term(vs));
+      atomicAdd(&count[b], 1u);
+    }
+  }
+  __syncthreads();
+  // ---- the region's exact mass, the tail's, and the normaliser in binary64
+  constexpr int kPer = kFinishCap / kFinishThreads;  // region entries per thread (and bins)
+  double r_local[kPer];
+  double r_base, r_mass;
+  {
+    double sum = 0.0;
+#pragma unroll
+    for (int q = 0; q < kPer; ++q) {
+      const int i = tid * kPer + q;
+      sum += i < n_reg ? S.cand_p[i] : 0.0;
+      r_local[q] = sum;
+    }
+    r_base = block_scan_f64(sum, S.wtmp, &r_mass) - sum;
+  }
+  static_assert(kDeepBins == kFinishCap, "one pass of kPer bins per thread");
+  double b_local[kPer];
+  double b_base, t_mass;
+  {
+    double sum = 0.0;
+#pragma unroll
+    for (int q = 0; q < kPer; ++q) {
+      sum += mass[tid * kPer + q];
+      b_local[q] = sum;
+    }
+    b_base = block_scan_f64(sum, S.wtmp, &t_mass) - sum;
+  }
+  const double total = r_mass + t_mass;
+  if (!(total < __builtin_inf()) || !(total > 0)) return kExactRequest | 0u;
+  // the region's exact mass in fixed point, for the exact refinement below
+  Fix128 r_fix{0ull, 0ull};
+  for (int i = tid; i < n_reg; i += kFinishThreads) r_fix = fix_add(r_fix, fix_of(S.cand_p[i]));
+  r_fix = block_fix_sum(r_fix, (uint64_t*)S.top);
+  const double target = u * total;       // the cursor, in units of e
+  const double mrg = margin * total;     // the decision margin, in the same units
+  // ---- the region with the recomputed normaliser
+  if (tid == 0) { S.first_idx = 0xFFFFFFFFu; S.route_exact = 0; }
+  __syncthreads();
+  {
+    uint32_t first = 0xFFFFFFFFu;
+    bool near = false;
+    for (int q = kPer - 1; q >= 0; --q) {
+      const int i = tid * kPer + q;
+      if (i >= n_reg) continue;
+      const double pre = r_base + r_local[q];
+      if (pre >= target) first = (uint32_t)i;
+      if ((pre >= target ? pre - target : target - pre) < mrg) near = true;
+    }
+    first = wave_min_u32(first);
+    const bool wn = __ballot(near) != 0;
+    if (lane == 0) {
+      if (first != 0xFFFFFFFFu) atomicMin(&S.first_idx, first);
+      if (wn) atomicOr(&S.route_exact, 1u);
+    }
+  }
+  __syncthreads();
+  if (S.route_exact) return kExactRequest | GS_FLAG_NEAR_TIE;
+  if (S.first_idx != 0xFFFFFFFFu) {
+    if (tid == 0) write_result(a, row, (int32_t)S.cand_id[S.first_idx], 0u, S.cand_p[S.first_idx] / total);
+    return 0;
+  }
+  // ---- the bins the cursor falls in (a neighbour too when its boundary lies
+  // within the margin)
+  {
+    uint32_t first = 0xFFFFFFFFu;
+    for (int q = kPer - 1; q >= 0; --q) {
+      if (r_mass + b_base + b_local[q] >= target) first = (uint32_t)(tid * kPer + q);
+    }
+    first = wave_min_u32(first);
+    if (lane == 0 && first != 0xFFFFFFFFu) atomicMin(&S.first_idx, first);
+  }
+  __syncthreads();
+  const int bc = (int)S.first_idx;
+  if (bc < 0 || bc >= kDeepBins - 1) return kExactRequest | 0u;  // past the bins' span
+  __syncthreads();
+  // cumulative mass before and after bin bc, from the thread holding it
+  // register arrays are read at static indices only (a dynamic one would put
+  // them in scratch memory)
+  auto pick_local = [&](const double (&arr)[kPer], int q) -> double {
+    double x = 0.0;
+#pragma unroll
+    for (int k = 0; k < kPer; ++k) x = k == q ? arr[k] : x;
+    return x;
+  };
+  if (tid == bc / kPer) {
+    const double after = r_mass + b_base + pick_local(b_local, bc % kPer);
+    const double before = after - mass[bc];
+    int lo = bc, hi = bc;
+    if (before >= target - mrg) lo = bc > 0 ? bc - 1 : 0;
+    if (after < target + mrg) hi = bc + 1;
+    S.sel[0] = (uint32_t)lo;
+    S.sel[1] = (uint32_t)hi;
+  }
+  __syncthreads();
+  const int b_lo = (int)S.sel[0], b_hi = (int)S.sel[1];
+  if (b_hi >= kDeepBins - 1) return kExactRequest | 0u;
+  uint32_t n_in = 0;
+  for (int b = b_lo; b <= b_hi; ++b) n_in += count[b];
+  if (n_in > (uint32_t)kFinishCap) return kExactRequest | 0u;  // a crowd of equal values
+  // mass of the bins above b_lo, with the region's
+  if (tid == (b_lo > 0 ? (b_lo - 1) / kPer : 0)) {
+    S.wsum[0] = b_lo > 0 ? r_mass + b_base + pick_local(b_local, (b_lo - 1) % kPer) : r_mass;
+  }
+  __syncthreads();
+  const double pre_before = S.wsum[0];
+  __syncthreads();
+  // ---- pass 2: gather the bins' entries (value key, id) into sorted / hash_ids
+  uint64_t* gkey = S.sorted;
+  uint32_t* gid = S.hash_ids;
+  auto gather = [&](double v, uint32_t id) {
+    const int b = deep_bin(v, vf);
+    if (b < b_lo || b > b_hi) return;
+    const uint32_t pos = atomicAdd(&S.deep_count, 1u);
+    if (pos < (uint32_t)kFinishCap) { gkey[pos] = f64_key(v); gid[pos] = id; }
+  };
+  auto visit2 = [&](float l, uint32_t id) {
+    if (cfg.softcap > 0) l = gsm::softcap_f32(l, cfg.softcap);
+    if (!(l > -__builtin_inff()) || f32_key(l) >= thr) return;
+    const double v = (double)l / T;
+    const int b = deep_bin(v, vf);
+    if (b < b_lo || b > b_hi || deep_is_special(spset, id)) return;
+    gather(v, id);
+  };
+  if (a.vector_ok) {
+    const bool bf16 = a.dtype == GS_BF16;
+    const int per = bf16 ? 8 : 4;
+    const int64_t n_vec = V / per;
+    const uint4* base = (const uint4*)((const char*)a.logits + row * a.row_stride * (bf16 ? 2 : 4));
+#pragma unroll 2
+    for (int64_t vi = tid; vi < n_vec; vi += kFinishThreads) {
+      const uint4 w = base[vi];
+      const uint32_t q[4] = {w.x, w.y, w.z, w.w};
+      const uint32_t id0 = (uint32_t)(vi * per);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        if (bf16) {
+          visit2(__builtin_bit_cast(float, q[j] << 16), id0 + 2 * j);
+          visit2(__builtin_bit_cast(float, q[j] & 0xFFFF0000u), id0 + 2 * j + 1);
+        } else {
+          visit2(__builtin_bit_cast(float, q[j]), id0 + j);
+        }
+      }
+    }
+  }
+  for (int64_t i = from + tid; i < V; i += kFinishThreads) visit2(load_logit(a, row, i), (uint32_t)i);
+  for (int i = tid; i < n_sp; i += kFinishThreads) {
+    const double vs = key_f64(S.sp_key[i]);
+    if (S.sp_key[i] < S.deep_floor && vs > -__builtin_inf()) gather(vs, S.sp_id[i]);
+  }
+  __syncthreads();
+  const int n_g = (int)S.deep_count;
+  if (n_g != (int)n_in || n_g == 0) return kExactRequest | 0u;
+  // ---- sort them (value desc, id asc) and walk them with exact exponentials
+  const int m2 = pow2_at_least(n_g);
+  for (int i = n_g + tid; i < m2; i += kFinishThreads) { gkey[i] = 0; gid[i] = 0xFFFFFFFFu; }
+  __syncthreads();
+  block_sort_pairs_desc(gkey, gid, m2);
+  for (int i = tid; i < n_g; i += kFinishThreads) S.cand_p[i] = gsm::js_exp(key_f64(gkey[i]) - M);
+  if (tid == 0) { S.first_idx = 0xFFFFFFFFu; S.route_exact = 0; }
+  __syncthreads();
+  {
+    double g_local[kPer];
+    double sum = 0.0;
+    for (int q = 0; q < kPer; ++q) {
+      const int i = tid * kPer + q;
+      sum += i < n_g ? S.cand_p[i] : 0.0;
+      g_local[q] = sum;
+    }
+    double g_total;
+    const double g_base = block_scan_f64(sum, S.wtmp, &g_total) - sum;
+    uint32_t first = 0xFFFFFFFFu;
+    bool near = false;
+    for (int q = kPer - 1; q >= 0; --q) {
+      const int i = tid * kPer + q;
+      if (i >= n_g) continue;
+      const double pre = pre_before + g_base + g_local[q];
+      if (pre >= target) first = (uint32_t)i;
+      if ((pre >= target ? pre - target : target - pre) < mrg) near = true;
+    }
+    first = wave_min_u32(first);
+    const bool wn = __ballot(near) != 0;
+    if (lane == 0) {
+      if (first != 0xFFFFFFFFu) atomicMin(&S.first_idx, first);
+      if (wn) atomicOr(&S.route_exact, 1u);
+    }
+  }
+  __syncthreads();
+  if (!S.route_exact) {
+    if (S.first_idx == 0xFFFFFFFFu) return kExactRequest | 0u;
+    if (tid == 0) write_result(a, row, (int32_t)gid[S.first_idx], 0u, S.cand_p[S.first_idx] / total);
+    return 0;
+  }
+  // ---- pass 3, for a cursor within the table exponential's margin: the
+  // normaliser and the mass above the gathered bins from the exact terms
+  // (js_exp, the reference's own), summed exactly in fixed point. They lie
+  // within 2^-79 of the real sums, which the reference's sequential sums
+  // approach within (2V + 2) 2^-53; the walk then needs only that margin.
+  Fix128 all{0ull, 0ull}, above{0ull, 0ull};
+  auto visit3 = [&](float l) {
+    if (cfg.softcap > 0) l = gsm::softcap_f32(l, cfg.softcap);
+    if (!(l > -__builtin_inff()) || f32_key(l) >= thr) return;
+    const double v = (double)l / T;
+    const Fix128 f = fix_of(gsm::js_exp(v - M));
+    all = fix_add(all, f);
+    if (deep_bin(v, vf) < b_lo) above = fix_add(above, f);
+  };
+  // (rare: one element at a time, two loads per thread in flight)
+#pragma unroll 2
+  for (int64_t i = tid; i < V; i += kFinishThreads) visit3(load_logit(a, row, i));
+  // specials: out with their raw values (exactly, as integers), in with their
+  // penalised ones below the floor
+  for (int i = tid; i < n_sp; i += kFinishThreads) {
+    float l = load_logit(a, row, S.sp_id[i]);
+    if (cfg.softcap > 0) l = gsm::softcap_f32(l, cfg.softcap);
+    if (l > -__builtin_inff() && f32_key(l) < thr) {
+      const double v = (double)l / T;
+      const Fix128 f = fix_neg(fix_of(gsm::js_exp(v - M)));
+      all = fix_add(all, f);
+      if (deep_bin(v, vf) < b_lo) above = fix_add(above, f);
+    }
+    const double vs = key_f64(S.sp_key[i]);
+    if (S.sp_key[i] < S.deep_floor && vs > -__builtin_inf()) {
+      const Fix128 f = fix_of(gsm::js_exp(vs - M));
+      all = fix_add(all, f);
+      if (deep_bin(vs, vf) < b_lo) above = fix_add(above, f);
+    }
+  }
+  all = block_fix_sum(all, (uint64_t*)S.top);
+  above = block_fix_sum(above, (uint64_t*)S.top);
+  const double total_x = fix_to_double(fix_add(r_fix, all));
+  const double before_x = fix_to_double(fix_add(r_fix, above));
+  const double target_x = u * total_x;
+  const double mrg_x = ((2.0 * (double)V + 2.0) * 0x1p-53 + kNearTie + 0x1p-46) * total_x;
+  if (tid == 0) { S.first_idx = 0xFFFFFFFFu; S.route_exact = 0; }
+  __syncthreads();
+  {
+    double g_local[kPer];
+    double sum = 0.0;
+#pragma unroll
+    for (int q = 0; q < kPer; ++q) {
+      const int i = tid * kPer + q;
+      sum += i < n_g ? S.cand_p[i] : 0.0;
+      g_local[q] = sum;
+    }
+    double g_total;
+    const double g_base = block_scan_f64(sum, S.wtmp, &g_total) - sum;
+    uint32_t first = 0xFFFFFFFFu;
+    bool near = false;
+#pragma unroll
+    for (int q = kPer - 1; q >= 0; --q) {
+      const int i = tid * kPer + q;
+      if (i >= n_g) continue;
+      const double pre = before_x + g_base + g_local[q];
+      if (pre >= target_x) first = (uint32_t)i;
+      if ((pre >= target_x ? pre - target_x : target_x - pre) < mrg_x) near = true;
+    }
+    first = wave_min_u32(first);
+    const bool wn = __ballot(near) != 0;
+    if (lane == 0) {
+      if (first != 0xFFFFFFFFu) atomicMin(&S.first_idx, first);
+      if (wn) atomicOr(&S.route_exact, 1u);
+    }
+  }
+  __syncthreads();
+  if (S.route_exact) return kExactRequest | GS_FLAG_NEAR_TIE;
+  if (S.first_idx == 0xFFFFFFFFu) return kExactRequest | 0u;
+  if (tid == 0) write_result(a, row, (int32_t)gid[S.first_idx], 0u, S.cand_p[S.first_idx] / total_x);
   return 0;
 }
 
 __global__ __launch_bounds__(kFinishThreads) void finish_kernel(SampleArgs a) {
   __shared__ FinishLds U;
-  const uint32_t r = finish_row(a, U);
+  uint32_t r = finish_row(a, U);
+  if (r == kDeepRequest) {
+    __syncthreads();
+    // a call of its own that reads the arguments where the kernel received
+    // them, so the kernel's copy never goes to the stack
+    r = deep_draw(*(const SampleArgs*)__builtin_amdgcn_kernarg_segment_ptr(), U);
+  }
   // the exact path is entered from here only, where nothing else is live
   if (r & kExactRequest) to_exact(a, U, blockIdx.x, r & ~kExactRequest);
 }

@@ -95,17 +95,22 @@ struct Plan {
   int32_t depth;  // per-chunk rank depth of the one-pass path
 };
 
+// Routes: greedy rows; top-k rows up to kMaxFastK (chunk lists min(topK, 16)
+// deep, typical-p among them: its pool is the top-k); every other row keeps
+// 64 entries per chunk (top-p and min-p cuts, top-k up to kFinishCap, draws
+// over the whole vocabulary), and the finish resolves what falls inside the
+// complete region; typical-p over a longer pool, extreme temperatures and
+// forced rows take the exact replay.
 __host__ __device__ __forceinline__ Plan plan_row(const gs_row_config& c) {
   if (c.temperature == 0) return Plan{kRouteGreedy, 1};
   if (c.options & GS_ROW_FORCE_EXACT) return Plan{kRouteExact, 0};
   // between these bounds l/T keeps the order and the ties of the f32 logits
   if (!(c.temperature >= 1.0e-200 && c.temperature <= 1.0e200)) return Plan{kRouteExact, 0};
-  if (c.typical_p < 1) return Plan{kRouteExact, 0};
-  if (c.top_k > 0)
-    return c.top_k <= kMaxFastK ? Plan{kRouteTopK, c.top_k < kTopKChunkDepth ? c.top_k : kTopKChunkDepth}
-                                : Plan{kRouteExact, 0};
-  if (c.top_p < 1 || c.min_p > 0) return Plan{kRouteTopP, kTopPListL};
-  return Plan{kRouteExact, 0};
+  const bool topk_fast = c.top_k > 0 && c.top_k <= kMaxFastK;
+  if (c.typical_p < 1 && !topk_fast) return Plan{kRouteExact, 0};
+  if (topk_fast) return Plan{kRouteTopK, c.top_k < kTopKChunkDepth ? c.top_k : kTopKChunkDepth};
+  if (c.top_k > kFinishCap) return Plan{kRouteExact, 0};
+  return Plan{kRouteTopP, kTopPListL};
 }
 // plan_row with every field read whatever the route (selects, not branches),
 // so that a kernel fetches the whole configuration at once instead of one
@@ -114,13 +119,12 @@ __device__ __forceinline__ Plan plan_row_flat(const gs_row_config& c) {
   const bool greedy = c.temperature == 0;
   const bool forced = (c.options & GS_ROW_FORCE_EXACT) != 0;
   const bool t_out = !(c.temperature >= 1.0e-200 && c.temperature <= 1.0e200);
-  const bool typical = c.typical_p < 1;
-  const bool topk = c.top_k > 0, topk_fast = c.top_k <= kMaxFastK;
-  const bool topp = c.top_p < 1 || c.min_p > 0;
+  const bool topk_fast = c.top_k > 0 && c.top_k <= kMaxFastK;
+  const bool typical_long = c.typical_p < 1 && !topk_fast;
   const int depth_k = c.top_k < kTopKChunkDepth ? c.top_k : kTopKChunkDepth;
-  const bool exact = forced || t_out || typical || (topk ? !topk_fast : !topp);
-  const int route = greedy ? kRouteGreedy : (exact ? kRouteExact : (topk ? kRouteTopK : kRouteTopP));
-  const int depth = greedy ? 1 : (exact ? 0 : (topk ? depth_k : kTopPListL));
+  const bool exact = forced || t_out || typical_long || c.top_k > kFinishCap;
+  const int route = greedy ? kRouteGreedy : (exact ? kRouteExact : (topk_fast ? kRouteTopK : kRouteTopP));
+  const int depth = greedy ? 1 : (exact ? 0 : (topk_fast ? depth_k : kTopPListL));
   return Plan{route, depth};
 }
 

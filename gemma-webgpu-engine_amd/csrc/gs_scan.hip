@@ -536,22 +536,24 @@ __device__ __forceinline__ void scan_group(const SampleArgs& a, const gs_row_con
   mark_specials<In, kMasked>(a, rr, gbase, nc * kChunk, hid0, hid1, fid0, S.special);
   lds_barrier();
 
-  // Chunk i is reduced from cur while chunk i+1 streams into nxt; then nxt
-  // moves over and chunk i+2 starts loading. The first chunk that truncates
-  // fixes the group's tau; the chunks after it take the stream path.
+  // Two buffers with fixed roles (the loop is unrolled by two, so no register
+  // rotation copies wait on loads just issued): chunk i is reduced from cur
+  // while chunk i+1 streams into nxt, then cur starts loading chunk i+2, and
+  // chunk i+1 is reduced from nxt while chunk i+2 streams in.
   uint32_t thr = 0;
 #pragma unroll 1
-  for (int i = 0; i < nc; ++i) {
-    const uint32_t t = chunk_stats<In, true, kMasked>(a, cfg, plan, row, c0 + i, kChunk, cur, mc,
-                                                      S.special + i * kChunkWords, S.tab, S.slots[i & 1], S.stage, thr);
+  for (int i = 0; i < nc; i += 2) {
+    uint32_t t = chunk_stats<In, true, kMasked>(a, cfg, plan, row, c0 + i, kChunk, cur, mc,
+                                                S.special + i * kChunkWords, S.tab, S.slots[0], S.stage, thr);
     thr = thr ? thr : t;
-#pragma unroll
-    for (int v = 0; v < kLoads; ++v) {
-      cur[v] = nxt[v];
-      mc[v] = mn[v];
-    }
-    load_group_logits<In>(lg, i + 2, nc, nxt);
-    if (kMasked) load_group_masks<In>(mk, i + 2, nc, mn);
+    load_group_logits<In>(lg, i + 2, nc, cur);
+    if (kMasked) load_group_masks<In>(mk, i + 2, nc, mc);
+    if (i + 1 >= nc) break;
+    t = chunk_stats<In, true, kMasked>(a, cfg, plan, row, c0 + i + 1, kChunk, nxt, mn,
+                                       S.special + (i + 1) * kChunkWords, S.tab, S.slots[1], S.stage, thr);
+    thr = thr ? thr : t;
+    load_group_logits<In>(lg, i + 3, nc, nxt);
+    if (kMasked) load_group_masks<In>(mk, i + 3, nc, mn);
   }
 }
 

@@ -1,0 +1,154 @@
+"""GPU parity of the option settings that used to fall onto the exact replay:
+a full-vocabulary draw (topK 0, topP 1: the generate() defaults with a
+temperature), top-k above 64, and typical-p with top-k up to 64. Ids are
+bit-exact against the oracle (sampling.ts:18-65); probabilities identical on
+exact-path rows and within PROB_RTOL relative on one-pass rows."""
+import numpy as np
+import pytest
+
+from oracle.oracle import Decoding
+
+pytestmark = pytest.mark.gpu
+
+PROB_RTOL = 4e-7
+V = 262144
+
+
+def _gs():
+    import gsample
+
+    return gsample
+
+
+def to_oracle_cfg(c):
+    return Decoding(temperature=c.temperature, topK=c.topK, topP=c.topP, minP=c.minP, typicalP=c.typicalP,
+                    repetitionPenalty=c.repetitionPenalty, repetitionWindow=c.repetitionWindow,
+                    frequencyPenalty=c.frequencyPenalty, presencePenalty=c.presencePenalty)
+
+
+def check(gs, oracle, label, out, xs, hists, cfgs, us):
+    exact = 0
+    for r in range(len(cfgs)):
+        t, tr = oracle.sample_token(xs[r], hists[r] if hists else [], to_oracle_cfg(cfgs[r]), us[r])
+        assert int(out.tokens[r]) == t, f"{label} row {r}: {int(out.tokens[r])} != {t} (flags {int(out.flags[r])})"
+        p = 1.0 if cfgs[r].temperature == 0 else tr.probability
+        if out.flags[r] & gs.GS_FLAG_EXACT_PATH:
+            exact += 1
+            assert out.probabilities[r] == p, (label, r)
+        else:
+            assert abs(out.probabilities[r] - p) <= PROB_RTOL * p, (label, r, out.probabilities[r], p)
+    return exact
+
+
+def test_full_vocabulary_draws(sampler, oracle):
+    """topK 0, topP 1: the draw walks the whole sorted vocabulary. Draws that
+    land inside the complete region of the chunk lists are settled there
+    (ctotal is the row's whole mass, 1 within (2V + 2) 2^-53); the rest
+    replay exactly. u spans [0, 1) including both ends."""
+    import torch
+
+    gs = _gs()
+    w = gs.workloads.multinomial(rows=list(range(48)))
+    us = [0.0, 1 - 2 ** -32] + [float(u) for u in np.random.default_rng(3).random(46)]
+    cfgs = [c.merged(temperature=t) for c, t in zip(w.configs, [0.8, 0.5, 1.0, 0.7] * 12)]
+    # with a penalty window on some rows (its ids among the row's largest logits)
+    hists = [np.argsort(-w.logits[r])[:30].tolist() if r % 3 == 0 else [] for r in range(48)]
+    cfgs = [c.merged(repetitionPenalty=1.2, repetitionWindow=64) if r % 3 == 0 else c for r, c in enumerate(cfgs)]
+    conf = np.stack([gs.runtime.row_config(c, uniform=u) for c, u in zip(cfgs, us)])
+    out = sampler.sample(torch.from_numpy(w.logits).cuda(), conf, histories=hists)
+    exact = check(gs, oracle, "full draw", out, w.logits, hists, cfgs, us)
+    assert exact < 24, exact  # most draws settle on the one-pass path
+
+
+def test_full_vocabulary_draw_boundary(sampler, oracle):
+    """u placed on a prefix-sum boundary of the sorted probabilities (within
+    1e-12 of it): the one-pass draw cannot decide it and the row replays
+    exactly, with the oracle's id."""
+    import torch
+
+    gs = _gs()
+    rng = np.random.default_rng(19)
+    x = rng.normal(0, 3, V).astype(np.float32)
+    T = 0.8
+    v = np.sort(x.astype(np.float64) / T)[::-1]
+    e = np.exp(v - v[0])
+    cum = np.cumsum(e / e.sum())
+    us, xs = [], []
+    for i in (0, 3, 40):
+        for d in (-1e-12, 1e-12):
+            us.append(float(cum[i] + d))
+            xs.append(x)
+    cfg = gs.DecodingConfig(temperature=T, topK=0, topP=1.0, repetitionWindow=0)
+    cfgs = [cfg] * len(us)
+    conf = np.stack([gs.runtime.row_config(c, uniform=u) for c, u in zip(cfgs, us)])
+    out = sampler.sample(torch.from_numpy(np.stack(xs)).cuda(), conf)
+    check(gs, oracle, "draw boundary", out, xs, None, cfgs, us)
+    assert np.all(out.flags & gs.GS_FLAG_EXACT_PATH), out.flags
+
+
+def test_topk_above_64(sampler, oracle):
+    """topK 65 .. 2000 keep 64 entries per chunk; the finish ranks the
+    complete region (block-wide) and cuts it at K."""
+    import torch
+
+    gs = _gs()
+    w = gs.workloads.topk_deep(rows=list(range(24)))
+    ks = [65, 100, 200, 500, 1000, 2000] * 4
+    ps = [1.0, 0.95, 0.9, 0.5] * 6
+    cfgs = [c.merged(topK=k, topP=p, minP=0.01 if r % 5 == 0 else 0.0) for r, (c, k, p) in
+            enumerate(zip(w.configs, ks, ps))]
+    us = [float(u) for u in np.random.default_rng(4).random(24)]
+    conf = np.stack([gs.runtime.row_config(c, uniform=u) for c, u in zip(cfgs, us)])
+    out = sampler.sample(torch.from_numpy(w.logits).cuda(), conf)
+    exact = check(gs, oracle, "topk>64", out, w.logits, None, cfgs, us)
+    assert exact <= 4, exact
+
+
+def test_typical_p_with_top_k(sampler, oracle):
+    """typicalP with topK <= 64: entropy, the surprise order, its leading
+    mass and the kept set back in list order, in one wave; with min-p, top-p
+    and penalties alongside."""
+    import torch
+
+    gs = _gs()
+    w = gs.workloads.typical(rows=list(range(32)))
+    rng = np.random.default_rng(6)
+    cfgs = []
+    for r, c in enumerate(w.configs):
+        cfgs.append(c.merged(topK=int(rng.choice([5, 20, 40, 64])), typicalP=float(rng.choice([0.9, 0.5, 0.3, 0.99])),
+                             topP=float(rng.choice([1.0, 0.95, 0.8])), minP=float(rng.choice([0.0, 0.0, 0.02])),
+                             temperature=float(rng.choice([0.6, 0.8, 1.0, 1.5]))))
+    hists = [rng.integers(0, V, 100).tolist() for _ in range(32)]
+    cfgs = [c.merged(repetitionPenalty=1.1, repetitionWindow=100) if r % 4 == 0 else c for r, c in enumerate(cfgs)]
+    us = [float(u) for u in rng.random(32)]
+    conf = np.stack([gs.runtime.row_config(c, uniform=u) for c, u in zip(cfgs, us)])
+    out = sampler.sample(torch.from_numpy(w.logits).cuda(), conf, histories=hists)
+    exact = check(gs, oracle, "typical", out, w.logits, hists, cfgs, us)
+    assert exact <= 4, exact
+
+
+def test_typical_p_ties_and_small_pools(oracle):
+    """typical-p on small vocabularies with repeated values (equal surprises,
+    stable order) and a pool of one, against the oracle."""
+    import torch
+
+    gs = _gs()
+    Vs = 5000
+    rng = np.random.default_rng(8)
+    rows, cfgs, us = [], [], []
+    for r in range(24):
+        x = rng.normal(0, 2, Vs).astype(np.float32)
+        if r % 2 == 0:
+            x = (np.round(x * 2) / 2).astype(np.float32)
+        rows.append(x)
+        cfgs.append(gs.DecodingConfig(temperature=1.0, topK=int(rng.choice([1, 3, 16, 64])),
+                                      typicalP=float(rng.choice([0.2, 0.6, 0.95])), topP=1.0, minP=0.0,
+                                      repetitionWindow=0))
+        us.append(float(rng.random()))
+    s = gs.Sampler(vocab_size=Vs, max_rows=32)
+    try:
+        conf = np.stack([gs.runtime.row_config(c, uniform=u) for c, u in zip(cfgs, us)])
+        out = s.sample(torch.from_numpy(np.stack(rows)).cuda(), conf)
+    finally:
+        s.close()
+    check(gs, oracle, "typical small", out, rows, None, cfgs, us)
