@@ -5,7 +5,7 @@ exponential 2^(y/256) = 2^(j/256) * 2^k * e^(s ln2/256), |s| <= 1/2.
 Every value is computed in 80-digit decimal arithmetic and rounded once to
 binary64 (Python's float(Decimal) rounds correctly):
   GS_EXP2_TABLE_256   2^(j/256), j = 0..255
-  GS_EXP2_256_C1/C2   Taylor coefficients (ln2/256)^k / k!, k = 1, 2
+  GS_EXP2_256_C1..C4  Taylor coefficients (ln2/256)^k / k!, k = 1..4
   GS_256_LOG2E        256 / ln 2
 
 usage: python gen_exp2_table.py [output path]   (default: next to this file)
@@ -39,9 +39,11 @@ def render() -> str:
     c = ln2 / 256
     lines += [
         "",
-        "// Taylor coefficients (ln2/256)^k / k!, k = 1, 2, and 256 / ln2",
+        "// Taylor coefficients (ln2/256)^k / k!, k = 1..4, and 256 / ln2",
         f"#define GS_EXP2_256_C1 {hexf(c)}",
         f"#define GS_EXP2_256_C2 {hexf(c * c / 2)}",
+        f"#define GS_EXP2_256_C3 {hexf(c * c * c / 6)}",
+        f"#define GS_EXP2_256_C4 {hexf(c * c * c * c / 24)}",
         f"#define GS_256_LOG2E {hexf(256 / ln2)}",
         "",
     ]

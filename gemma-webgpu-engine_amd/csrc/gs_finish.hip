@@ -1751,7 +1751,7 @@ __device__ __forceinline__ uint32_t finish_row(const SampleArgs& a, FinishLds& U
         S.deep_thr = thr;
         S.deep_floor = region_floor;
         S.deep_n = (uint32_t)n;
-        S.deep_margin = margin_fine + full_mass_rel + kNearTie;
+        S.deep_margin = full_mass_rel + kNearTie;
       }
       return kDeepRequest;
     }
@@ -1777,6 +1777,32 @@ __device__ __forceinline__ int deep_bin(double v, double vf) {
   return z < (double)(kDeepBins - 1) ? (int)z : kDeepBins - 1;
 }
 
+// Bin b's terms e^(v - M) are summed in units of 2^(k - kDeepFracBits), k =
+// deep_scale(b): the bin's values are at most vf - b kDeepSpan / kDeepBins
+// (up to rounding), so every term lies below 2^k (the ceiling and the + 1
+// leave a factor 2 over that bound), and, but in the last bin, above 2^(k - 3)
+// (a bin spans kDeepSpan / kDeepBins < ln 2 / 8 of v). A term then rounds to
+// a whole number of units below 2^42 with a relative error under 2^-40, and a
+// bin of at most 2^21 + kSpecialCap terms sums below 2^64 in a u64.
+constexpr int kDeepFracBits = 42;
+__device__ __forceinline__ int deep_scale(int b, double vf, double M) {
+  const double top = (vf - M) - (double)b * (kDeepSpan / kDeepBins);
+  return (int)__builtin_ceil(top * (GS_256_LOG2E / 256.0)) + 1;
+}
+// e in units of 2^(k - kDeepFracBits), rounded to nearest: e 2^(42 - k) < 2^52,
+// so adding 2^52 leaves the rounded integer in the mantissa field
+__device__ __forceinline__ uint64_t deep_units(double e, int k) {
+  const double x = __builtin_ldexp(e, kDeepFracBits - k) + 0x1p52;
+  return __builtin_bit_cast(uint64_t, x) & ((1ull << 52) - 1);
+}
+// a term of the deep draw: the quartic table exponential of v - M (relative
+// error below 1e-15 against e^(v - M), with the argument's rounding 2e-14),
+// zero below e^-60 of the maximum
+__device__ __forceinline__ double deep_term(double v, double M, const double* tab) {
+  const double y = (v - M) * GS_256_LOG2E;
+  return y > kSkipY ? exp2_256_tight(y, tab) : 0.0;
+}
+
 // Exact sums of exponentials in 128-bit fixed point (units of 2^-100): a
 // term e in (0, 1] is its 53-bit mantissa shifted to that scale, truncated
 // below 2^-100 (at most V 2^-100 over a row); integer addition is exact and
@@ -1790,24 +1816,21 @@ __device__ __forceinline__ Fix128 fix_add(Fix128 a, Fix128 b) {
   r.hi = a.hi + b.hi + (r.lo < a.lo ? 1ull : 0ull);
   return r;
 }
-__device__ __forceinline__ Fix128 fix_neg(Fix128 a) {
-  Fix128 r;
-  r.lo = ~a.lo + 1ull;
-  r.hi = ~a.hi + (r.lo == 0 ? 1ull : 0ull);
-  return r;
+// u 2^s in units of 2^-100 (the bits below 2^-100 dropped)
+__device__ __forceinline__ Fix128 fix_shift(uint64_t u, int s) {
+  if (s <= -64) return Fix128{0ull, 0ull};
+  if (s < 0) return Fix128{u >> (-s), 0ull};
+  if (s == 0) return Fix128{u, 0ull};
+  if (s < 64) return Fix128{u << s, u >> (64 - s)};
+  if (s < 128) return Fix128{0ull, u << (s - 64)};
+  return Fix128{0ull, 0ull};
 }
 __device__ __forceinline__ Fix128 fix_of(double e) {
-  Fix128 r{0ull, 0ull};
-  if (!(e > 0)) return r;
+  if (!(e > 0)) return Fix128{0ull, 0ull};
   int ex;
   const double m = __builtin_frexp(e, &ex);            // e = m 2^ex, m in [0.5, 1)
   const uint64_t mi = (uint64_t)__builtin_ldexp(m, 53);  // 53-bit integer mantissa
-  const int sh = ex - 53 + 100;                        // e 2^100 = mi 2^sh
-  if (sh <= -64) return r;
-  if (sh < 0) { r.lo = mi >> (-sh); return r; }
-  if (sh < 64) { r.lo = mi << sh; r.hi = sh ? mi >> (64 - sh) : 0ull; return r; }
-  r.hi = mi << (sh - 64);
-  return r;
+  return fix_shift(mi, ex - 53 + 100);                 // e 2^100 = mi 2^(ex - 53 + 100)
 }
 __device__ __forceinline__ double fix_to_double(Fix128 a) {
   return __builtin_ldexp((double)a.hi, -36) + __builtin_ldexp((double)a.lo, -100);
@@ -1830,6 +1853,33 @@ __device__ __forceinline__ Fix128 block_fix_sum(Fix128 v, uint64_t* s_w) {
   __syncthreads();
   return t;
 }
+// the exclusive block-wide prefix of one Fix128 per thread (thread order),
+// and the block total in *total; s_w holds 2 * kWaves u64 of LDS
+__device__ __forceinline__ Fix128 block_fix_scan(Fix128 v, uint64_t* s_w, Fix128* total) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  // the wave's exclusive prefix: a butterfly that keeps, per lane, the sum of
+  // the lower lanes of each pair of halves it joins
+  Fix128 incl = v, pre{0ull, 0ull};
+  for (int m = 1; m < 64; m <<= 1) {
+    Fix128 o;
+    o.lo = shfl_xor_u64(incl.lo, m);
+    o.hi = shfl_xor_u64(incl.hi, m);
+    if (lane & m) pre = fix_add(pre, o);
+    incl = fix_add(incl, o);  // the sum of the 2m lanes of this lane's group
+  }
+  __syncthreads();
+  if (lane == 0) { s_w[2 * wave] = incl.lo; s_w[2 * wave + 1] = incl.hi; }
+  __syncthreads();
+  Fix128 off{0ull, 0ull}, t{0ull, 0ull};
+  for (int w = 0; w < kWaves; ++w) {
+    const Fix128 x{s_w[2 * w], s_w[2 * w + 1]};
+    if (w < wave) off = fix_add(off, x);
+    t = fix_add(t, x);
+  }
+  __syncthreads();
+  *total = t;
+  return fix_add(off, pre);
+}
 
 // Slot of id in the LDS hash set of the row's special ids (-1: absent).
 __device__ __forceinline__ bool deep_is_special(const uint32_t* set, uint32_t id) {
@@ -1843,53 +1893,21 @@ __device__ __forceinline__ bool deep_is_special(const uint32_t* set, uint32_t id
   return false;
 }
 
-// A full-vocabulary draw (topK 0, topP 1, no min-p or typical-p) whose cursor
-// lies past the complete region of the chunk lists, or within the scan
-// normaliser's margin of one of its prefix sums (sampling.ts:58-64 over the
-// whole sorted list). finish_row left the region's candidates in list order
-// with their exact exponentials (cand_p / cand_id, deep_n of them), the row's
-// specials (sp_key / sp_id) and M, u, the region floor and the decision
-// margin. One pass over the row's logits below the floor builds a binary64
-// mass histogram over value bins (the table exponential, 4.2e-10 per term),
-// which also gives the normaliser to that accuracy; the region is walked
-// again with it; failing that, the bins the cursor falls in are gathered,
-// sorted by (value desc, id asc), given their exact exponentials and walked.
-// Returns 0 with the result written, or kExactRequest | flags. Unconstrained
-// rows only; the whole block calls it.
-__device__ __noinline__ uint32_t deep_draw(const SampleArgs& a, FinishLds& U) {
-  Shared& S = U.fin;
-  const int tid = threadIdx.x, lane = tid & 63;
-  const int64_t row = blockIdx.x;
-  const gs_row_config cfg = a.configs[row];
-  const double T = cfg.temperature;
-  const double M = S.deep_m, u = S.deep_u, margin = S.deep_margin;
-  const uint32_t thr = S.deep_thr;
-  const int n_reg = (int)S.deep_n;
-  const int n_sp = (int)(S.n_special < (uint32_t)kSpecialCap ? S.n_special : (uint32_t)kSpecialCap);
-  const double vf = (double)key_f32(thr) / T;  // the region floor's value
+// The deep draw's tail histogram: every finite logit below the region floor
+// (thr) adds its term e^(l/T - M), in its bin's units, and 1 to its bin
+// (specials are corrected by the caller). LDS atomics on integers, so the
+// sums do not depend on their order; the whole block calls it.
+__device__ __noinline__ void deep_histogram(const SampleArgs& a, int64_t row, double cap, double T, double M,
+                                            uint32_t thr, double vf, uint64_t* mass, uint32_t* count,
+                                            const double* tab) {
+  const int tid = threadIdx.x;
   const int64_t V = a.vocab;
-  double* mass = (double*)S.sorted;   // [kDeepBins]
-  uint32_t* count = S.hash_ids;       // [kDeepBins]
-  uint32_t* spset = S.hash_counts;    // hash set of the special ids
-  for (int b = tid; b < kDeepBins; b += kFinishThreads) { mass[b] = 0.0; count[b] = 0; spset[b] = 0xFFFFFFFFu; }
-  if (tid < 256) S.tab[tid] = c_exp2_256[tid];
-  if (tid == 0) S.deep_count = 0;
-  __syncthreads();
-  for (int i = tid; i < n_sp; i += kFinishThreads) special_insert(SpecialTable{spset, S.hist}, S.sp_id[i], 1u);
-  // the term e^(v - M) of a value v, by the table exponential
-  auto term = [&](double v) -> double {
-    const double y = (v - M) * GS_256_LOG2E;
-    const double e = exp2_256(y, S.tab);
-    return y > kSkipY ? e : 0.0;
-  };
-  // ---- pass 1: the tail's mass and count per bin. Every finite logit below
-  // the floor counts with its own value (specials too; corrected below)
   auto visit = [&](float l) {
-    if (cfg.softcap > 0) l = gsm::softcap_f32(l, cfg.softcap);
+    if (cap > 0) l = gsm::softcap_f32(l, cap);
     if (!(l > -__builtin_inff()) || f32_key(l) >= thr) return;
     const double v = (double)l / T;
     const int b = deep_bin(v, vf);
-    atomicAdd(&mass[b], term(v));
+    atomicAdd(&mass[b], deep_units(deep_term(v, M, tab), deep_scale(b, vf, M)));
     atomicAdd(&count[b], 1u);
   };
   int64_t from = 0;
@@ -1915,9 +1933,92 @@ __device__ __noinline__ uint32_t deep_draw(const SampleArgs& a, FinishLds& U) {
     from = n_vec * per;
   }
   for (int64_t i = from + tid; i < V; i += kFinishThreads) visit(load_logit(a, row, i));
+}
+
+// The deep draw's gather: the (value key, id) of every non-special finite
+// logit in bins b_lo .. b_hi into gkey / gid at positions from *counter
+// (at most kFinishCap kept). The whole block calls it.
+__device__ __noinline__ void deep_gather(const SampleArgs& a, int64_t row, double cap, double T, uint32_t thr,
+                                         double vf, int b_lo, int b_hi, const uint32_t* spset, uint64_t* gkey,
+                                         uint32_t* gid, uint32_t* counter) {
+  const int tid = threadIdx.x;
+  const int64_t V = a.vocab;
+  auto visit = [&](float l, uint32_t id) {
+    if (cap > 0) l = gsm::softcap_f32(l, cap);
+    if (!(l > -__builtin_inff()) || f32_key(l) >= thr) return;
+    const double v = (double)l / T;
+    const int b = deep_bin(v, vf);
+    if (b < b_lo || b > b_hi || deep_is_special(spset, id)) return;
+    const uint32_t pos = atomicAdd(counter, 1u);
+    if (pos < (uint32_t)kFinishCap) { gkey[pos] = f64_key(v); gid[pos] = id; }
+  };
+  int64_t from = 0;
+  if (a.vector_ok) {
+    const bool bf16 = a.dtype == GS_BF16;
+    const int per = bf16 ? 8 : 4;
+    const int64_t n_vec = V / per;
+    const uint4* base = (const uint4*)((const char*)a.logits + row * a.row_stride * (bf16 ? 2 : 4));
+#pragma unroll 2
+    for (int64_t vi = tid; vi < n_vec; vi += kFinishThreads) {
+      const uint4 w = base[vi];
+      const uint32_t q[4] = {w.x, w.y, w.z, w.w};
+      const uint32_t id0 = (uint32_t)(vi * per);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        if (bf16) {
+          visit(__builtin_bit_cast(float, q[j] << 16), id0 + 2 * j);
+          visit(__builtin_bit_cast(float, q[j] & 0xFFFF0000u), id0 + 2 * j + 1);
+        } else {
+          visit(__builtin_bit_cast(float, q[j]), id0 + j);
+        }
+      }
+    }
+    from = n_vec * per;
+  }
+  for (int64_t i = from + tid; i < V; i += kFinishThreads) visit(load_logit(a, row, i), (uint32_t)i);
+}
+
+// A full-vocabulary draw (topK 0, topP 1, no min-p or typical-p) whose cursor
+// lies past the complete region of the chunk lists, or within the scan
+// normaliser's margin of one of its prefix sums (sampling.ts:58-64 over the
+// whole sorted list). finish_row left the region's candidates in list order
+// with their exact exponentials (cand_p / cand_id, deep_n of them), the row's
+// specials (sp_key / sp_id) and M, u, the region floor and the reference's
+// own rounding margin. One pass over the row's logits below the floor builds
+// a fixed-point mass histogram over value bins (terms within 2^-40 relative),
+// which gives the normaliser and every bin's prefix mass to that accuracy; the
+// region is walked again with them; failing that, the bins the cursor falls
+// in are gathered, sorted by (value desc, id asc), given their exact
+// exponentials and walked. Returns 0 with the result written, or
+// kExactRequest | flags. Unconstrained rows only; the whole block calls it.
+__device__ __forceinline__ uint32_t deep_draw(const SampleArgs& a, FinishLds& U) {
+  Shared& S = U.fin;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int64_t row = blockIdx.x;
+  const gs_row_config cfg = a.configs[row];
+  const double T = cfg.temperature;
+  const double M = S.deep_m, u = S.deep_u;
+  const uint32_t thr = S.deep_thr;
+  const int n_reg = (int)S.deep_n;
+  const int n_sp = (int)(S.n_special < (uint32_t)kSpecialCap ? S.n_special : (uint32_t)kSpecialCap);
+  const double vf = (double)key_f32(thr) / T;  // the region floor's value
+  // every term below the floor at most 1, so the fixed-point sums stay below
+  // 2^22 (M is the row's largest value; a floor above it is left to the
+  // exact path)
+  if (!(vf <= M)) return kExactRequest | 0u;
+  uint64_t* mass = S.sorted;          // [kDeepBins] in units of 2^(deep_scale(b) - kDeepFracBits)
+  uint32_t* count = S.hash_ids;       // [kDeepBins]
+  uint32_t* spset = S.hash_counts;    // hash set of the special ids
+  for (int b = tid; b < kDeepBins; b += kFinishThreads) { mass[b] = 0ull; count[b] = 0; spset[b] = 0xFFFFFFFFu; }
+  if (tid < 256) S.tab[tid] = c_exp2_256[tid];
+  if (tid == 0) S.deep_count = 0;
   __syncthreads();
-  // specials: out with their raw values (where the pass counted them), in with
-  // their penalised ones when those lie below the floor
+  for (int i = tid; i < n_sp; i += kFinishThreads) special_insert(SpecialTable{spset, S.hist}, S.sp_id[i], 1u);
+  // ---- pass 1: the tail's mass and count per bin
+  deep_histogram(a, row, cfg.softcap, T, M, thr, vf, mass, count, S.tab);
+  __syncthreads();
+  // specials: out with their raw values (where the pass counted them; the
+  // same units, so exactly), in with their penalised ones below the floor
   for (int i = tid; i < n_sp; i += kFinishThreads) {
     const uint32_t id = S.sp_id[i];
     float l = load_logit(a, row, id);
@@ -1925,23 +2026,24 @@ __device__ __noinline__ uint32_t deep_draw(const SampleArgs& a, FinishLds& U) {
     if (l > -__builtin_inff() && f32_key(l) < thr) {
       const double v = (double)l / T;
       const int b = deep_bin(v, vf);
-      atomicAdd(&mass[b], -term(v));
+      atomicAdd(&mass[b], 0ull - deep_units(deep_term(v, M, S.tab), deep_scale(b, vf, M)));
       atomicSub(&count[b], 1u);
     }
     const double vs = key_f64(S.sp_key[i]);
     if (S.sp_key[i] < S.deep_floor && vs > -__builtin_inf()) {
       const int b = deep_bin(vs, vf);
-      atomicAdd(&mass[b], term(vs));
+      atomicAdd(&mass[b], deep_units(deep_term(vs, M, S.tab), deep_scale(b, vf, M)));
       atomicAdd(&count[b], 1u);
     }
   }
   __syncthreads();
-  // ---- the region's exact mass, the tail's, and the normaliser in binary64
+  // ---- the region's exact mass, and the bins' prefix masses in fixed point
   constexpr int kPer = kFinishCap / kFinishThreads;  // region entries per thread (and bins)
+  static_assert(kDeepBins == kFinishCap, "kPer bins per thread");
   double r_local[kPer];
-  double r_base, r_mass;
+  double r_base;
   {
-    double sum = 0.0;
+    double sum = 0.0, r_mass;
 #pragma unroll
     for (int q = 0; q < kPer; ++q) {
       const int i = tid * kPer + q;
@@ -1950,26 +2052,32 @@ __device__ __noinline__ uint32_t deep_draw(const SampleArgs& a, FinishLds& U) {
     }
     r_base = block_scan_f64(sum, S.wtmp, &r_mass) - sum;
   }
-  static_assert(kDeepBins == kFinishCap, "one pass of kPer bins per thread");
-  double b_local[kPer];
-  double b_base, t_mass;
-  {
-    double sum = 0.0;
-#pragma unroll
-    for (int q = 0; q < kPer; ++q) {
-      sum += mass[tid * kPer + q];
-      b_local[q] = sum;
-    }
-    b_base = block_scan_f64(sum, S.wtmp, &t_mass) - sum;
-  }
-  const double total = r_mass + t_mass;
-  if (!(total < __builtin_inf()) || !(total > 0)) return kExactRequest | 0u;
-  // the region's exact mass in fixed point, for the exact refinement below
   Fix128 r_fix{0ull, 0ull};
   for (int i = tid; i < n_reg; i += kFinishThreads) r_fix = fix_add(r_fix, fix_of(S.cand_p[i]));
   r_fix = block_fix_sum(r_fix, (uint64_t*)S.top);
-  const double target = u * total;       // the cursor, in units of e
-  const double mrg = margin * total;     // the decision margin, in the same units
+  // b_after[q]: the mass of the region and of bins 0 .. tid kPer + q, in binary64
+  double b_after[kPer];
+  double total;
+  {
+    Fix128 f[kPer];
+    Fix128 sum{0ull, 0ull};
+#pragma unroll
+    for (int q = 0; q < kPer; ++q) {
+      const int b = tid * kPer + q;
+      sum = fix_add(sum, fix_shift(mass[b], deep_scale(b, vf, M) - kDeepFracBits + 100));
+      f[q] = sum;
+    }
+    Fix128 t_fix;
+    const Fix128 base = fix_add(r_fix, block_fix_scan(sum, (uint64_t*)S.top, &t_fix));
+#pragma unroll
+    for (int q = 0; q < kPer; ++q) b_after[q] = fix_to_double(fix_add(base, f[q]));
+    total = fix_to_double(fix_add(r_fix, t_fix));
+  }
+  if (!(total < __builtin_inf()) || !(total > 0)) return kExactRequest | 0u;
+  const double target = u * total;  // the cursor, in units of e
+  // the decision margin: the reference's own rounding, the near-tie report
+  // and the histogram's terms (2^-40 relative) with the binary64 sums (2^-40)
+  const double mrg = (S.deep_margin + 0x1p-38) * total;
   // ---- the region with the recomputed normaliser
   if (tid == 0) { S.first_idx = 0xFFFFFFFFu; S.route_exact = 0; }
   __syncthreads();
@@ -1996,12 +2104,12 @@ __device__ __noinline__ uint32_t deep_draw(const SampleArgs& a, FinishLds& U) {
     if (tid == 0) write_result(a, row, (int32_t)S.cand_id[S.first_idx], 0u, S.cand_p[S.first_idx] / total);
     return 0;
   }
-  // ---- the bins the cursor falls in (a neighbour too when its boundary lies
-  // within the margin)
+  // ---- the bin the cursor falls in, and a neighbour where a boundary lies
+  // within the margin
   {
     uint32_t first = 0xFFFFFFFFu;
     for (int q = kPer - 1; q >= 0; --q) {
-      if (r_mass + b_base + b_local[q] >= target) first = (uint32_t)(tid * kPer + q);
+      if (b_after[q] >= target) first = (uint32_t)(tid * kPer + q);
     }
     first = wave_min_u32(first);
     if (lane == 0 && first != 0xFFFFFFFFu) atomicMin(&S.first_idx, first);
@@ -2009,77 +2117,45 @@ __device__ __noinline__ uint32_t deep_draw(const SampleArgs& a, FinishLds& U) {
   __syncthreads();
   const int bc = (int)S.first_idx;
   if (bc < 0 || bc >= kDeepBins - 1) return kExactRequest | 0u;  // past the bins' span
-  __syncthreads();
-  // cumulative mass before and after bin bc, from the thread holding it
-  // register arrays are read at static indices only (a dynamic one would put
-  // them in scratch memory)
-  auto pick_local = [&](const double (&arr)[kPer], int q) -> double {
+  // the mass through bin b, on the thread holding bin b; register arrays are
+  // read at static indices only (a dynamic one would put them in scratch)
+  auto after_of = [&](int b) -> double {
     double x = 0.0;
 #pragma unroll
-    for (int k = 0; k < kPer; ++k) x = k == q ? arr[k] : x;
+    for (int k = 0; k < kPer; ++k) x = tid * kPer + k == b ? b_after[k] : x;
     return x;
   };
-  if (tid == bc / kPer) {
-    const double after = r_mass + b_base + pick_local(b_local, bc % kPer);
-    const double before = after - mass[bc];
-    int lo = bc, hi = bc;
-    if (before >= target - mrg) lo = bc > 0 ? bc - 1 : 0;
-    if (after < target + mrg) hi = bc + 1;
-    S.sel[0] = (uint32_t)lo;
-    S.sel[1] = (uint32_t)hi;
-  }
   __syncthreads();
-  const int b_lo = (int)S.sel[0], b_hi = (int)S.sel[1];
+  const double r_total = fix_to_double(r_fix);
+  if (tid == bc / kPer) S.sel[1] = (uint32_t)(after_of(bc) < target + mrg ? bc + 1 : bc);
+  if (tid == (bc > 0 ? (bc - 1) / kPer : 0)) S.wsum[0] = bc > 0 ? after_of(bc - 1) : r_total;
+  __syncthreads();
+  const int b_hi = (int)S.sel[1];
+  // bin bc - 1 taken in too when the mass before bc lies within the margin
+  const bool take_prev = bc > 0 && S.wsum[0] >= target - mrg;
+  const int b_lo = take_prev ? bc - 1 : bc;
+  if (take_prev) {
+    if (tid == (b_lo > 0 ? (b_lo - 1) / kPer : 0)) S.wsum[1] = b_lo > 0 ? after_of(b_lo - 1) : r_total;
+    __syncthreads();
+  }
+  const double pre_before = take_prev ? S.wsum[1] : S.wsum[0];
+  // the walk below starts after pre_before: the cursor must lie clearly past it
+  if (pre_before >= target - mrg) return kExactRequest | GS_FLAG_NEAR_TIE;
   if (b_hi >= kDeepBins - 1) return kExactRequest | 0u;
   uint32_t n_in = 0;
   for (int b = b_lo; b <= b_hi; ++b) n_in += count[b];
   if (n_in > (uint32_t)kFinishCap) return kExactRequest | 0u;  // a crowd of equal values
-  // mass of the bins above b_lo, with the region's
-  if (tid == (b_lo > 0 ? (b_lo - 1) / kPer : 0)) {
-    S.wsum[0] = b_lo > 0 ? r_mass + b_base + pick_local(b_local, (b_lo - 1) % kPer) : r_mass;
-  }
-  __syncthreads();
-  const double pre_before = S.wsum[0];
   __syncthreads();
   // ---- pass 2: gather the bins' entries (value key, id) into sorted / hash_ids
   uint64_t* gkey = S.sorted;
   uint32_t* gid = S.hash_ids;
+  deep_gather(a, row, cfg.softcap, T, thr, vf, b_lo, b_hi, spset, gkey, gid, &S.deep_count);
   auto gather = [&](double v, uint32_t id) {
     const int b = deep_bin(v, vf);
     if (b < b_lo || b > b_hi) return;
     const uint32_t pos = atomicAdd(&S.deep_count, 1u);
     if (pos < (uint32_t)kFinishCap) { gkey[pos] = f64_key(v); gid[pos] = id; }
   };
-  auto visit2 = [&](float l, uint32_t id) {
-    if (cfg.softcap > 0) l = gsm::softcap_f32(l, cfg.softcap);
-    if (!(l > -__builtin_inff()) || f32_key(l) >= thr) return;
-    const double v = (double)l / T;
-    const int b = deep_bin(v, vf);
-    if (b < b_lo || b > b_hi || deep_is_special(spset, id)) return;
-    gather(v, id);
-  };
-  if (a.vector_ok) {
-    const bool bf16 = a.dtype == GS_BF16;
-    const int per = bf16 ? 8 : 4;
-    const int64_t n_vec = V / per;
-    const uint4* base = (const uint4*)((const char*)a.logits + row * a.row_stride * (bf16 ? 2 : 4));
-#pragma unroll 2
-    for (int64_t vi = tid; vi < n_vec; vi += kFinishThreads) {
-      const uint4 w = base[vi];
-      const uint32_t q[4] = {w.x, w.y, w.z, w.w};
-      const uint32_t id0 = (uint32_t)(vi * per);
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        if (bf16) {
-          visit2(__builtin_bit_cast(float, q[j] << 16), id0 + 2 * j);
-          visit2(__builtin_bit_cast(float, q[j] & 0xFFFF0000u), id0 + 2 * j + 1);
-        } else {
-          visit2(__builtin_bit_cast(float, q[j]), id0 + j);
-        }
-      }
-    }
-  }
-  for (int64_t i = from + tid; i < V; i += kFinishThreads) visit2(load_logit(a, row, i), (uint32_t)i);
   for (int i = tid; i < n_sp; i += kFinishThreads) {
     const double vs = key_f64(S.sp_key[i]);
     if (S.sp_key[i] < S.deep_floor && vs > -__builtin_inf()) gather(vs, S.sp_id[i]);
@@ -2098,6 +2174,7 @@ __device__ __noinline__ uint32_t deep_draw(const SampleArgs& a, FinishLds& U) {
   {
     double g_local[kPer];
     double sum = 0.0;
+#pragma unroll
     for (int q = 0; q < kPer; ++q) {
       const int i = tid * kPer + q;
       sum += i < n_g ? S.cand_p[i] : 0.0;
@@ -2107,6 +2184,7 @@ __device__ __noinline__ uint32_t deep_draw(const SampleArgs& a, FinishLds& U) {
     const double g_base = block_scan_f64(sum, S.wtmp, &g_total) - sum;
     uint32_t first = 0xFFFFFFFFu;
     bool near = false;
+#pragma unroll
     for (int q = kPer - 1; q >= 0; --q) {
       const int i = tid * kPer + q;
       if (i >= n_g) continue;
@@ -2122,86 +2200,9 @@ __device__ __noinline__ uint32_t deep_draw(const SampleArgs& a, FinishLds& U) {
     }
   }
   __syncthreads();
-  if (!S.route_exact) {
-    if (S.first_idx == 0xFFFFFFFFu) return kExactRequest | 0u;
-    if (tid == 0) write_result(a, row, (int32_t)gid[S.first_idx], 0u, S.cand_p[S.first_idx] / total);
-    return 0;
-  }
-  // ---- pass 3, for a cursor within the table exponential's margin: the
-  // normaliser and the mass above the gathered bins from the exact terms
-  // (js_exp, the reference's own), summed exactly in fixed point. They lie
-  // within 2^-79 of the real sums, which the reference's sequential sums
-  // approach within (2V + 2) 2^-53; the walk then needs only that margin.
-  Fix128 all{0ull, 0ull}, above{0ull, 0ull};
-  auto visit3 = [&](float l) {
-    if (cfg.softcap > 0) l = gsm::softcap_f32(l, cfg.softcap);
-    if (!(l > -__builtin_inff()) || f32_key(l) >= thr) return;
-    const double v = (double)l / T;
-    const Fix128 f = fix_of(gsm::js_exp(v - M));
-    all = fix_add(all, f);
-    if (deep_bin(v, vf) < b_lo) above = fix_add(above, f);
-  };
-  // (rare: one element at a time, two loads per thread in flight)
-#pragma unroll 2
-  for (int64_t i = tid; i < V; i += kFinishThreads) visit3(load_logit(a, row, i));
-  // specials: out with their raw values (exactly, as integers), in with their
-  // penalised ones below the floor
-  for (int i = tid; i < n_sp; i += kFinishThreads) {
-    float l = load_logit(a, row, S.sp_id[i]);
-    if (cfg.softcap > 0) l = gsm::softcap_f32(l, cfg.softcap);
-    if (l > -__builtin_inff() && f32_key(l) < thr) {
-      const double v = (double)l / T;
-      const Fix128 f = fix_neg(fix_of(gsm::js_exp(v - M)));
-      all = fix_add(all, f);
-      if (deep_bin(v, vf) < b_lo) above = fix_add(above, f);
-    }
-    const double vs = key_f64(S.sp_key[i]);
-    if (S.sp_key[i] < S.deep_floor && vs > -__builtin_inf()) {
-      const Fix128 f = fix_of(gsm::js_exp(vs - M));
-      all = fix_add(all, f);
-      if (deep_bin(vs, vf) < b_lo) above = fix_add(above, f);
-    }
-  }
-  all = block_fix_sum(all, (uint64_t*)S.top);
-  above = block_fix_sum(above, (uint64_t*)S.top);
-  const double total_x = fix_to_double(fix_add(r_fix, all));
-  const double before_x = fix_to_double(fix_add(r_fix, above));
-  const double target_x = u * total_x;
-  const double mrg_x = ((2.0 * (double)V + 2.0) * 0x1p-53 + kNearTie + 0x1p-46) * total_x;
-  if (tid == 0) { S.first_idx = 0xFFFFFFFFu; S.route_exact = 0; }
-  __syncthreads();
-  {
-    double g_local[kPer];
-    double sum = 0.0;
-#pragma unroll
-    for (int q = 0; q < kPer; ++q) {
-      const int i = tid * kPer + q;
-      sum += i < n_g ? S.cand_p[i] : 0.0;
-      g_local[q] = sum;
-    }
-    double g_total;
-    const double g_base = block_scan_f64(sum, S.wtmp, &g_total) - sum;
-    uint32_t first = 0xFFFFFFFFu;
-    bool near = false;
-#pragma unroll
-    for (int q = kPer - 1; q >= 0; --q) {
-      const int i = tid * kPer + q;
-      if (i >= n_g) continue;
-      const double pre = before_x + g_base + g_local[q];
-      if (pre >= target_x) first = (uint32_t)i;
-      if ((pre >= target_x ? pre - target_x : target_x - pre) < mrg_x) near = true;
-    }
-    first = wave_min_u32(first);
-    const bool wn = __ballot(near) != 0;
-    if (lane == 0) {
-      if (first != 0xFFFFFFFFu) atomicMin(&S.first_idx, first);
-      if (wn) atomicOr(&S.route_exact, 1u);
-    }
-  }
-  __syncthreads();
   if (S.route_exact) return kExactRequest | GS_FLAG_NEAR_TIE;
   if (S.first_idx == 0xFFFFFFFFu) return kExactRequest | 0u;
-  if (tid == 0) write_result(a, row, (int32_t)gid[S.first_idx], 0u, S.cand_p[S.first_idx] / total_x);
+  if (tid == 0) write_result(a, row, (int32_t)gid[S.first_idx], 0u, S.cand_p[S.first_idx] / total);
   return 0;
 }
 
