@@ -109,58 +109,53 @@ __device__ void block_sort_pairs_desc(uint64_t* key, uint32_t* id, int n) {
 __device__ __forceinline__ uint64_t umax64(uint64_t a, uint64_t b) { return a > b ? a : b; }
 __device__ __forceinline__ uint64_t umin64(uint64_t a, uint64_t b) { return a > b ? b : a; }
 
-// Bitonic sort, descending, of kFinishThreads * E entries; thread t holds
-// entries t*E .. t*E+E-1 in v[]. Stages whose partner is in the same thread
-// compare registers, stages within a wave exchange through cross-lane
-// shuffles, and only the stages that cross waves go through LDS -- two
-// buffers alternate, so each such stage needs one barrier.
+// One merge round: sorted (descending) runs of length L in src become runs
+// of 2L in dst, each thread writing E consecutive outputs p .. p+E-1 of its
+// merged run. A binary search finds how many of the first p outputs come from
+// the first run (its entries first on ties); those outputs are then the E
+// largest of the next E of each run (an exhausted run reads 0, no larger than
+// any entry): the element-wise maximum of one and the other reversed is
+// bitonic, and half-cleaners sort it.
 template <int E>
-__device__ void sort_desc_regs(uint64_t (&v)[E], uint64_t* buf0, uint64_t* buf1) {
-  const int t = threadIdx.x;
-  constexpr int n2 = kFinishThreads * E;
-  int lds_stage = 0;
-  for (int k = 2; k <= n2; k <<= 1) {
-    for (int j = k >> 1; j > 0; j >>= 1) {
-      if (j < E) {
+__device__ __forceinline__ void merge_round(const uint64_t* src, uint64_t* dst, int L) {
+  const int p0 = threadIdx.x * E;
+  const int base = p0 & ~(2 * L - 1);
+  const uint64_t* A = src + base;
+  const uint64_t* B = src + base + L;
+  const int p = p0 - base;
+  int lo = p - L > 0 ? p - L : 0, hi = p < L ? p : L;
+  while (lo < hi) {
+    const int i = (lo + hi) >> 1;
+    if (A[i] >= B[p - i - 1]) lo = i + 1; else hi = i;
+  }
+  const int i = lo, j = p - lo;
+  uint64_t c[E];
 #pragma unroll
-        for (int q = 0; q < E; ++q) {
-          const int qp = q ^ j;
-          if (qp > q) {
-            const int i = t * E + q;
-            const uint64_t x = v[q], y = v[qp];
-            const bool desc = (i & k) == 0;
-            v[q] = desc ? umax64(x, y) : umin64(x, y);
-            v[qp] = desc ? umin64(x, y) : umax64(x, y);
-          }
-        }
-      } else if (j < 64 * E) {
-        const int m = j / E;  // partner lane distance
+  for (int q = 0; q < E; ++q) {
+    const uint64_t x = i + q < L ? A[i + q] : 0ull;
+    const uint64_t y = j + E - 1 - q < L ? B[j + E - 1 - q] : 0ull;
+    c[q] = umax64(x, y);
+  }
 #pragma unroll
-        for (int q = 0; q < E; ++q) {
-          const int i = t * E + q;
-          const uint64_t y = shfl_xor_u64(v[q], m);
-          const bool keep_max = ((i & j) == 0) == ((i & k) == 0);
-          v[q] = keep_max ? umax64(v[q], y) : umin64(v[q], y);
-        }
-      } else {
-        uint64_t* buf = (lds_stage++ & 1) ? buf1 : buf0;
+  for (int d = E >> 1; d > 0; d >>= 1) {
 #pragma unroll
-        for (int q = 0; q < E; ++q) buf[t * E + q] = v[q];
-        __syncthreads();
-#pragma unroll
-        for (int q = 0; q < E; ++q) {
-          const int i = t * E + q;
-          const uint64_t y = buf[i ^ j];
-          const bool keep_max = ((i & j) == 0) == ((i & k) == 0);
-          v[q] = keep_max ? umax64(v[q], y) : umin64(v[q], y);
-        }
+    for (int q = 0; q < E; ++q) {
+      if ((q & d) == 0) {
+        const uint64_t x = c[q], y = c[q + d];
+        c[q] = umax64(x, y);
+        c[q + d] = umin64(x, y);
       }
     }
   }
+#pragma unroll
+  for (int q = 0; q < E; ++q) dst[base + p + q] = c[q];
 }
 
-// Sorts s[0..n) descending (n <= kFinishCap), zero-padded; buf is kFinishCap
-// entries of scratch. Ends with a barrier.
+// Sorts s[0..n) descending (n <= kFinishThreads * E), zero-padded to
+// kFinishThreads * E entries; buf is as many entries of scratch. Each thread
+// sorts its E entries in registers, then merge rounds double the sorted runs
+// (a bitonic network over the whole block costs about three times as much:
+// its cross-lane stages are many). Ends with a barrier.
 template <int E>
 __device__ void sort_region(uint64_t* s, int n, uint64_t* buf) {
   uint64_t v[E];
@@ -169,12 +164,40 @@ __device__ void sort_region(uint64_t* s, int n, uint64_t* buf) {
     const int i = threadIdx.x * E + q;
     v[q] = i < n ? s[i] : 0ull;
   }
-  __syncthreads();  // s is the first LDS buffer of the sort
-  sort_desc_regs<E>(v, s, buf);
-  __syncthreads();
+#pragma unroll
+  for (int k = 2; k <= E; k <<= 1) {
+#pragma unroll
+    for (int j = k >> 1; j > 0; j >>= 1) {
+#pragma unroll
+      for (int q = 0; q < E; ++q) {
+        const int qp = q ^ j;
+        if (qp > q) {
+          const uint64_t x = v[q], y = v[qp];
+          const bool desc = (q & k) == 0;
+          v[q] = desc ? umax64(x, y) : umin64(x, y);
+          v[qp] = desc ? umin64(x, y) : umax64(x, y);
+        }
+      }
+    }
+  }
+  __syncthreads();  // s may still be read by the caller's threads
 #pragma unroll
   for (int q = 0; q < E; ++q) s[threadIdx.x * E + q] = v[q];
   __syncthreads();
+  uint64_t* src = s;
+  uint64_t* dst = buf;
+  for (int L = E; L < kFinishThreads * E; L <<= 1) {
+    merge_round<E>(src, dst, L);
+    __syncthreads();
+    uint64_t* t = src;
+    src = dst;
+    dst = t;
+  }
+  if (src != s) {
+#pragma unroll
+    for (int q = 0; q < E; ++q) s[threadIdx.x * E + q] = src[threadIdx.x * E + q];
+    __syncthreads();
+  }
 }
 
 // Descending bitonic sort of the 64*E entries one wave holds (lane l holds
@@ -439,7 +462,7 @@ struct Shared {
   double tab[256];                    // the table exponential's table (deep draw)
   double deep_m, deep_u, deep_margin; // a deep draw's inputs, left by finish_row
   uint64_t deep_floor;
-  uint32_t deep_thr, deep_n, deep_count;
+  uint32_t deep_thr, deep_n, deep_count, deep_final;
   uint32_t sel[4];
   double wsum[kWaves];
   double wtmp[kWaves];
@@ -777,9 +800,13 @@ __device__ double recompute_nonspecial_sum(const SampleArgs& a, int64_t row, con
   const int tid = threadIdx.x;
   const double T = cfg.temperature;
   const uint32_t* mrow = constrained ? a.mask_table + (int64_t)cfg.mask_slot * a.mask_words : nullptr;
+  // y = (l / T - M) 256 log2(e) in one fma: the quotient's and the products'
+  // rounding move y by about 2^-52 |l| 256 log2(e) / T, 1e-14 relative on a
+  // term, far inside the table exponential's error
+  const double yA = (1.0 / T) * GS_256_LOG2E, yB = -M * GS_256_LOG2E;
   auto term = [&](float l) -> double {
     if (cfg.softcap > 0) l = gsm::softcap_f32(l, cfg.softcap);
-    const double y = ((double)l / T - M) * GS_256_LOG2E;
+    const double y = __builtin_fma((double)l, yA, yB);
     // evaluated for every y (no branch), so that independent terms overlap;
     // exp2_256 reads its table at an index masked to 0..255 for any y
     const double e = exp2_256(y, c_exp2_256);
@@ -1772,35 +1799,49 @@ __device__ __forceinline__ uint32_t finish_row(const SampleArgs& a, FinishLds& U
 // region floor's value, bin 0 the highest, values further down in the last.
 // A non-increasing function of v, so the bins are contiguous runs of the
 // reference's sorted list.
+__device__ __forceinline__ double deep_z(double v, double vf) {
+  return (vf - v) * ((double)kDeepBins / kDeepSpan);
+}
 __device__ __forceinline__ int deep_bin(double v, double vf) {
-  const double z = (vf - v) * ((double)kDeepBins / kDeepSpan);
+  const double z = deep_z(v, vf);
   return z < (double)(kDeepBins - 1) ? (int)z : kDeepBins - 1;
 }
-
-// Bin b's terms e^(v - M) are summed in units of 2^(k - kDeepFracBits), k =
-// deep_scale(b): the bin's values are at most vf - b kDeepSpan / kDeepBins
-// (up to rounding), so every term lies below 2^k (the ceiling and the + 1
-// leave a factor 2 over that bound), and, but in the last bin, above 2^(k - 3)
-// (a bin spans kDeepSpan / kDeepBins < ln 2 / 8 of v). A term then rounds to
-// a whole number of units below 2^42 with a relative error under 2^-40, and a
-// bin of at most 2^21 + kSpecialCap terms sums below 2^64 in a u64.
-constexpr int kDeepFracBits = 42;
-__device__ __forceinline__ int deep_scale(int b, double vf, double M) {
-  const double top = (vf - M) - (double)b * (kDeepSpan / kDeepBins);
-  return (int)__builtin_ceil(top * (GS_256_LOG2E / 256.0)) + 1;
+// A value's term relative to its bin's centre c_b = vf - (b + 1/2) w, w =
+// kDeepSpan / kDeepBins: e^(v - c_b) = e^x with x = (b + 1/2 - z) w, |x| <=
+// w / 2 (up to z's rounding, 1e-12 of a bin), by its degree-4 Taylor
+// polynomial (remainder below 3e-14), in units of 2^-40 rounded to nearest
+// (4.6e-13 relative): every term of a bin is about 2^40 units, and a bin of
+// at most 2^21 + kSpecialCap of them sums below 2^62. The bin's mass is then
+// its units times 2^-40 e^(c_b - M). For b < kDeepBins - 1 only.
+__device__ __forceinline__ uint64_t deep_units(double z, int b) {
+  const double x = (0.5 - (z - (double)b)) * (kDeepSpan / kDeepBins);
+  double p = __builtin_fma(x, 1.0 / 24.0, 1.0 / 6.0);
+  p = __builtin_fma(x, p, 0.5);
+  p = __builtin_fma(x, p, 1.0);
+  p = __builtin_fma(x, p, 1.0);
+  // p 2^40 < 2^52: adding 2^52 leaves the rounded integer in the mantissa field
+  return __builtin_bit_cast(uint64_t, __builtin_fma(p, 0x1p40, 0x1p52)) & ((1ull << 52) - 1);
 }
-// e in units of 2^(k - kDeepFracBits), rounded to nearest: e 2^(42 - k) < 2^52,
-// so adding 2^52 leaves the rounded integer in the mantissa field
-__device__ __forceinline__ uint64_t deep_units(double e, int k) {
-  const double x = __builtin_ldexp(e, kDeepFracBits - k) + 0x1p52;
-  return __builtin_bit_cast(uint64_t, x) & ((1ull << 52) - 1);
-}
-// a term of the deep draw: the quartic table exponential of v - M (relative
-// error below 1e-15 against e^(v - M), with the argument's rounding 2e-14),
-// zero below e^-60 of the maximum
+// a term of the last bin (values kDeepSpan or more below the floor): the
+// quartic table exponential of v - M (1e-15 relative, the argument's rounding
+// 2e-14), zero below e^-60 of the maximum
 __device__ __forceinline__ double deep_term(double v, double M, const double* tab) {
   const double y = (v - M) * GS_256_LOG2E;
   return y > kSkipY ? exp2_256_tight(y, tab) : 0.0;
+}
+// adds value v's term to the histogram (mass) or to the last bin's sum
+// (*tail); negate: subtracts it
+__device__ __forceinline__ void deep_add(double v, double vf, double M, const double* tab, uint64_t* mass,
+                                         double* tail, bool negate) {
+  const double z = deep_z(v, vf);
+  if (z < (double)(kDeepBins - 1)) {
+    const int b = (int)z;
+    const uint64_t n = deep_units(z, b);
+    atomicAdd(&mass[b], negate ? 0ull - n : n);
+  } else {
+    const double t = deep_term(v, M, tab);
+    *tail += negate ? -t : t;
+  }
 }
 
 // Exact sums of exponentials in 128-bit fixed point (units of 2^-100): a
@@ -1893,89 +1934,86 @@ __device__ __forceinline__ bool deep_is_special(const uint32_t* set, uint32_t id
   return false;
 }
 
-// The deep draw's tail histogram: every finite logit below the region floor
-// (thr) adds its term e^(l/T - M), in its bin's units, and 1 to its bin
-// (specials are corrected by the caller). LDS atomics on integers, so the
-// sums do not depend on their order; the whole block calls it.
-__device__ __noinline__ void deep_histogram(const SampleArgs& a, int64_t row, double cap, double T, double M,
-                                            uint32_t thr, double vf, uint64_t* mass, uint32_t* count,
-                                            const double* tab) {
+// Calls visit(l, id) for every logit of the row, the whole block over it:
+// kB 16-byte loads per thread go out before any is used, so that kB *
+// kFinishThreads * 16 bytes are in flight (one block reads a row alone here,
+// and its loads would otherwise wait on one memory latency each).
+template <int kB, typename F>
+__device__ __forceinline__ void visit_row(const SampleArgs& a, int64_t row, F&& visit) {
   const int tid = threadIdx.x;
   const int64_t V = a.vocab;
-  auto visit = [&](float l) {
-    if (cap > 0) l = gsm::softcap_f32(l, cap);
-    if (!(l > -__builtin_inff()) || f32_key(l) >= thr) return;
-    const double v = (double)l / T;
-    const int b = deep_bin(v, vf);
-    atomicAdd(&mass[b], deep_units(deep_term(v, M, tab), deep_scale(b, vf, M)));
-    atomicAdd(&count[b], 1u);
-  };
   int64_t from = 0;
   if (a.vector_ok) {
     const bool bf16 = a.dtype == GS_BF16;
     const int per = bf16 ? 8 : 4;
     const int64_t n_vec = V / per;
     const uint4* base = (const uint4*)((const char*)a.logits + row * a.row_stride * (bf16 ? 2 : 4));
-#pragma unroll 2
-    for (int64_t vi = tid; vi < n_vec; vi += kFinishThreads) {
-      const uint4 w = base[vi];
-      const uint32_t q[4] = {w.x, w.y, w.z, w.w};
+    for (int64_t v0 = tid; v0 < n_vec; v0 += (int64_t)kB * kFinishThreads) {
+      uint4 w[kB];
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        if (bf16) {
-          visit(__builtin_bit_cast(float, q[j] << 16));
-          visit(__builtin_bit_cast(float, q[j] & 0xFFFF0000u));
-        } else {
-          visit(__builtin_bit_cast(float, q[j]));
-        }
+      for (int k = 0; k < kB; ++k) {
+        const int64_t vi = v0 + (int64_t)k * kFinishThreads;
+        w[k] = vi < n_vec ? base[vi] : make_uint4(0u, 0u, 0u, 0u);
       }
-    }
-    from = n_vec * per;
-  }
-  for (int64_t i = from + tid; i < V; i += kFinishThreads) visit(load_logit(a, row, i));
-}
-
-// The deep draw's gather: the (value key, id) of every non-special finite
-// logit in bins b_lo .. b_hi into gkey / gid at positions from *counter
-// (at most kFinishCap kept). The whole block calls it.
-__device__ __noinline__ void deep_gather(const SampleArgs& a, int64_t row, double cap, double T, uint32_t thr,
-                                         double vf, int b_lo, int b_hi, const uint32_t* spset, uint64_t* gkey,
-                                         uint32_t* gid, uint32_t* counter) {
-  const int tid = threadIdx.x;
-  const int64_t V = a.vocab;
-  auto visit = [&](float l, uint32_t id) {
-    if (cap > 0) l = gsm::softcap_f32(l, cap);
-    if (!(l > -__builtin_inff()) || f32_key(l) >= thr) return;
-    const double v = (double)l / T;
-    const int b = deep_bin(v, vf);
-    if (b < b_lo || b > b_hi || deep_is_special(spset, id)) return;
-    const uint32_t pos = atomicAdd(counter, 1u);
-    if (pos < (uint32_t)kFinishCap) { gkey[pos] = f64_key(v); gid[pos] = id; }
-  };
-  int64_t from = 0;
-  if (a.vector_ok) {
-    const bool bf16 = a.dtype == GS_BF16;
-    const int per = bf16 ? 8 : 4;
-    const int64_t n_vec = V / per;
-    const uint4* base = (const uint4*)((const char*)a.logits + row * a.row_stride * (bf16 ? 2 : 4));
-#pragma unroll 2
-    for (int64_t vi = tid; vi < n_vec; vi += kFinishThreads) {
-      const uint4 w = base[vi];
-      const uint32_t q[4] = {w.x, w.y, w.z, w.w};
-      const uint32_t id0 = (uint32_t)(vi * per);
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        if (bf16) {
-          visit(__builtin_bit_cast(float, q[j] << 16), id0 + 2 * j);
-          visit(__builtin_bit_cast(float, q[j] & 0xFFFF0000u), id0 + 2 * j + 1);
-        } else {
-          visit(__builtin_bit_cast(float, q[j]), id0 + j);
+      for (int k = 0; k < kB; ++k) {
+        const int64_t vi = v0 + (int64_t)k * kFinishThreads;
+        if (vi >= n_vec) break;
+        const uint32_t q[4] = {w[k].x, w[k].y, w[k].z, w[k].w};
+        const uint32_t id0 = (uint32_t)(vi * per);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          if (bf16) {
+            visit(__builtin_bit_cast(float, q[j] << 16), id0 + 2 * j);
+            visit(__builtin_bit_cast(float, q[j] & 0xFFFF0000u), id0 + 2 * j + 1);
+          } else {
+            visit(__builtin_bit_cast(float, q[j]), id0 + j);
+          }
         }
       }
     }
     from = n_vec * per;
   }
   for (int64_t i = from + tid; i < V; i += kFinishThreads) visit(load_logit(a, row, i), (uint32_t)i);
+}
+
+// The deep draw's tail histogram: every finite logit below the region floor
+// (thr) adds its term to its bin (LDS atomics on integers, so the sums do not
+// depend on their order), or to the returned per-thread sum of the last bin;
+// specials are corrected by the caller. The whole block calls it.
+__device__ __noinline__ double deep_histogram(const SampleArgs& a, int64_t row, double cap, double T, double rT,
+                                              double M, uint32_t thr, double vf, uint64_t* mass,
+                                              const double* tab) {
+  double tail = 0.0;
+  visit_row<4>(a, row, [&](float l, uint32_t) {
+    if (cap > 0) l = gsm::softcap_f32(l, cap);
+    if (!(l > -__builtin_inff()) || f32_key(l) >= thr) return;
+    deep_add(div_by_temperature((double)l, T, rT), vf, M, tab, mass, &tail, false);
+  });
+  return tail;
+}
+
+// The deep draw's gather, first step: every finite logit in [l_lo, l_hi] (a
+// float range that holds the wanted bins' logits with room to spare) and
+// below the region floor (thr), as (float bits << 32 | id), appended to stage
+// from *counter (at most kFinishCap kept; one LDS atomic per wave and
+// logit position). The exact test runs on the few staged entries only. The
+// whole block calls it.
+__device__ __noinline__ void deep_stage(const SampleArgs& a, int64_t row, double cap, uint32_t thr, float l_lo,
+                                        float l_hi, uint64_t* stage, uint32_t* counter) {
+  const int lane = threadIdx.x & 63;
+  visit_row<8>(a, row, [&](float l, uint32_t id) {
+    if (cap > 0) l = gsm::softcap_f32(l, cap);
+    const bool pass = l >= l_lo && l <= l_hi && f32_key(l) < thr;
+    const uint64_t m = __ballot(pass);
+    if (m == 0) return;
+    const int leader = __builtin_ctzll(m);
+    uint32_t base = 0;
+    if (lane == leader) base = atomicAdd(counter, (uint32_t)__popcll(m));
+    base = (uint32_t)__shfl((int)base, leader, 64);
+    const uint32_t pos = base + (uint32_t)__popcll(m & ((1ull << lane) - 1ull));
+    if (pass && pos < (uint32_t)kFinishCap) stage[pos] = ((uint64_t)__builtin_bit_cast(uint32_t, l) << 32) | id;
+  });
 }
 
 // A full-vocabulary draw (topK 0, topP 1, no min-p or typical-p) whose cursor
@@ -1991,7 +2029,7 @@ __device__ __noinline__ void deep_gather(const SampleArgs& a, int64_t row, doubl
 // in are gathered, sorted by (value desc, id asc), given their exact
 // exponentials and walked. Returns 0 with the result written, or
 // kExactRequest | flags. Unconstrained rows only; the whole block calls it.
-__device__ __forceinline__ uint32_t deep_draw(const SampleArgs& a, FinishLds& U) {
+__device__ __noinline__ uint32_t deep_draw(const SampleArgs& a, FinishLds& U) {
   Shared& S = U.fin;
   const int tid = threadIdx.x, lane = tid & 63;
   const int64_t row = blockIdx.x;
@@ -2004,18 +2042,19 @@ __device__ __forceinline__ uint32_t deep_draw(const SampleArgs& a, FinishLds& U)
   const double vf = (double)key_f32(thr) / T;  // the region floor's value
   // every term below the floor at most 1, so the fixed-point sums stay below
   // 2^22 (M is the row's largest value; a floor above it is left to the
-  // exact path)
-  if (!(vf <= M)) return kExactRequest | 0u;
-  uint64_t* mass = S.sorted;          // [kDeepBins] in units of 2^(deep_scale(b) - kDeepFracBits)
-  uint32_t* count = S.hash_ids;       // [kDeepBins]
+  // exact path); the quotient l / T by div_by_temperature, whose range this
+  // bounds
+  if (!(vf <= M) || !(T >= 0x1p-20 && T <= 0x1p20)) return kExactRequest | 0u;
+  const double rT = 1.0 / T;
+  uint64_t* mass = S.sorted;          // [kDeepBins - 1] terms in units of 2^-40 e^(c_b - M)
   uint32_t* spset = S.hash_counts;    // hash set of the special ids
-  for (int b = tid; b < kDeepBins; b += kFinishThreads) { mass[b] = 0ull; count[b] = 0; spset[b] = 0xFFFFFFFFu; }
+  for (int b = tid; b < kDeepBins; b += kFinishThreads) { mass[b] = 0ull; spset[b] = 0xFFFFFFFFu; }
   if (tid < 256) S.tab[tid] = c_exp2_256[tid];
   if (tid == 0) S.deep_count = 0;
   __syncthreads();
   for (int i = tid; i < n_sp; i += kFinishThreads) special_insert(SpecialTable{spset, S.hist}, S.sp_id[i], 1u);
-  // ---- pass 1: the tail's mass and count per bin
-  deep_histogram(a, row, cfg.softcap, T, M, thr, vf, mass, count, S.tab);
+  // ---- pass 1: the tail's mass per bin
+  double tail = deep_histogram(a, row, cfg.softcap, T, rT, M, thr, vf, mass, S.tab);
   __syncthreads();
   // specials: out with their raw values (where the pass counted them; the
   // same units, so exactly), in with their penalised ones below the floor
@@ -2024,39 +2063,24 @@ __device__ __forceinline__ uint32_t deep_draw(const SampleArgs& a, FinishLds& U)
     float l = load_logit(a, row, id);
     if (cfg.softcap > 0) l = gsm::softcap_f32(l, cfg.softcap);
     if (l > -__builtin_inff() && f32_key(l) < thr) {
-      const double v = (double)l / T;
-      const int b = deep_bin(v, vf);
-      atomicAdd(&mass[b], 0ull - deep_units(deep_term(v, M, S.tab), deep_scale(b, vf, M)));
-      atomicSub(&count[b], 1u);
+      deep_add(div_by_temperature((double)l, T, rT), vf, M, S.tab, mass, &tail, true);
     }
     const double vs = key_f64(S.sp_key[i]);
-    if (S.sp_key[i] < S.deep_floor && vs > -__builtin_inf()) {
-      const int b = deep_bin(vs, vf);
-      atomicAdd(&mass[b], deep_units(deep_term(vs, M, S.tab), deep_scale(b, vf, M)));
-      atomicAdd(&count[b], 1u);
-    }
+    if (S.sp_key[i] < S.deep_floor && vs > -__builtin_inf()) deep_add(vs, vf, M, S.tab, mass, &tail, false);
   }
+  double tail_mass;
+  block_scan_f64(tail, S.wtmp, &tail_mass);  // the last bin's mass (a fixed order)
   __syncthreads();
   // ---- the region's exact mass, and the bins' prefix masses in fixed point
   constexpr int kPer = kFinishCap / kFinishThreads;  // region entries per thread (and bins)
   static_assert(kDeepBins == kFinishCap, "kPer bins per thread");
-  double r_local[kPer];
-  double r_base;
-  {
-    double sum = 0.0, r_mass;
-#pragma unroll
-    for (int q = 0; q < kPer; ++q) {
-      const int i = tid * kPer + q;
-      sum += i < n_reg ? S.cand_p[i] : 0.0;
-      r_local[q] = sum;
-    }
-    r_base = block_scan_f64(sum, S.wtmp, &r_mass) - sum;
-  }
   Fix128 r_fix{0ull, 0ull};
   for (int i = tid; i < n_reg; i += kFinishThreads) r_fix = fix_add(r_fix, fix_of(S.cand_p[i]));
   r_fix = block_fix_sum(r_fix, (uint64_t*)S.top);
-  // b_after[q]: the mass of the region and of bins 0 .. tid kPer + q, in binary64
-  double b_after[kPer];
+  const double r_total = fix_to_double(r_fix);
+  // after[b] (over mass[b], in place): the mass of the region and of bins
+  // 0 .. b, in binary64 from exact fixed-point sums of the bins' masses
+  double* after = (double*)S.sorted;
   double total;
   {
     Fix128 f[kPer];
@@ -2064,30 +2088,46 @@ __device__ __forceinline__ uint32_t deep_draw(const SampleArgs& a, FinishLds& U)
 #pragma unroll
     for (int q = 0; q < kPer; ++q) {
       const int b = tid * kPer + q;
-      sum = fix_add(sum, fix_shift(mass[b], deep_scale(b, vf, M) - kDeepFracBits + 100));
+      double m = tail_mass;
+      if (b < kDeepBins - 1) {
+        // e^(c_b - M), c_b = vf - (b + 1/2) w
+        const double y = __builtin_fma(-(b + 0.5), kDeepSpan / kDeepBins, vf - M) * GS_256_LOG2E;
+        m = (double)mass[b] * 0x1p-40 * exp2_256_tight(y, S.tab);
+      }
+      sum = fix_add(sum, fix_of(m));
       f[q] = sum;
     }
     Fix128 t_fix;
     const Fix128 base = fix_add(r_fix, block_fix_scan(sum, (uint64_t*)S.top, &t_fix));
 #pragma unroll
-    for (int q = 0; q < kPer; ++q) b_after[q] = fix_to_double(fix_add(base, f[q]));
+    for (int q = 0; q < kPer; ++q) after[tid * kPer + q] = fix_to_double(fix_add(base, f[q]));
     total = fix_to_double(fix_add(r_fix, t_fix));
   }
   if (!(total < __builtin_inf()) || !(total > 0)) return kExactRequest | 0u;
   const double target = u * total;  // the cursor, in units of e
   // the decision margin: the reference's own rounding, the near-tie report
-  // and the histogram's terms (2^-40 relative) with the binary64 sums (2^-40)
+  // and the histogram (terms within 5e-13 relative, the bin masses' and
+  // the binary64 sums' rounding)
   const double mrg = (S.deep_margin + 0x1p-38) * total;
   // ---- the region with the recomputed normaliser
   if (tid == 0) { S.first_idx = 0xFFFFFFFFu; S.route_exact = 0; }
-  __syncthreads();
   {
+    double local[kPer];
+    double sum = 0.0, r_mass;
+#pragma unroll
+    for (int q = 0; q < kPer; ++q) {
+      const int i = tid * kPer + q;
+      sum += i < n_reg ? S.cand_p[i] : 0.0;
+      local[q] = sum;
+    }
+    const double r_base = block_scan_f64(sum, S.wtmp, &r_mass) - sum;
     uint32_t first = 0xFFFFFFFFu;
     bool near = false;
+#pragma unroll
     for (int q = kPer - 1; q >= 0; --q) {
       const int i = tid * kPer + q;
       if (i >= n_reg) continue;
-      const double pre = r_base + r_local[q];
+      const double pre = r_base + local[q];
       if (pre >= target) first = (uint32_t)i;
       if ((pre >= target ? pre - target : target - pre) < mrg) near = true;
     }
@@ -2108,8 +2148,9 @@ __device__ __forceinline__ uint32_t deep_draw(const SampleArgs& a, FinishLds& U)
   // within the margin
   {
     uint32_t first = 0xFFFFFFFFu;
+#pragma unroll
     for (int q = kPer - 1; q >= 0; --q) {
-      if (b_after[q] >= target) first = (uint32_t)(tid * kPer + q);
+      if (after[tid * kPer + q] >= target) first = (uint32_t)(tid * kPer + q);
     }
     first = wave_min_u32(first);
     if (lane == 0 && first != 0xFFFFFFFFu) atomicMin(&S.first_idx, first);
@@ -2117,52 +2158,53 @@ __device__ __forceinline__ uint32_t deep_draw(const SampleArgs& a, FinishLds& U)
   __syncthreads();
   const int bc = (int)S.first_idx;
   if (bc < 0 || bc >= kDeepBins - 1) return kExactRequest | 0u;  // past the bins' span
-  // the mass through bin b, on the thread holding bin b; register arrays are
-  // read at static indices only (a dynamic one would put them in scratch)
-  auto after_of = [&](int b) -> double {
-    double x = 0.0;
-#pragma unroll
-    for (int k = 0; k < kPer; ++k) x = tid * kPer + k == b ? b_after[k] : x;
-    return x;
-  };
-  __syncthreads();
-  const double r_total = fix_to_double(r_fix);
-  if (tid == bc / kPer) S.sel[1] = (uint32_t)(after_of(bc) < target + mrg ? bc + 1 : bc);
-  if (tid == (bc > 0 ? (bc - 1) / kPer : 0)) S.wsum[0] = bc > 0 ? after_of(bc - 1) : r_total;
-  __syncthreads();
-  const int b_hi = (int)S.sel[1];
+  const int b_hi = after[bc] < target + mrg ? bc + 1 : bc;
   // bin bc - 1 taken in too when the mass before bc lies within the margin
-  const bool take_prev = bc > 0 && S.wsum[0] >= target - mrg;
+  const bool take_prev = bc > 0 && after[bc - 1] >= target - mrg;
   const int b_lo = take_prev ? bc - 1 : bc;
-  if (take_prev) {
-    if (tid == (b_lo > 0 ? (b_lo - 1) / kPer : 0)) S.wsum[1] = b_lo > 0 ? after_of(b_lo - 1) : r_total;
-    __syncthreads();
-  }
-  const double pre_before = take_prev ? S.wsum[1] : S.wsum[0];
+  const double pre_before = b_lo > 0 ? after[b_lo - 1] : r_total;
   // the walk below starts after pre_before: the cursor must lie clearly past it
   if (pre_before >= target - mrg) return kExactRequest | GS_FLAG_NEAR_TIE;
   if (b_hi >= kDeepBins - 1) return kExactRequest | 0u;
-  uint32_t n_in = 0;
-  for (int b = b_lo; b <= b_hi; ++b) n_in += count[b];
-  if (n_in > (uint32_t)kFinishCap) return kExactRequest | 0u;  // a crowd of equal values
-  __syncthreads();
-  // ---- pass 2: gather the bins' entries (value key, id) into sorted / hash_ids
+  // the float range of (capped) logits whose values can fall in bins b_lo ..
+  // b_hi: v in [vf - (b_hi + 1) w, vf - b_lo w] up to rounding, times T,
+  // widened by 1e-6 relative (more than rounding the bounds to float moves them)
+  double l_hi = (vf - b_lo * (kDeepSpan / kDeepBins)) * T;
+  double l_lo = (vf - (b_hi + 1) * (kDeepSpan / kDeepBins)) * T;
+  l_hi += 1e-6 * (1.0 + __builtin_fabs(l_hi));
+  l_lo -= 1e-6 * (1.0 + __builtin_fabs(l_lo));
+  if (tid == 0) S.deep_final = 0;
+  __syncthreads();  // every read of after[] done before the gather reuses the array
+  // ---- pass 2: stage the logits in the bins' float range (in cand_p), then
+  // keep those whose exact value falls in the bins, specials aside, as (value
+  // key, id) in sorted / hash_ids
+  uint64_t* stage = (uint64_t*)S.cand_p;
   uint64_t* gkey = S.sorted;
   uint32_t* gid = S.hash_ids;
-  deep_gather(a, row, cfg.softcap, T, thr, vf, b_lo, b_hi, spset, gkey, gid, &S.deep_count);
+  deep_stage(a, row, cfg.softcap, thr, (float)l_lo, (float)l_hi, stage, &S.deep_count);
+  __syncthreads();
+  if (S.deep_count > (uint32_t)kFinishCap) return kExactRequest | 0u;  // a crowd of equal values
+  const int n_s = (int)S.deep_count;
   auto gather = [&](double v, uint32_t id) {
     const int b = deep_bin(v, vf);
     if (b < b_lo || b > b_hi) return;
-    const uint32_t pos = atomicAdd(&S.deep_count, 1u);
+    const uint32_t pos = atomicAdd(&S.deep_final, 1u);
     if (pos < (uint32_t)kFinishCap) { gkey[pos] = f64_key(v); gid[pos] = id; }
   };
+  for (int i = tid; i < n_s; i += kFinishThreads) {
+    const uint64_t e = stage[i];
+    const uint32_t id = (uint32_t)e;
+    if (!deep_is_special(spset, id)) {
+      gather(div_by_temperature((double)__builtin_bit_cast(float, (uint32_t)(e >> 32)), T, rT), id);
+    }
+  }
   for (int i = tid; i < n_sp; i += kFinishThreads) {
     const double vs = key_f64(S.sp_key[i]);
     if (S.sp_key[i] < S.deep_floor && vs > -__builtin_inf()) gather(vs, S.sp_id[i]);
   }
   __syncthreads();
-  const int n_g = (int)S.deep_count;
-  if (n_g != (int)n_in || n_g == 0) return kExactRequest | 0u;
+  const int n_g = (int)S.deep_final;
+  if (n_g > kFinishCap || n_g == 0) return kExactRequest | 0u;
   // ---- sort them (value desc, id asc) and walk them with exact exponentials
   const int m2 = pow2_at_least(n_g);
   for (int i = n_g + tid; i < m2; i += kFinishThreads) { gkey[i] = 0; gid[i] = 0xFFFFFFFFu; }

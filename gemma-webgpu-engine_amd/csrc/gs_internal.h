@@ -82,6 +82,17 @@ __host__ __device__ __forceinline__ uint64_t pack_entry(uint32_t key, uint32_t i
 __host__ __device__ __forceinline__ uint32_t entry_key(uint64_t e) { return (uint32_t)(e >> 32); }
 __host__ __device__ __forceinline__ uint32_t entry_id(uint64_t e) { return ~(uint32_t)e; }
 
+// l / T rounded to nearest, from r = 1 / T rounded to nearest: q0 = l r
+// lies within an ulp of l / T, the remainder l - q0 T is exact in one fma,
+// and q0 + (l - q0 T) r rounded is l / T rounded (Markstein's theorem; it
+// needs no overflow or underflow in the quotient and the remainder, which
+// |l| < 2^128 with T in [2^-20, 2^20] guarantees). Three operations instead
+// of the division's iteration. -0 gives +0, which the keys treat alike.
+__device__ __forceinline__ double div_by_temperature(double l, double T, double r) {
+  const double q0 = l * r;
+  return __builtin_fma(__builtin_fma(-q0, T, l), r, q0);
+}
+
 // ---------------------------------------------------------- row routing
 enum Route : int32_t {
   kRouteGreedy = 0,  // temperature 0: argmax, first maximum wins
