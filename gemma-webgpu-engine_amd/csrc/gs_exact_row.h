@@ -251,7 +251,7 @@ __device__ __noinline__ void process_row(const SampleArgs& a, Lds& L, Scratch S,
     for (int64_t i = tid; i < N; i += kExactThreads) {
       if (i < V) {
         float x = load_logit(a, row, i);
-        if (cfg.softcap > 0) x = gsm::softcap_f32(x, cfg.softcap);
+        if (cfg.softcap > 0) x = softcap_call(x, cfg.softcap);
         const uint32_t count = counts[i], kd = kinds[i];
         bool allowed = true;
         if (constrained) {

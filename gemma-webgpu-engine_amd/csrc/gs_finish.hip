@@ -805,7 +805,7 @@ __device__ double recompute_nonspecial_sum(const SampleArgs& a, int64_t row, con
   // term, far inside the table exponential's error
   const double yA = (1.0 / T) * GS_256_LOG2E, yB = -M * GS_256_LOG2E;
   auto term = [&](float l) -> double {
-    if (cfg.softcap > 0) l = gsm::softcap_f32(l, cfg.softcap);
+    if (cfg.softcap > 0) l = softcap_call(l, cfg.softcap);
     const double y = __builtin_fma((double)l, yA, yB);
     // evaluated for every y (no branch), so that independent terms overlap;
     // exp2_256 reads its table at an index masked to 0..255 for any y
@@ -1281,7 +1281,7 @@ __device__ __forceinline__ uint32_t finish_row(const SampleArgs& a, FinishLds& U
         x32 = __builtin_bit_cast(float, a.dtype == GS_BF16 ? b << 16 : b);
         mword = omw[r < kOwn ? r : 0];
       }
-      if (cfg.softcap > 0) x32 = gsm::softcap_f32(x32, cfg.softcap);
+      if (cfg.softcap > 0) x32 = softcap_call(x32, cfg.softcap);
       bool allowed = true;
       if (constrained) {
         const bool term = kinds & GS_FORCED_TERMINATION;
@@ -1799,22 +1799,25 @@ __device__ __forceinline__ uint32_t finish_row(const SampleArgs& a, FinishLds& U
 // region floor's value, bin 0 the highest, values further down in the last.
 // A non-increasing function of v, so the bins are contiguous runs of the
 // reference's sorted list.
-__device__ __forceinline__ double deep_z(double v, double vf) {
-  return (vf - v) * ((double)kDeepBins / kDeepSpan);
+// (vfc = vf kDeepBins / kDeepSpan: z = (vf - v) kDeepBins / kDeepSpan in one fma)
+__device__ __forceinline__ double deep_z(double v, double vfc) {
+  return __builtin_fma(v, -((double)kDeepBins / kDeepSpan), vfc);
 }
-__device__ __forceinline__ int deep_bin(double v, double vf) {
-  const double z = deep_z(v, vf);
+__device__ __forceinline__ int deep_bin(double v, double vfc) {
+  const double z = deep_z(v, vfc);
   return z < (double)(kDeepBins - 1) ? (int)z : kDeepBins - 1;
 }
 // A value's term relative to its bin's centre c_b = vf - (b + 1/2) w, w =
-// kDeepSpan / kDeepBins: e^(v - c_b) = e^x with x = (b + 1/2 - z) w, |x| <=
+// kDeepSpan / kDeepBins: e^(v - c_b) = e^x with x = (b + 1/2 - z) w (b w and
+// (b + 1/2) w are exact, so x is z w rounded once from there), |x| <=
 // w / 2 (up to z's rounding, 1e-12 of a bin), by its degree-4 Taylor
 // polynomial (remainder below 3e-14), in units of 2^-40 rounded to nearest
 // (4.6e-13 relative): every term of a bin is about 2^40 units, and a bin of
 // at most 2^21 + kSpecialCap of them sums below 2^62. The bin's mass is then
 // its units times 2^-40 e^(c_b - M). For b < kDeepBins - 1 only.
 __device__ __forceinline__ uint64_t deep_units(double z, int b) {
-  const double x = (0.5 - (z - (double)b)) * (kDeepSpan / kDeepBins);
+  constexpr double w = kDeepSpan / kDeepBins;
+  const double x = __builtin_fma(-z, w, __builtin_fma((double)b, w, 0.5 * w));
   double p = __builtin_fma(x, 1.0 / 24.0, 1.0 / 6.0);
   p = __builtin_fma(x, p, 0.5);
   p = __builtin_fma(x, p, 1.0);
@@ -1831,9 +1834,9 @@ __device__ __forceinline__ double deep_term(double v, double M, const double* ta
 }
 // adds value v's term to the histogram (mass) or to the last bin's sum
 // (*tail); negate: subtracts it
-__device__ __forceinline__ void deep_add(double v, double vf, double M, const double* tab, uint64_t* mass,
+__device__ __forceinline__ void deep_add(double v, double vfc, double M, const double* tab, uint64_t* mass,
                                          double* tail, bool negate) {
-  const double z = deep_z(v, vf);
+  const double z = deep_z(v, vfc);
   if (z < (double)(kDeepBins - 1)) {
     const int b = (int)z;
     const uint64_t n = deep_units(z, b);
@@ -1934,16 +1937,20 @@ __device__ __forceinline__ bool deep_is_special(const uint32_t* set, uint32_t id
   return false;
 }
 
-// Calls visit(l, id) for every logit of the row, the whole block over it:
-// kB 16-byte loads per thread go out before any is used, so that kB *
-// kFinishThreads * 16 bytes are in flight (one block reads a row alone here,
-// and its loads would otherwise wait on one memory latency each).
+// Calls visit(l, id) for every logit l of the row (soft-capped when cap > 0),
+// the whole block over it: kB 16-byte loads per thread go out before any is
+// used. Capped rows take a plain loop with the cap's call, so that the
+// unrolled loop stays small.
 template <int kB, typename F>
-__device__ __forceinline__ void visit_row(const SampleArgs& a, int64_t row, F&& visit) {
+__device__ __forceinline__ void visit_row(const SampleArgs& a, int64_t row, double cap, F&& visit) {
   const int tid = threadIdx.x;
   const int64_t V = a.vocab;
   int64_t from = 0;
-  if (a.vector_ok) {
+  if (cap > 0) {
+    from = V;
+#pragma unroll 1
+    for (int64_t i = tid; i < V; i += kFinishThreads) visit(softcap_call(load_logit(a, row, i), cap), (uint32_t)i);
+  } else if (a.vector_ok) {
     const bool bf16 = a.dtype == GS_BF16;
     const int per = bf16 ? 8 : 4;
     const int64_t n_vec = V / per;
@@ -1978,33 +1985,31 @@ __device__ __forceinline__ void visit_row(const SampleArgs& a, int64_t row, F&& 
 }
 
 // The deep draw's tail histogram: every finite logit below the region floor
-// (thr) adds its term to its bin (LDS atomics on integers, so the sums do not
+// (l <= l_below) adds its term to its bin (LDS atomics on integers, so the sums do not
 // depend on their order), or to the returned per-thread sum of the last bin;
 // specials are corrected by the caller. The whole block calls it.
 __device__ __noinline__ double deep_histogram(const SampleArgs& a, int64_t row, double cap, double T, double rT,
-                                              double M, uint32_t thr, double vf, uint64_t* mass,
+                                              double M, float l_below, double vfc, uint64_t* mass,
                                               const double* tab) {
   double tail = 0.0;
-  visit_row<4>(a, row, [&](float l, uint32_t) {
-    if (cap > 0) l = gsm::softcap_f32(l, cap);
-    if (!(l > -__builtin_inff()) || f32_key(l) >= thr) return;
-    deep_add(div_by_temperature((double)l, T, rT), vf, M, tab, mass, &tail, false);
+  visit_row<4>(a, row, cap, [&](float l, uint32_t) {
+    if (!(l > -__builtin_inff() && l <= l_below)) return;
+    deep_add(div_by_temperature((double)l, T, rT), vfc, M, tab, mass, &tail, false);
   });
   return tail;
 }
 
-// The deep draw's gather, first step: every finite logit in [l_lo, l_hi] (a
-// float range that holds the wanted bins' logits with room to spare) and
-// below the region floor (thr), as (float bits << 32 | id), appended to stage
+// The deep draw's gather, first step: every logit in [l_lo, l_hi] (a float
+// range below the region floor that holds the wanted bins' logits with room
+// to spare), as (float bits << 32 | id), appended to stage
 // from *counter (at most kFinishCap kept; one LDS atomic per wave and
 // logit position). The exact test runs on the few staged entries only. The
 // whole block calls it.
-__device__ __noinline__ void deep_stage(const SampleArgs& a, int64_t row, double cap, uint32_t thr, float l_lo,
-                                        float l_hi, uint64_t* stage, uint32_t* counter) {
+__device__ __noinline__ void deep_stage(const SampleArgs& a, int64_t row, double cap, float l_lo, float l_hi,
+                                        uint64_t* stage, uint32_t* counter) {
   const int lane = threadIdx.x & 63;
-  visit_row<8>(a, row, [&](float l, uint32_t id) {
-    if (cap > 0) l = gsm::softcap_f32(l, cap);
-    const bool pass = l >= l_lo && l <= l_hi && f32_key(l) < thr;
+  visit_row<4>(a, row, cap, [&](float l, uint32_t id) {
+    const bool pass = l >= l_lo && l <= l_hi;
     const uint64_t m = __ballot(pass);
     if (m == 0) return;
     const int leader = __builtin_ctzll(m);
@@ -2040,6 +2045,10 @@ __device__ __noinline__ uint32_t deep_draw(const SampleArgs& a, FinishLds& U) {
   const int n_reg = (int)S.deep_n;
   const int n_sp = (int)(S.n_special < (uint32_t)kSpecialCap ? S.n_special : (uint32_t)kSpecialCap);
   const double vf = (double)key_f32(thr) / T;  // the region floor's value
+  const double vfc = vf * ((double)kDeepBins / kDeepSpan);
+  // the largest float below the floor's logit: l <= l_below iff f32_key(l) < thr
+  // (NaN aside; -0 and +0 share a key, and the float below both is -2^-149)
+  const float l_below = key_f32(thr - 1u);
   // every term below the floor at most 1, so the fixed-point sums stay below
   // 2^22 (M is the row's largest value; a floor above it is left to the
   // exact path); the quotient l / T by div_by_temperature, whose range this
@@ -2054,19 +2063,19 @@ __device__ __noinline__ uint32_t deep_draw(const SampleArgs& a, FinishLds& U) {
   __syncthreads();
   for (int i = tid; i < n_sp; i += kFinishThreads) special_insert(SpecialTable{spset, S.hist}, S.sp_id[i], 1u);
   // ---- pass 1: the tail's mass per bin
-  double tail = deep_histogram(a, row, cfg.softcap, T, rT, M, thr, vf, mass, S.tab);
+  double tail = deep_histogram(a, row, cfg.softcap, T, rT, M, l_below, vfc, mass, S.tab);
   __syncthreads();
   // specials: out with their raw values (where the pass counted them; the
   // same units, so exactly), in with their penalised ones below the floor
   for (int i = tid; i < n_sp; i += kFinishThreads) {
     const uint32_t id = S.sp_id[i];
     float l = load_logit(a, row, id);
-    if (cfg.softcap > 0) l = gsm::softcap_f32(l, cfg.softcap);
+    if (cfg.softcap > 0) l = softcap_call(l, cfg.softcap);
     if (l > -__builtin_inff() && f32_key(l) < thr) {
-      deep_add(div_by_temperature((double)l, T, rT), vf, M, S.tab, mass, &tail, true);
+      deep_add(div_by_temperature((double)l, T, rT), vfc, M, S.tab, mass, &tail, true);
     }
     const double vs = key_f64(S.sp_key[i]);
-    if (S.sp_key[i] < S.deep_floor && vs > -__builtin_inf()) deep_add(vs, vf, M, S.tab, mass, &tail, false);
+    if (S.sp_key[i] < S.deep_floor && vs > -__builtin_inf()) deep_add(vs, vfc, M, S.tab, mass, &tail, false);
   }
   double tail_mass;
   block_scan_f64(tail, S.wtmp, &tail_mass);  // the last bin's mass (a fixed order)
@@ -2181,12 +2190,13 @@ __device__ __noinline__ uint32_t deep_draw(const SampleArgs& a, FinishLds& U) {
   uint64_t* stage = (uint64_t*)S.cand_p;
   uint64_t* gkey = S.sorted;
   uint32_t* gid = S.hash_ids;
-  deep_stage(a, row, cfg.softcap, thr, (float)l_lo, (float)l_hi, stage, &S.deep_count);
+  const float l_top = (float)l_hi < l_below ? (float)l_hi : l_below;
+  deep_stage(a, row, cfg.softcap, (float)l_lo, l_top, stage, &S.deep_count);
   __syncthreads();
   if (S.deep_count > (uint32_t)kFinishCap) return kExactRequest | 0u;  // a crowd of equal values
   const int n_s = (int)S.deep_count;
   auto gather = [&](double v, uint32_t id) {
-    const int b = deep_bin(v, vf);
+    const int b = deep_bin(v, vfc);
     if (b < b_lo || b > b_hi) return;
     const uint32_t pos = atomicAdd(&S.deep_final, 1u);
     if (pos < (uint32_t)kFinishCap) { gkey[pos] = f64_key(v); gid[pos] = id; }

@@ -82,6 +82,12 @@ __host__ __device__ __forceinline__ uint64_t pack_entry(uint32_t key, uint32_t i
 __host__ __device__ __forceinline__ uint32_t entry_key(uint64_t e) { return (uint32_t)(e >> 32); }
 __host__ __device__ __forceinline__ uint32_t entry_id(uint64_t e) { return ~(uint32_t)e; }
 
+// gsm::softcap_f32 as a call of its own: its binary64 divisions and
+// exponential are some hundred instructions, which, expanded at every logit
+// of an unrolled loop, would overflow the instruction cache for the rows that
+// never use it
+[[maybe_unused]] static __device__ __noinline__ float softcap_call(float x, double cap) { return gsm::softcap_f32(x, cap); }
+
 // l / T rounded to nearest, from r = 1 / T rounded to nearest: q0 = l r
 // lies within an ulp of l / T, the remainder l - q0 T is exact in one fma,
 // and q0 + (l - q0 T) r rounded is l / T rounded (Markstein's theorem; it

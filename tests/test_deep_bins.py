@@ -41,7 +41,7 @@ def exp2_256_tight(y, table, c):
 
 
 def deep_units(z, b, c4=1.0 / 24.0):
-    x = mul(0.5 - (z - float(b)), SPAN / BINS)
+    x = fma(-z, W, fma(float(b), W, 0.5 * W))
     p = fma(x, c4, 1.0 / 6.0)
     p = fma(x, p, 0.5)
     p = fma(x, p, 1.0)
