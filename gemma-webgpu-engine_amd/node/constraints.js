@@ -5,14 +5,14 @@
  *                                 acceptBytes / validateFinal (:32-113)
  *   maskConstraintLogits          (:159-173)
  *   selectConstrainedToken        (src/runtime/gemma-session.ts:1305-1329)
- * The DFA is given as tables: next[state * 256 + byte] (-1: no edge),
- * finals[state], an initial state. Viable states (co-reachable to a final
- * state, constraints.ts:300-322) are derived by the library. Compiling
- * regex / JSON / JSON-schema constraints into such tables is not part of
- * this engine: those types are rejected with the reference's
- * "Unsupported generation constraint" error prefix.
+ * The engine works on byte-level DFA tables: next[state * 256 + byte] (-1:
+ * no edge), finals[state], an initial state. Viable states (co-reachable to a
+ * final state, constraints.ts:300-322) are derived by the library. regex,
+ * json, json-object and json-schema constraints are compiled into such tables
+ * (constraint-compiler.js, regex-dfa.js); "byte-dfa" takes tables as given.
  */
 const { Engine } = require("./engine");
+const { compileConstraintTables } = require("./constraint-compiler");
 const { engineFor, sampleToken } = require("./sampling");
 
 const EOS_TOKEN_IDS = Object.freeze([1, 50, 106]);
@@ -82,15 +82,15 @@ class CompiledGenerationConstraint {
   }
 }
 
-/* compileGenerationConstraint (constraints.ts:115): byte-level DFA tables
- * only. */
+/* compileGenerationConstraint (constraints.ts:115-157): regex, json,
+ * json-object and json-schema constraints compiled to byte-level tables, or
+ * "byte-dfa" tables as given. */
 function compileGenerationConstraint(constraint) {
   if (constraint && constraint.type === "byte-dfa") {
     return new CompiledGenerationConstraint(new ByteLevelDfa(constraint), constraint.validateOutput);
   }
-  const type = constraint && constraint.type;
-  throw new Error("Unsupported generation constraint: " + type +
-    " constraints need compiling to byte-level DFA tables; pass { type: \"byte-dfa\", next, finals }");
+  const tables = compileConstraintTables(constraint);
+  return new CompiledGenerationConstraint(new ByteLevelDfa(tables.dfa), tables.validateOutput);
 }
 
 function maskConstraintLogits(rawLogits, legalTokenIds, terminationTokenIds) {

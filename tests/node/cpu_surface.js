@@ -107,9 +107,12 @@ test("token byte table: null and empty tokens are skipped", () => {
   assert.deepStrictEqual(Array.from(trie.tokenBytes(3)), [97, 98]);
 });
 
-test("constraint compilation: byte-level tables only", () => {
-  assert.throws(() => g.compileGenerationConstraint({ type: "regex", pattern: "a+" }),
-    /^Error: Unsupported generation constraint: regex/);
+test("constraint compilation: compiled patterns and byte-level tables", () => {
+  const r = g.compileGenerationConstraint({ type: "regex", pattern: "a+" });
+  assert.strictEqual(r.accepting, false);
+  assert.strictEqual(r.dfa.finals[r.dfa.next[r.dfa.initial * 256 + 97]], 1);
+  assert.throws(() => g.compileGenerationConstraint({ type: "regex", pattern: "a$" }),
+    /^Error: Unsupported generation constraint: regex assertions are not supported$/);
   assert.throws(() => new g.ByteLevelDfa({ next: [0], finals: [1] }), /stateCount \* 256/);
   const next = new Array(256).fill(-1);
   next[97] = 0;

@@ -305,6 +305,73 @@ test("selectConstrainedToken matches the oracle on the masked row", () => {
   }), /^Error: Generation constraint reached a tokenization dead end$/);
 });
 
+test("compiled regex and JSON constraints through the engine (constraints.spec.ts:27-93)", () => {
+  const enc = new TextEncoder();
+  const trieOfBytes = (tokens) => new g.TokenByteTrie({
+    vocabularySize: tokens.length,
+    tokenBytes: (id) => (tokens[id] === null ? null : typeof tokens[id] === "string" ? enc.encode(tokens[id]) : tokens[id]),
+  });
+  // the reference's own patterns, compiled
+  let trie = trieOfBytes([null, "a", "b", "c", "ab", "ac", "x"]);
+  let c = g.compileGenerationConstraint({ type: "regex", pattern: "a(?:b|c)" });
+  assert.deepStrictEqual(Array.from(c.legalTokenIds(trie)), [1, 4, 5]);
+  c.acceptToken(enc.encode("a"));
+  assert.strictEqual(c.accepting, false);
+  assert.deepStrictEqual(Array.from(c.legalTokenIds(trie)), [2, 3]);
+  c.acceptToken(enc.encode("b"));
+  assert.strictEqual(c.accepting, true);
+  c.validateFinal("ab");
+  const arabic = enc.encode("\u0623");
+  trie = trieOfBytes([null, arabic.slice(0, 1), arabic.slice(1), arabic, Uint8Array.of(0xff)]);
+  c = g.compileGenerationConstraint({ type: "regex", pattern: "\u0623" });
+  assert.deepStrictEqual(Array.from(c.legalTokenIds(trie)), [1, 3]);
+  c.acceptToken(arabic.slice(0, 1));
+  assert.deepStrictEqual(Array.from(c.legalTokenIds(trie)), [2]);
+  c.acceptToken(arabic.slice(1));
+  assert.strictEqual(c.accepting, true);
+  trie = trieOfBytes([null, Uint8Array.of(0xef), Uint8Array.of(0xbf), Uint8Array.of(0xbd), "{"]);
+  assert.deepStrictEqual(Array.from(g.compileGenerationConstraint({ type: "regex", pattern: "\\{" }).legalTokenIds(trie)), [4]);
+  const obj = g.compileGenerationConstraint({ type: "json-object", maxDepth: 3, whitespace: "none" });
+  obj.acceptBytes(enc.encode("{\"city\":\"Paris\",\"facts\":[true,2]}"));
+  obj.validateFinal("{\"city\":\"Paris\",\"facts\":[true,2]}");
+  assert.throws(() => g.compileGenerationConstraint({ type: "json", maxDepth: 2 }).acceptBytes(enc.encode("{]")),
+    /^Error: Selected token violates the generation constraint$/);
+
+  // a JSON grammar over a vocab of JSON fragments: the mask kernel's legal
+  // ids against the definition, along a generated document
+  const pieces = ["{", "}", "[", "]", ":", ",", "\"", " ", "\"a", "b\"", "1", "23", "-", ".5", "e+", "true", "fals", "e",
+    "null", "\\n", "\u00e9", "\u05e9\u05dc", "\ud83d\ude00", "\"k\":", "},{", "[[", "]]", "\":\""];
+  const rngw = new oracle.SeededRandom(77);
+  const words = [];
+  for (let id = 0; id < 5000; id += 1) {
+    if (id % 101 === 0) { words.push(null); continue; }
+    const n = 1 + Math.floor(rngw.next() * 3);
+    let w = "";
+    for (let k = 0; k < n; k += 1) w += pieces[Math.floor(rngw.next() * pieces.length)];
+    words.push(w);
+  }
+  // split some multi-byte characters across tokens
+  const bytesOf = words.map((w) => (w === null ? null : enc.encode(w)));
+  for (let id = 4000; id < 4100; id += 1) if (bytesOf[id] && bytesOf[id].length > 1) bytesOf[id] = bytesOf[id].slice(0, bytesOf[id].length - 1);
+  trie = new g.TokenByteTrie({ vocabularySize: bytesOf.length, tokenBytes: (id) => bytesOf[id] });
+  c = g.compileGenerationConstraint({ type: "json", maxDepth: 3, whitespace: "compact" });
+  const dfa = c.dfa;
+  const viable = viableStates(dfa);
+  const doc = enc.encode("{\"k\": [1, \"a\\n\u00e9\ud83d\ude00\", {\"b\": null}], \"x\": -23.5e+1}");
+  let checked = 0;
+  for (let i = 0; i <= doc.length; i += 3) {
+    c.state = dfa.initial;
+    c.acceptBytes(doc.slice(0, i));
+    const got = Array.from(c.legalTokenIds(trie));
+    assert.deepStrictEqual(got, bruteLegal(bytesOf, dfa, viable, c.state), "after " + i + " bytes");
+    checked += got.length;
+  }
+  assert.ok(checked > 100, checked);
+  c.state = dfa.initial;
+  c.acceptBytes(doc);
+  assert.strictEqual(c.accepting, true);
+});
+
 test("Engine.sampleRows: batched rows with histories and draw indices", () => {
   const V = 40000;
   const R = 32;

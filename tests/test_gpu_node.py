@@ -10,4 +10,4 @@ pytestmark = pytest.mark.gpu
 
 def test_node_host_parity_on_gpu():
     out = run_node_tests("gpu_parity.js", 280)
-    assert "all 10 passed" in out
+    assert "all 11 passed" in out

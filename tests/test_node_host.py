@@ -30,3 +30,11 @@ def test_node_host_surface_without_gpu():
         pytest.fail("gsample_node.node is not built; run __graft_entry__.build()")
     out = run_node_tests("cpu_surface.js", 120)
     assert "all 9 passed" in out
+
+
+def test_constraint_compiler_without_gpu():
+    """Regex / JSON / JSON Schema constraints compiled to byte-level DFA
+    tables: the reference's constraint known answers, RegExp full-match
+    acceptance, and the reference's pending UTF-8 byte walk."""
+    out = run_node_tests("constraint_compiler.js", 300)
+    assert "all 14 passed" in out
