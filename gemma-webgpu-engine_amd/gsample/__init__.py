@@ -17,6 +17,7 @@ from .config import (  # noqa: F401
     uses_gemma_gpu_greedy,
     validate_decoding_config,
 )
+from . import vocab  # noqa: F401
 from .runtime import (  # noqa: F401
     GS_F32,
     GS_BF16,

@@ -15,7 +15,7 @@ const { Engine } = require("./engine");
 const { compileConstraintTables } = require("./constraint-compiler");
 const { engineFor, sampleToken } = require("./sampling");
 
-const EOS_TOKEN_IDS = Object.freeze([1, 50, 106]);
+const { EOS_TOKEN_IDS } = require("./token-bytes");
 
 class ByteLevelDfa {
   constructor(spec) {

@@ -161,3 +161,14 @@ export class Engine {
 }
 
 export const ADDON_PATH: string;
+
+// token-bytes.js: the Gemma token byte table (gemma-tokenizer.ts:17-19,346-360)
+export const GEMMA_START_CHANNEL_TOKEN_ID: number;
+export const GEMMA_END_CHANNEL_TOKEN_ID: number;
+export function createTokenByteTable(
+  vocabulary: Map<string, number> | Record<string, number>, specialIds: Iterable<number>): (Uint8Array | null)[];
+export function readTokenizerJson(path: string): { vocabulary: Map<string, number>; specialIds: number[] };
+export function loadTokenizerJson(path: string): (Uint8Array | null)[];
+export function tokenByteSource(table: (Uint8Array | null)[]): TokenByteSource;
+export function writeTokenByteTable(path: string, table: (Uint8Array | null)[]): void;
+export function readTokenByteTable(path: string): (Uint8Array | null)[];

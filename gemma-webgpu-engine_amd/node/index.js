@@ -9,10 +9,11 @@ const generationConfig = require("./generation-config");
 const sampling = require("./sampling");
 const constraints = require("./constraints");
 const trie = require("./token-byte-trie");
+const tokenBytes = require("./token-bytes");
 const engine = require("./engine");
 const { native, ADDON_PATH } = require("./native");
 
-module.exports = Object.assign({}, decoding, generationConfig, sampling, constraints, trie, engine, {
+module.exports = Object.assign({}, decoding, generationConfig, sampling, constraints, trie, tokenBytes, engine, {
   native,
   ADDON_PATH,
 });
