@@ -11,9 +11,10 @@ const constraints = require("./constraints");
 const trie = require("./token-byte-trie");
 const tokenBytes = require("./token-bytes");
 const engine = require("./engine");
+const session = require("./session");
 const { native, ADDON_PATH } = require("./native");
 
-module.exports = Object.assign({}, decoding, generationConfig, sampling, constraints, trie, tokenBytes, engine, {
+module.exports = Object.assign({}, decoding, generationConfig, sampling, constraints, trie, tokenBytes, engine, { generate: session.generate, session,
   native,
   ADDON_PATH,
 });
