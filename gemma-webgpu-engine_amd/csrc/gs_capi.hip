@@ -862,6 +862,38 @@ int gs_lmhead(gs_context* ctx, const void* hidden, const void* weight, int32_t m
   return GS_OK;
 }
 
+int gs_qat_lmhead(gs_context* ctx, const float* x, int32_t m_rows, int32_t width, const uint32_t* packed_codes,
+                  int32_t layout, const float* row_scales, float input_scale, float output_scale, float* logits,
+                  void* stream) {
+  if (!ctx || !x || !packed_codes || !row_scales || !logits || m_rows <= 0 || width <= 0)
+    return fail(ctx, GS_ERR_INVALID_ARGUMENT, "bad arguments");
+  if (width % 64 != 0 || width > 4096) return fail(ctx, GS_ERR_UNSUPPORTED, "QAT lm_head width must be a multiple of 64, at most 4096");
+  if (layout != GS_QAT_ROW_MAJOR && layout != GS_QAT_BLOCK_MAJOR) return fail(ctx, GS_ERR_INVALID_ARGUMENT, "unknown QAT weight layout");
+  if (!aligned16(x) || !aligned16(packed_codes)) return fail(ctx, GS_ERR_INVALID_ARGUMENT, "x and the codes must be 16-byte aligned");
+  if (!(input_scale >= 0) || !(output_scale >= 0)) return fail(ctx, GS_ERR_INVALID_ARGUMENT, "SRQ scales must be >= 0");
+  GS_HIP(ctx, hipSetDevice(ctx->device));
+  hipStream_t s = pick_stream(ctx, stream);
+  const int32_t slot = timing_slot(ctx);
+  launch_qat_lmhead(x, m_rows, width, packed_codes, layout == GS_QAT_BLOCK_MAJOR, row_scales, ctx->vocab, input_scale,
+                    output_scale, logits, s, stage_events(ctx, slot, GS_STAGE_LMHEAD));
+  GS_HIP(ctx, hipGetLastError());
+  return GS_OK;
+}
+
+int gs_qat_lmhead_sample(gs_context* ctx, const float* x, int32_t width, const uint32_t* packed_codes,
+                         int32_t layout, const float* row_scales, float input_scale, float output_scale,
+                         float* logits_scratch, const gs_batch* batch, void* stream) {
+  if (!batch) return fail(ctx, GS_ERR_INVALID_ARGUMENT, "bad arguments");
+  int st = gs_qat_lmhead(ctx, x, batch->rows, width, packed_codes, layout, row_scales, input_scale, output_scale,
+                         logits_scratch, stream);
+  if (st != GS_OK) return st;
+  gs_batch b = *batch;
+  b.logits = logits_scratch;
+  b.dtype = GS_F32;
+  b.row_stride = ctx->vocab;
+  return gs_sample(ctx, &b, stream);
+}
+
 int gs_lmhead_sample(gs_context* ctx, const void* hidden, const void* weight, int32_t width, float softcap,
                      float* logits_scratch, const gs_batch* batch, void* stream) {
   if (!batch) return fail(ctx, GS_ERR_INVALID_ARGUMENT, "null batch");

@@ -19,6 +19,7 @@ PKG = os.path.dirname(HERE)
 LIB_PATH = os.path.join(PKG, "lib", "libgsample.so")
 
 GS_F32, GS_BF16 = 0, 1
+GS_QAT_ROW_MAJOR, GS_QAT_BLOCK_MAJOR = 0, 1
 GS_RNG_SEEDED, GS_RNG_EXPLICIT = 0, 1
 GS_ROW_FORCE_EXACT = 1
 GS_FORCED_TERMINATION, GS_FORCED_EXTRA = 1, 2
@@ -106,7 +107,7 @@ EXPORTED_SYMBOLS = (
     "gs_abi_version", "gs_device_count", "gs_seeded_random", "gs_js_exp", "gs_js_log", "gs_softcap",
     "gs_validate_configs", "gs_create", "gs_destroy", "gs_last_error", "gs_synchronize", "gs_stream",
     "gs_sample", "gs_sample_noalloc", "gs_sample_sync", "gs_token_log_prob", "gs_token_log_prob_host", "gs_set_vocab", "gs_set_dfa",
-    "gs_build_masks", "gs_dfa_advance", "gs_dfa_accepting", "gs_lmhead", "gs_lmhead_sample", "gs_timing_begin",
+    "gs_build_masks", "gs_dfa_advance", "gs_dfa_accepting", "gs_lmhead", "gs_lmhead_sample", "gs_qat_lmhead", "gs_qat_lmhead_sample", "gs_timing_begin",
     "gs_timing_end", "gs_check_exp2",
 )
 
@@ -155,6 +156,8 @@ def library():
     L.gs_dfa_accepting.argtypes = [vp, i32, C.POINTER(C.c_int32)]
     L.gs_lmhead.argtypes = [vp, vp, vp, i32, i32, C.c_float, vp, vp]
     L.gs_lmhead_sample.argtypes = [vp, vp, vp, i32, C.c_float, vp, C.POINTER(Batch), vp]
+    L.gs_qat_lmhead.argtypes = [vp, vp, i32, i32, vp, i32, vp, C.c_float, C.c_float, vp, vp]
+    L.gs_qat_lmhead_sample.argtypes = [vp, vp, i32, vp, i32, vp, C.c_float, C.c_float, vp, C.POINTER(Batch), vp]
     L.gs_timing_begin.argtypes = [vp, i32]
     L.gs_timing_end.argtypes = [vp, vp, vp]
     L.gs_check_exp2.argtypes = [vp, C.c_float, C.c_float, C.POINTER(C.c_double), C.POINTER(C.c_float)]
@@ -441,6 +444,42 @@ class Sampler:
         if stream is None:
             self.synchronize()
         return out
+
+    def qat_lmhead(self, x, packed_codes, row_scales, layout: int = 0, input_scale: float = 0.0,
+                   output_scale: float = 0.0, out=None, stream: Optional[int] = None):
+        """gs_qat_lmhead: the int2 QAT LM head (cpuQatLinear, src/reference/qat-linear.ts:78-148).
+        x: f32 [M][width]; packed_codes: int32/uint32 words (GS_QAT_ROW_MAJOR [V][width/16] or
+        GS_QAT_BLOCK_MAJOR [width/64][V][4]); row_scales: f32 [V]; all on the device."""
+        torch = self.torch
+        m, width = int(x.shape[0]), int(x.shape[1])
+        if out is None:
+            out = torch.empty((m, self.vocab), dtype=torch.float32, device=self.device)
+        if stream is None:
+            torch.cuda.current_stream(self.device).synchronize()
+        self._check(self.lib.gs_qat_lmhead(self.ctx, C.c_void_p(x.data_ptr()), m, width,
+                                           C.c_void_p(packed_codes.data_ptr()), int(layout),
+                                           C.c_void_p(row_scales.data_ptr()), float(input_scale),
+                                           float(output_scale), C.c_void_p(out.data_ptr()), C.c_void_p(stream or 0)))
+        if stream is None:
+            self.synchronize()
+        return out
+
+    def qat_lmhead_sample(self, x, packed_codes, row_scales, logits_scratch, configs: np.ndarray, layout: int = 0,
+                          input_scale: float = 0.0, output_scale: float = 0.0, histories=None, forced=None,
+                          mask_table=None) -> "SampleOutput":
+        """gs_qat_lmhead_sample: the int2 QAT head into `logits_scratch` ([rows][V] f32), then the
+        sampler on it, one call; returns the rows' results."""
+        b, keep = self.prepare(logits_scratch, configs, histories, forced, mask_table)
+        self.torch.cuda.current_stream(self.device).synchronize()
+        self._check(self.lib.gs_qat_lmhead_sample(self.ctx, C.c_void_p(x.data_ptr()), int(x.shape[1]),
+                                                  C.c_void_p(packed_codes.data_ptr()), int(layout),
+                                                  C.c_void_p(row_scales.data_ptr()), float(input_scale),
+                                                  float(output_scale), C.c_void_p(logits_scratch.data_ptr()),
+                                                  C.byref(b), None))
+        self.synchronize()
+        res = keep[-1].cpu().numpy().view(np.uint8).reshape(-1)[: b.rows * 16].view(RESULT_DTYPE)
+        del keep
+        return SampleOutput(res["token"].copy(), res["probability"].copy(), res["flags"].copy())
 
     def lmhead_sample_launch(self, hidden, weight, softcap_value: float, logits_scratch, batch: Batch,
                              stream: Optional[int] = None):

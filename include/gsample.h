@@ -266,6 +266,29 @@ int gs_lmhead(gs_context* ctx, const void* hidden, const void* weight, int32_t m
 int gs_lmhead_sample(gs_context* ctx, const void* hidden, const void* weight, int32_t width, float softcap,
                      float* logits_scratch, const gs_batch* batch, void* stream);
 
+/* int2 QAT LM head, the reference's own logits producer
+ * (src/webgpu/decode-lm-head.ts:262-340, weights src/model/gemma-output-weights.ts:72-81),
+ * as its CPU definition cpuQatLinear states it (src/reference/qat-linear.ts:78-148):
+ *   logits[m][v] = srq(row_scales[v] * sum_k (code[v][k] - 2) * srq(x[m][k], input_scale), output_scale)
+ * with srq(y, s) = y for s = 0, else clamp(rint(y / s), -128, 127) * s rounded to float
+ * (applySrq). x: f32 [m_rows][width]; packed_codes: 2-bit codes, code k of a row at bits
+ * 2k..2k+1 of word k / 16 (packInt2Rows), as GS_QAT_ROW_MAJOR ([V][width / 16] words, the
+ * checkpoint's lm_head.weight) or GS_QAT_BLOCK_MAJOR (4-word blocks [width / 64][V], the
+ * reference's GPU order); row_scales: f32 [V]; logits: f32 [m_rows][V]; all device memory,
+ * 16-byte aligned. width a multiple of 64, at most 4096. Each row's sum runs in column order in
+ * binary64, so the logits equal cpuQatLinear's bit for bit. */
+#define GS_QAT_ROW_MAJOR 0
+#define GS_QAT_BLOCK_MAJOR 1
+int gs_qat_lmhead(gs_context* ctx, const float* x, int32_t m_rows, int32_t width, const uint32_t* packed_codes,
+                  int32_t layout, const float* row_scales, float input_scale, float output_scale, float* logits,
+                  void* stream);
+
+/* gs_qat_lmhead followed by gs_sample on its output (batch->logits is ignored and replaced by
+ * `logits_scratch`, [batch->rows][V] f32 device memory; m_rows = batch->rows). */
+int gs_qat_lmhead_sample(gs_context* ctx, const float* x, int32_t width, const uint32_t* packed_codes,
+                         int32_t layout, const float* row_scales, float input_scale, float output_scale,
+                         float* logits_scratch, const gs_batch* batch, void* stream);
+
 /* Self-check of the bound the chunk scan's normaliser rests on; no
  * counterpart in the reference. Largest relative error of the hardware
  * binary32 exp2 (v_exp_f32, which the scan evaluates every term with) over
@@ -284,7 +307,7 @@ int gs_check_exp2(gs_context* ctx, float lo, float hi, double* max_rel_err, floa
  * those events, writes per stage the summed milliseconds
  * (stage_ms[GS_STAGE_COUNT]) and the number of calls that ran that stage
  * (calls[GS_STAGE_COUNT]), and stops timing. */
-#define GS_STAGE_LMHEAD 0 /* lmhead_kernel */
+#define GS_STAGE_LMHEAD 0 /* lmhead_kernel or qat_lmhead_kernel */
 #define GS_STAGE_SCAN 1   /* scan_kernel: the one HBM pass over the logits */
 #define GS_STAGE_FINISH 2 /* finish_kernel: per-row merge, filters and draw */
 #define GS_STAGE_EXACT 3  /* exact_kernel: replay of rows beyond the context's exact slots */

@@ -88,6 +88,17 @@ def lib():
                                         C.POINTER(C.c_uint32)]
         L.or_mask_logits.restype = None
         L.or_mask_logits.argtypes = [fp, C.c_int64, ip, C.c_int64, ip, C.c_int64, fp]
+        u32p = C.POINTER(C.c_uint32)
+        L.or_pack_int2_rows.restype = C.c_int
+        L.or_pack_int2_rows.argtypes = [u8p, C.c_int64, C.c_int64, u32p]
+        L.or_unpack_int2.restype = C.c_int
+        L.or_unpack_int2.argtypes = [u32p, C.c_int64]
+        L.or_apply_srq.restype = C.c_double
+        L.or_apply_srq.argtypes = [C.c_double, C.c_double]
+        L.or_qat_linear_int2.restype = None
+        L.or_qat_linear_int2.argtypes = [fp, u32p, fp, C.c_int64, C.c_int64, C.c_double, C.c_double, fp]
+        L.or_repack_block_major.restype = None
+        L.or_repack_block_major.argtypes = [u32p, C.c_int64, C.c_int64, u32p]
         _lib = L
     return _lib
 
@@ -202,3 +213,46 @@ def mask_logits(logits, legal, termination) -> np.ndarray:
 def mask_bits_to_ids(mask: np.ndarray, V: int) -> np.ndarray:
     bits = np.unpackbits(mask.view(np.uint8), bitorder="little")[:V]
     return np.nonzero(bits)[0].astype(np.int32)
+
+
+# ------------------------------------------------ int2 QAT linear (qat_ref.c)
+def pack_int2_rows(codes, out_features: int, in_features: int) -> np.ndarray:
+    """packInt2Rows (src/reference/qat-linear.ts:45-71); raises the reference's errors."""
+    if in_features % 16 != 0:
+        raise ValueError("Int2 input width must be divisible by 16")
+    c = np.ascontiguousarray(codes, dtype=np.uint8)
+    if c.size != out_features * in_features:
+        raise ValueError("Int2 code count does not match the matrix shape")
+    words = np.zeros(c.size // 16, dtype=np.uint32)
+    if lib().or_pack_int2_rows(_ptr(c, C.c_uint8), out_features, in_features, _ptr(words, C.c_uint32)) == -1:
+        raise ValueError("Int2 codes must be between 0 and 3")
+    return words
+
+
+def unpack_int2(words, index: int) -> int:
+    w = np.ascontiguousarray(words, dtype=np.uint32)
+    return int(lib().or_unpack_int2(_ptr(w, C.c_uint32), index))
+
+
+def apply_srq(value: float, scale: float) -> float:
+    return float(lib().or_apply_srq(value, scale))
+
+
+def qat_linear_int2(inputs, words, row_scales, in_features: int, out_features: int, input_scale: float = 0.0,
+                    output_scale: float = 0.0) -> np.ndarray:
+    """cpuQatLinear with bits 2 (src/reference/qat-linear.ts:78-116) over row-major words."""
+    x = np.ascontiguousarray(inputs, dtype=np.float32)
+    w = np.ascontiguousarray(words, dtype=np.uint32)
+    sc = np.ascontiguousarray(row_scales, dtype=np.float32)
+    assert x.size == in_features and sc.size == out_features and w.size * 16 == in_features * out_features
+    out = np.zeros(out_features, dtype=np.float32)
+    lib().or_qat_linear_int2(_ptr(x, C.c_float), _ptr(w, C.c_uint32), _ptr(sc, C.c_float), in_features, out_features,
+                             input_scale, output_scale, _ptr(out, C.c_float))
+    return out
+
+
+def repack_block_major(words, out_features: int, in_features: int) -> np.ndarray:
+    w = np.ascontiguousarray(words, dtype=np.uint32)
+    out = np.zeros_like(w)
+    lib().or_repack_block_major(_ptr(w, C.c_uint32), out_features, in_features, _ptr(out, C.c_uint32))
+    return out
