@@ -54,6 +54,7 @@ for _p in (ROOT, PKG):
 METRIC = "sampled rows/sec at vocab 262144, batch 256; achieved HBM GB/s (% of peak)"
 HBM_PEAK_GBPS = 8000.0       # MI355X HBM3E, AMD public specification
 BF16_PEAK_TFLOPS = 2500.0    # MI355X dense bf16 MFMA
+F64_VECTOR_PEAK_TFLOPS = 78.6  # MI355X fp64 (vector and matrix)
 V = 262144
 
 
@@ -86,7 +87,7 @@ def parse_args():
     ap.add_argument("--steps", type=int, default=100)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--workload", default="penalties",
-                    choices=["penalties", "single_row", "heavy_tail", "constrained", "lmhead", "multinomial",
+                    choices=["penalties", "single_row", "heavy_tail", "constrained", "lmhead", "qat", "multinomial",
                              "topk_deep", "typical"])
     ap.add_argument("--cpu-rows", type=int, default=128,
                     help="rows of the one-thread CPU baseline sample (about 13 s on one core)")
@@ -200,6 +201,32 @@ def build_workload(name, gs, torch, device):
                    desc=f"lmhead: H {M} x {D} bf16 ~ N(0,1), W {V} x {D} bf16 ~ N(0, 0.02^2), softcap 30, "
                         "256-id histories (window 256), DFA masks, topK 64, topP 0.95, T 1, seed = row")
         return out
+    if name == "qat":
+        # the reference's own producer: one decode row through the int2 QAT
+        # head (V x 1536 2-bit codes, block-major), then the sampler
+        M, D = 1, 1536
+        rng = np.random.default_rng(5)
+        n_words = V * D // 16
+        # three copies of the 96 MiB of codes (more than the 256 MB Infinity
+        # Cache), step i reading copy i mod 3
+        codes = [torch.from_numpy(rng.integers(0, 2 ** 32, n_words, dtype=np.uint64).astype(np.uint32)
+                                  .view(np.int32)).to(device) for _ in range(3)]
+        scales = torch.from_numpy((0.0008 + (np.arange(V) % 29) * 0.000025).astype(np.float32)).to(device)
+        x = torch.from_numpy(rng.normal(0, 1.5, (M, D)).astype(np.float32)).to(device)
+        cfg = gs.DecodingConfig(temperature=0.8, topK=40, topP=0.95)
+        s = gs.Sampler(vocab_size=V, max_rows=M)
+        conf = np.stack([rt.row_config(cfg, seed=42)])
+        scratch = torch.empty((M, V), dtype=torch.float32, device=device)
+        batch, keep = s.prepare(scratch, conf)
+        out.update(rows=M, sampler=s, batches=[(batch, keep)], dtype_in="f32", qat=(x, codes, scales),
+                   scratch=scratch, histories=None, states=None,
+                   lm_bytes=V * D // 4 + 4 * V + 4 * M * D, lm_logits_bytes=4 * M * V, lm_flops=2 * M * D * V,
+                   step_bytes=V * D // 4 + 4 * V + 4 * M * D + 8 * M * V + 16 * M, dominant="lmhead",
+                   kernel="qat_lmhead_kernel", config_obj=cfg,
+                   desc=(f"qat: 1 x {D} f32 activation ~ N(0, 1.5^2) through the int2 QAT head, {V} x {D} "
+                         "2-bit codes (block-major, 3 rotated copies), row scales 0.0008 + (r mod 29) 2.5e-5, "
+                         "output SRQ 0.125; then the sampler, T 0.8, topK 40, topP 0.95, seed 42"))
+        return out
     raise SystemExit(f"unknown workload {name}")
 
 
@@ -208,8 +235,18 @@ def launch_step(wl, i, stream):
     batch = wl["batches"][i % len(wl["batches"])][0]
     if wl["name"] == "lmhead":
         s.lmhead_sample_launch(wl["hidden"], wl["weight"], 30.0, wl["scratch"], batch, stream)
+    elif wl["name"] == "qat":
+        x, codes, scales = wl["qat"]
+        s.qat_lmhead_sample_launch(x, codes[i % len(codes)], scales, wl["scratch"], batch,
+                                   layout=gs_layout_block_major(), output_scale=0.125, stream=stream)
     else:
         s.launch(batch, stream)
+
+
+def gs_layout_block_major():
+    import gsample
+
+    return gsample.runtime.GS_QAT_BLOCK_MAJOR
 
 
 # -------------------------------------------------------------- CPU baseline
@@ -229,6 +266,8 @@ def cpu_inputs(wl):
 
         cfgs = [gsample.workloads.LMHEAD_CONFIG] * wl["rows"]
         return logits, "f32", cfgs, list(range(wl["rows"])), wl["histories"], wl["states"]
+    if wl["name"] == "qat":
+        return wl["scratch"].cpu().numpy(), "f32", [wl["config_obj"]] * wl["rows"], [42], None, None
     w = wl["workload"]
     return w.logits, wl["dtype_in"], w.configs, w.seeds, w.histories, (w.states if wl["name"] == "constrained"
                                                                        else None)
@@ -306,6 +345,8 @@ def cpu_baseline(wl, tokens, probs, n_rows, threads_cap):
         "legal-id walk (cached per state) + maskConstraintLogits + the sampler")
     if wl["name"] == "lmhead":
         what += " on the GPU-produced logits (no CPU bf16 GEMM exists in the reference)"
+    if wl["name"] == "qat":
+        what += " on the GPU-produced logits (the QAT head's CPU leg is timed in qat_cpu)"
     base = {"value": round(len(pick1) / r1["seconds"], 2), "unit": "rows/s", "cores": 1, "kind": "port",
             "sample": (f"{len(pick1)} of the {rows} rows (one in {step}), {r1['seconds']:.2f} s; JavaScript "
                        f"restatement of {what} on Node {r1['node']}, {r1['cpu_model']} ({r1['host_cpus']} host cpus)"),
@@ -314,6 +355,27 @@ def cpu_baseline(wl, tokens, probs, n_rows, threads_cap):
                                      f"(one per host core, at most {threads_cap}), {rn['seconds']:.2f} s")}}
     parity = {"rows_checked": checked, "token_mismatches": mism, "max_prob_rel_diff": rel}
     return base, parity
+
+
+def qat_cpu_leg(wl):
+    """The QAT head's CPU leg: the C restatement of cpuQatLinear (oracle/qat_ref.c,
+    one thread, binary64 as the reference's JavaScript) on the step's activation and
+    the codes copy the last timed step read, compared bit for bit with the GPU's
+    logits."""
+    from oracle import oracle
+
+    x, codes, scales = wl["qat"]
+    V, D = wl["scratch"].shape[1], x.shape[1]
+    bm = codes[0].cpu().numpy().view(np.uint32).reshape(D // 64, V, 4)
+    row_major = np.ascontiguousarray(bm.transpose(1, 0, 2)).reshape(-1)
+    t0 = time.time()
+    want = oracle.qat_linear_int2(x.cpu().numpy()[0], row_major, scales.cpu().numpy(), D, V, 0.0, 0.125)
+    sec = time.time() - t0
+    s = wl["sampler"]
+    got = s.qat_lmhead(x, codes[0], scales, layout=gs_layout_block_major(), output_scale=0.125).cpu().numpy()[0]
+    return {"value": round(1.0 / sec, 3), "unit": "rows/s", "cores": 1, "kind": "port",
+            "sample": f"1 row: cpuQatLinear restated in C (oracle/qat_ref.c), {sec:.2f} s",
+            "bit_exact_with_gpu": bool(np.array_equal(got.view(np.uint32), want.view(np.uint32)))}
 
 
 # ---------------------------------------------------------------------- main
@@ -377,6 +439,8 @@ def main():
     # results of the last step
     last = (2 * args.steps - 1) % n_rot
     res = wl["batches"][last][1][-1] if wl["name"] != "lmhead" else wl["batches"][0][1][-4]
+    if wl["name"] == "qat":
+        res = wl["batches"][0][1][-1]
     raw = res.cpu().numpy().view(np.uint8).reshape(-1)[: wl["rows"] * 16]
     rr = raw.view(gs.runtime.RESULT_DTYPE)
     tokens, probs, flags = rr["token"], rr["probability"], rr["flags"]
@@ -396,13 +460,19 @@ def main():
         algo = rows * wl["scan_bytes_per_row"]
         mfma_tflops = None
     achieved = algo / (dom_avg_ms * 1e6)
-    kname = {"scan": "scan_kernel", "lmhead": "lmhead_kernel"}[dom]
+    kname = wl.get("kernel") or {"scan": "scan_kernel", "lmhead": "lmhead_kernel"}[dom]
     roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                 "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": profiled_traffic(wl["name"], kname),
                 "kernel": kname, "algorithmic_bytes_per_launch": int(algo),
                 "kernel_avg_us": round(dom_avg_ms * 1000, 2),
                 "stage_avg_us": {k: round(v[0] / v[1] * 1000, 2) for k, v in stages.items() if v[1]},
                 "rotated_logits_buffers": n_rot}
+    if wl["name"] == "qat":
+        # binary64 fused multiply-adds on the vector units, not MFMA
+        roofline["f64_tflops"] = round(mfma_tflops, 2)
+        roofline["f64_frac_vector_peak"] = round(mfma_tflops / F64_VECTOR_PEAK_TFLOPS, 4)
+        roofline["logits_write_bytes"] = wl["lm_logits_bytes"]
+        mfma_tflops = None
     if mfma_tflops is not None:
         roofline["mfma_tflops"] = round(mfma_tflops, 1)
         roofline["mfma_frac_bf16_dense"] = round(mfma_tflops / BF16_PEAK_TFLOPS, 4)
@@ -432,6 +502,7 @@ def main():
     base, parity = (None, None)
     if not args.no_cpu:
         base, parity = cpu_baseline(wl, tokens, probs, args.cpu_rows, args.cpu_threads)
+    qat_cpu = qat_cpu_leg(wl) if wl["name"] == "qat" and not args.no_cpu else None
 
     line = {
         "metric": METRIC, "value": round(value, 1), "unit": "rows/s", "n_gpus": 1, "steps": args.steps,
@@ -448,6 +519,8 @@ def main():
     }
     if parity is not None:
         line["parity_sample"] = parity
+    if qat_cpu is not None:
+        line["qat_cpu"] = qat_cpu
     s.synchronize()
     print(json.dumps(line), flush=True)
     s.close()

@@ -481,6 +481,17 @@ class Sampler:
         del keep
         return SampleOutput(res["token"].copy(), res["probability"].copy(), res["flags"].copy())
 
+    def qat_lmhead_sample_launch(self, x, packed_codes, row_scales, logits_scratch, batch: Batch, layout: int = 0,
+                                 input_scale: float = 0.0, output_scale: float = 0.0, stream: Optional[int] = None):
+        """gs_qat_lmhead_sample on `stream`: the int2 QAT head into `logits_scratch`, then the sampler."""
+        if stream is None:
+            self.torch.cuda.current_stream(self.device).synchronize()
+        self._check(self.lib.gs_qat_lmhead_sample(self.ctx, C.c_void_p(x.data_ptr()), int(x.shape[1]),
+                                                  C.c_void_p(packed_codes.data_ptr()), int(layout),
+                                                  C.c_void_p(row_scales.data_ptr()), float(input_scale),
+                                                  float(output_scale), C.c_void_p(logits_scratch.data_ptr()),
+                                                  C.byref(batch), C.c_void_p(stream or 0)))
+
     def lmhead_sample_launch(self, hidden, weight, softcap_value: float, logits_scratch, batch: Batch,
                              stream: Optional[int] = None):
         """gs_lmhead_sample: lm_head into `logits_scratch`, then the sampler on it."""
