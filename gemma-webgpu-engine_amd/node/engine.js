@@ -306,6 +306,33 @@ class Engine {
     return logits;
   }
 
+  /* The int2 QAT head (the reference's producer, cpuQatLinear bit for bit):
+   * logits[m][v] = srq(rowScales[v] * sum_k (code[v][k] - 2) * srq(x[m][k], inputScale), outputScale).
+   * x: f32 [mRows][width], codes: 2-bit codes as u32 words, layout "row-major" ([vocabSize][width/16],
+   * the checkpoint's) or "block-major" ([width/64][vocabSize][4]), rowScales: f32 [vocabSize]; all
+   * DeviceBuffers. */
+  qatLmhead(x, mRows, width, codes, layout, rowScales, inputScale, outputScale, logits) {
+    if (!Number.isInteger(mRows) || mRows <= 0 || !Number.isInteger(width) || width <= 0) {
+      throw new RangeError("mRows and width must be positive integers");
+    }
+    if (x.bytes < 4 * mRows * width || codes.bytes < this.vocabSize * width / 4 || rowScales.bytes < 4 * this.vocabSize ||
+        logits.bytes < 4 * mRows * this.vocabSize) {
+      throw new RangeError("QAT head buffers are smaller than [mRows][width] f32, vocabSize x width 2-bit codes, " +
+        "[vocabSize] f32 and [mRows][vocabSize] f32");
+    }
+    const code = layout === "block-major" ? 1 : layout === "row-major" || layout === undefined ? 0 : -1;
+    if (code < 0) throw new RangeError("layout must be \"row-major\" or \"block-major\"");
+    native().qatLmhead(this.context(), x.handle, mRows, width, codes.handle, code, rowScales.handle,
+      inputScale || 0, outputScale || 0, logits.handle);
+    return logits;
+  }
+
+  /* the QAT head into `scratch` (f32 [rows][vocabSize]), then sampleRows on it. */
+  qatLmheadSample(x, width, codes, layout, rowScales, inputScale, outputScale, scratch, request) {
+    this.qatLmhead(x, request.rows, width, codes, layout, rowScales, inputScale, outputScale, scratch);
+    return this.sampleRows(Object.assign({}, request, { logits: scratch, dtype: "f32", rowStride: this.vocabSize }));
+  }
+
   /* lm_head into `scratch` (f32 [rows][vocabSize]), then sampleRows on it. */
   lmheadSample(hidden, weight, width, softcap, scratch, request) {
     this.lmhead(hidden, weight, request.rows, width, softcap, scratch);

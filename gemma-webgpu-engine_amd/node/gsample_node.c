@@ -594,6 +594,27 @@ static napi_value js_lmhead(napi_env env, napi_callback_info info) {
   return NULL;
 }
 
+/* qatLmhead(ctx, x, mRows, width, codes, layout, rowScales, inputScale, outputScale, logits) -- device
+ * Externals: the int2 QAT head (gs_qat_lmhead) */
+static napi_value js_qat_lmhead(napi_env env, napi_callback_info info) {
+  ARGS(10);
+  CTX_ARG(0);
+  void* x = argc > 1 ? get_ptr(env, argv[1]) : NULL;
+  void* codes = argc > 4 ? get_ptr(env, argv[4]) : NULL;
+  void* scales = argc > 6 ? get_ptr(env, argv[6]) : NULL;
+  void* out = argc > 9 ? get_ptr(env, argv[9]) : NULL;
+  int32_t m, width, layout;
+  double in_scale, out_scale;
+  if (!x || !codes || !scales || !out || !get_i32(env, argv[2], &m) || !get_i32(env, argv[3], &width) ||
+      !get_i32(env, argv[5], &layout) || !get_f64(env, argv[7], &in_scale) || !get_f64(env, argv[8], &out_scale))
+    return throw_error(env, "GS_ERR_INVALID_ARGUMENT",
+                       "qatLmhead(ctx, x, mRows, width, codes, layout, rowScales, inputScale, outputScale, logits)");
+  GS_CALL(ctx, gs_qat_lmhead(ctx, (const float*)x, m, width, (const uint32_t*)codes, layout, (const float*)scales,
+                             (float)in_scale, (float)out_scale, (float*)out, NULL));
+  GS_CALL(ctx, gs_synchronize(ctx));
+  return NULL;
+}
+
 /* ---- timing ---------------------------------------------------------------- */
 
 static napi_value js_timing_begin(napi_env env, napi_callback_info info) {
@@ -655,6 +676,7 @@ static napi_value init(napi_env env, napi_value exports) {
       {"dfaAdvanceBytes", js_dfa_advance_bytes},
       {"dfaAccepting", js_dfa_accepting},
       {"lmhead", js_lmhead},
+      {"qatLmhead", js_qat_lmhead},
       {"timingBegin", js_timing_begin},
       {"timingEnd", js_timing_end},
   };

@@ -154,6 +154,11 @@ export class Engine {
   dfaAccepting(state: number): boolean;
   lmhead(hidden: DeviceBuffer, weight: DeviceBuffer, mRows: number, width: number, softcap: number,
          logits: DeviceBuffer): DeviceBuffer;
+  qatLmhead(x: DeviceBuffer, mRows: number, width: number, codes: DeviceBuffer, layout: "row-major" | "block-major",
+            rowScales: DeviceBuffer, inputScale: number, outputScale: number, logits: DeviceBuffer): DeviceBuffer;
+  qatLmheadSample(x: DeviceBuffer, width: number, codes: DeviceBuffer, layout: "row-major" | "block-major",
+                  rowScales: DeviceBuffer, inputScale: number, outputScale: number, scratch: DeviceBuffer,
+                  request: SampleRequest): SampleResult;
   lmheadSample(hidden: DeviceBuffer, weight: DeviceBuffer, width: number, softcap: number, scratch: DeviceBuffer,
                request: SampleRequest): SampleResult;
   timingBegin(maxCalls: number): void;

@@ -17,7 +17,7 @@ const ADDON_FUNCTIONS = [
   "abiVersion", "deviceCount", "seededRandom", "jsExp", "jsLog", "softcap", "layouts", "validateConfigs",
   "create", "destroy", "synchronize", "deviceAlloc", "deviceFree", "copyToDevice", "copyToHost", "sampleHost",
   "tokenLogProbHost", "maskLogitsHost", "setVocab", "setDfa", "buildMasks", "legalTokenIds", "dfaAdvance",
-  "dfaAdvanceBytes", "dfaAccepting", "lmhead", "timingBegin", "timingEnd",
+  "dfaAdvanceBytes", "dfaAccepting", "lmhead", "qatLmhead", "timingBegin", "timingEnd",
 ];
 
 test("addon loads and exports every entry point", () => {

@@ -473,5 +473,93 @@ test("lm_head through device buffers feeds the sampler", () => {
   }
 });
 
+/* row-major words ([V][D/16]) to the block-major order ([D/64][V][4]) */
+function blockMajor(words, V, D) {
+  const blocks = D / 64;
+  const out = new Uint32Array(words.length);
+  for (let r = 0; r < V; r += 1) {
+    for (let b = 0; b < blocks; b += 1) {
+      for (let j = 0; j < 4; j += 1) out[(b * V + r) * 4 + j] = words[r * (D / 16) + b * 4 + j];
+    }
+  }
+  return out;
+}
+
+test("int2 QAT head: the reference's known answer (qat-linear-gpu.spec.ts:1307-1397)", () => {
+  const V = 8, W = 1536;
+  const engine = new g.Engine({ vocabSize: V, maxRows: 1 });
+  try {
+    const words = new Uint32Array(V * W / 16).fill(0xAAAAAAAA);
+    words.fill(0xFFFFFFFF, 96, 192);
+    words.fill(0x55555555, 192, 288);
+    const x = engine.allocate(4 * W).write(new Float32Array(W).fill(1));
+    const scales = engine.allocate(4 * V).write(new Float32Array([1, 0.5, 0.25, 1, 1, 1, 1, 1]));
+    const out = engine.allocate(4 * V);
+    for (const [layout, w] of [["row-major", words], ["block-major", blockMajor(words, V, W)]]) {
+      const codes = engine.allocate(w.byteLength).write(w);
+      engine.qatLmhead(x, 1, W, codes, layout, scales, 0, 0, out);
+      assert.deepStrictEqual(Array.from(out.read(new Float32Array(V))), [0, 768, -384, 0, 0, 0, 0, 0], layout);
+      codes.free();
+    }
+    [x, scales, out].forEach((b) => b.free());
+  } finally {
+    engine.destroy();
+  }
+});
+
+test("int2 QAT head: random codes bit-exact, fused into the sampler", () => {
+  const M = 3, W = 256, V = 8192, inScale = Math.fround(0.03), outScale = Math.fround(0.02);
+  const engine = new g.Engine({ vocabSize: V, maxRows: M });
+  try {
+    const rng = new oracle.SeededRandom(77);
+    const words = new Uint32Array(V * W / 16);
+    for (let i = 0; i < words.length; i += 1) words[i] = Math.floor(rng.next() * 4294967296) >>> 0;
+    const rowScales = new Float32Array(V);
+    for (let r = 0; r < V; r += 1) rowScales[r] = 0.05 + (r % 29) * 0.004;
+    const xf = normalRow(78, M * W, 1.5);
+    // cpuQatLinear (qat-linear.ts:78-148): binary64 sum over k in order, SRQ
+    // with ties to even, stored as float
+    const srq = (v, s) => {
+      if (s === 0) return v;
+      const t = v / s;
+      const f = Math.floor(t);
+      let q = t - f > 0.5 || (t - f === 0.5 && f % 2 !== 0) ? f + 1 : f;
+      q = Math.min(127, Math.max(-128, q)) + 0;
+      return Math.fround(q * s);
+    };
+    const want = new Float32Array(M * V);
+    for (let m = 0; m < M; m += 1) {
+      const act = Array.from({ length: W }, (_, k) => srq(xf[m * W + k], inScale));
+      for (let r = 0; r < V; r += 1) {
+        let dot = 0;
+        for (let k = 0; k < W; k += 1) dot += (((words[r * (W / 16) + (k >> 4)] >>> (2 * (k & 15))) & 3) - 2) * act[k];
+        want[m * V + r] = srq(dot * rowScales[r], outScale);
+      }
+    }
+    const x = engine.allocate(4 * M * W).write(xf);
+    const scales = engine.allocate(4 * V).write(rowScales);
+    const scratch = engine.allocate(4 * M * V);
+    const configs = Array.from({ length: M }, (_, r) => Object.assign({}, D, { temperature: 0.8, topK: 40, topP: 0.95, seed: 5 + r }));
+    for (const [layout, w] of [["row-major", words], ["block-major", blockMajor(words, V, W)]]) {
+      const codes = engine.allocate(w.byteLength).write(w);
+      const out = engine.qatLmheadSample(x, W, codes, layout, scales, inScale, outScale, scratch,
+        { rows: M, configs, histories: null });
+      const got = scratch.read(new Float32Array(M * V));
+      for (let i = 0; i < M * V; i += 1) {
+        if (!Object.is(got[i], want[i])) assert.fail(layout + " logit " + i + ": " + got[i] + " vs " + want[i]);
+      }
+      for (let m = 0; m < M; m += 1) {
+        const ro = new oracle.SeededRandom(configs[m].seed);
+        const s = oracle.sampleWithProbability(want.subarray(m * V, (m + 1) * V), [], configs[m], () => ro.next());
+        assert.strictEqual(out.tokens[m], s.token, layout + " row " + m);
+      }
+      codes.free();
+    }
+    [x, scales, scratch].forEach((b) => b.free());
+  } finally {
+    engine.destroy();
+  }
+});
+
 run();
 g.releaseEngines();

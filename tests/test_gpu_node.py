@@ -10,7 +10,7 @@ pytestmark = pytest.mark.gpu
 
 def test_node_host_parity_on_gpu():
     out = run_node_tests("gpu_parity.js", 280)
-    assert "all 11 passed" in out
+    assert "all 13 passed" in out
 
 
 def test_node_decode_loop_on_gpu():
