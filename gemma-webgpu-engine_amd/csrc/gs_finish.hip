@@ -292,6 +292,74 @@ __device__ __forceinline__ int top_select_shift(uint32_t lo, uint32_t hi) {
   return shift;
 }
 
+// Appends thread-held entries (valid bits) with key >= floor_key to out[] at
+// positions counted in sel[3] (one LDS atomic per wave); positions past 128
+// are counted, not stored.
+template <int kE>
+__device__ __forceinline__ void compact_entries(const uint64_t (&e)[kE], uint32_t valid, uint32_t floor_key,
+                                                uint32_t* sel, uint64_t* out) {
+  const int lane = threadIdx.x & 63;
+  constexpr int kOut = 128;
+#pragma unroll
+  for (int q = 0; q < kE; ++q) {
+    const bool keep = ((valid >> q) & 1u) && entry_key(e[q]) >= floor_key;
+    const uint64_t m = __ballot(keep);
+    uint32_t base = 0;
+    if (lane == 0 && m) base = atomicAdd(&sel[3], (uint32_t)__popcll(m));
+    base = readlane_u32(base, 0);
+    if (keep) {
+      const uint32_t pos =
+          base + __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
+      if (pos < (uint32_t)kOut) out[pos] = e[q];
+    }
+  }
+}
+
+// The kTopR largest of the n_src (<= 128) distinct entries in src, descending
+// into top[0..kTopR) and zero-padded. Ends with a barrier.
+__device__ __forceinline__ void rank_survivors(const uint64_t* src, int n_src, uint64_t* top) {
+  const int tid = threadIdx.x;
+  // rank the survivors (at most 128) by counting: the entries are distinct,
+  // so survivor i's place is the number of survivors above it. Eight threads
+  // share survivor tid / 8, each counting over 16 of the survivors (out holds
+  // at least 128 entries), and the eight counts meet by DPP; places past the
+  // survivors stay zero.
+  {
+    const int i = tid >> 3, part = tid & 7;
+    uint64_t ei = 0;
+    uint32_t cnt = 0;
+    if (i < n_src) {
+      ei = src[i];
+      const uint4* p = (const uint4*)(src + part * 16);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const uint4 w = p[j];
+        const int k = part * 16 + 2 * j;
+        const uint64_t x0 = ((uint64_t)w.y << 32) | w.x, x1 = ((uint64_t)w.w << 32) | w.z;
+        cnt += (k < n_src && x0 > ei) ? 1u : 0u;
+        cnt += (k + 1 < n_src && x1 > ei) ? 1u : 0u;
+      }
+    }
+    cnt += dpp_u32<kDppQuad1032, 0xF>(0u, cnt);
+    cnt += dpp_u32<kDppQuad2301, 0xF>(0u, cnt);
+    cnt += dpp_u32<kDppRowHalfMirror, 0xF>(0u, cnt);  // lane l of 8 meets lane 7 - l: the other quad
+    if (part == 0 && i < n_src && cnt < (uint32_t)kTopR) top[cnt] = ei;
+    if (tid >= n_src && tid < kTopR) top[tid] = 0;
+  }
+  __syncthreads();
+}
+
+// The selection over entries the threads hold in registers, given a floor
+// with at least kTopR valid entries at or above it (top_floor): those entries
+// are compacted straight away and, when at most 128, ranked without a
+// histogram; more run the histogram selection among themselves. *n_out
+// counts every valid entry, as top_select_regs does with n = -1; sel[3] is
+// zero on entry. Ends with a barrier.
+template <int kE>
+__device__ __forceinline__ bool top_select_regs_floor(const uint64_t (&e)[kE], uint32_t valid, uint32_t top_floor,
+                                                      uint32_t hi, uint32_t* hist, uint32_t* sel, uint64_t* out,
+                                                      uint64_t* top, uint32_t* n_out);
+
 // The selection over entries the threads hold in registers: thread t's e[q]
 // is an entry when bit q of `valid` is set. n (block-uniform) counts them, or
 // is -1: then the first histogram pass also counts them into *n_out (zero on
@@ -362,51 +430,33 @@ __device__ __forceinline__ bool top_select_regs(const uint64_t (&e)[kE], uint32_
   // compact the survivors into out[] (one LDS atomic per wave)
   if (tid == 0) sel[3] = 0;
   __syncthreads();
+  compact_entries<kE>(e, valid, floor_key, sel, out);
+  __syncthreads();
+  rank_survivors(out, (int)(sel[3] < (uint32_t)kOut ? sel[3] : (uint32_t)kOut), top);
+  return true;
+}
+
+template <int kE>
+__device__ __forceinline__ bool top_select_regs_floor(const uint64_t (&e)[kE], uint32_t valid, uint32_t top_floor,
+                                                      uint32_t hi, uint32_t* hist, uint32_t* sel, uint64_t* out,
+                                                      uint64_t* top, uint32_t* n_out) {
+  const int lane = threadIdx.x & 63;
+  constexpr int kOut = 128;
+  const uint32_t w = wave_sum_u32((uint32_t)__popc(valid));
+  if (lane == 0 && w) atomicAdd(n_out, w);
+  compact_entries<kE>(e, valid, top_floor, sel, out);
+  __syncthreads();
+  const uint32_t n_top = sel[3];
+  if (n_top <= (uint32_t)kOut) {
+    rank_survivors(out, (int)n_top, top);
+    return true;
+  }
+  uint32_t vtop = 0;
 #pragma unroll
   for (int q = 0; q < kE; ++q) {
-    const bool keep = ((valid >> q) & 1u) && entry_key(e[q]) >= floor_key;
-    const uint64_t m = __ballot(keep);
-    uint32_t base = 0;
-    if (lane == 0 && m) base = atomicAdd(&sel[3], (uint32_t)__popcll(m));
-    base = readlane_u32(base, 0);
-    if (keep) {
-      const uint32_t pos =
-          base + __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
-      if (pos < (uint32_t)kOut) out[pos] = e[q];
-    }
+    if (((valid >> q) & 1u) && entry_key(e[q]) >= top_floor) vtop |= 1u << q;
   }
-  __syncthreads();
-  const uint64_t* src = out;
-  const int n_src = (int)(sel[3] < (uint32_t)kOut ? sel[3] : (uint32_t)kOut);
-  // rank the survivors (at most 128) by counting: the entries are distinct,
-  // so survivor i's place is the number of survivors above it. Eight threads
-  // share survivor tid / 8, each counting over 16 of the survivors (out holds
-  // at least 128 entries), and the eight counts meet by DPP; places past the
-  // survivors stay zero.
-  {
-    const int i = tid >> 3, part = tid & 7;
-    uint64_t ei = 0;
-    uint32_t cnt = 0;
-    if (i < n_src) {
-      ei = src[i];
-      const uint4* p = (const uint4*)(src + part * 16);
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const uint4 w = p[j];
-        const int k = part * 16 + 2 * j;
-        const uint64_t x0 = ((uint64_t)w.y << 32) | w.x, x1 = ((uint64_t)w.w << 32) | w.z;
-        cnt += (k < n_src && x0 > ei) ? 1u : 0u;
-        cnt += (k + 1 < n_src && x1 > ei) ? 1u : 0u;
-      }
-    }
-    cnt += dpp_u32<kDppQuad1032, 0xF>(0u, cnt);
-    cnt += dpp_u32<kDppQuad2301, 0xF>(0u, cnt);
-    cnt += dpp_u32<kDppRowHalfMirror, 0xF>(0u, cnt);  // lane l of 8 meets lane 7 - l: the other quad
-    if (part == 0 && i < n_src && cnt < (uint32_t)kTopR) top[cnt] = ei;
-    if (tid >= n_src && tid < kTopR) top[tid] = 0;
-  }
-  __syncthreads();
-  return true;
+  return top_select_regs<kE>(e, vtop, (int)n_top, top_floor, hi, hist, sel, out, top, nullptr);
 }
 
 // The selection over the region s[0..n) in LDS (n <= kFinishCap).
@@ -474,6 +524,9 @@ struct Shared {
   uint32_t max_key;
   uint32_t thr_max;
   uint32_t any_truncated;
+  // per wave holding chunk statistics: a key with at least kTopR / (those
+  // waves) of its wave maxima at or above it (0: none)
+  uint32_t top_floor[kFinishThreads / 64];
   uint32_t n_sorted;
   uint32_t n_special;
   uint32_t n_sp_in;
@@ -973,6 +1026,7 @@ __device__ __forceinline__ uint32_t finish_row(const SampleArgs& a, FinishLds& U
 
   if (tid == 0) {
     S.flags = 0; S.max_key = 0; S.thr_max = 0; S.any_truncated = 0; S.n_sorted = 0; S.n_special = 0;
+    S.sel[3] = 0;
     S.n_sp_in = 0; S.route_exact = 0; S.status_flags = 0; S.first_idx = 0xFFFFFFFFu; S.legal_bits = 0;
     S.special_legal = 0; S.best_entry = 0; S.sp_max = 0; S.fast_done = 0;
   }
@@ -995,6 +1049,20 @@ __device__ __forceinline__ uint32_t finish_row(const SampleArgs& a, FinishLds& U
       if (fl) atomicOr(&S.flags, fl);
       if (mk) atomicMax(&S.max_key, mk);
       if (tr) { atomicMax(&S.thr_max, th); atomicOr(&S.any_truncated, 1u); }
+    }
+    // A floor for the fast path's top kTopR: each wave holding statistics
+    // takes the d-th largest of its wave maxima (d = kTopR / those waves,
+    // rounded up), so the smallest of these floors has at least kTopR wave
+    // maxima -- distinct non-special logits -- at or above it.
+    const int n_sw = (n_wstats + 63) / 64;
+    if (wave < n_sw) {
+      const uint32_t d = (uint32_t)((kTopR + n_sw - 1) / n_sw);
+      const uint32_t key = has_w && w_max > kKeyNegInf ? w_max : 0u;
+      uint32_t khi, klo;
+      wave_max_min_u32(key, &khi, &klo);
+      const uint32_t live = (uint32_t)__popcll(__ballot(key != 0u));
+      const uint32_t f = live >= d ? wave_kth_key(key, d, klo, khi) : 0u;
+      if (lane == 0) S.top_floor[wave] = f;
     }
   }
   // the owned specials' logits and mask words start loading now; they are
@@ -1192,8 +1260,15 @@ __device__ __forceinline__ uint32_t finish_row(const SampleArgs& a, FinishLds& U
           if (entry_key(e[q]) >= thr) valid |= 1u << q;
         }
       }
-      top_ok = top_select_regs<kSpecQ>(e, valid, -1, sel_lo, sel_hi, S.hist, S.sel, (uint64_t*)S.cand_p, S.top,
-                                       &S.n_sorted);
+      // the tightest floor the wave maxima give (every stats wave found one)
+      uint32_t tfl = 0xFFFFFFFFu;
+      for (int w = 0; w < (n_wstats + 63) / 64; ++w) tfl = S.top_floor[w] < tfl ? S.top_floor[w] : tfl;
+      if (tfl > sel_lo && tfl != 0xFFFFFFFFu)
+        top_ok = top_select_regs_floor<kSpecQ>(e, valid, tfl, sel_hi, S.hist, S.sel, (uint64_t*)S.cand_p, S.top,
+                                               &S.n_sorted);
+      else
+        top_ok = top_select_regs<kSpecQ>(e, valid, -1, sel_lo, sel_hi, S.hist, S.sel, (uint64_t*)S.cand_p, S.top,
+                                         &S.n_sorted);
       n_region = (int)S.n_sorted;
     } else {
       fill_region();

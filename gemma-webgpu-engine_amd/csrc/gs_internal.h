@@ -319,6 +319,25 @@ __device__ __forceinline__ double wave_sum_f64_dpp(double v) {
 #undef GS_SUM_STEP
   return readlane_f64(v, 63);
 }
+// A lower bound t of the d-th largest of the wave's lane keys (d >= 1), at
+// most 2^14 below it: the largest t whose low 14 bits are zero with at least
+// d keys >= t, found bit by bit with ballots. Bits above the first one where
+// the smallest and largest keys differ are common to every key and to the
+// answer, so the search starts below them. (For binary32 keys 2^14 units are
+// 2^-9 relative: a threshold that low admits a few more list entries.)
+__device__ __forceinline__ uint32_t wave_kth_key(uint32_t key, uint32_t d, uint32_t lo, uint32_t hi) {
+  constexpr int kFloorBit = 14;
+  const uint32_t diff = lo ^ hi;
+  if (diff >> kFloorBit == 0) return lo & ~((1u << kFloorBit) - 1u);
+  const int top = 31 - __builtin_clz(diff);
+  uint32_t t = lo & ~((2u << top) - 1u);  // the common prefix; every key is >= it
+  for (int b = top; b >= kFloorBit; --b) {
+    const uint32_t c = t | (1u << b);
+    if ((uint32_t)__popcll(__ballot(key >= c)) >= d) t = c;
+  }
+  return t;
+}
+
 // Inclusive prefix sums across the wave: within each row of 16 lanes by
 // row_shr 1, 2, 4, 8 (lanes without a source add zero), then the last lane
 // of row 0 into rows 1 and 3 and the last lane of row 1 into rows 2 and 3.

@@ -89,25 +89,6 @@ struct VecTraits<uint16_t> {
 
 __device__ __noinline__ float capped(float x, double cap) { return gsm::softcap_f32(x, cap); }
 
-// A lower bound t of the d-th largest of the wave's lane keys (d >= 1), at
-// most 2^14 below it: the largest t whose low 14 bits are zero with at least
-// d keys >= t, found bit by bit with ballots. Bits above the first one where
-// the smallest and largest keys differ are common to every key and to the
-// answer, so the search starts below them. (For binary32 keys 2^14 units are
-// 2^-9 relative: a threshold that low admits a few more list entries.)
-__device__ __forceinline__ uint32_t wave_kth_key(uint32_t key, uint32_t d, uint32_t lo, uint32_t hi) {
-  constexpr int kFloorBit = 14;
-  const uint32_t diff = lo ^ hi;
-  if (diff >> kFloorBit == 0) return lo & ~((1u << kFloorBit) - 1u);
-  const int top = 31 - __builtin_clz(diff);
-  uint32_t t = lo & ~((2u << top) - 1u);  // the common prefix; every key is >= it
-  for (int b = top; b >= kFloorBit; --b) {
-    const uint32_t c = t | (1u << b);
-    if ((uint32_t)__popcll(__ballot(key >= c)) >= d) t = c;
-  }
-  return t;
-}
-
 // Per-wave results of a group's first chunk, exchanged through LDS.
 struct WaveSlots {
   uint32_t wbad[kScanWaves];
@@ -343,7 +324,9 @@ __device__ __forceinline__ uint32_t chunk_stats(const SampleArgs& a, const gs_ro
   bool selected = true;
   if (!stream) {
     const uint32_t depth = (uint32_t)plan.depth;
-    const uint32_t dw = (depth + 3u) / 4u + 2u;
+    // per wave: a quarter of the depth; top-p rows take two more each, which
+    // lowers tau a little, so that the fast path's top 64 rarely lies below it
+    const uint32_t dw = (depth + 3u) / 4u + (plan.route == kRouteTopK ? 0u : 2u);
     const uint32_t wl = (uint32_t)__popcll(__ballot(mykey != 0u));
     const uint32_t wt = wl >= dw ? wave_kth_key(mykey, dw, wlo, wm) : 0u;
     if (lane == 0) {
