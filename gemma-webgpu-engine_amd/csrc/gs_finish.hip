@@ -839,6 +839,53 @@ __device__ __forceinline__ int filters_and_draw_wave(const SampleArgs& a, int64_
   return 0;
 }
 
+// Calls visit(l, id) for every logit l of the row (soft-capped when cap > 0),
+// the whole block over it: kB 16-byte loads per thread go out before any is
+// used. Capped rows take a plain loop with the cap's call, so that the
+// unrolled loop stays small.
+template <int kB, typename F>
+__device__ __forceinline__ void visit_row(const SampleArgs& a, int64_t row, double cap, F&& visit) {
+  const int tid = threadIdx.x;
+  const int64_t V = a.vocab;
+  int64_t from = 0;
+  if (cap > 0) {
+    from = V;
+#pragma unroll 1
+    for (int64_t i = tid; i < V; i += kFinishThreads) visit(softcap_call(load_logit(a, row, i), cap), (uint32_t)i);
+  } else if (a.vector_ok) {
+    const bool bf16 = a.dtype == GS_BF16;
+    const int per = bf16 ? 8 : 4;
+    const int64_t n_vec = V / per;
+    const uint4* base = (const uint4*)((const char*)a.logits + row * a.row_stride * (bf16 ? 2 : 4));
+    for (int64_t v0 = tid; v0 < n_vec; v0 += (int64_t)kB * kFinishThreads) {
+      uint4 w[kB];
+#pragma unroll
+      for (int k = 0; k < kB; ++k) {
+        const int64_t vi = v0 + (int64_t)k * kFinishThreads;
+        w[k] = vi < n_vec ? base[vi] : make_uint4(0u, 0u, 0u, 0u);
+      }
+#pragma unroll
+      for (int k = 0; k < kB; ++k) {
+        const int64_t vi = v0 + (int64_t)k * kFinishThreads;
+        if (vi >= n_vec) break;
+        const uint32_t q[4] = {w[k].x, w[k].y, w[k].z, w[k].w};
+        const uint32_t id0 = (uint32_t)(vi * per);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          if (bf16) {
+            visit(__builtin_bit_cast(float, q[j] << 16), id0 + 2 * j);
+            visit(__builtin_bit_cast(float, q[j] & 0xFFFF0000u), id0 + 2 * j + 1);
+          } else {
+            visit(__builtin_bit_cast(float, q[j]), id0 + j);
+          }
+        }
+      }
+    }
+    from = n_vec * per;
+  }
+  for (int64_t i = from + tid; i < V; i += kFinishThreads) visit(load_logit(a, row, i), (uint32_t)i);
+}
+
 // The normaliser's non-special part from scratch in binary64
 // (sampling.ts:36-41): the sum over the row's allowed logits l (mask bit set,
 // or every id of an unconstrained row) of e^(l/T - M) by the table
@@ -846,10 +893,11 @@ __device__ __forceinline__ int filters_and_draw_wave(const SampleArgs& a, int64_
 // allowed special ids, which the normaliser counts with their penalised
 // values instead. Identical terms cancel exactly, so the difference keeps the
 // sum's accuracy while the specials hold at most half of it; otherwise, or
-// when a sum overflows, it returns -1. The whole block calls it.
+// when a sum overflows, it returns -1. tab: the exponential's table in LDS.
+// The whole block calls it.
 __device__ double recompute_nonspecial_sum(const SampleArgs& a, int64_t row, const gs_row_config& cfg,
                                            bool constrained, double M, int n_sp, const uint32_t* sp_id,
-                                           double* s_w) {
+                                           double* s_w, const double* tab) {
   const int tid = threadIdx.x;
   const double T = cfg.temperature;
   const uint32_t* mrow = constrained ? a.mask_table + (int64_t)cfg.mask_slot * a.mask_words : nullptr;
@@ -857,13 +905,16 @@ __device__ double recompute_nonspecial_sum(const SampleArgs& a, int64_t row, con
   // rounding move y by about 2^-52 |l| 256 log2(e) / T, 1e-14 relative on a
   // term, far inside the table exponential's error
   const double yA = (1.0 / T) * GS_256_LOG2E, yB = -M * GS_256_LOG2E;
-  auto term = [&](float l) -> double {
-    if (cfg.softcap > 0) l = softcap_call(l, cfg.softcap);
+  auto term_of_capped = [&](float l) -> double {
     const double y = __builtin_fma((double)l, yA, yB);
     // evaluated for every y (no branch), so that independent terms overlap;
     // exp2_256 reads its table at an index masked to 0..255 for any y
-    const double e = exp2_256(y, c_exp2_256);
+    const double e = exp2_256(y, tab);
     return y > kSkipY ? e : 0.0;
+  };
+  auto term = [&](float l) -> double {
+    if (cfg.softcap > 0) l = softcap_call(l, cfg.softcap);
+    return term_of_capped(l);
   };
   double all = 0.0, sp = 0.0;
   const int64_t V = a.vocab;
@@ -903,26 +954,9 @@ __device__ double recompute_nonspecial_sum(const SampleArgs& a, int64_t row, con
       }
     }
   }
-  // unconstrained rows: every id. The loads of kBatch elements go out
-  // together (one memory round trip per batch, not per element) and their
-  // terms overlap; the sum keeps each thread's order
-  constexpr int kBatch = 4;
-  for (int64_t i0 = mrow ? V : tid; i0 < V; i0 += (int64_t)kBatch * kFinishThreads) {
-    float l[kBatch];
-    bool ok[kBatch];
-#pragma unroll
-    for (int k = 0; k < kBatch; ++k) {
-      const int64_t i = i0 + (int64_t)k * kFinishThreads;
-      const int64_t ic = i < V ? i : V - 1;  // in bounds; dropped below
-      l[k] = load_logit(a, row, ic);
-      ok[k] = i < V;
-    }
-    double t[kBatch];
-#pragma unroll
-    for (int k = 0; k < kBatch; ++k) t[k] = term(l[k]);
-#pragma unroll
-    for (int k = 0; k < kBatch; ++k) all += ok[k] ? t[k] : 0.0;
-  }
+  // unconstrained rows: every id, four 16-byte loads per thread in flight
+  // (visit_row); the sum keeps each thread's order
+  if (!mrow) visit_row<4>(a, row, cfg.softcap, [&](float l, uint32_t) { all += term_of_capped(l); });
   for (int i = tid; i < n_sp; i += kFinishThreads) {
     const uint32_t id = sp_id[i];
     if (mrow && !((mrow[id >> 5] >> (id & 31)) & 1u)) continue;
@@ -1549,7 +1583,10 @@ __device__ __forceinline__ uint32_t finish_row(const SampleArgs& a, FinishLds& U
   // after a recomputed normaliser: the new total and the tight margin (the
   // whole block calls it; false when the row must take the exact path)
   auto refine = [&]() -> bool {
-    const double part = recompute_nonspecial_sum(a, row, cfg, constrained, M, n_sp, S.sp_id, S.wsum);
+    // the table exponential's table into LDS (the deep draw's copy, if any, is the same)
+    if (tid < 256) S.tab[tid] = c_exp2_256[tid];
+    __syncthreads();
+    const double part = recompute_nonspecial_sum(a, row, cfg, constrained, M, n_sp, S.sp_id, S.wsum, S.tab);
     if (!(part >= 0)) return false;
     total = part + S.total_sp;
     margin = margin_fine;
@@ -2010,53 +2047,6 @@ __device__ __forceinline__ bool deep_is_special(const uint32_t* set, uint32_t id
     h = (h + 1) & (kHashSize - 1);
   }
   return false;
-}
-
-// Calls visit(l, id) for every logit l of the row (soft-capped when cap > 0),
-// the whole block over it: kB 16-byte loads per thread go out before any is
-// used. Capped rows take a plain loop with the cap's call, so that the
-// unrolled loop stays small.
-template <int kB, typename F>
-__device__ __forceinline__ void visit_row(const SampleArgs& a, int64_t row, double cap, F&& visit) {
-  const int tid = threadIdx.x;
-  const int64_t V = a.vocab;
-  int64_t from = 0;
-  if (cap > 0) {
-    from = V;
-#pragma unroll 1
-    for (int64_t i = tid; i < V; i += kFinishThreads) visit(softcap_call(load_logit(a, row, i), cap), (uint32_t)i);
-  } else if (a.vector_ok) {
-    const bool bf16 = a.dtype == GS_BF16;
-    const int per = bf16 ? 8 : 4;
-    const int64_t n_vec = V / per;
-    const uint4* base = (const uint4*)((const char*)a.logits + row * a.row_stride * (bf16 ? 2 : 4));
-    for (int64_t v0 = tid; v0 < n_vec; v0 += (int64_t)kB * kFinishThreads) {
-      uint4 w[kB];
-#pragma unroll
-      for (int k = 0; k < kB; ++k) {
-        const int64_t vi = v0 + (int64_t)k * kFinishThreads;
-        w[k] = vi < n_vec ? base[vi] : make_uint4(0u, 0u, 0u, 0u);
-      }
-#pragma unroll
-      for (int k = 0; k < kB; ++k) {
-        const int64_t vi = v0 + (int64_t)k * kFinishThreads;
-        if (vi >= n_vec) break;
-        const uint32_t q[4] = {w[k].x, w[k].y, w[k].z, w[k].w};
-        const uint32_t id0 = (uint32_t)(vi * per);
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          if (bf16) {
-            visit(__builtin_bit_cast(float, q[j] << 16), id0 + 2 * j);
-            visit(__builtin_bit_cast(float, q[j] & 0xFFFF0000u), id0 + 2 * j + 1);
-          } else {
-            visit(__builtin_bit_cast(float, q[j]), id0 + j);
-          }
-        }
-      }
-    }
-    from = n_vec * per;
-  }
-  for (int64_t i = from + tid; i < V; i += kFinishThreads) visit(load_logit(a, row, i), (uint32_t)i);
 }
 
 // The deep draw's tail histogram: every finite logit below the region floor
