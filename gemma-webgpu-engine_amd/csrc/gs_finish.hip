@@ -843,8 +843,11 @@ __device__ __forceinline__ int filters_and_draw_wave(const SampleArgs& a, int64_
 // the whole block over it: kB 16-byte loads per thread go out before any is
 // used. Capped rows take a plain loop with the cap's call, so that the
 // unrolled loop stays small.
-template <int kB, typename F>
-__device__ __forceinline__ void visit_row(const SampleArgs& a, int64_t row, double cap, F&& visit) {
+// kRanged: only 16-byte pieces where some lane holds a logit in [lo, hi] are
+// visited (one ballot per piece), for a visit that ignores every other logit.
+template <int kB, bool kRanged = false, typename F>
+__device__ __forceinline__ void visit_row(const SampleArgs& a, int64_t row, double cap, F&& visit, float lo = 0.0f,
+                                          float hi = 0.0f) {
   const int tid = threadIdx.x;
   const int64_t V = a.vocab;
   int64_t from = 0;
@@ -870,6 +873,17 @@ __device__ __forceinline__ void visit_row(const SampleArgs& a, int64_t row, doub
         if (vi >= n_vec) break;
         const uint32_t q[4] = {w[k].x, w[k].y, w[k].z, w[k].w};
         const uint32_t id0 = (uint32_t)(vi * per);
+        if (kRanged) {
+          bool hit = false;
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            const float x0 = __builtin_bit_cast(float, bf16 ? q[j] << 16 : q[j]);
+            const float x1 = __builtin_bit_cast(float, q[j] & 0xFFFF0000u);
+            hit |= x0 >= lo && x0 <= hi;
+            if (bf16) hit |= x1 >= lo && x1 <= hi;
+          }
+          if (!__ballot(hit)) continue;
+        }
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
           if (bf16) {
@@ -2073,7 +2087,7 @@ __device__ __noinline__ double deep_histogram(const SampleArgs& a, int64_t row, 
 __device__ __noinline__ void deep_stage(const SampleArgs& a, int64_t row, double cap, float l_lo, float l_hi,
                                         uint64_t* stage, uint32_t* counter) {
   const int lane = threadIdx.x & 63;
-  visit_row<4>(a, row, cap, [&](float l, uint32_t id) {
+  visit_row<4, true>(a, row, cap, [&](float l, uint32_t id) {
     const bool pass = l >= l_lo && l <= l_hi;
     const uint64_t m = __ballot(pass);
     if (m == 0) return;
@@ -2083,7 +2097,7 @@ __device__ __noinline__ void deep_stage(const SampleArgs& a, int64_t row, double
     base = (uint32_t)__shfl((int)base, leader, 64);
     const uint32_t pos = base + (uint32_t)__popcll(m & ((1ull << lane) - 1ull));
     if (pass && pos < (uint32_t)kFinishCap) stage[pos] = ((uint64_t)__builtin_bit_cast(uint32_t, l) << 32) | id;
-  });
+  }, l_lo, l_hi);
 }
 
 // A full-vocabulary draw (topK 0, topP 1, no min-p or typical-p) whose cursor
