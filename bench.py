@@ -436,8 +436,9 @@ def main():
     stages = s.timing_end()
     log(f"stage timing over {args.steps} more steps: {stages}")
 
-    # results of the last step
-    last = (2 * args.steps - 1) % n_rot
+    # results of the last step (each loop above counts its steps from 0, so
+    # the last launch used buffer (steps - 1) mod n_rot)
+    last = (args.steps - 1) % n_rot
     res = wl["batches"][last][1][-1] if wl["name"] != "lmhead" else wl["batches"][0][1][-4]
     if wl["name"] == "qat":
         res = wl["batches"][0][1][-1]
