@@ -24,8 +24,8 @@
 // whose extent is one chunk, so the prefetch past the group's last chunk
 // returns zeros without a memory access and no load sits under a branch.
 // The group's first chunk takes its tau from the lane maxima: the smallest of
-// the four waves' d-th largest lane maxima (d = ceil(depth/4) + 2, found with
-// ballots), exchanged at one LDS-only barrier. That tau serves every later
+// the four waves' d-th largest lane maxima (d = ceil(depth/4), plus 2 for
+// top-p rows; found with ballots), exchanged at one LDS-only barrier. That tau serves every later
 // chunk of the group as well -- the first chunk alone holds `depth` logits
 // at or above it, so the group's top-`depth` are all >= it -- and the later
 // chunks need no barrier and no exchange at all: each wave reduces, gathers
@@ -88,6 +88,15 @@ struct VecTraits<uint16_t> {
 };
 
 __device__ __noinline__ float capped(float x, double cap) { return gsm::softcap_f32(x, cap); }
+
+// The calling wave's instruction-issue priority, 0..3 (s_setprio takes an
+// immediate).
+__device__ __forceinline__ void set_wave_priority(int p) {
+  if (p >= 3) __builtin_amdgcn_s_setprio(3);
+  else if (p == 2) __builtin_amdgcn_s_setprio(2);
+  else if (p == 1) __builtin_amdgcn_s_setprio(1);
+  else __builtin_amdgcn_s_setprio(0);
+}
 
 // Per-wave results of a group's first chunk, exchanged through LDS.
 struct WaveSlots {
@@ -526,6 +535,12 @@ __device__ __forceinline__ void scan_group(const SampleArgs& a, const gs_row_con
   uint32_t thr = 0;
 #pragma unroll 1
   for (int i = 0; i < nc; i += 2) {
+    // Issue priority by the share of the group's chunks still to scan: a
+    // CU's four workgroups start together, and by age alone the first
+    // dispatched would run ahead and leave the last to finish with the CU
+    // a quarter occupied; falling priority keeps them level, so the CU's
+    // waves stay many until its last chunks (-3 us at 256 x 262144)
+    set_wave_priority((4 * (nc - i) - 1) / nc);
     uint32_t t = chunk_stats<In, true, kMasked>(a, cfg, plan, row, c0 + i, kChunk, cur, mc,
                                                 S.special + i * kChunkWords, S.tab, S.slots[0], S.stage, thr);
     thr = thr ? thr : t;
