@@ -86,6 +86,33 @@ def test_full_vocabulary_draw_boundary(sampler, oracle):
     assert np.all(out.flags & gs.GS_FLAG_EXACT_PATH), out.flags
 
 
+def test_full_vocabulary_draws_bf16_and_softcap(sampler, oracle):
+    """Full-vocabulary draws whose cursors sit deep in the tail (u near 1),
+    so that most rows take the deep draw: bf16 rows (its gather reads eight
+    logits per 16-byte piece), and f32 and bf16 rows with softcap 30 (the
+    capped loop), each against the oracle on the same values."""
+    import torch
+
+    gs = _gs()
+    n = 16
+    w = gs.workloads.multinomial(rows=list(range(n)))
+    us = [1 - 2 ** -32, 0.9999, 0.999, 0.995, 0.99, 0.98, 0.97, 0.95] * 2
+    temps = [1.0, 0.9, 1.0, 0.8] * 4
+    cfgs = [c.merged(temperature=t) for c, t in zip(w.configs, temps)]
+    bits = gs.workloads.to_bf16_bits(w.logits)
+    xb = gs.workloads.bf16_bits_to_f32(bits).reshape(n, V)
+    dev_b = torch.from_numpy(bits.view(np.int16)).cuda().view(torch.bfloat16)
+    deep = 0
+    for label, dev, xin, cap in (("bf16", dev_b, xb, 0.0), ("f32 softcap", torch.from_numpy(w.logits).cuda(),
+                                                         w.logits, 30.0), ("bf16 softcap", dev_b, xb, 30.0)):
+        conf = np.stack([gs.runtime.row_config(c, uniform=u, softcap_value=cap) for c, u in zip(cfgs, us)])
+        out = sampler.sample(dev, conf)
+        vals = [oracle.softcap(xin[r], cap) if cap > 0 else xin[r] for r in range(n)]
+        check(gs, oracle, label, out, vals, None, cfgs, us)
+        deep += int(np.sum((out.flags & gs.GS_FLAG_EXACT_PATH) == 0))
+    assert deep > 0
+
+
 def test_topk_above_64(sampler, oracle):
     """topK 65 .. 2000 keep 64 entries per chunk; the finish ranks the
     complete region (block-wide) and cuts it at K."""
