@@ -49,7 +49,14 @@ constexpr uint32_t kExactRequest = 1u << 31;  // finish_row's answer: the row go
 constexpr uint32_t kDeepRequest = 1u << 30;   // finish_row's answer: a full-vocabulary draw for deep_draw
 constexpr int kDeepBins = 4096;                // value bins of the deep draw's tail histogram
 constexpr double kDeepSpan = 40.0;             // natural-log span of those bins below the region floor
+constexpr int kPrefixMin = 256;  // regions up to this size are sorted whole by the slow path
 static_assert(kFinishMaxChunks * kScanWaves <= kFinishThreads, "one thread per chunk wave");
+
+// e^x (x <= 0, binary32) in units of 2^-40, rounded down: the slow path's
+// mass histogram
+__device__ __forceinline__ unsigned long long mass_units(float x) {
+  return (unsigned long long)(__builtin_amdgcn_exp2f(x * 1.44269504088896341f) * 0x1p40f);
+}
 
 __device__ __forceinline__ double block_scan_f64(double v, double* s_w, double* total) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -151,51 +158,46 @@ __device__ __forceinline__ void merge_round(const uint64_t* src, uint64_t* dst, 
   for (int q = 0; q < E; ++q) dst[base + p + q] = c[q];
 }
 
-// Sorts s[0..n) descending (n <= kFinishThreads * E), zero-padded to
-// kFinishThreads * E entries; buf is as many entries of scratch. Each thread
-// sorts its E entries in registers, then merge rounds double the sorted runs
-// (a bitonic network over the whole block costs about three times as much:
-// its cross-lane stages are many). Ends with a barrier.
 template <int E>
-__device__ void sort_region(uint64_t* s, int n, uint64_t* buf) {
+__device__ __forceinline__ void wave_sort_desc_regs(uint64_t (&v)[E]);
+
+// Sorts src[0..n) descending into s[0..len), zero-padded: len is a power of
+// two with n <= len and E <= len <= kFinishThreads * E; buf is len entries of
+// scratch; src may be s or buf. Each wave sorts its 64 * E entries in
+// registers and cross-lane steps, then merge rounds double the sorted runs (a
+// bitonic network over the whole block costs about three times as much: its
+// cross-wave stages need a barrier each). Threads past len / E only take the
+// barriers. Ends with a barrier.
+template <int E>
+__device__ void sort_region(const uint64_t* src, int n, int len, uint64_t* s, uint64_t* buf) {
+  const bool active = (int)threadIdx.x * E < len;
   uint64_t v[E];
 #pragma unroll
   for (int q = 0; q < E; ++q) {
     const int i = threadIdx.x * E + q;
-    v[q] = i < n ? s[i] : 0ull;
+    v[q] = i < n ? src[i] : 0ull;
   }
+  wave_sort_desc_regs<E>(v);
+  __syncthreads();  // src and s may still be read by the caller's threads
+  if (active) {
 #pragma unroll
-  for (int k = 2; k <= E; k <<= 1) {
-#pragma unroll
-    for (int j = k >> 1; j > 0; j >>= 1) {
-#pragma unroll
-      for (int q = 0; q < E; ++q) {
-        const int qp = q ^ j;
-        if (qp > q) {
-          const uint64_t x = v[q], y = v[qp];
-          const bool desc = (q & k) == 0;
-          v[q] = desc ? umax64(x, y) : umin64(x, y);
-          v[qp] = desc ? umin64(x, y) : umax64(x, y);
-        }
-      }
-    }
+    for (int q = 0; q < E; ++q) s[threadIdx.x * E + q] = v[q];
   }
-  __syncthreads();  // s may still be read by the caller's threads
-#pragma unroll
-  for (int q = 0; q < E; ++q) s[threadIdx.x * E + q] = v[q];
   __syncthreads();
-  uint64_t* src = s;
-  uint64_t* dst = buf;
-  for (int L = E; L < kFinishThreads * E; L <<= 1) {
-    merge_round<E>(src, dst, L);
+  uint64_t* from = s;
+  uint64_t* to = buf;
+  for (int L = 64 * E; L < len; L <<= 1) {
+    if (active) merge_round<E>(from, to, L);
     __syncthreads();
-    uint64_t* t = src;
-    src = dst;
-    dst = t;
+    uint64_t* t = from;
+    from = to;
+    to = t;
   }
-  if (src != s) {
+  if (from != s) {
+    if (active) {
 #pragma unroll
-    for (int q = 0; q < E; ++q) s[threadIdx.x * E + q] = src[threadIdx.x * E + q];
+      for (int q = 0; q < E; ++q) s[threadIdx.x * E + q] = from[threadIdx.x * E + q];
+    }
     __syncthreads();
   }
 }
@@ -1704,28 +1706,157 @@ __device__ __forceinline__ uint32_t finish_row(const SampleArgs& a, FinishLds& U
     if (S.fast_done) return 0;
   }
 
-  // ---- slow path: the whole region sorted, then the filters block-wide
+  // ---- slow path: the candidates ranked block-wide, then the filters
   // (typical-p needs its whole pool among the fast path's candidates)
   if (cfg.typical_p < 1) {
     return kExactRequest | 0u;
   }
+  // Only the candidates up to the pool's end are ranked: the first topK, or
+  // those up to where the cumulative probability passes topP by twice the
+  // margin of its comparisons (sampling.ts:44,56,82-90; min-p only shortens
+  // the pool, and a cut inside the pool is the same whatever follows it). A
+  // histogram of the region's keys, with each bin's mass e^(v - M) summed in
+  // binary32, finds the highest bin boundary above which either bound is met.
+  // Both undercount: the count takes non-specials only, the mass is scaled
+  // down by 2^-10 (its binary32 terms err by under 1e-5 relative, and their
+  // truncation to 2^-40 units only lowers it). The candidates whose
+  // value is at or above the boundary's, specials included, are then the
+  // candidate list's first n_pre + n_sp_pre: every other one ranks below
+  // them all. The top-p pass checks the mass it sums over them.
+  int n_pre = n_ns, n_sp_pre = n_sp_in;
+  bool pre_cut = false;  // the ranked candidates end before the region does
   {
     uint64_t* scratch = (uint64_t*)S.cand_p;
     need_region();
-    if (n_ns <= kFinishThreads) sort_region<1>(S.sorted, n_ns, scratch);
-    else if (n_ns <= 2 * kFinishThreads) sort_region<2>(S.sorted, n_ns, scratch);
-    else sort_region<4>(S.sorted, n_ns, scratch);
+    const bool by_rank = cfg.top_k > 0 && cfg.top_k < n_ns + n_sp_in;
+    const bool by_mass = cfg.top_p < 1;
+    if ((by_rank || by_mass) && n_ns > kPrefixMin) {
+      const int shift = top_select_shift(sel_lo, sel_hi);
+      // masses in units of 2^-40 e^0 (integer LDS atomics: binary32 ones
+      // serialise badly); the table exponential's table is free until a
+      // recomputation or a deep draw fills it
+      uint64_t* bmass = (uint64_t*)S.tab;
+      if (tid < 256) bmass[tid] = 0ull;
+      __syncthreads();
+      const double rT = 1.0 / T;
+      for (int i = tid; i < n_ns; i += kFinishThreads) {
+        const uint32_t key = entry_key(S.sorted[i]);
+        if (key < sel_lo) continue;  // -inf (below every boundary, no mass)
+        const uint32_t d = (key - sel_lo) >> shift;
+        const uint32_t bin = d < 255u ? d : 255u;
+        const float x = (float)((double)key_f32(key) * rT - M);
+        atomicAdd(&S.hist[bin], 1u);
+        atomicAdd((unsigned long long*)&bmass[bin], mass_units(x));
+      }
+      // the region's specials add mass (not count) to the bin of a key no
+      // higher than their value times T: a boundary at or below that bin keeps
+      // them among the ranked candidates
+      for (int j = tid; j < n_sp_in; j += kFinishThreads) {
+        const double v = key_f64(in_key[j]);
+        const double l = v * T;
+        const double l_lo = l - (l < 0 ? -l : l) * 0x1p-40;
+        const float lf = (float)l_lo;
+        const uint32_t key = f32_key(lf) - ((double)lf > l_lo ? 1u : 0u);
+        if (key < sel_lo) continue;
+        const uint32_t d = (key - sel_lo) >> shift;
+        const uint32_t bin = d < 255u ? d : 255u;
+        atomicAdd((unsigned long long*)&bmass[bin], mass_units((float)(v - M)));
+      }
+      __syncthreads();
+      if (wave == 0) {
+        // lane l holds bins 255-4l .. 252-4l, highest first
+        uint32_t h[4], c = 0;
+        double m[4], ms = 0.0;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          h[q] = S.hist[255 - 4 * lane - q];
+          m[q] = (double)bmass[255 - 4 * lane - q] * 0x1p-40;
+          c += h[q];
+          ms += m[q];
+        }
+        const uint32_t incl = wave_scan_u32(c);
+        const double mincl = wave_scan_f64(ms);
+        const uint32_t want_n = by_rank ? (uint32_t)cfg.top_k : 0xFFFFFFFFu;
+        const double want_m = by_mass ? (cfg.top_p + 2.0 * margin) * total : __builtin_inf();
+        constexpr double kUnder = 1.0 - 0x1p-10;
+        // the boundary bin of each bound (-1: not met in the region)
+        int bn = -1, bm = -1;
+        const uint64_t hit_n = __ballot(incl >= want_n);
+        const uint64_t hit_m = __ballot(mincl * kUnder >= want_m);
+        if (hit_n) {
+          const int f = __ffsll((unsigned long long)hit_n) - 1;
+          if (lane == f) {
+            uint32_t cum = incl - c;
+            int q = 0;
+            while (q < 3 && cum + h[q] < want_n) { cum += h[q]; ++q; }
+            bn = 255 - 4 * lane - q;
+          }
+          bn = __shfl(bn, f, 64);
+        }
+        if (hit_m) {
+          const int f = __ffsll((unsigned long long)hit_m) - 1;
+          if (lane == f) {
+            double cum = mincl - ms;
+            int q = 0;
+            while (q < 3 && (cum + m[q]) * kUnder < want_m) { cum += m[q]; ++q; }
+            bm = 255 - 4 * lane - q;
+          }
+          bm = __shfl(bm, f, 64);
+        }
+        const int b = bn > bm ? bn : bm;  // the higher boundary: fewer candidates
+        if (lane == 0) S.sel[0] = b >= 0 ? (uint32_t)b : 0xFFFFFFFFu;
+      }
+      __syncthreads();
+      const uint32_t b = S.sel[0];
+      if (tid < 256) S.hist[tid] = 0;  // zero again for the next use
+      if (b != 0xFFFFFFFFu && b > 0u) {
+        // compact the non-specials at or above the boundary into scratch
+        const uint32_t floor_key = sel_lo + (b << shift);
+        if (tid == 0) S.sel[3] = 0;
+        __syncthreads();
+        for (int i0 = 0; i0 < n_ns; i0 += kFinishThreads) {
+          const int i = i0 + tid;
+          const uint64_t e = i < n_ns ? S.sorted[i] : 0ull;
+          const bool keep = i < n_ns && entry_key(e) >= floor_key;
+          const uint64_t mk = __ballot(keep);
+          uint32_t base = 0;
+          if (lane == 0 && mk) base = atomicAdd(&S.sel[3], (uint32_t)__popcll(mk));
+          base = readlane_u32(base, 0);
+          if (keep) {
+            scratch[base + __builtin_amdgcn_mbcnt_hi((uint32_t)(mk >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)mk, 0u))] =
+                e;
+          }
+        }
+        __syncthreads();
+        n_pre = (int)S.sel[3];
+        // specials at or above the boundary's value (in_key is descending)
+        const uint64_t vfloor = f64_key((double)key_f32(floor_key) / T);
+        int lo = 0, hi = n_sp_in;
+        while (lo < hi) {
+          const int mid = (lo + hi) >> 1;
+          if (in_key[mid] >= vfloor) lo = mid + 1; else hi = mid;
+        }
+        n_sp_pre = lo;
+        pre_cut = true;
+      }
+      __syncthreads();
+    }
+    const uint64_t* src = pre_cut ? scratch : S.sorted;
+    const int len = pow2_at_least(n_pre);
+    if (n_pre <= kFinishThreads) sort_region<1>(src, n_pre, len > 1 ? len : 1, S.sorted, scratch);
+    else if (n_pre <= 2 * kFinishThreads) sort_region<2>(src, n_pre, len, S.sorted, scratch);
+    else sort_region<4>(src, n_pre, len, S.sorted, scratch);
   }
-  const int n_cand = n_ns + n_sp_in;
+  const int n_cand = n_pre + n_sp_pre;
   if (n_cand > kFinishCap) {
     return kExactRequest | 0u;
   }
   // merge by rank into (value, id), then probabilities (sampling.ts:39,42)
-  for (int i = tid; i < n_ns; i += kFinishThreads) {
+  for (int i = tid; i < n_pre; i += kFinishThreads) {
     const uint64_t e = S.sorted[i];
     const uint32_t id = entry_id(e);
     const uint64_t k = f64_key(nonspecial_value(e, T));
-    int lo = 0, hi = n_sp_in;  // specials ranked before this entry
+    int lo = 0, hi = n_sp_pre;  // specials ranked before this entry
     while (lo < hi) {
       const int mid = (lo + hi) >> 1;
       if (ranks_before(in_key[mid], in_id[mid], k, id)) lo = mid + 1; else hi = mid;
@@ -1733,10 +1864,10 @@ __device__ __forceinline__ uint32_t finish_row(const SampleArgs& a, FinishLds& U
     S.cand_p[i + lo] = key_f64(k);
     S.cand_id[i + lo] = id;
   }
-  for (int j = tid; j < n_sp_in; j += kFinishThreads) {
+  for (int j = tid; j < n_sp_pre; j += kFinishThreads) {
     const uint64_t k = in_key[j];
     const uint32_t id = in_id[j];
-    int lo = 0, hi = n_ns;  // non-specials ranked before this special
+    int lo = 0, hi = n_pre;  // non-specials ranked before this special
     while (lo < hi) {
       const int mid = (lo + hi) >> 1;
       const uint64_t e = S.sorted[mid];
@@ -1752,8 +1883,8 @@ __device__ __forceinline__ uint32_t finish_row(const SampleArgs& a, FinishLds& U
 
   // ---- top-k (sampling.ts:44)
   int n = n_cand;
-  bool n_complete = region_complete;
-  if (cfg.top_k > 0 && cfg.top_k < n) {
+  bool n_complete = region_complete && !pre_cut;
+  if (cfg.top_k > 0 && (cfg.top_k < n || (pre_cut && cfg.top_k == n))) {
     n = cfg.top_k;
     n_complete = true;  // the first topK of the sorted list are all present
   }
@@ -1793,7 +1924,7 @@ __device__ __forceinline__ uint32_t finish_row(const SampleArgs& a, FinishLds& U
   uint32_t tie_report = 0;
   if (cfg.top_p < 1) {
     double local[kPer];
-    double base;
+    double base, tot;
     for (;;) {
       double s = 0.0;
       for (int q = 0; q < kPer; ++q) {
@@ -1801,7 +1932,6 @@ __device__ __forceinline__ uint32_t finish_row(const SampleArgs& a, FinishLds& U
         s += i < n ? S.cand_p[i] / total : 0.0;
         local[q] = s;
       }
-      double tot;
       base = block_scan_f64(s, S.wtmp, &tot) - s;
       uint32_t my_first = 0xFFFFFFFFu;
       bool my_near = false;
@@ -1829,6 +1959,11 @@ __device__ __forceinline__ uint32_t finish_row(const SampleArgs& a, FinishLds& U
         return kExactRequest | GS_FLAG_NEAR_TIE;
       }
       __syncthreads();
+    }
+    if (pre_cut && !n_complete && !(tot >= cfg.top_p + 2.0 * margin)) {
+      // the ranked candidates do not settle the comparisons past them (their
+      // sums lie at least the margin above topP, rounding aside)
+      return kExactRequest | 0u;
     }
     int cut = (int)S.first_idx;  // index of the item that reached topP
     if (S.first_idx == 0xFFFFFFFFu) {

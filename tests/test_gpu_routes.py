@@ -131,6 +131,36 @@ def test_topk_above_64(sampler, oracle):
     assert exact <= 4, exact
 
 
+def test_pools_past_64_with_window_ids(sampler, oracle):
+    """Top-p pools of hundreds of candidates, and top-k ones of 300 and 1500:
+    the finish ranks only the prefix of the candidate list that holds the pool
+    (a key histogram with each bin's mass picks where ranking may stop), so
+    window ids ranked inside the pool, around its end and below it (raised by
+    a repetition penalty below 1, lowered by one above it) must land where the
+    reference puts them; min-p rows beside them."""
+    import torch
+
+    gs = _gs()
+    rows = 24
+    g = np.random.default_rng(11)
+    xs = g.normal(0, 3, (rows, V)).astype(np.float32)
+    hists, cfgs = [], []
+    for r in range(rows):
+        order = np.argsort(-xs[r], kind="stable")
+        hists.append(order[g.integers(0, 3000, 300)].tolist())
+        cfgs.append(gs.DecodingConfig(
+            temperature=[1.0, 0.8, 0.9, 1.0, 0.8, 1.0][r % 6], topK=[0, 0, 0, 1500, 300, 0][r % 6],
+            topP=[0.5, 0.8, 0.75, 0.95, 0.8, 0.95][r % 6], minP=0.001 if r % 6 == 5 or r % 4 == 0 else 0.0,
+            typicalP=1.0,
+            repetitionPenalty=[1.05, 0.9, 1.0, 1.2][r % 4], repetitionWindow=512,
+            frequencyPenalty=0.05 if r % 2 else 0.0, presencePenalty=0.2 if r % 4 == 2 else 0.0))
+    us = [float(u) for u in g.random(rows)]
+    conf = np.stack([gs.runtime.row_config(c, uniform=u) for c, u in zip(cfgs, us)])
+    out = sampler.sample(torch.from_numpy(xs).cuda(), conf, histories=hists)
+    exact = check(gs, oracle, "pools>64", out, xs, hists, cfgs, us)
+    assert exact <= 4, exact
+
+
 def test_typical_p_with_top_k(sampler, oracle):
     """typicalP with topK <= 64: entropy, the surprise order, its leading
     mass and the kept set back in list order, in one wave; with min-p, top-p
