@@ -294,6 +294,122 @@ __device__ __forceinline__ int top_select_shift(uint32_t lo, uint32_t hi) {
   return shift;
 }
 
+// The slow path's ranking boundary (the comment at its call says why it is
+// one): over the region s[0..n_ns) in LDS (keys in [sel_lo, sel_hi]) and the
+// region's specials in_key[0..n_sp_in), the key above which either the first
+// topK candidates (counting non-specials only) or a mass of
+// (topP + 2 margin) total (scaled down by 2^-10) lies; 0 when none is met in
+// the region or the boundary keeps all of it. Its non-specials are compacted
+// into out[0..sel[3]). hist: 256 counters, zero on entry and on return; bmass:
+// 256 words of scratch. Called by the whole block; ends with a barrier.
+__device__ __forceinline__ uint32_t prefix_floor(const uint64_t* region, int n_ns, const uint64_t* in_key, int n_sp_in,
+                                              uint32_t sel_lo, uint32_t sel_hi, double T, double M, int top_k,
+                                              double top_p, double margin, double total, uint32_t* hist,
+                                              uint64_t* bmass, uint32_t* sel, uint64_t* out) {
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const bool by_rank = top_k > 0 && top_k < n_ns + n_sp_in;
+  const bool by_mass = top_p < 1;
+  if (!(by_rank || by_mass) || n_ns <= kPrefixMin) return 0;
+  const int shift = top_select_shift(sel_lo, sel_hi);
+  // masses in units of 2^-40 e^0 (integer LDS atomics: binary32 ones
+  // serialise badly)
+  if (tid < 256) bmass[tid] = 0ull;
+  __syncthreads();
+  const double rT = 1.0 / T;
+  for (int i = tid; i < n_ns; i += kFinishThreads) {
+    const uint32_t key = entry_key(region[i]);
+    if (key < sel_lo) continue;  // -inf (below every boundary, no mass)
+    const uint32_t d = (key - sel_lo) >> shift;
+    const uint32_t bin = d < 255u ? d : 255u;
+    const float x = (float)((double)key_f32(key) * rT - M);
+    atomicAdd(&hist[bin], 1u);
+    atomicAdd((unsigned long long*)&bmass[bin], mass_units(x));
+  }
+  // the region's specials add mass (not count) to the bin of a key no
+  // higher than their value times T: a boundary at or below that bin keeps
+  // them among the ranked candidates
+  for (int j = tid; j < n_sp_in; j += kFinishThreads) {
+    const double v = key_f64(in_key[j]);
+    const double l = v * T;
+    const double l_lo = l - (l < 0 ? -l : l) * 0x1p-40;
+    const float lf = (float)l_lo;
+    const uint32_t key = f32_key(lf) - ((double)lf > l_lo ? 1u : 0u);
+    if (key < sel_lo) continue;
+    const uint32_t d = (key - sel_lo) >> shift;
+    const uint32_t bin = d < 255u ? d : 255u;
+    atomicAdd((unsigned long long*)&bmass[bin], mass_units((float)(v - M)));
+  }
+  __syncthreads();
+  if (wave == 0) {
+    // lane l holds bins 255-4l .. 252-4l, highest first
+    uint32_t h[4], c = 0;
+    double m[4], ms = 0.0;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      h[q] = hist[255 - 4 * lane - q];
+      m[q] = (double)bmass[255 - 4 * lane - q] * 0x1p-40;
+      c += h[q];
+      ms += m[q];
+    }
+    const uint32_t incl = wave_scan_u32(c);
+    const double mincl = wave_scan_f64(ms);
+    const uint32_t want_n = by_rank ? (uint32_t)top_k : 0xFFFFFFFFu;
+    const double want_m = by_mass ? (top_p + 2.0 * margin) * total : __builtin_inf();
+    constexpr double kUnder = 1.0 - 0x1p-10;
+    // the boundary bin of each bound (-1: not met in the region)
+    int bn = -1, bm = -1;
+    const uint64_t hit_n = __ballot(incl >= want_n);
+    const uint64_t hit_m = __ballot(mincl * kUnder >= want_m);
+    if (hit_n) {
+      const int f = __ffsll((unsigned long long)hit_n) - 1;
+      if (lane == f) {
+        uint32_t cum = incl - c;
+        int q = 0;
+        while (q < 3 && cum + h[q] < want_n) { cum += h[q]; ++q; }
+        bn = 255 - 4 * lane - q;
+      }
+      bn = __shfl(bn, f, 64);
+    }
+    if (hit_m) {
+      const int f = __ffsll((unsigned long long)hit_m) - 1;
+      if (lane == f) {
+        double cum = mincl - ms;
+        int q = 0;
+        while (q < 3 && (cum + m[q]) * kUnder < want_m) { cum += m[q]; ++q; }
+        bm = 255 - 4 * lane - q;
+      }
+      bm = __shfl(bm, f, 64);
+    }
+    const int b = bn > bm ? bn : bm;  // the higher boundary: fewer candidates
+    if (lane == 0) {
+      sel[0] = b > 0 ? (uint32_t)b : 0u;
+      sel[3] = 0;
+    }
+  }
+  __syncthreads();
+  const uint32_t b = sel[0];
+  if (tid < 256) hist[tid] = 0;  // zero again for the next use
+  if (b == 0u) {
+    __syncthreads();
+    return 0;
+  }
+  // compact the non-specials at or above the boundary into out (one LDS
+  // atomic per wave)
+  const uint32_t floor_key = sel_lo + (b << shift);
+  for (int i0 = 0; i0 < n_ns; i0 += kFinishThreads) {
+    const int i = i0 + tid;
+    const uint64_t e = i < n_ns ? region[i] : 0ull;
+    const bool keep = i < n_ns && entry_key(e) >= floor_key;
+    const uint64_t mk = __ballot(keep);
+    uint32_t base = 0;
+    if (lane == 0 && mk) base = atomicAdd(&sel[3], (uint32_t)__popcll(mk));
+    base = readlane_u32(base, 0);
+    if (keep) out[base + __builtin_amdgcn_mbcnt_hi((uint32_t)(mk >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)mk, 0u))] = e;
+  }
+  __syncthreads();
+  return floor_key;
+}
+
 // Appends thread-held entries (valid bits) with key >= floor_key to out[] at
 // positions counted in sel[3] (one LDS atomic per wave); positions past 128
 // are counted, not stored.
@@ -540,6 +656,7 @@ struct Shared {
   uint32_t fast_done;
   uint32_t exact_flags;
   uint64_t best_entry;
+  uint32_t short_sum;  // the slow path's ranked candidates end short of the pool's end
 };
 
 __device__ void enqueue_exact(const SampleArgs& a, int64_t row, uint32_t flags) {
@@ -1078,7 +1195,7 @@ __device__ __forceinline__ uint32_t finish_row(const SampleArgs& a, FinishLds& U
     S.flags = 0; S.max_key = 0; S.thr_max = 0; S.any_truncated = 0; S.n_sorted = 0; S.n_special = 0;
     S.sel[3] = 0;
     S.n_sp_in = 0; S.route_exact = 0; S.status_flags = 0; S.first_idx = 0xFFFFFFFFu; S.legal_bits = 0;
-    S.special_legal = 0; S.best_entry = 0; S.sp_max = 0; S.fast_done = 0;
+    S.special_legal = 0; S.best_entry = 0; S.sp_max = 0; S.fast_done = 0; S.short_sum = 0;
   }
   for (int h = tid; h < kHashSize; h += kFinishThreads) { S.hash_ids[h] = 0xFFFFFFFFu; S.hash_counts[h] = 0; }
   if (tid < 256) S.hist[tid] = 0;
@@ -1715,8 +1832,9 @@ __device__ __forceinline__ uint32_t finish_row(const SampleArgs& a, FinishLds& U
   // those up to where the cumulative probability passes topP by twice the
   // margin of its comparisons (sampling.ts:44,56,82-90; min-p only shortens
   // the pool, and a cut inside the pool is the same whatever follows it). A
-  // histogram of the region's keys, with each bin's mass e^(v - M) summed in
-  // binary32, finds the highest bin boundary above which either bound is met.
+  // histogram of the region's keys, with each bin's mass e^(v - M) (binary32
+  // exponentials summed as integers), finds the highest bin boundary above
+  // which either bound is met.
   // Both undercount: the count takes non-specials only, the mass is scaled
   // down by 2^-10 (its binary32 terms err by under 1e-5 relative, and their
   // truncation to 2^-40 units only lowers it). The candidates whose
@@ -1728,118 +1846,19 @@ __device__ __forceinline__ uint32_t finish_row(const SampleArgs& a, FinishLds& U
   {
     uint64_t* scratch = (uint64_t*)S.cand_p;
     need_region();
-    const bool by_rank = cfg.top_k > 0 && cfg.top_k < n_ns + n_sp_in;
-    const bool by_mass = cfg.top_p < 1;
-    if ((by_rank || by_mass) && n_ns > kPrefixMin) {
-      const int shift = top_select_shift(sel_lo, sel_hi);
-      // masses in units of 2^-40 e^0 (integer LDS atomics: binary32 ones
-      // serialise badly); the table exponential's table is free until a
-      // recomputation or a deep draw fills it
-      uint64_t* bmass = (uint64_t*)S.tab;
-      if (tid < 256) bmass[tid] = 0ull;
-      __syncthreads();
-      const double rT = 1.0 / T;
-      for (int i = tid; i < n_ns; i += kFinishThreads) {
-        const uint32_t key = entry_key(S.sorted[i]);
-        if (key < sel_lo) continue;  // -inf (below every boundary, no mass)
-        const uint32_t d = (key - sel_lo) >> shift;
-        const uint32_t bin = d < 255u ? d : 255u;
-        const float x = (float)((double)key_f32(key) * rT - M);
-        atomicAdd(&S.hist[bin], 1u);
-        atomicAdd((unsigned long long*)&bmass[bin], mass_units(x));
+    const uint32_t floor_key = prefix_floor(S.sorted, n_ns, in_key, n_sp_in, sel_lo, sel_hi, T, M, cfg.top_k,
+                                            cfg.top_p, margin, total, S.hist, (uint64_t*)S.tab, S.sel, scratch);
+    if (floor_key) {
+      n_pre = (int)S.sel[3];
+      // specials at or above the boundary's value (in_key is descending)
+      const uint64_t vfloor = f64_key((double)key_f32(floor_key) / T);
+      int lo = 0, hi = n_sp_in;
+      while (lo < hi) {
+        const int mid = (lo + hi) >> 1;
+        if (in_key[mid] >= vfloor) lo = mid + 1; else hi = mid;
       }
-      // the region's specials add mass (not count) to the bin of a key no
-      // higher than their value times T: a boundary at or below that bin keeps
-      // them among the ranked candidates
-      for (int j = tid; j < n_sp_in; j += kFinishThreads) {
-        const double v = key_f64(in_key[j]);
-        const double l = v * T;
-        const double l_lo = l - (l < 0 ? -l : l) * 0x1p-40;
-        const float lf = (float)l_lo;
-        const uint32_t key = f32_key(lf) - ((double)lf > l_lo ? 1u : 0u);
-        if (key < sel_lo) continue;
-        const uint32_t d = (key - sel_lo) >> shift;
-        const uint32_t bin = d < 255u ? d : 255u;
-        atomicAdd((unsigned long long*)&bmass[bin], mass_units((float)(v - M)));
-      }
-      __syncthreads();
-      if (wave == 0) {
-        // lane l holds bins 255-4l .. 252-4l, highest first
-        uint32_t h[4], c = 0;
-        double m[4], ms = 0.0;
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          h[q] = S.hist[255 - 4 * lane - q];
-          m[q] = (double)bmass[255 - 4 * lane - q] * 0x1p-40;
-          c += h[q];
-          ms += m[q];
-        }
-        const uint32_t incl = wave_scan_u32(c);
-        const double mincl = wave_scan_f64(ms);
-        const uint32_t want_n = by_rank ? (uint32_t)cfg.top_k : 0xFFFFFFFFu;
-        const double want_m = by_mass ? (cfg.top_p + 2.0 * margin) * total : __builtin_inf();
-        constexpr double kUnder = 1.0 - 0x1p-10;
-        // the boundary bin of each bound (-1: not met in the region)
-        int bn = -1, bm = -1;
-        const uint64_t hit_n = __ballot(incl >= want_n);
-        const uint64_t hit_m = __ballot(mincl * kUnder >= want_m);
-        if (hit_n) {
-          const int f = __ffsll((unsigned long long)hit_n) - 1;
-          if (lane == f) {
-            uint32_t cum = incl - c;
-            int q = 0;
-            while (q < 3 && cum + h[q] < want_n) { cum += h[q]; ++q; }
-            bn = 255 - 4 * lane - q;
-          }
-          bn = __shfl(bn, f, 64);
-        }
-        if (hit_m) {
-          const int f = __ffsll((unsigned long long)hit_m) - 1;
-          if (lane == f) {
-            double cum = mincl - ms;
-            int q = 0;
-            while (q < 3 && (cum + m[q]) * kUnder < want_m) { cum += m[q]; ++q; }
-            bm = 255 - 4 * lane - q;
-          }
-          bm = __shfl(bm, f, 64);
-        }
-        const int b = bn > bm ? bn : bm;  // the higher boundary: fewer candidates
-        if (lane == 0) S.sel[0] = b >= 0 ? (uint32_t)b : 0xFFFFFFFFu;
-      }
-      __syncthreads();
-      const uint32_t b = S.sel[0];
-      if (tid < 256) S.hist[tid] = 0;  // zero again for the next use
-      if (b != 0xFFFFFFFFu && b > 0u) {
-        // compact the non-specials at or above the boundary into scratch
-        const uint32_t floor_key = sel_lo + (b << shift);
-        if (tid == 0) S.sel[3] = 0;
-        __syncthreads();
-        for (int i0 = 0; i0 < n_ns; i0 += kFinishThreads) {
-          const int i = i0 + tid;
-          const uint64_t e = i < n_ns ? S.sorted[i] : 0ull;
-          const bool keep = i < n_ns && entry_key(e) >= floor_key;
-          const uint64_t mk = __ballot(keep);
-          uint32_t base = 0;
-          if (lane == 0 && mk) base = atomicAdd(&S.sel[3], (uint32_t)__popcll(mk));
-          base = readlane_u32(base, 0);
-          if (keep) {
-            scratch[base + __builtin_amdgcn_mbcnt_hi((uint32_t)(mk >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)mk, 0u))] =
-                e;
-          }
-        }
-        __syncthreads();
-        n_pre = (int)S.sel[3];
-        // specials at or above the boundary's value (in_key is descending)
-        const uint64_t vfloor = f64_key((double)key_f32(floor_key) / T);
-        int lo = 0, hi = n_sp_in;
-        while (lo < hi) {
-          const int mid = (lo + hi) >> 1;
-          if (in_key[mid] >= vfloor) lo = mid + 1; else hi = mid;
-        }
-        n_sp_pre = lo;
-        pre_cut = true;
-      }
-      __syncthreads();
+      n_sp_pre = lo;
+      pre_cut = true;
     }
     const uint64_t* src = pre_cut ? scratch : S.sorted;
     const int len = pow2_at_least(n_pre);
@@ -1924,7 +1943,7 @@ __device__ __forceinline__ uint32_t finish_row(const SampleArgs& a, FinishLds& U
   uint32_t tie_report = 0;
   if (cfg.top_p < 1) {
     double local[kPer];
-    double base, tot;
+    double base;
     for (;;) {
       double s = 0.0;
       for (int q = 0; q < kPer; ++q) {
@@ -1932,6 +1951,7 @@ __device__ __forceinline__ uint32_t finish_row(const SampleArgs& a, FinishLds& U
         s += i < n ? S.cand_p[i] / total : 0.0;
         local[q] = s;
       }
+      double tot;
       base = block_scan_f64(s, S.wtmp, &tot) - s;
       uint32_t my_first = 0xFFFFFFFFu;
       bool my_near = false;
@@ -1942,6 +1962,10 @@ __device__ __forceinline__ uint32_t finish_row(const SampleArgs& a, FinishLds& U
         if (cum >= cfg.top_p) my_first = (uint32_t)i;
         const double d = cum >= cfg.top_p ? cum - cfg.top_p : cfg.top_p - cum;
         if (d < margin) my_near = true;
+        // ranked candidates that end before the pool does settle the
+        // comparisons past them only when their sum passes topP by twice the
+        // margin (the last one's cumulative sum, set on every pass)
+        if (i == n - 1 && pre_cut && !n_complete) S.short_sum = cum >= cfg.top_p + 2.0 * margin ? 0u : 1u;
       }
       // one LDS atomic per wave
       my_first = wave_min_u32(my_first);
@@ -1960,13 +1984,8 @@ __device__ __forceinline__ uint32_t finish_row(const SampleArgs& a, FinishLds& U
       }
       __syncthreads();
     }
-    if (pre_cut && !n_complete && !(tot >= cfg.top_p + 2.0 * margin)) {
-      // the ranked candidates do not settle the comparisons past them (their
-      // sums lie at least the margin above topP, rounding aside)
-      return kExactRequest | 0u;
-    }
     int cut = (int)S.first_idx;  // index of the item that reached topP
-    if (S.first_idx == 0xFFFFFFFFu) {
+    if (S.first_idx == 0xFFFFFFFFu || S.short_sum) {
       if (!n_complete) {
         return kExactRequest | 0u;
       }
