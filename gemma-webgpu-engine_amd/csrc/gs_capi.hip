@@ -24,6 +24,8 @@ struct gs_context {
   uint64_t* d_lists = nullptr;
   ExactQueue* d_queue = nullptr;
   uint8_t* d_exact = nullptr;
+  DeepRow* d_deep_rows = nullptr;   // [max_rows] records of the multi-workgroup deep draw
+  DeepQueue* d_deep_queue = nullptr;
   int64_t exact_cap = 0;
   int64_t exact_slot_bytes = 0;
   int32_t exact_slots = 0;
@@ -166,7 +168,16 @@ struct Workspace {
   ExactQueue* queue = nullptr;
   uint8_t* exact = nullptr;
   int64_t exact_slot_bytes = 0, exact_cap = 0;
+  DeepRow* deep_rows = nullptr;  // none: the finish's workgroups take their own deep draws
+  DeepQueue* deep_queue = nullptr;
+  int32_t deep_max_rows = 0;
 };
+
+// true when the batch hints at full-vocabulary draws and the workspace has
+// the deep draw's records
+bool deep_launch(const Workspace& w, const gs_batch* b) {
+  return (b->hints & GS_BATCH_FULL_DRAWS) && w.deep_rows && w.deep_queue && b->rows <= w.deep_max_rows;
+}
 
 // Enqueues the sampling kernels of one checked batch on stream s (ev: the
 // timing events of each stage, none when not timing). The exact-path queue is
@@ -200,12 +211,22 @@ hipError_t launch_sample(const Workspace& w, const gs_batch* b, hipStream_t s, c
   a.exact_slot_bytes = w.exact_slot_bytes;
   a.exact_capacity = w.exact_cap;
   a.cu_count = w.cu_count;
+  const bool deep = deep_launch(w, b);
+  a.deep_rows = deep ? w.deep_rows : nullptr;
+  a.deep_queue = deep ? w.deep_queue : nullptr;
+  a.deep_max_rows = deep ? w.deep_max_rows : 0;
   launch_scan(a, s, ev[GS_STAGE_SCAN]);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   launch_finish(a, s, ev[GS_STAGE_FINISH]);
   e = hipGetLastError();
   if (e != hipSuccess) return e;
+  if (deep) {
+    // rows queued by the finish kernel for the multi-workgroup deep draw
+    launch_deep(a, s, ev[GS_STAGE_DEEP]);
+    e = hipGetLastError();
+    if (e != hipSuccess) return e;
+  }
   if (b->rows > w.exact_slots) {
     // rows past the slots were queued by the finish kernel
     launch_exact(a, s, ev[GS_STAGE_EXACT]);
@@ -375,6 +396,10 @@ int gs_create(int device, int32_t vocab_size, int32_t max_rows, gs_context** out
   if (hipMalloc(&ctx->d_queue, queue_bytes) != hipSuccess) return cleanup(GS_ERR_HIP, "queue");
   if (hipMalloc(&ctx->d_exact, (size_t)ctx->exact_slot_bytes * ctx->exact_slots) != hipSuccess)
     return cleanup(GS_ERR_HIP, "exact scratch");
+  if (hipMalloc(&ctx->d_deep_rows, sizeof(DeepRow) * (size_t)max_rows) != hipSuccess)
+    return cleanup(GS_ERR_HIP, "deep draw records");
+  if (hipMalloc(&ctx->d_deep_queue, sizeof(DeepQueue) + sizeof(uint32_t) * 2 * (size_t)max_rows) != hipSuccess)
+    return cleanup(GS_ERR_HIP, "deep draw queue");
   *out = ctx;
   return GS_OK;
 }
@@ -387,6 +412,8 @@ int gs_destroy(gs_context* ctx) {
   free_dev(ctx->d_lists);
   free_dev(ctx->d_queue);
   free_dev(ctx->d_exact);
+  free_dev(ctx->d_deep_rows);
+  free_dev(ctx->d_deep_queue);
   free_dev(ctx->d_vocab_offsets);
   free_dev(ctx->d_vocab_bytes);
   free_dev(ctx->d_next);
@@ -459,9 +486,13 @@ int gs_sample(gs_context* ctx, const gs_batch* b, void* stream) {
   w.exact = ctx->d_exact;
   w.exact_slot_bytes = ctx->exact_slot_bytes;
   w.exact_cap = ctx->exact_cap;
+  w.deep_rows = ctx->d_deep_rows;
+  w.deep_queue = ctx->d_deep_queue;
+  w.deep_max_rows = ctx->max_rows;
   const int32_t slot = timing_slot(ctx);
   LaunchEvents ev[GS_STAGE_COUNT];
   for (int k = GS_STAGE_SCAN; k <= GS_STAGE_FINISH; ++k) ev[k] = stage_events(ctx, slot, k);
+  if (deep_launch(w, b)) ev[GS_STAGE_DEEP] = stage_events(ctx, slot, GS_STAGE_DEEP);
   if (b->rows > ctx->exact_slots) ev[GS_STAGE_EXACT] = stage_events(ctx, slot, GS_STAGE_EXACT);
   const hipError_t e = launch_sample(w, b, pick_stream(ctx, stream), ev);
   if (e != hipSuccess) return fail(ctx, GS_ERR_HIP, std::string("kernel launch: ") + hipGetErrorString(e));
@@ -553,6 +584,11 @@ int gs_sample_host(gs_context* ctx, const gs_batch* b, int32_t logits_on_device,
     db.forced_kinds = d + o_fk;
   }
   db.results = (gs_row_result*)(d + o_res);
+  for (int32_t r = 0; r < R; ++r) {
+    const gs_row_config& c = b->configs[r];
+    if (c.temperature > 0 && c.top_k <= 0 && c.top_p >= 1 && !(c.min_p > 0) && c.typical_p >= 1 && c.mask_slot < 0)
+      db.hints |= GS_BATCH_FULL_DRAWS;
+  }
   st = gs_sample(ctx, &db, s);
   if (st != GS_OK) return st;
   GS_HIP(ctx, hipMemcpyAsync(host_results, d + o_res, sizeof(gs_row_result) * R, hipMemcpyDeviceToHost, s));

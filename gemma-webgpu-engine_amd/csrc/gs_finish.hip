@@ -47,7 +47,6 @@ constexpr uint32_t kDeepLists = 1u << 30;  // row flag: some sub-list holds more
 constexpr uint32_t kSpecialOverflow = 1u << 29;  // row flag: an id found no hash slot (exact path)
 constexpr uint32_t kExactRequest = 1u << 31;  // finish_row's answer: the row goes to the exact path
 constexpr uint32_t kDeepRequest = 1u << 30;   // finish_row's answer: a full-vocabulary draw for deep_draw
-constexpr int kDeepBins = 4096;                // value bins of the deep draw's tail histogram
 constexpr double kDeepSpan = 40.0;             // natural-log span of those bins below the region floor
 constexpr int kPrefixMin = 256;  // regions up to this size are sorted whole by the slow path
 static_assert(kFinishMaxChunks * kScanWaves <= kFinishThreads, "one thread per chunk wave");
@@ -631,6 +630,7 @@ struct Shared {
   double deep_m, deep_u, deep_margin; // a deep draw's inputs, left by finish_row
   uint64_t deep_floor;
   uint32_t deep_thr, deep_n, deep_count, deep_final;
+  DeepPlan plan;                      // the deep draw's pass-2 plan
   uint32_t sel[4];
   double wsum[kWaves];
   double wtmp[kWaves];
@@ -2254,51 +2254,67 @@ __device__ __noinline__ void deep_stage(const SampleArgs& a, int64_t row, double
   }, l_lo, l_hi);
 }
 
-// A full-vocabulary draw (topK 0, topP 1, no min-p or typical-p) whose cursor
-// lies past the complete region of the chunk lists, or within the scan
-// normaliser's margin of one of its prefix sums (sampling.ts:58-64 over the
-// whole sorted list). finish_row left the region's candidates in list order
-// with their exact exponentials (cand_p / cand_id, deep_n of them), the row's
-// specials (sp_key / sp_id) and M, u, the region floor and the reference's
-// own rounding margin. One pass over the row's logits below the floor builds
-// a fixed-point mass histogram over value bins (terms within 2^-40 relative),
-// which gives the normaliser and every bin's prefix mass to that accuracy; the
-// region is walked again with them; failing that, the bins the cursor falls
-// in are gathered, sorted by (value desc, id asc), given their exact
-// exponentials and walked. Returns 0 with the result written, or
-// kExactRequest | flags. Unconstrained rows only; the whole block calls it.
-__device__ __noinline__ uint32_t deep_draw(const SampleArgs& a, FinishLds& U) {
-  Shared& S = U.fin;
+// Adds id to the LDS hash set of the row's special ids (kHashSize slots, at
+// most kSpecialCap ids, so a free slot is always found).
+__device__ __forceinline__ void deep_set_insert(uint32_t* set, uint32_t id) {
+  uint32_t h = hash_id(id) & (kHashSize - 1);
+  for (int probe = 0; probe < kHashSize; ++probe) {
+    const uint32_t prev = atomicCAS(&set[h], 0xFFFFFFFFu, id);
+    if (prev == 0xFFFFFFFFu || prev == id) return;
+    h = (h + 1) & (kHashSize - 1);
+  }
+}
+
+// The deep draw's LDS set-up, with the row's specials in sp_id[0..n_sp): the
+// hash set of their ids (hash_counts), the exponential's table, the gather
+// counters, and the mass histogram (sorted) zeroed unless it is loaded.
+__device__ __noinline__ void deep_setup(Shared& S, int n_sp, bool zero_mass) {
+  const int tid = threadIdx.x;
+  for (int b = tid; b < kDeepBins; b += kFinishThreads) {
+    if (zero_mass) S.sorted[b] = 0ull;
+    S.hash_counts[b] = 0xFFFFFFFFu;
+  }
+  if (tid < 256) S.tab[tid] = c_exp2_256[tid];
+  if (tid == 0) {
+    S.deep_count = 0;
+    S.deep_final = 0;
+  }
+  __syncthreads();
+  for (int i = tid; i < n_sp; i += kFinishThreads) deep_set_insert(S.hash_counts, S.sp_id[i]);
+  __syncthreads();
+}
+
+// The deep draw's inputs hold: the region floor at or below the row's
+// largest value (every term below the floor at most 1, so the fixed-point
+// sums stay below 2^22; a floor above it is left to the exact path) and a
+// temperature div_by_temperature's range covers.
+__device__ __forceinline__ bool deep_inputs_ok(const Shared& S, double T) {
+  const double vf = (double)key_f32(S.deep_thr) / T;
+  return vf <= S.deep_m && T >= 0x1p-20 && T <= 0x1p20;
+}
+
+// What pass 1 leaves (the mass histogram in sorted, each thread's last-bin
+// sum in `tail`) is completed and used: the specials go out of the
+// histogram with their raw values and in with their penalised ones, the
+// normaliser and every bin's prefix mass are summed in fixed point, and the
+// region is walked with them. Returns 0 with the result written,
+// kExactRequest | flags, or kDeepPass2 with S.plan holding the bins the
+// cursor falls in and the logit range to gather.
+constexpr uint32_t kDeepPass2 = 1u << 27;
+__device__ __noinline__ uint32_t deep_mid(const SampleArgs& a, Shared& S, int64_t row, int n_sp, double tail) {
   const int tid = threadIdx.x, lane = tid & 63;
-  const int64_t row = blockIdx.x;
   const gs_row_config cfg = a.configs[row];
-  const double T = cfg.temperature;
+  const double T = cfg.temperature, rT = 1.0 / T;
   const double M = S.deep_m, u = S.deep_u;
   const uint32_t thr = S.deep_thr;
   const int n_reg = (int)S.deep_n;
-  const int n_sp = (int)(S.n_special < (uint32_t)kSpecialCap ? S.n_special : (uint32_t)kSpecialCap);
   const double vf = (double)key_f32(thr) / T;  // the region floor's value
   const double vfc = vf * ((double)kDeepBins / kDeepSpan);
   // the largest float below the floor's logit: l <= l_below iff f32_key(l) < thr
   // (NaN aside; -0 and +0 share a key, and the float below both is -2^-149)
   const float l_below = key_f32(thr - 1u);
-  // every term below the floor at most 1, so the fixed-point sums stay below
-  // 2^22 (M is the row's largest value; a floor above it is left to the
-  // exact path); the quotient l / T by div_by_temperature, whose range this
-  // bounds
-  if (!(vf <= M) || !(T >= 0x1p-20 && T <= 0x1p20)) return kExactRequest | 0u;
-  const double rT = 1.0 / T;
-  uint64_t* mass = S.sorted;          // [kDeepBins - 1] terms in units of 2^-40 e^(c_b - M)
-  uint32_t* spset = S.hash_counts;    // hash set of the special ids
-  for (int b = tid; b < kDeepBins; b += kFinishThreads) { mass[b] = 0ull; spset[b] = 0xFFFFFFFFu; }
-  if (tid < 256) S.tab[tid] = c_exp2_256[tid];
-  if (tid == 0) S.deep_count = 0;
-  __syncthreads();
-  for (int i = tid; i < n_sp; i += kFinishThreads) special_insert(SpecialTable{spset, S.hist}, S.sp_id[i], 1u);
-  // ---- pass 1: the tail's mass per bin
-  double tail = deep_histogram(a, row, cfg.softcap, T, rT, M, l_below, vfc, mass, S.tab);
-  __syncthreads();
-  // specials: out with their raw values (where the pass counted them; the
+  uint64_t* mass = S.sorted;  // [kDeepBins - 1] terms in units of 2^-40 e^(c_b - M)
+  // specials: out with their raw values (where pass 1 counted them; the
   // same units, so exactly), in with their penalised ones below the floor
   for (int i = tid; i < n_sp; i += kFinishThreads) {
     const uint32_t id = S.sp_id[i];
@@ -2415,22 +2431,42 @@ __device__ __noinline__ uint32_t deep_draw(const SampleArgs& a, FinishLds& U) {
   double l_lo = (vf - (b_hi + 1) * (kDeepSpan / kDeepBins)) * T;
   l_hi += 1e-6 * (1.0 + __builtin_fabs(l_hi));
   l_lo -= 1e-6 * (1.0 + __builtin_fabs(l_lo));
-  if (tid == 0) S.deep_final = 0;
   __syncthreads();  // every read of after[] done before the gather reuses the array
-  // ---- pass 2: stage the logits in the bins' float range (in cand_p), then
-  // keep those whose exact value falls in the bins, specials aside, as (value
-  // key, id) in sorted / hash_ids
-  uint64_t* stage = (uint64_t*)S.cand_p;
+  if (tid == 0) {
+    S.plan.total = total;
+    S.plan.target = target;
+    S.plan.mrg = mrg;
+    S.plan.pre_before = pre_before;
+    S.plan.l_lo = (float)l_lo;
+    S.plan.l_top = (float)l_hi < l_below ? (float)l_hi : l_below;
+    S.plan.b_lo = b_lo;
+    S.plan.b_hi = b_hi;
+    S.deep_final = 0;
+  }
+  __syncthreads();
+  return kDeepPass2;
+}
+
+// Pass 2's staged logits (in cand_p as (float bits << 32 | id), deep_count of
+// them) are tested against the plan's bins exactly, joined by the specials
+// whose penalised values fall there, sorted (value desc, id asc) and walked
+// with exact exponentials from the mass before the bins. Returns as deep_mid.
+__device__ __noinline__ uint32_t deep_final(const SampleArgs& a, Shared& S, int64_t row, int n_sp) {
+  const int tid = threadIdx.x, lane = tid & 63;
+  const double T = a.configs[row].temperature, rT = 1.0 / T;
+  const double M = S.deep_m;
+  const double vfc = (double)key_f32(S.deep_thr) / T * ((double)kDeepBins / kDeepSpan);
+  const DeepPlan plan = S.plan;
+  constexpr int kPer = kFinishCap / kFinishThreads;
+  if (S.deep_count > (uint32_t)kFinishCap) return kExactRequest | 0u;  // a crowd of equal values
+  const uint64_t* stage = (const uint64_t*)S.cand_p;
   uint64_t* gkey = S.sorted;
   uint32_t* gid = S.hash_ids;
-  const float l_top = (float)l_hi < l_below ? (float)l_hi : l_below;
-  deep_stage(a, row, cfg.softcap, (float)l_lo, l_top, stage, &S.deep_count);
-  __syncthreads();
-  if (S.deep_count > (uint32_t)kFinishCap) return kExactRequest | 0u;  // a crowd of equal values
+  const uint32_t* spset = S.hash_counts;
   const int n_s = (int)S.deep_count;
   auto gather = [&](double v, uint32_t id) {
     const int b = deep_bin(v, vfc);
-    if (b < b_lo || b > b_hi) return;
+    if (b < plan.b_lo || b > plan.b_hi) return;
     const uint32_t pos = atomicAdd(&S.deep_final, 1u);
     if (pos < (uint32_t)kFinishCap) { gkey[pos] = f64_key(v); gid[pos] = id; }
   };
@@ -2473,9 +2509,9 @@ __device__ __noinline__ uint32_t deep_draw(const SampleArgs& a, FinishLds& U) {
     for (int q = kPer - 1; q >= 0; --q) {
       const int i = tid * kPer + q;
       if (i >= n_g) continue;
-      const double pre = pre_before + g_base + g_local[q];
-      if (pre >= target) first = (uint32_t)i;
-      if ((pre >= target ? pre - target : target - pre) < mrg) near = true;
+      const double pre = plan.pre_before + g_base + g_local[q];
+      if (pre >= plan.target) first = (uint32_t)i;
+      if ((pre >= plan.target ? pre - plan.target : plan.target - pre) < plan.mrg) near = true;
     }
     first = wave_min_u32(first);
     const bool wn = __ballot(near) != 0;
@@ -2487,8 +2523,342 @@ __device__ __noinline__ uint32_t deep_draw(const SampleArgs& a, FinishLds& U) {
   __syncthreads();
   if (S.route_exact) return kExactRequest | GS_FLAG_NEAR_TIE;
   if (S.first_idx == 0xFFFFFFFFu) return kExactRequest | 0u;
-  if (tid == 0) write_result(a, row, (int32_t)gid[S.first_idx], 0u, S.cand_p[S.first_idx] / total);
+  if (tid == 0) write_result(a, row, (int32_t)gid[S.first_idx], 0u, S.cand_p[S.first_idx] / plan.total);
   return 0;
+}
+
+// A full-vocabulary draw (topK 0, topP 1, no min-p or typical-p) whose cursor
+// lies past the complete region of the chunk lists, or within the scan
+// normaliser's margin of one of its prefix sums (sampling.ts:58-64 over the
+// whole sorted list), on the row's own workgroup. finish_row left the
+// region's candidates in list order with their exact exponentials (cand_p /
+// cand_id, deep_n of them), the row's specials (sp_key / sp_id) and M, u,
+// the region floor and the reference's own rounding margin. One pass over the
+// row's logits below the floor builds a fixed-point mass histogram over value
+// bins (terms within 2^-40 relative), which gives the normaliser and every
+// bin's prefix mass to that accuracy; the region is walked again with them;
+// failing that, the bins the cursor falls in are gathered, sorted by (value
+// desc, id asc), given their exact exponentials and walked. Returns 0 with
+// the result written, or kExactRequest | flags. Unconstrained rows only; the
+// whole block calls it.
+__device__ __noinline__ uint32_t deep_draw(const SampleArgs& a, FinishLds& U) {
+  Shared& S = U.fin;
+  const int64_t row = blockIdx.x;
+  const gs_row_config cfg = a.configs[row];
+  const double T = cfg.temperature;
+  if (!deep_inputs_ok(S, T)) return kExactRequest | 0u;
+  const int n_sp = (int)(S.n_special < (uint32_t)kSpecialCap ? S.n_special : (uint32_t)kSpecialCap);
+  const double rT = 1.0 / T;
+  const double vfc = (double)key_f32(S.deep_thr) / T * ((double)kDeepBins / kDeepSpan);
+  const float l_below = key_f32(S.deep_thr - 1u);
+  deep_setup(S, n_sp, true);
+  // ---- pass 1: the tail's mass per bin
+  const double tail = deep_histogram(a, row, cfg.softcap, T, rT, S.deep_m, l_below, vfc, S.sorted, S.tab);
+  __syncthreads();
+  const uint32_t r = deep_mid(a, S, row, n_sp, tail);
+  if (r != kDeepPass2) return r;
+  // ---- pass 2: stage the logits in the bins' float range (in cand_p)
+  deep_stage(a, row, cfg.softcap, S.plan.l_lo, S.plan.l_top, (uint64_t*)S.cand_p, &S.deep_count);
+  __syncthreads();
+  return deep_final(a, S, row, n_sp);
+}
+
+// ---- the deep draw over many workgroups
+// The finish leaves a deep row's inputs in its DeepRow (the region's
+// candidates, the specials, M, u, the floor, the margin, a zeroed histogram)
+// and queues it. Four launches follow, each one workgroup per compute unit
+// taking items from the queues until they are drained (nothing waits for
+// another workgroup; the launch boundaries order every write before the next
+// launch's reads):
+// - deep1_kernel: pass 1 over a part of a queued row (a run of chunks) into an
+//   LDS histogram, added to the row's with 64-bit global atomics (integers:
+//   the sums do not depend on the order), and the part's last-bin sum;
+// - deep_mid_kernel: per queued row, the histogram and the walk (deep_mid);
+//   a row that needs pass 2 is queued again;
+// - deep2_kernel: pass 2 over a part of such a row, its logits in the plan's
+//   range appended to the row's stage;
+// - deep_final_kernel: per such row, deep_final.
+// Parts are as many per row as there are compute units per queued row (at
+// most one per chunk), so a lone row still spreads over many workgroups.
+
+// The finish workgroup's hand-over of a deep row: 0, or kExactRequest when
+// the inputs are out of the deep draw's range (the whole block calls it).
+__device__ __noinline__ uint32_t deep_export(const SampleArgs& a, Shared& S) {
+  const int tid = threadIdx.x;
+  const int64_t row = blockIdx.x;
+  if (!deep_inputs_ok(S, a.configs[row].temperature)) return kExactRequest | 0u;
+  DeepRow& D = a.deep_rows[row];
+  const int n_reg = (int)S.deep_n;
+  const int n_sp = (int)(S.n_special < (uint32_t)kSpecialCap ? S.n_special : (uint32_t)kSpecialCap);
+  for (int i = tid; i < n_reg; i += kFinishThreads) { D.cand_p[i] = S.cand_p[i]; D.cand_id[i] = S.cand_id[i]; }
+  for (int i = tid; i < n_sp; i += kFinishThreads) { D.sp_key[i] = S.sp_key[i]; D.sp_id[i] = S.sp_id[i]; }
+  for (int b = tid; b < kDeepBins; b += kFinishThreads) D.hist[b] = 0ull;
+  if (tid == 0) {
+    D.M = S.deep_m;
+    D.u = S.deep_u;
+    D.margin = S.deep_margin;
+    D.floor = S.deep_floor;
+    D.thr = S.deep_thr;
+    D.n_reg = (uint32_t)n_reg;
+    D.n_sp = (uint32_t)n_sp;
+    D.n_stage = 0;
+    const uint32_t q = atomicAdd(&a.deep_queue->count1, 1u);
+    a.deep_queue->rows[q] = (uint32_t)row;
+  }
+  return 0;
+}
+
+// The logits of ids [i0, i1) of a row (i0 a multiple of 8), softcapped when
+// cap > 0, as visit(l, id), two 16-byte pieces per thread in flight; kRanged:
+// pieces with no logit in [lo, hi] are skipped after one ballot.
+template <bool kRanged, typename F>
+__device__ __forceinline__ void visit_range(const SampleArgs& a, int64_t row, double cap, int64_t i0, int64_t i1,
+                                            F&& visit, float lo = 0.0f, float hi = 0.0f) {
+  const int tid = threadIdx.x;
+  int64_t from = i0;
+  if (cap > 0) {
+    from = i1;
+#pragma unroll 1
+    for (int64_t i = i0 + tid; i < i1; i += kFinishThreads) visit(softcap_call(load_logit(a, row, i), cap), (uint32_t)i);
+  } else if (a.vector_ok) {
+    const bool bf16 = a.dtype == GS_BF16;
+    const int per = bf16 ? 8 : 4;
+    const int64_t v0 = i0 / per, v1 = i1 / per;
+    const uint4* base = (const uint4*)((const char*)a.logits + row * a.row_stride * (bf16 ? 2 : 4));
+    constexpr int kB = 2;
+    for (int64_t vb = v0 + tid; vb < v1; vb += (int64_t)kB * kFinishThreads) {
+      uint4 w[kB];
+#pragma unroll
+      for (int k = 0; k < kB; ++k) {
+        const int64_t vi = vb + (int64_t)k * kFinishThreads;
+        w[k] = vi < v1 ? base[vi] : make_uint4(0u, 0u, 0u, 0u);
+      }
+#pragma unroll
+      for (int k = 0; k < kB; ++k) {
+        const int64_t vi = vb + (int64_t)k * kFinishThreads;
+        const uint32_t q[4] = {w[k].x, w[k].y, w[k].z, w[k].w};
+        if (kRanged) {
+          bool hit = false;
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            const float x0 = __builtin_bit_cast(float, bf16 ? q[j] << 16 : q[j]);
+            const float x1 = __builtin_bit_cast(float, q[j] & 0xFFFF0000u);
+            hit |= vi < v1 && x0 >= lo && x0 <= hi;
+            if (bf16) hit |= vi < v1 && x1 >= lo && x1 <= hi;
+          }
+          if (!__ballot(hit)) continue;
+        }
+        if (vi >= v1) continue;
+        const uint32_t id0 = (uint32_t)(vi * per);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          if (bf16) {
+            visit(__builtin_bit_cast(float, q[j] << 16), id0 + 2 * j);
+            visit(__builtin_bit_cast(float, q[j] & 0xFFFF0000u), id0 + 2 * j + 1);
+          } else {
+            visit(__builtin_bit_cast(float, q[j]), id0 + j);
+          }
+        }
+      }
+    }
+    from = v1 * per;
+  }
+  for (int64_t i = from + tid; i < i1; i += kFinishThreads) visit(load_logit(a, row, i), (uint32_t)i);
+}
+
+// Parts per queued row when `rows` rows are queued: about one compute unit
+// each, at most one per chunk; chunks_per_part is set to cover the row.
+__device__ __forceinline__ uint32_t deep_parts(const SampleArgs& a, uint32_t rows, uint32_t* chunks_per_part) {
+  const uint32_t nc = (uint32_t)a.n_chunks;
+  uint32_t p = rows ? (uint32_t)a.cu_count / rows : 1u;
+  p = p < 1u ? 1u : (p > nc ? nc : p);
+  const uint32_t cpp = (nc + p - 1u) / p;
+  *chunks_per_part = cpp;
+  return (nc + cpp - 1u) / cpp;
+}
+
+// Takes the next work item (every thread of the block gets it).
+__device__ __forceinline__ uint32_t deep_take(Shared& S, uint32_t* next) {
+  if (threadIdx.x == 0) S.sel[0] = atomicAdd(next, 1u);
+  __syncthreads();
+  const uint32_t item = S.sel[0];
+  __syncthreads();
+  return item;
+}
+
+// The row's inputs back into LDS for deep_mid / deep_final (the whole block).
+__device__ __noinline__ void deep_import(const DeepRow& D, Shared& S, bool with_region) {
+  const int tid = threadIdx.x;
+  const int n_sp = (int)D.n_sp;
+  for (int i = tid; i < n_sp; i += kFinishThreads) { S.sp_key[i] = D.sp_key[i]; S.sp_id[i] = D.sp_id[i]; }
+  if (with_region) {
+    const int n_reg = (int)D.n_reg;
+    for (int i = tid; i < n_reg; i += kFinishThreads) { S.cand_p[i] = D.cand_p[i]; S.cand_id[i] = D.cand_id[i]; }
+  }
+  if (tid == 0) {
+    S.deep_m = D.M;
+    S.deep_u = D.u;
+    S.deep_margin = D.margin;
+    S.deep_floor = D.floor;
+    S.deep_thr = D.thr;
+    S.deep_n = D.n_reg;
+  }
+  __syncthreads();
+}
+
+// Pass 1 over ids [i0, i1) of a queued row: its logits below the region
+// floor into an LDS histogram, added to the row's global one, and the part's
+// last-bin sum into tail[part] (the whole block calls it).
+__device__ __noinline__ void deep1_part(const SampleArgs& a, Shared& S, int64_t row, int part, int64_t i0,
+                                        int64_t i1) {
+  const int tid = threadIdx.x;
+  DeepRow& D = a.deep_rows[row];
+  const gs_row_config cfg = a.configs[row];
+  const double T = cfg.temperature, rT = 1.0 / T;
+  const double M = D.M;
+  const uint32_t thr = D.thr;
+  const double vfc = (double)key_f32(thr) / T * ((double)kDeepBins / kDeepSpan);
+  const float l_below = key_f32(thr - 1u);
+  uint64_t* mass = S.sorted;
+  for (int b = tid; b < kDeepBins; b += kFinishThreads) mass[b] = 0ull;
+  if (tid < 256) S.tab[tid] = c_exp2_256[tid];
+  __syncthreads();
+  double tail = 0.0;
+  visit_range<false>(a, row, cfg.softcap, i0, i1, [&](float l, uint32_t) {
+    if (!(l > -__builtin_inff() && l <= l_below)) return;
+    deep_add(div_by_temperature((double)l, T, rT), vfc, M, S.tab, mass, &tail, false);
+  });
+  double t_all;
+  block_scan_f64(tail, S.wtmp, &t_all);
+  __syncthreads();
+  for (int b = tid; b < kDeepBins; b += kFinishThreads) {
+    const uint64_t m = mass[b];
+    if (m) atomicAdd((unsigned long long*)&D.hist[b], (unsigned long long)m);
+  }
+  if (tid == 0) D.tail[part] = t_all;
+}
+
+__global__ __launch_bounds__(kFinishThreads) void deep1_kernel(SampleArgs) {
+  __shared__ FinishLds U;
+  Shared& S = U.fin;
+  // the arguments read where the kernel received them (never copied to the stack)
+  const SampleArgs& a = *(const SampleArgs*)__builtin_amdgcn_kernarg_segment_ptr();
+  uint32_t cpp;
+  const uint32_t parts = deep_parts(a, a.deep_queue->count1, &cpp);
+  const uint32_t n_items = a.deep_queue->count1 * parts;
+  for (;;) {
+    const uint32_t item = deep_take(S, &a.deep_queue->next1);
+    if (item >= n_items) break;
+    const int64_t row = a.deep_queue->rows[item / parts];
+    const int part = (int)(item % parts);
+    const int64_t i0 = (int64_t)part * cpp * kChunk;
+    const int64_t i1 = i0 + (int64_t)cpp * kChunk < (int64_t)a.vocab ? i0 + (int64_t)cpp * kChunk : (int64_t)a.vocab;
+    deep1_part(a, S, row, part, i0, i1);
+    __syncthreads();
+  }
+}
+
+// Per queued row: the histogram and the walk; a row that needs pass 2 is
+// queued for it (the whole block calls it).
+__device__ __noinline__ uint32_t deep_mid_row(const SampleArgs& a, Shared& S, int64_t row, uint32_t parts) {
+  const int tid = threadIdx.x;
+  DeepRow& D = a.deep_rows[row];
+  deep_import(D, S, true);
+  for (int b = tid; b < kDeepBins; b += kFinishThreads) S.sorted[b] = D.hist[b];
+  deep_setup(S, (int)D.n_sp, false);
+  const double tail = tid < (int)parts ? D.tail[tid] : 0.0;
+  const uint32_t r = deep_mid(a, S, row, (int)D.n_sp, tail);
+  if (r != kDeepPass2) return r;
+  if (tid == 0) {
+    D.plan = S.plan;
+    const uint32_t q = atomicAdd(&a.deep_queue->count2, 1u);
+    a.deep_queue->rows[a.deep_max_rows + q] = (uint32_t)row;
+  }
+  return 0;
+}
+
+__global__ __launch_bounds__(kFinishThreads) void deep_mid_kernel(SampleArgs) {
+  __shared__ FinishLds U;
+  Shared& S = U.fin;
+  const SampleArgs& a = *(const SampleArgs*)__builtin_amdgcn_kernarg_segment_ptr();
+  uint32_t cpp;
+  const uint32_t parts = deep_parts(a, a.deep_queue->count1, &cpp);
+  const uint32_t n_rows = a.deep_queue->count1;
+  for (uint32_t i = blockIdx.x; i < n_rows; i += gridDim.x) {
+    const int64_t row = a.deep_queue->rows[i];
+    const uint32_t r = deep_mid_row(a, S, row, parts);
+    if (r & kExactRequest) to_exact(a, U, row, r & ~kExactRequest);
+    __syncthreads();
+  }
+}
+
+// Pass 2 over ids [i0, i1) of a queued row: its logits in the plan's float
+// range into the row's stage (one global atomic per wave and logit position;
+// at most kFinishCap kept, all counted). The whole block calls it.
+__device__ __noinline__ void deep2_part(const SampleArgs& a, int64_t row, int64_t i0, int64_t i1) {
+  const int lane = threadIdx.x & 63;
+  DeepRow& D = a.deep_rows[row];
+  const float l_lo = D.plan.l_lo, l_top = D.plan.l_top;
+  visit_range<true>(a, row, a.configs[row].softcap, i0, i1, [&](float l, uint32_t id) {
+    const bool pass = l >= l_lo && l <= l_top;
+    const uint64_t m = __ballot(pass);
+    if (m == 0) return;
+    const int leader = __builtin_ctzll(m);
+    uint32_t base = 0;
+    if (lane == leader) base = atomicAdd(&D.n_stage, (uint32_t)__popcll(m));
+    base = (uint32_t)__shfl((int)base, leader, 64);
+    const uint32_t pos = base + (uint32_t)__popcll(m & ((1ull << lane) - 1ull));
+    if (pass && pos < (uint32_t)kFinishCap) D.stage[pos] = ((uint64_t)__builtin_bit_cast(uint32_t, l) << 32) | id;
+  }, l_lo, l_top);
+}
+
+__global__ __launch_bounds__(kFinishThreads) void deep2_kernel(SampleArgs) {
+  __shared__ FinishLds U;
+  Shared& S = U.fin;
+  const SampleArgs& a = *(const SampleArgs*)__builtin_amdgcn_kernarg_segment_ptr();
+  uint32_t cpp;
+  const uint32_t parts = deep_parts(a, a.deep_queue->count2, &cpp);
+  const uint32_t n_items = a.deep_queue->count2 * parts;
+  for (;;) {
+    const uint32_t item = deep_take(S, &a.deep_queue->next2);
+    if (item >= n_items) break;
+    const int64_t row = a.deep_queue->rows[a.deep_max_rows + item / parts];
+    const int64_t i0 = (int64_t)(item % parts) * cpp * kChunk;
+    const int64_t i1 = i0 + (int64_t)cpp * kChunk < (int64_t)a.vocab ? i0 + (int64_t)cpp * kChunk : (int64_t)a.vocab;
+    deep2_part(a, row, i0, i1);
+    __syncthreads();
+  }
+}
+
+// Per row queued for pass 2: the exact test, the sort and the walk (the whole
+// block calls it).
+__device__ __noinline__ uint32_t deep_final_row(const SampleArgs& a, Shared& S, int64_t row) {
+  const int tid = threadIdx.x;
+  const DeepRow& D = a.deep_rows[row];
+  deep_import(D, S, false);
+  deep_setup(S, (int)D.n_sp, false);
+  const uint32_t n_stage = D.n_stage;
+  const int n_keep = (int)(n_stage < (uint32_t)kFinishCap ? n_stage : (uint32_t)kFinishCap);
+  for (int i = tid; i < n_keep; i += kFinishThreads) ((uint64_t*)S.cand_p)[i] = D.stage[i];
+  if (tid == 0) {
+    S.plan = D.plan;
+    S.deep_count = n_stage;
+  }
+  __syncthreads();
+  return deep_final(a, S, row, (int)D.n_sp);
+}
+
+__global__ __launch_bounds__(kFinishThreads) void deep_final_kernel(SampleArgs) {
+  __shared__ FinishLds U;
+  Shared& S = U.fin;
+  const SampleArgs& a = *(const SampleArgs*)__builtin_amdgcn_kernarg_segment_ptr();
+  const uint32_t n_rows = a.deep_queue->count2;
+  for (uint32_t i = blockIdx.x; i < n_rows; i += gridDim.x) {
+    const int64_t row = a.deep_queue->rows[a.deep_max_rows + i];
+    const uint32_t r = deep_final_row(a, S, row);
+    if (r & kExactRequest) to_exact(a, U, row, r & ~kExactRequest);
+    __syncthreads();
+  }
 }
 
 __global__ __launch_bounds__(kFinishThreads) void finish_kernel(SampleArgs a) {
@@ -2496,9 +2866,11 @@ __global__ __launch_bounds__(kFinishThreads) void finish_kernel(SampleArgs a) {
   uint32_t r = finish_row(a, U);
   if (r == kDeepRequest) {
     __syncthreads();
-    // a call of its own that reads the arguments where the kernel received
-    // them, so the kernel's copy never goes to the stack
-    r = deep_draw(*(const SampleArgs*)__builtin_amdgcn_kernarg_segment_ptr(), U);
+    // calls of their own that read the arguments where the kernel received
+    // them, so the kernel's copy never goes to the stack; with deep records
+    // the deep kernels take the row from here
+    const SampleArgs& ka = *(const SampleArgs*)__builtin_amdgcn_kernarg_segment_ptr();
+    r = a.deep_rows ? deep_export(ka, U.fin) : deep_draw(ka, U);
   }
   // the exact path is entered from here only, where nothing else is live
   if (r & kExactRequest) to_exact(a, U, blockIdx.x, r & ~kExactRequest);
@@ -2508,6 +2880,16 @@ __global__ __launch_bounds__(kFinishThreads) void finish_kernel(SampleArgs a) {
 
 void launch_finish(const SampleArgs& a, hipStream_t s, LaunchEvents ev) {
   hipExtLaunchKernelGGL(finish_kernel, dim3(a.rows), dim3(kFinishThreads), 0, s, ev.start, ev.stop, 0, a);
+}
+
+void launch_deep(const SampleArgs& a, hipStream_t s, LaunchEvents ev) {
+  // one workgroup per compute unit (each holds the finish's LDS), taking items
+  // until the queues are drained
+  const dim3 grid(a.cu_count), block(kFinishThreads);
+  hipExtLaunchKernelGGL(deep1_kernel, grid, block, 0, s, ev.start, nullptr, 0, a);
+  hipExtLaunchKernelGGL(deep_mid_kernel, grid, block, 0, s, nullptr, nullptr, 0, a);
+  hipExtLaunchKernelGGL(deep2_kernel, grid, block, 0, s, nullptr, nullptr, 0, a);
+  hipExtLaunchKernelGGL(deep_final_kernel, grid, block, 0, s, nullptr, ev.stop, 0, a);
 }
 
 }  // namespace gs

@@ -177,6 +177,37 @@ struct ExactQueue {
   uint32_t rows[1];
 };
 
+// The multi-workgroup deep draw (full-vocabulary draws whose cursor falls
+// past the finish's region): the finish leaves each such row's inputs in a
+// DeepRow and queues the row; the deep kernels then split its two passes
+// over the row's logits into parts (runs of chunks) across workgroups, with
+// a launch per row in between and after.
+constexpr int kDeepBins = 4096;  // value bins of the deep draw's tail histogram
+struct DeepPlan {
+  double total, target, mrg, pre_before;  // the normaliser, the cursor, the margin, the mass before b_lo
+  float l_lo, l_top;                      // the logit range pass 2 stages
+  int32_t b_lo, b_hi;                     // the bins the cursor falls in
+};
+struct DeepRow {
+  double M, u, margin;   // the row's maximum value, its uniform, the reference's rounding margin
+  uint64_t floor;        // the region floor's value key
+  uint32_t thr, n_reg, n_sp, pad;  // the region floor's logit key, region candidates, specials
+  DeepPlan plan;
+  uint32_t n_stage, pad2;                // pass-2 entries staged
+  double tail[kFinishMaxChunks];         // pass 1: each part's last-bin sum
+  uint64_t hist[kDeepBins];              // pass 1: bin sums in fixed point (global atomics)
+  double cand_p[kFinishCap];             // the region's candidates: exact exponentials
+  uint32_t cand_id[kFinishCap];
+  uint64_t sp_key[kSpecialCap];          // the row's specials
+  uint32_t sp_id[kSpecialCap];
+  uint64_t stage[kFinishCap];            // pass 2: logits in the plan's range (value bits << 32 | id)
+};
+struct DeepQueue {
+  uint32_t count1, next1;  // rows queued for pass 1, its work items taken
+  uint32_t count2, next2;  // rows queued for pass 2, its work items taken
+  uint32_t rows[1];        // [2 * max rows]: pass-1 rows, then pass-2 rows
+};
+
 // Arguments every sampling kernel reads.
 struct SampleArgs {
   const void* logits;
@@ -204,6 +235,9 @@ struct SampleArgs {
   int64_t exact_slot_bytes;
   int64_t exact_capacity;  // entries per slot (power of two >= vocab)
   int32_t cu_count;        // compute units of the device
+  DeepRow* deep_rows;      // [rows], or null: the finish's own workgroup takes its deep draws
+  DeepQueue* deep_queue;
+  int32_t deep_max_rows;   // pass-2 rows start at deep_queue->rows + deep_max_rows
 };
 
 // --------------------------------------------------------- wave helpers
@@ -456,6 +490,7 @@ void launch_scan(const SampleArgs& a, hipStream_t s, LaunchEvents ev = {});
 void launch_exp2_check(uint32_t first, uint32_t count, unsigned long long* worst, hipStream_t s);
 void launch_finish(const SampleArgs& a, hipStream_t s, LaunchEvents ev = {});
 void launch_exact(const SampleArgs& a, hipStream_t s, LaunchEvents ev = {});
+void launch_deep(const SampleArgs& a, hipStream_t s, LaunchEvents ev = {});
 void launch_logprob(const void* logits, int32_t dtype, int32_t rows, int64_t stride, int32_t vocab,
                     const int32_t* tokens, double* out, hipStream_t s);
 void launch_mask_logits(const float* raw, int64_t n, const int32_t* ids, int64_t n_ids, float* out, hipStream_t s);

@@ -609,13 +609,19 @@ __global__ __launch_bounds__(kScanThreads, (scan_wg_per_cu<In, kMaskable>())) vo
       }
     }
   }
-  // reset the queue the finish kernel fills for the exact kernel (both run
-  // after this kernel on the same stream). It is the kernel's last store, so
-  // the loads above of the row's options and history offsets may use the
-  // scalar cache.
+  // reset the queues the finish kernel fills for the exact and deep kernels
+  // (all run after this kernel on the same stream). It is the kernel's last
+  // store, so the loads above of the row's options and history offsets may
+  // use the scalar cache.
   if (row == 0 && blockIdx.x == 0 && threadIdx.x == 0) {
     a.queue->count = 0;
     a.queue->next = 0;
+    if (a.deep_queue) {
+      a.deep_queue->count1 = 0;
+      a.deep_queue->next1 = 0;
+      a.deep_queue->count2 = 0;
+      a.deep_queue->next2 = 0;
+    }
   }
 }
 

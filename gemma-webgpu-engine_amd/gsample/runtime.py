@@ -22,6 +22,7 @@ GS_F32, GS_BF16 = 0, 1
 GS_QAT_ROW_MAJOR, GS_QAT_BLOCK_MAJOR = 0, 1
 GS_RNG_SEEDED, GS_RNG_EXPLICIT = 0, 1
 GS_ROW_FORCE_EXACT = 1
+GS_BATCH_FULL_DRAWS = 1  # gs_batch.hints: a row may take a full-vocabulary draw
 GS_FORCED_TERMINATION, GS_FORCED_EXTRA = 1, 2
 GS_FLAG_TOPP_TIE = 1
 GS_FLAG_EXACT_PATH = 2
@@ -87,7 +88,7 @@ class Batch(C.Structure):
         ("forced_kinds", C.c_void_p),
         ("mask_table", C.c_void_p),
         ("mask_slots", C.c_int32),
-        ("reserved", C.c_int32),
+        ("hints", C.c_int32),
         ("results", C.c_void_p),
     ]
 
@@ -112,7 +113,7 @@ EXPORTED_SYMBOLS = (
 )
 
 # kernel stages reported by gs_timing_end (include/gsample.h GS_STAGE_*)
-STAGES = ("lmhead", "scan", "finish", "exact")
+STAGES = ("lmhead", "scan", "finish", "exact", "deep")
 
 _lib = None
 
@@ -232,6 +233,15 @@ class SampleOutput:
     flags: np.ndarray
 
 
+def full_draw_rows(cfg: np.ndarray) -> bool:
+    """Whether any packed row config may take a full-vocabulary draw
+    (temperature > 0, topK 0, topP 1, no min-p or typical-p, no mask): the
+    batch hint GS_BATCH_FULL_DRAWS (include/gsample.h)."""
+    c = np.asarray(cfg).reshape(-1)
+    return bool(np.any((c["temperature"] > 0) & (c["top_k"] <= 0) & (c["top_p"] >= 1) & ~(c["min_p"] > 0)
+                       & (c["typical_p"] >= 1) & (c["mask_slot"] < 0)))
+
+
 def _csr(lists: Optional[Sequence[Sequence[int]]], rows: int):
     if lists is None:
         return None, None
@@ -295,8 +305,11 @@ class Sampler:
         self._check(self.lib.gs_validate_configs(self.ctx, _np_ptr(cfg), cfg.size))
 
     # -- batched sampling ------------------------------------------------
-    def prepare(self, logits, configs: np.ndarray, histories=None, forced=None, mask_table=None):
-        """Device-side batch for gs_sample; returns (Batch, keepalive)."""
+    def prepare(self, logits, configs: np.ndarray, histories=None, forced=None, mask_table=None,
+                hints: Optional[int] = None):
+        """Device-side batch for gs_sample; returns (Batch, keepalive). hints:
+        the GS_BATCH_* bits, by default GS_BATCH_FULL_DRAWS when a row may take
+        a full-vocabulary draw."""
         torch = self.torch
         rows = int(logits.shape[0])
         if logits.dtype == torch.float32:
@@ -322,6 +335,7 @@ class Sampler:
         b.dtype = dtype
         b.rows = rows
         b.configs = d_cfg.data_ptr()
+        b.hints = (GS_BATCH_FULL_DRAWS if full_draw_rows(cfg) else 0) if hints is None else int(hints)
         if histories is not None:
             if isinstance(histories, tuple):
                 off, ids = histories
@@ -354,8 +368,8 @@ class Sampler:
         self._check(self.lib.gs_sample(self.ctx, C.byref(batch), C.c_void_p(stream or 0)))
 
     def sample(self, logits, configs: np.ndarray, histories=None, forced=None, mask_table=None,
-               raise_on_failure: bool = True) -> SampleOutput:
-        b, keep = self.prepare(logits, configs, histories, forced, mask_table)
+               raise_on_failure: bool = True, hints: Optional[int] = None) -> SampleOutput:
+        b, keep = self.prepare(logits, configs, histories, forced, mask_table, hints)
         self.torch.cuda.current_stream(self.device).synchronize()
         out = np.zeros(b.rows, dtype=RESULT_DTYPE)
         st = self.lib.gs_sample_sync(self.ctx, C.byref(b), _np_ptr(out))

@@ -34,7 +34,7 @@ const FLAGS = Object.freeze({
   INVALID_SLOT: 256,
 });
 
-const STAGES = Object.freeze(["lmhead", "scan", "finish", "exact"]);
+const STAGES = Object.freeze(["lmhead", "scan", "finish", "exact", "deep"]);
 
 let layoutCache = null;
 function layouts() {

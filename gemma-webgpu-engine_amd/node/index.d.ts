@@ -128,7 +128,7 @@ export const FLAGS: {
   readonly TOPP_TIE: 1; readonly EXACT_PATH: 2; readonly NEAR_TIE: 4; readonly DEAD_END: 8;
   readonly NONFINITE: 16; readonly EMPTY_CANDIDATES: 32; readonly GREEDY: 64; readonly UNSUPPORTED: 128;
 };
-export const STAGES: readonly ["lmhead", "scan", "finish", "exact"];
+export const STAGES: readonly ["lmhead", "scan", "finish", "exact", "deep"];
 
 export class DeviceBuffer {
   readonly bytes: number;
@@ -162,7 +162,7 @@ export class Engine {
   lmheadSample(hidden: DeviceBuffer, weight: DeviceBuffer, width: number, softcap: number, scratch: DeviceBuffer,
                request: SampleRequest): SampleResult;
   timingBegin(maxCalls: number): void;
-  timingEnd(): Record<"lmhead" | "scan" | "finish" | "exact", [number, number]>;
+  timingEnd(): Record<"lmhead" | "scan" | "finish" | "exact" | "deep", [number, number]>;
 }
 
 export const ADDON_PATH: string;

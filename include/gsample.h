@@ -24,7 +24,7 @@
 extern "C" {
 #endif
 
-#define GSAMPLE_ABI_VERSION 1
+#define GSAMPLE_ABI_VERSION 2
 
 typedef enum gs_status {
   GS_OK = 0,
@@ -111,9 +111,18 @@ typedef struct gs_batch {
   const uint8_t* forced_kinds;       /* GS_FORCED_* per forced id */
   const uint32_t* mask_table;        /* [slots][ceil(V/32)] legal-token bitmasks (gs_build_masks) */
   int32_t mask_slots;
-  int32_t reserved;
+  int32_t hints;                     /* GS_BATCH_* bits (0: none) */
   gs_row_result* results;            /* [rows] */
 } gs_batch;
+
+/* Batch hint: some row may take a full-vocabulary draw (temperature > 0,
+ * topK 0, topP 1, no min-p or typical-p, no mask). Such a draw whose cursor
+ * falls past the candidates the finish ranks is then spread over many
+ * workgroups by four more launches (stage GS_STAGE_DEEP) instead of taking
+ * the row's one workgroup; the results are identical either way. Without
+ * the hint those launches are skipped. gs_sample_host sets it itself from
+ * its host configs. */
+#define GS_BATCH_FULL_DRAWS 1
 
 /* Library / device identity. */
 int gs_abi_version(void);
@@ -311,7 +320,8 @@ int gs_check_exp2(gs_context* ctx, float lo, float hi, double* max_rel_err, floa
 #define GS_STAGE_SCAN 1   /* scan_kernel: the one HBM pass over the logits */
 #define GS_STAGE_FINISH 2 /* finish_kernel: per-row merge, filters and draw */
 #define GS_STAGE_EXACT 3  /* exact_kernel: replay of rows beyond the context's exact slots */
-#define GS_STAGE_COUNT 4
+#define GS_STAGE_DEEP 4   /* deep1_kernel .. deep_final_kernel: full-vocabulary draws over many workgroups */
+#define GS_STAGE_COUNT 5
 int gs_timing_begin(gs_context* ctx, int32_t max_calls);
 int gs_timing_end(gs_context* ctx, double* stage_ms, int32_t* calls);
 

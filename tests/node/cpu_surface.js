@@ -23,7 +23,7 @@ const ADDON_FUNCTIONS = [
 test("addon loads and exports every entry point", () => {
   const a = g.native();
   for (const name of ADDON_FUNCTIONS) assert.strictEqual(typeof a[name], "function", name);
-  assert.strictEqual(a.abiVersion(), 1);
+  assert.strictEqual(a.abiVersion(), 2);
   const L = a.layouts();
   assert.strictEqual(L.rowConfig.size, 112);
   assert.strictEqual(L.rowResult.size, 16);

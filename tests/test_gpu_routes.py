@@ -90,7 +90,8 @@ def test_full_vocabulary_draws_bf16_and_softcap(sampler, oracle):
     """Full-vocabulary draws whose cursors sit deep in the tail (u near 1),
     so that most rows take the deep draw: bf16 rows (its gather reads eight
     logits per 16-byte piece), and f32 and bf16 rows with softcap 30 (the
-    capped loop), each against the oracle on the same values."""
+    capped loop), each against the oracle on the same values, once with the
+    deep draws spread over many workgroups and once on each row's own."""
     import torch
 
     gs = _gs()
@@ -106,10 +107,14 @@ def test_full_vocabulary_draws_bf16_and_softcap(sampler, oracle):
     for label, dev, xin, cap in (("bf16", dev_b, xb, 0.0), ("f32 softcap", torch.from_numpy(w.logits).cuda(),
                                                          w.logits, 30.0), ("bf16 softcap", dev_b, xb, 30.0)):
         conf = np.stack([gs.runtime.row_config(c, uniform=u, softcap_value=cap) for c, u in zip(cfgs, us)])
-        out = sampler.sample(dev, conf)
         vals = [oracle.softcap(xin[r], cap) if cap > 0 else xin[r] for r in range(n)]
-        check(gs, oracle, label, out, vals, None, cfgs, us)
-        deep += int(np.sum((out.flags & gs.GS_FLAG_EXACT_PATH) == 0))
+        # the deep draw over many workgroups (the batch hint), then on each
+        # row's own workgroup (no hint): the same ids
+        outs = [sampler.sample(dev, conf), sampler.sample(dev, conf, hints=0)]
+        for tag, out in zip(("multi", "single"), outs):
+            check(gs, oracle, f"{label} {tag}", out, vals, None, cfgs, us)
+            deep += int(np.sum((out.flags & gs.GS_FLAG_EXACT_PATH) == 0))
+        assert np.array_equal(outs[0].tokens, outs[1].tokens)
     assert deep > 0
 
 
