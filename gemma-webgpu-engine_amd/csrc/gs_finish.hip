@@ -296,19 +296,24 @@ __device__ __forceinline__ int top_select_shift(uint32_t lo, uint32_t hi) {
 // The slow path's ranking boundary (the comment at its call says why it is
 // one): over the region s[0..n_ns) in LDS (keys in [sel_lo, sel_hi]) and the
 // region's specials in_key[0..n_sp_in), the key above which either the first
-// topK candidates (counting non-specials only) or a mass of
-// (topP + 2 margin) total (scaled down by 2^-10) lies; 0 when none is met in
+// topK candidates (counting non-specials only) or a mass of want_mass
+// (scaled down by 2^-10; infinite: no such bound) lies; 0 when none is met in
 // the region or the boundary keeps all of it. Its non-specials are compacted
-// into out[0..sel[3]). hist: 256 counters, zero on entry and on return; bmass:
-// 256 words of scratch. Called by the whole block; ends with a barrier.
+// into out[0..sel[3]). *region_mass: the region's mass e^(v - M) summed in
+// binary32 terms (within 1e-5 relative), infinite when not summed. hist: 256
+// counters, zero on entry and on return; bmass: 256 words of scratch. Called
+// by the whole block; ends with a barrier.
 __device__ __forceinline__ uint32_t prefix_floor(const uint64_t* region, int n_ns, const uint64_t* in_key, int n_sp_in,
                                               uint32_t sel_lo, uint32_t sel_hi, double T, double M, int top_k,
-                                              double top_p, double margin, double total, uint32_t* hist,
-                                              uint64_t* bmass, uint32_t* sel, uint64_t* out) {
+                                              double want_mass, uint32_t* hist, uint64_t* bmass, uint32_t* sel,
+                                              uint64_t* out, double* region_mass) {
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const bool by_rank = top_k > 0 && top_k < n_ns + n_sp_in;
-  const bool by_mass = top_p < 1;
-  if (!(by_rank || by_mass) || n_ns <= kPrefixMin) return 0;
+  const bool by_mass = want_mass < __builtin_inf();
+  if (!(by_rank || by_mass) || n_ns <= kPrefixMin) {
+    if (tid == 0) *region_mass = __builtin_inf();
+    return 0;
+  }
   const int shift = top_select_shift(sel_lo, sel_hi);
   // masses in units of 2^-40 e^0 (integer LDS atomics: binary32 ones
   // serialise badly)
@@ -325,16 +330,15 @@ __device__ __forceinline__ uint32_t prefix_floor(const uint64_t* region, int n_n
     atomicAdd((unsigned long long*)&bmass[bin], mass_units(x));
   }
   // the region's specials add mass (not count) to the bin of a key no
-  // higher than their value times T: a boundary at or below that bin keeps
-  // them among the ranked candidates
+  // higher than their value times T (the lowest bin below sel_lo): a
+  // boundary at or below that bin keeps them among the ranked candidates
   for (int j = tid; j < n_sp_in; j += kFinishThreads) {
     const double v = key_f64(in_key[j]);
     const double l = v * T;
     const double l_lo = l - (l < 0 ? -l : l) * 0x1p-40;
     const float lf = (float)l_lo;
     const uint32_t key = f32_key(lf) - ((double)lf > l_lo ? 1u : 0u);
-    if (key < sel_lo) continue;
-    const uint32_t d = (key - sel_lo) >> shift;
+    const uint32_t d = key < sel_lo ? 0u : (key - sel_lo) >> shift;
     const uint32_t bin = d < 255u ? d : 255u;
     atomicAdd((unsigned long long*)&bmass[bin], mass_units((float)(v - M)));
   }
@@ -352,8 +356,9 @@ __device__ __forceinline__ uint32_t prefix_floor(const uint64_t* region, int n_n
     }
     const uint32_t incl = wave_scan_u32(c);
     const double mincl = wave_scan_f64(ms);
+    if (lane == 63) *region_mass = mincl;
     const uint32_t want_n = by_rank ? (uint32_t)top_k : 0xFFFFFFFFu;
-    const double want_m = by_mass ? (top_p + 2.0 * margin) * total : __builtin_inf();
+    const double want_m = want_mass;
     constexpr double kUnder = 1.0 - 0x1p-10;
     // the boundary bin of each bound (-1: not met in the region)
     int bn = -1, bm = -1;
@@ -657,6 +662,7 @@ struct Shared {
   uint32_t exact_flags;
   uint64_t best_entry;
   uint32_t short_sum;  // the slow path's ranked candidates end short of the pool's end
+  double pre_mass;     // the slow path's region mass estimate
 };
 
 __device__ void enqueue_exact(const SampleArgs& a, int64_t row, uint32_t flags) {
@@ -1843,11 +1849,42 @@ __device__ __forceinline__ uint32_t finish_row(const SampleArgs& a, FinishLds& U
   // them all. The top-p pass checks the mass it sums over them.
   int n_pre = n_ns, n_sp_pre = n_sp_in;
   bool pre_cut = false;  // the ranked candidates end before the region does
+  // a draw whose pool is the whole row (the draw's margin as below)
+  const bool draw_pool = cfg.top_p >= 1 && cfg.top_k <= 0 && !(cfg.min_p > 0) && !constrained;
+  const double u_draw = cfg.rng_mode == GS_RNG_EXPLICIT ? cfg.uniform : gsm::mulberry32_draw(cfg.seed, cfg.draw_index);
+  const double draw_margin = margin + full_mass_rel + kNearTie;
   {
     uint64_t* scratch = (uint64_t*)S.cand_p;
     need_region();
-    const uint32_t floor_key = prefix_floor(S.sorted, n_ns, in_key, n_sp_in, sel_lo, sel_hi, T, M, cfg.top_k,
-                                            cfg.top_p, margin, total, S.hist, (uint64_t*)S.tab, S.sel, scratch);
+    // a full-vocabulary draw ranks up to its cursor u, by twice the draw's margin
+    const double want_m = cfg.top_p < 1 ? (cfg.top_p + 2.0 * margin) * total
+                                        : (draw_pool ? (u_draw + 2.0 * draw_margin) * total : __builtin_inf());
+    const uint32_t floor_key = prefix_floor(S.sorted, n_ns, in_key, n_sp_in, sel_lo, sel_hi, T, M, cfg.top_k, want_m,
+                                            S.hist, (uint64_t*)S.tab, S.sel, scratch, &S.pre_mass);
+    if (draw_pool && n_ns + n_sp_in <= kFinishCap &&
+        S.pre_mass * (1.0 + 0x1p-10) + 1e-30 < (u_draw - 2.0 * draw_margin) * total) {
+      // the cursor lies past the region, with room: the deep draw needs only
+      // the candidates' exact terms, in any order
+      for (int i = tid; i < n_ns; i += kFinishThreads) {
+        const uint64_t e = S.sorted[i];
+        S.cand_p[i] = gsm::js_exp(nonspecial_value(e, T) - M);
+        S.cand_id[i] = entry_id(e);
+      }
+      for (int j = tid; j < n_sp_in; j += kFinishThreads) {
+        S.cand_p[n_ns + j] = gsm::js_exp(key_f64(in_key[j]) - M);
+        S.cand_id[n_ns + j] = in_id[j];
+      }
+      if (tid == 0) {
+        S.deep_m = M;
+        S.deep_u = u_draw;
+        S.deep_thr = thr;
+        S.deep_floor = region_floor;
+        S.deep_n = (uint32_t)(n_ns + n_sp_in);
+        S.deep_margin = full_mass_rel + kNearTie;
+      }
+      __syncthreads();
+      return kDeepRequest;
+    }
     if (floor_key) {
       n_pre = (int)S.sel[3];
       // specials at or above the boundary's value (in_key is descending)
@@ -2015,7 +2052,7 @@ __device__ __forceinline__ uint32_t finish_row(const SampleArgs& a, FinishLds& U
   // ---- draw (sampling.ts:58-64): first i with prefix_i >= u * sum_{j<n} p_j
   // (with a full pool: u * 1, the prefix sums carrying the normaliser's error,
   // settled again with the recomputed normaliser when within that margin)
-  const double u = cfg.rng_mode == GS_RNG_EXPLICIT ? cfg.uniform : gsm::mulberry32_draw(cfg.seed, cfg.draw_index);
+  const double u = u_draw;
   {
     double local[kPer];
     double s = 0.0;
@@ -2041,6 +2078,9 @@ __device__ __forceinline__ uint32_t finish_row(const SampleArgs& a, FinishLds& U
       if (pre >= cursor) my_first = (uint32_t)i;
       const double d = pre >= cursor ? pre - cursor : cursor - pre;
       if (d < dmargin) my_near = true;
+      // ranked candidates that end before the pool does settle the draw only
+      // when their sum passes the cursor by twice the margin
+      if (i == n - 1 && pre_cut && !(pre >= cursor + 2.0 * dmargin)) S.short_sum = 1u;
     }
     my_first = wave_min_u32(my_first);
     const bool wave_near = __ballot(my_near) != 0;
@@ -2049,7 +2089,7 @@ __device__ __forceinline__ uint32_t finish_row(const SampleArgs& a, FinishLds& U
       if (wave_near) atomicOr(&S.route_exact, 8u);
     }
     __syncthreads();
-    if (full_mass && !constrained && (S.route_exact == 8u || S.first_idx == 0xFFFFFFFFu)) {
+    if (full_mass && !constrained && !pre_cut && (S.route_exact == 8u || S.first_idx == 0xFFFFFFFFu)) {
       // a full-vocabulary draw within the scan normaliser's margin or past
       // the region: the deep draw takes it from the region's candidates
       if (tid == 0) {
@@ -2062,8 +2102,8 @@ __device__ __forceinline__ uint32_t finish_row(const SampleArgs& a, FinishLds& U
       }
       return kDeepRequest;
     }
-    if (S.route_exact || S.first_idx == 0xFFFFFFFFu) {
-      // a near tie, or a full-vocabulary draw past the region
+    if (S.route_exact || S.first_idx == 0xFFFFFFFFu || S.short_sum) {
+      // a near tie, or a full-vocabulary draw past the ranked candidates
       return kExactRequest | (S.route_exact ? GS_FLAG_NEAR_TIE : 0u);
     }
     if (tid == 0) {
@@ -2293,6 +2333,43 @@ __device__ __forceinline__ bool deep_inputs_ok(const Shared& S, double T) {
   return vf <= S.deep_m && T >= 0x1p-20 && T <= 0x1p20;
 }
 
+// The deep draw's exact masses: the region's (over cand_p[0..n_reg)) into
+// *r_total, and after[b] (over the histogram in sorted, in place) the mass of
+// the region and of bins 0 .. b, in binary64 from exact fixed-point sums of
+// the bins' masses (units x 2^-40 x e^(c_b - M), the last bin tail_mass).
+// Returns the normaliser. The whole block calls it.
+__device__ __noinline__ double deep_prefix_masses(Shared& S, int n_reg, double tail_mass, double vf, double M,
+                                                  double* r_total) {
+  const int tid = threadIdx.x;
+  constexpr int kPer = kFinishCap / kFinishThreads;  // region entries per thread (and bins)
+  static_assert(kDeepBins == kFinishCap, "kPer bins per thread");
+  const uint64_t* mass = S.sorted;
+  Fix128 r_fix{0ull, 0ull};
+  for (int i = tid; i < n_reg; i += kFinishThreads) r_fix = fix_add(r_fix, fix_of(S.cand_p[i]));
+  r_fix = block_fix_sum(r_fix, (uint64_t*)S.top);
+  *r_total = fix_to_double(r_fix);
+  double* after = (double*)S.sorted;
+  Fix128 f[kPer];
+  Fix128 sum{0ull, 0ull};
+#pragma unroll
+  for (int q = 0; q < kPer; ++q) {
+    const int b = tid * kPer + q;
+    double m = tail_mass;
+    if (b < kDeepBins - 1) {
+      // e^(c_b - M), c_b = vf - (b + 1/2) w
+      const double y = __builtin_fma(-(b + 0.5), kDeepSpan / kDeepBins, vf - M) * GS_256_LOG2E;
+      m = (double)mass[b] * 0x1p-40 * exp2_256_tight(y, S.tab);
+    }
+    sum = fix_add(sum, fix_of(m));
+    f[q] = sum;
+  }
+  Fix128 t_fix;
+  const Fix128 base = fix_add(r_fix, block_fix_scan(sum, (uint64_t*)S.top, &t_fix));
+#pragma unroll
+  for (int q = 0; q < kPer; ++q) after[tid * kPer + q] = fix_to_double(fix_add(base, f[q]));
+  return fix_to_double(fix_add(r_fix, t_fix));
+}
+
 // What pass 1 leaves (the mass histogram in sorted, each thread's last-bin
 // sum in `tail`) is completed and used: the specials go out of the
 // histogram with their raw values and in with their penalised ones, the
@@ -2331,36 +2408,9 @@ __device__ __noinline__ uint32_t deep_mid(const SampleArgs& a, Shared& S, int64_
   __syncthreads();
   // ---- the region's exact mass, and the bins' prefix masses in fixed point
   constexpr int kPer = kFinishCap / kFinishThreads;  // region entries per thread (and bins)
-  static_assert(kDeepBins == kFinishCap, "kPer bins per thread");
-  Fix128 r_fix{0ull, 0ull};
-  for (int i = tid; i < n_reg; i += kFinishThreads) r_fix = fix_add(r_fix, fix_of(S.cand_p[i]));
-  r_fix = block_fix_sum(r_fix, (uint64_t*)S.top);
-  const double r_total = fix_to_double(r_fix);
-  // after[b] (over mass[b], in place): the mass of the region and of bins
-  // 0 .. b, in binary64 from exact fixed-point sums of the bins' masses
-  double* after = (double*)S.sorted;
-  double total;
-  {
-    Fix128 f[kPer];
-    Fix128 sum{0ull, 0ull};
-#pragma unroll
-    for (int q = 0; q < kPer; ++q) {
-      const int b = tid * kPer + q;
-      double m = tail_mass;
-      if (b < kDeepBins - 1) {
-        // e^(c_b - M), c_b = vf - (b + 1/2) w
-        const double y = __builtin_fma(-(b + 0.5), kDeepSpan / kDeepBins, vf - M) * GS_256_LOG2E;
-        m = (double)mass[b] * 0x1p-40 * exp2_256_tight(y, S.tab);
-      }
-      sum = fix_add(sum, fix_of(m));
-      f[q] = sum;
-    }
-    Fix128 t_fix;
-    const Fix128 base = fix_add(r_fix, block_fix_scan(sum, (uint64_t*)S.top, &t_fix));
-#pragma unroll
-    for (int q = 0; q < kPer; ++q) after[tid * kPer + q] = fix_to_double(fix_add(base, f[q]));
-    total = fix_to_double(fix_add(r_fix, t_fix));
-  }
+  double r_total;
+  const double total = deep_prefix_masses(S, n_reg, tail_mass, vf, M, &r_total);
+  const double* after = (const double*)S.sorted;
   if (!(total < __builtin_inf()) || !(total > 0)) return kExactRequest | 0u;
   const double target = u * total;  // the cursor, in units of e
   // the decision margin: the reference's own rounding, the near-tie report
@@ -2485,10 +2535,29 @@ __device__ __noinline__ uint32_t deep_final(const SampleArgs& a, Shared& S, int6
   const int n_g = (int)S.deep_final;
   if (n_g > kFinishCap || n_g == 0) return kExactRequest | 0u;
   // ---- sort them (value desc, id asc) and walk them with exact exponentials
-  const int m2 = pow2_at_least(n_g);
-  for (int i = n_g + tid; i < m2; i += kFinishThreads) { gkey[i] = 0; gid[i] = 0xFFFFFFFFu; }
-  __syncthreads();
-  block_sort_pairs_desc(gkey, gid, m2);
+  if (n_g <= 512) {
+    // the usual few (a bin or two): each finds its place by counting the
+    // entries ranked before it (the ids are distinct)
+    uint64_t k = 0;
+    uint32_t id = 0;
+    int rank = 0;
+    if (tid < n_g) {
+      k = gkey[tid];
+      id = gid[tid];
+      for (int j = 0; j < n_g; ++j) rank += ranks_before(gkey[j], gid[j], k, id) ? 1 : 0;
+    }
+    __syncthreads();
+    if (tid < n_g) {
+      gkey[rank] = k;
+      gid[rank] = id;
+    }
+    __syncthreads();
+  } else {
+    const int m2 = pow2_at_least(n_g);
+    for (int i = n_g + tid; i < m2; i += kFinishThreads) { gkey[i] = 0; gid[i] = 0xFFFFFFFFu; }
+    __syncthreads();
+    block_sort_pairs_desc(gkey, gid, m2);
+  }
   for (int i = tid; i < n_g; i += kFinishThreads) S.cand_p[i] = gsm::js_exp(key_f64(gkey[i]) - M);
   if (tid == 0) { S.first_idx = 0xFFFFFFFFu; S.route_exact = 0; }
   __syncthreads();
