@@ -226,7 +226,7 @@ __device__ __forceinline__ void wave_sort_desc_regs(uint64_t (&v)[E]) {
 #pragma unroll
         for (int q = 0; q < E; ++q) {
           const int i = lane * E + q;
-          const uint64_t y = shfl_xor_u64(v[q], j / E);
+          const uint64_t y = xlane_u64(v[q], j / E);
           const bool keep_max = ((i & j) == 0) == ((i & k) == 0);
           v[q] = keep_max ? umax64(v[q], y) : umin64(v[q], y);
         }
@@ -263,7 +263,7 @@ __device__ void top_r(const uint64_t* s, int n, uint64_t* tmp, uint64_t* top) {
       x = umax64(tmp[wave * 64 + lane], tmp[(wave + half) * 64 + 63 - lane]);
 #pragma unroll
       for (int j = 32; j > 0; j >>= 1) {
-        const uint64_t y = shfl_xor_u64(x, j);
+        const uint64_t y = xlane_u64(x, j);
         x = (lane & j) == 0 ? umax64(x, y) : umin64(x, y);
       }
     }

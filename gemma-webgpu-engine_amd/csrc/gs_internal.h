@@ -260,6 +260,7 @@ constexpr int kDppRowShr1 = 0x111;
 constexpr int kDppRowShr2 = 0x112;
 constexpr int kDppRowShr4 = 0x114;
 constexpr int kDppRowShr8 = 0x118;
+constexpr int kDppRowShl4 = 0x104;
 constexpr int kDppRowRor4 = 0x124;
 constexpr int kDppRowRor8 = 0x128;
 constexpr int kDppRowHalfMirror = 0x141;  // lane l of each 8 to lane 7 - l
@@ -397,6 +398,38 @@ __device__ __forceinline__ double wave_scan_f64(double v) {
 __device__ __forceinline__ uint32_t shfl_xor_u32(uint32_t v, int m) { return (uint32_t)__shfl_xor((int)v, m, 64); }
 __device__ __forceinline__ uint64_t shfl_xor_u64(uint64_t v, int m) {
   const uint32_t lo = shfl_xor_u32((uint32_t)v, m), hi = shfl_xor_u32((uint32_t)(v >> 32), m);
+  return ((uint64_t)hi << 32) | lo;
+}
+// The value of lane (lane ^ m), m a power of two up to 32, moved in the
+// VALU: quad_perm for 1 and 2, row_shl/row_shr 4 (each lane takes the one
+// that stays in its row), row_ror 8, and gfx950's v_permlane16_swap /
+// v_permlane32_swap for 16 and 32 (each lane takes the half it did not
+// keep). For m known at compile time (unrolled loops) the switch folds away.
+__device__ __forceinline__ uint32_t xlane_u32(uint32_t v, int m) {
+  const int lane = threadIdx.x & 63;
+  switch (m) {
+    case 1:
+      return dpp_u32<kDppQuad1032, 0xF>(0u, v);
+    case 2:
+      return dpp_u32<kDppQuad2301, 0xF>(0u, v);
+    case 4: {
+      const uint32_t up = dpp_u32<kDppRowShl4, 0xF>(0u, v), down = dpp_u32<kDppRowShr4, 0xF>(0u, v);
+      return (lane & 4) ? down : up;
+    }
+    case 8:
+      return dpp_u32<kDppRowRor8, 0xF>(0u, v);
+    case 16: {
+      const auto p = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+      return (lane & 16) ? p[0] : p[1];
+    }
+    default: {
+      const auto p = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+      return (lane & 32) ? p[0] : p[1];
+    }
+  }
+}
+__device__ __forceinline__ uint64_t xlane_u64(uint64_t v, int m) {
+  const uint32_t lo = xlane_u32((uint32_t)v, m), hi = xlane_u32((uint32_t)(v >> 32), m);
   return ((uint64_t)hi << 32) | lo;
 }
 __device__ __forceinline__ double shfl_xor_f64(double v, int m) {
