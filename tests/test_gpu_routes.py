@@ -118,6 +118,36 @@ def test_full_vocabulary_draws_bf16_and_softcap(sampler, oracle):
     assert deep > 0
 
 
+def test_lone_row_deep_draws(sampler, oracle):
+    """One-row calls (interactive decoding) whose cursor sits deep in the
+    tail: the lone row's two passes are split into a part per chunk across
+    workgroups; penalty-window ids below the region floor on some rows. Each
+    call also runs on the row's own workgroup (no batch hint): the same ids
+    as the oracle either way."""
+    import torch
+
+    gs = _gs()
+    w = gs.workloads.multinomial(rows=list(range(6)))
+    us = [1 - 2 ** -32, 0.9999, 0.999, 0.9995, 0.99995, 0.9999]
+    temps = [1.0, 0.8, 1.0, 0.9, 1.0, 0.8]
+    deep = 0
+    for r in range(6):
+        cfg = w.configs[r].merged(temperature=temps[r])
+        hist = None
+        if r % 2:
+            # window ids from the tail (ranks 5000..50000), lowered by the penalty
+            order = np.argsort(-w.logits[r])
+            hist = [order[5000:50000:1500].tolist()]
+            cfg = cfg.merged(repetitionPenalty=1.3, repetitionWindow=64)
+        conf = np.stack([gs.runtime.row_config(cfg, uniform=us[r])])
+        x = torch.from_numpy(w.logits[r:r + 1]).cuda()
+        for hints in (None, 0):
+            out = sampler.sample(x, conf, histories=hist, hints=hints)
+            check(gs, oracle, f"lone row {r} hints {hints}", out, [w.logits[r]], hist, [cfg], [us[r]])
+            deep += int((out.flags[0] & gs.GS_FLAG_EXACT_PATH) == 0)
+    assert deep > 0
+
+
 def test_topk_above_64(sampler, oracle):
     """topK 65 .. 2000 keep 64 entries per chunk; the finish ranks the
     complete region (block-wide) and cuts it at K."""
