@@ -173,10 +173,17 @@ struct Workspace {
   int32_t deep_max_rows = 0;
 };
 
-// true when the batch hints at full-vocabulary draws and the workspace has
-// the deep draw's records
+// Batches of fewer rows keep their deep draws on the rows' own workgroups:
+// the four deep launches cost about 17 us even when no row needs them, more
+// than a lone row's expected saving (a deep draw takes one draw in ten or
+// fewer, ~60 us faster over many workgroups).
+constexpr int32_t kDeepMinRows = 4;
+
+// true when the batch hints at full-vocabulary draws, has kDeepMinRows rows
+// or more, and the workspace has the deep draw's records
 bool deep_launch(const Workspace& w, const gs_batch* b) {
-  return (b->hints & GS_BATCH_FULL_DRAWS) && w.deep_rows && w.deep_queue && b->rows <= w.deep_max_rows;
+  return (b->hints & GS_BATCH_FULL_DRAWS) && b->rows >= kDeepMinRows && w.deep_rows && w.deep_queue &&
+         b->rows <= w.deep_max_rows;
 }
 
 // Enqueues the sampling kernels of one checked batch on stream s (ev: the

@@ -120,8 +120,9 @@ typedef struct gs_batch {
  * falls past the candidates the finish ranks is then spread over many
  * workgroups by four more launches (stage GS_STAGE_DEEP) instead of taking
  * the row's one workgroup; the results are identical either way. Without
- * the hint those launches are skipped. gs_sample_host sets it itself from
- * its host configs. */
+ * the hint, and for batches of fewer than 4 rows (where the launches cost
+ * more than they save on average), those launches are skipped.
+ * gs_sample_host sets the hint itself from its host configs. */
 #define GS_BATCH_FULL_DRAWS 1
 
 /* Library / device identity. */

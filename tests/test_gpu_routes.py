@@ -119,11 +119,11 @@ def test_full_vocabulary_draws_bf16_and_softcap(sampler, oracle):
 
 
 def test_lone_row_deep_draws(sampler, oracle):
-    """One-row calls (interactive decoding) whose cursor sits deep in the
-    tail: the lone row's two passes are split into a part per chunk across
-    workgroups; penalty-window ids below the region floor on some rows. Each
-    call also runs on the row's own workgroup (no batch hint): the same ids
-    as the oracle either way."""
+    """Small calls (interactive decoding) whose cursor sits deep in the tail:
+    one-row calls keep the deep draw on the row's own workgroup, and a
+    four-row call of the same rows spreads it over many workgroups (a part per
+    chunk for each row); penalty-window ids below the region floor on some
+    rows. The same ids as the oracle either way."""
     import torch
 
     gs = _gs()
@@ -141,10 +141,15 @@ def test_lone_row_deep_draws(sampler, oracle):
             cfg = cfg.merged(repetitionPenalty=1.3, repetitionWindow=64)
         conf = np.stack([gs.runtime.row_config(cfg, uniform=us[r])])
         x = torch.from_numpy(w.logits[r:r + 1]).cuda()
-        for hints in (None, 0):
-            out = sampler.sample(x, conf, histories=hist, hints=hints)
-            check(gs, oracle, f"lone row {r} hints {hints}", out, [w.logits[r]], hist, [cfg], [us[r]])
-            deep += int((out.flags[0] & gs.GS_FLAG_EXACT_PATH) == 0)
+        out = sampler.sample(x, conf, histories=hist)
+        check(gs, oracle, f"lone row {r}", out, [w.logits[r]], hist, [cfg], [us[r]])
+        deep += int((out.flags[0] & gs.GS_FLAG_EXACT_PATH) == 0)
+        # the row four times in one call: the multi-workgroup deep draw
+        out4 = sampler.sample(torch.from_numpy(np.repeat(w.logits[r:r + 1], 4, axis=0)).cuda(),
+                              np.concatenate([conf] * 4), histories=hist * 4 if hist else None)
+        for k in range(4):
+            assert int(out4.tokens[k]) == int(out.tokens[0]), (r, k)
+            assert abs(out4.probabilities[k] - out.probabilities[0]) <= PROB_RTOL * out.probabilities[0]
     assert deep > 0
 
 
