@@ -204,3 +204,41 @@ def test_mask_slot_outside_the_table_is_an_error():
             s.sample(x, conf, mask_table=table)
     finally:
         s.close()
+
+
+def test_full_penalty_batch_mixed_routes_repeated(sampler, oracle):
+    """256 f32 rows at the full vocabulary (four scan groups per row, one
+    generation of workgroups): penalised top-k/top-p rows, greedy rows and
+    rows forced onto the exact path in one batch. It is launched three times
+    with a two-row batch (another grid) in between: every launch gives
+    identical results, and the rows checked (every 8th, the greedy ones
+    among them and the forced ones) match the oracle."""
+    import torch
+
+    gs = _gs()
+    w = gs.workloads.penalties()
+    cfgs = list(w.configs)
+    greedy = gs.DecodingConfig(temperature=0.0, repetitionPenalty=1.1, repetitionWindow=512,
+                               frequencyPenalty=0.3, presencePenalty=0.5)
+    for r in range(3, 256, 8):
+        cfgs[r] = greedy
+    force = {r for r in range(5, 256, 64)}
+    conf = np.stack([gs.runtime.row_config(c, seed=s, force_exact=(r in force))
+                     for r, (c, s) in enumerate(zip(cfgs, w.seeds))])
+    x = torch.from_numpy(w.logits).cuda()
+    outs = []
+    for rep in range(3):
+        outs.append(sampler.sample(x, conf, histories=w.histories))
+        small = sampler.sample(x[:2], conf[:2], histories=w.histories[:2])
+        assert np.array_equal(small.tokens, outs[0].tokens[:2])
+    for o in outs[1:]:
+        assert np.array_equal(o.tokens, outs[0].tokens)
+        assert np.array_equal(o.probabilities, outs[0].probabilities)
+        assert np.array_equal(o.flags, outs[0].flags)
+    out = outs[0]
+    for r in sorted(set(range(0, 256, 8)) | set(range(3, 256, 64)) | force):
+        t, tr = oracle.sample_token(w.logits[r], list(w.histories[r]), to_oracle_cfg(cfgs[r]),
+                                    oracle.draw(w.seeds[r], 0))
+        check_row(gs, "mixed routes", r, out.tokens[r], out.probabilities[r], out.flags[r], t, tr.probability)
+    for r in force:
+        assert out.flags[r] & gs.GS_FLAG_EXACT_PATH
