@@ -120,8 +120,10 @@ __global__ __launch_bounds__(kLmThreads) void lmhead_kernel(const uint16_t* __re
       x0 = cap * tanhf(x0 / cap);
       x1 = cap * tanhf(x1 / cap);
     }
-    if (m0 + row < M) out[(size_t)(m0 + row) * V + n] = x0;
-    if (m0 + 32 + row < M) out[(size_t)(m0 + 32 + row) * V + n] = x1;
+    // non-temporal stores: the 64 x V logits stream past the caches (-11 us
+    // of 261 at M 64, D 2048, V 262144, against write-back stores)
+    if (m0 + row < M) __builtin_nontemporal_store(x0, &out[(size_t)(m0 + row) * V + n]);
+    if (m0 + 32 + row < M) __builtin_nontemporal_store(x1, &out[(size_t)(m0 + 32 + row) * V + n]);
   }
 }
 
