@@ -151,6 +151,13 @@ __device__ __forceinline__ void load_chunk(const SampleArgs& a, int64_t row, int
   }
 }
 
+// Cache policy of the logits loads: non-temporal (gfx950's NT bit, bit 1 of
+// a buffer load's cache-policy operand). Every logit is read once, and
+// marking the stream non-temporal keeps it from displacing what the caches
+// hold for reuse: the penalties batch (256 x 262144 f32) scans in 46 us
+// instead of 54.5 us.
+constexpr int32_t kLoadNT = 2;
+
 // Loads of chunk lc of a group (logits, and mask words for constrained rows).
 // Each chunk gets a buffer resource of its own whose extent is the chunk
 // (lc < nc) or empty (lc >= nc): loads of an empty one return zeros without
@@ -167,7 +174,7 @@ __device__ __forceinline__ void load_group_logits(const char* lbase, int lc, int
       (void*)(lbase + (int64_t)lc * kChunkBytes), (short)0, lc < nc ? kChunkBytes : 0, kBufferWord3);
 #pragma unroll
   for (int v = 0; v < kLoads; ++v) {
-    const u32x4 w = __builtin_amdgcn_raw_buffer_load_b128(lg, tid * 16, v * kScanThreads * 16, 0);
+    const u32x4 w = __builtin_amdgcn_raw_buffer_load_b128(lg, tid * 16, v * kScanThreads * 16, kLoadNT);
     raw[v] = make_uint4(w.x, w.y, w.z, w.w);
   }
 }
