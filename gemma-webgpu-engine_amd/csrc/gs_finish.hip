@@ -990,7 +990,7 @@ __device__ __forceinline__ void visit_row(const SampleArgs& a, int64_t row, doub
 #pragma unroll
       for (int k = 0; k < kB; ++k) {
         const int64_t vi = v0 + (int64_t)k * kFinishThreads;
-        w[k] = vi < n_vec ? base[vi] : make_uint4(0u, 0u, 0u, 0u);
+        w[k] = vi < n_vec ? load_nt16(base + vi) : make_uint4(0u, 0u, 0u, 0u);
       }
 #pragma unroll
       for (int k = 0; k < kB; ++k) {
@@ -2700,7 +2700,7 @@ __device__ __forceinline__ void visit_range(const SampleArgs& a, int64_t row, do
 #pragma unroll
       for (int k = 0; k < kB; ++k) {
         const int64_t vi = vb + (int64_t)k * kFinishThreads;
-        w[k] = vi < v1 ? base[vi] : make_uint4(0u, 0u, 0u, 0u);
+        w[k] = vi < v1 ? load_nt16(base + vi) : make_uint4(0u, 0u, 0u, 0u);
       }
 #pragma unroll
       for (int k = 0; k < kB; ++k) {

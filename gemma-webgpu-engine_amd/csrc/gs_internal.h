@@ -240,6 +240,14 @@ struct SampleArgs {
   int32_t deep_max_rows;   // pass-2 rows start at deep_queue->rows + deep_max_rows
 };
 
+// A 16-byte load marked non-temporal, for rows streamed once: the stream
+// does not displace what the caches hold for reuse.
+__device__ __forceinline__ uint4 load_nt16(const uint4* p) {
+  typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+  const u32x4 v = __builtin_nontemporal_load((const u32x4*)p);
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
+
 // --------------------------------------------------------- wave helpers
 // Workgroup barrier for LDS traffic only: LDS stores before it are visible to
 // every wave after it, and global loads in flight are not waited for.

@@ -68,7 +68,7 @@ __global__ __launch_bounds__(kQatThreads) void qat_lmhead_kernel(QatArgs a, int3
   const int blocks = D / 64;
   const uint4* w4 = (const uint4*)a.words;
   for (int b = 0; b < blocks; ++b) {
-    const uint4 w = a.block_major ? w4[(int64_t)b * a.V + r] : w4[r * blocks + b];
+    const uint4 w = load_nt16(a.block_major ? w4 + (int64_t)b * a.V + r : w4 + r * blocks + b);
     const uint32_t q[4] = {w.x, w.y, w.z, w.w};
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
