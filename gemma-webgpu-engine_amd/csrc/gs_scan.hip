@@ -60,10 +60,12 @@ constexpr int kChunkWords = kChunk / 32;  // special-bitmap words of one chunk
 constexpr int kMaxGroupChunks = 16;       // chunks one group workgroup streams
 // Resident scan workgroups per CU (the launch bound). The constrained
 // variants carry the masked and the unmasked group scan in one kernel and
-// need more registers: bound at 4 they spill (f32: 117 VGPRs), so they trade
-// occupancy for a spill-free loop (f32 189 VGPRs, bf16 143).
+// need more registers: bound at 4 they spill (f32: 117 VGPRs) and crawl, so
+// they run at 3 (bf16 spill-free at 163 VGPRs; f32 at 168 with 20 spilled,
+// which scans 128 constrained rows in 31.4 us against 35.4 us spill-free at
+// 2 per CU).
 template <typename In, bool kMaskable>
-constexpr int scan_wg_per_cu() { return !kMaskable ? 4 : sizeof(In) == 4 ? 2 : 3; }
+constexpr int scan_wg_per_cu() { return !kMaskable ? 4 : 3; }
 // word 3 of a raw buffer resource on gfx9-family parts (gfx950 included)
 constexpr int32_t kBufferWord3 = 0x00020000;
 
