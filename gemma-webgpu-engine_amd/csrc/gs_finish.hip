@@ -2021,12 +2021,15 @@ __device__ __forceinline__ uint32_t finish_row(const SampleArgs& a, FinishLds& U
       }
       __syncthreads();
     }
-    int cut = (int)S.first_idx;  // index of the item that reached topP
-    if (S.first_idx == 0xFFFFFFFFu || S.short_sum) {
+    const uint32_t cut_idx = S.first_idx;
+    int cut = (int)cut_idx;  // index of the item that reached topP
+    if (cut_idx == 0xFFFFFFFFu || S.short_sum) {
       if (!n_complete) {
         return kExactRequest | 0u;
       }
       cut = n - 1;
+    } else if (cut_idx >= (uint32_t)n) {
+      return kExactRequest | GS_FLAG_INDEX_CHECK;
     } else if (tid == cut / kPer) {
       // 1e-6 boundary ties, as the reference comparison plan reports them
       const double cum = base + local[cut % kPer];
@@ -2106,10 +2109,9 @@ __device__ __forceinline__ uint32_t finish_row(const SampleArgs& a, FinishLds& U
       // a near tie, or a full-vocabulary draw past the ranked candidates
       return kExactRequest | (S.route_exact ? GS_FLAG_NEAR_TIE : 0u);
     }
-    if (tid == 0) {
-      const int i = (int)S.first_idx;
-      write_result(a, row, (int32_t)S.cand_id[i], tie_report, S.cand_p[i] / total);
-    }
+    const uint32_t i = S.first_idx;
+    if (i >= (uint32_t)n) return kExactRequest | GS_FLAG_INDEX_CHECK;
+    if (tid == 0) write_result(a, row, (int32_t)S.cand_id[i], tie_report, S.cand_p[i] / total);
     return 0;
   }
 }
@@ -2447,13 +2449,20 @@ __device__ __noinline__ uint32_t deep_mid(const SampleArgs& a, Shared& S, int64_
     }
   }
   __syncthreads();
-  if (S.route_exact) return kExactRequest | GS_FLAG_NEAR_TIE;
-  if (S.first_idx != 0xFFFFFFFFu) {
-    if (tid == 0) write_result(a, row, (int32_t)S.cand_id[S.first_idx], 0u, S.cand_p[S.first_idx] / total);
+  // every wave reads the walk's outcome before any wave's bin search below
+  // writes first_idx again (without this barrier a fast wave's bin index
+  // could be read here as a region index)
+  const bool walk_near = S.route_exact != 0;
+  const uint32_t walk_first = S.first_idx;
+  __syncthreads();
+  if (walk_near) return kExactRequest | GS_FLAG_NEAR_TIE;
+  if (walk_first != 0xFFFFFFFFu) {
+    if (walk_first >= (uint32_t)n_reg) return kExactRequest | GS_FLAG_INDEX_CHECK;
+    if (tid == 0) write_result(a, row, (int32_t)S.cand_id[walk_first], 0u, S.cand_p[walk_first] / total);
     return 0;
   }
   // ---- the bin the cursor falls in, and a neighbour where a boundary lies
-  // within the margin
+  // within the margin (first_idx is still 0xFFFFFFFF: the walk found none)
   {
     uint32_t first = 0xFFFFFFFFu;
 #pragma unroll
@@ -2591,8 +2600,10 @@ __device__ __noinline__ uint32_t deep_final(const SampleArgs& a, Shared& S, int6
   }
   __syncthreads();
   if (S.route_exact) return kExactRequest | GS_FLAG_NEAR_TIE;
-  if (S.first_idx == 0xFFFFFFFFu) return kExactRequest | 0u;
-  if (tid == 0) write_result(a, row, (int32_t)gid[S.first_idx], 0u, S.cand_p[S.first_idx] / plan.total);
+  const uint32_t first = S.first_idx;
+  if (first == 0xFFFFFFFFu) return kExactRequest | 0u;
+  if (first >= (uint32_t)n_g) return kExactRequest | GS_FLAG_INDEX_CHECK;
+  if (tid == 0) write_result(a, row, (int32_t)gid[first], 0u, S.cand_p[first] / plan.total);
   return 0;
 }
 

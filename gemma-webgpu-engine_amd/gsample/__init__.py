@@ -30,6 +30,7 @@ from .runtime import (  # noqa: F401
     GS_FLAG_TOPP_TIE,
     GS_FLAG_UNSUPPORTED,
     GS_FLAG_INVALID_SLOT,
+    GS_FLAG_INDEX_CHECK,
     GSampleError,
     LIB_PATH,
     RowConfig,

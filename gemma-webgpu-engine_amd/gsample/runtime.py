@@ -33,6 +33,7 @@ GS_FLAG_EMPTY_CANDIDATES = 32
 GS_FLAG_GREEDY = 64
 GS_FLAG_UNSUPPORTED = 128
 GS_FLAG_INVALID_SLOT = 256
+GS_FLAG_INDEX_CHECK = 512  # a workspace index failed its range check (row replayed exactly)
 
 GS_OK = 0
 GS_ERR_DEAD_END = 4

@@ -32,6 +32,7 @@ const FLAGS = Object.freeze({
   GREEDY: 64,
   UNSUPPORTED: 128,
   INVALID_SLOT: 256,
+  INDEX_CHECK: 512,
 });
 
 const STAGES = Object.freeze(["lmhead", "scan", "finish", "exact", "deep"]);

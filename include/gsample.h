@@ -86,6 +86,8 @@ typedef struct gs_row_config {
 #define GS_FLAG_GREEDY 64u
 #define GS_FLAG_UNSUPPORTED 128u  /* beyond a documented size limit */
 #define GS_FLAG_INVALID_SLOT 256u /* mask_slot >= 0 but not below the batch's mask_slots (row not sampled) */
+#define GS_FLAG_INDEX_CHECK 512u  /* an index the finish read back from its workspace failed its range
+                                     check; the row was re-resolved on the exact path (never expected) */
 
 typedef struct gs_row_result {
   int32_t token;         /* sampled id; -1 when the row failed (see flags) */

@@ -38,6 +38,7 @@ def to_oracle_cfg(c):
 
 def check_row(gs, label, r, token, prob, flags, t, p):
     assert int(token) == t, f"{label} row {r}: token {int(token)} != {t} (flags {int(flags)})"
+    assert not flags & gs.GS_FLAG_INDEX_CHECK, (label, r, int(flags))
     if flags & gs.GS_FLAG_EXACT_PATH:
         assert prob == p, (label, r, prob, p)
     else:
@@ -119,25 +120,28 @@ def test_heavy_tail_full_batch(sampler, oracle):
 
 
 @pytest.mark.parametrize("greedy", [False, True])
-def test_constrained_full_batch(sampler, oracle, greedy):
+def test_constrained_full_batch(sampler, oracle, synthetic_constraint, greedy):
     """The full 128-row constrained batch (64-state DFA masks, the constrained
-    scan variant's grid): every other row against the oracle on the masked
-    logits."""
+    scan variant's grid). The GPU's mask table is compared with the oracle's
+    masks for all 64 states first (constraints.ts:56-92,253-265,300-322);
+    then every other row is sampled against the oracle on logits masked with
+    the oracle's own masks."""
     import torch
 
     gs = _gs()
-    offsets, data = gs.workloads.synthetic_vocab()
-    nxt, finals = gs.workloads.synthetic_dfa()
+    offsets, data, nxt, finals, ref_masks = synthetic_constraint
     sampler.set_vocab(offsets, data)
     sampler.set_dfa(nxt, finals)
     table = sampler.build_masks(list(range(64)))
     words = table.cpu().numpy().view(np.uint32)
+    for s in range(64):
+        assert np.array_equal(words[s], ref_masks[s]), f"state {s}: GPU mask differs from the oracle's"
     w = gs.workloads.constrained(greedy=greedy)
     conf = np.stack([gs.runtime.row_config(c, seed=s, mask_slot=int(st))
                      for c, s, st in zip(w.configs, w.seeds, w.states)])
     out = sampler.sample(torch.from_numpy(w.logits).cuda(), conf, mask_table=table)
     for r in range(0, 128, 2):
-        legal = oracle.mask_bits_to_ids(words[w.states[r]], V)
+        legal = oracle.mask_bits_to_ids(ref_masks[w.states[r]], V)
         masked = oracle.mask_logits(w.logits[r], legal, [])
         t, tr = oracle.sample_token(masked, [], to_oracle_cfg(w.configs[r]), oracle.draw(w.seeds[r], 0))
         check_row(gs, f"constrained full greedy={greedy}", r, out.tokens[r], out.probabilities[r], out.flags[r],

@@ -75,7 +75,7 @@ def test_lmhead_partial_row_block(sampler, lm_inputs):
     assert bool((out[m:] == 7.0).all())
 
 
-def test_lmhead_sample_bit_exact_on_gpu_logits(sampler, lm_inputs, oracle):
+def test_lmhead_sample_bit_exact_on_gpu_logits(sampler, lm_inputs, oracle, synthetic_constraint):
     """gs_lmhead_sample over the config-5 pipeline: penalties from 256-id
     histories, the synthetic DFA's masks, topK 64 / topP 0.95, T 1, seed = row.
     Token ids must equal the oracle's on the GPU-produced logits."""
@@ -84,8 +84,7 @@ def test_lmhead_sample_bit_exact_on_gpu_logits(sampler, lm_inputs, oracle):
     gs = _gs()
     W = gs.workloads
     hidden, weight = lm_inputs
-    offsets, data = W.synthetic_vocab()
-    nxt, finals = W.synthetic_dfa()
+    offsets, data, nxt, finals, ref_masks = synthetic_constraint
     sampler.set_vocab(offsets, data)
     sampler.set_dfa(nxt, finals)
     table = sampler.build_masks(list(range(64)))
@@ -101,11 +100,13 @@ def test_lmhead_sample_bit_exact_on_gpu_logits(sampler, lm_inputs, oracle):
     logits = scratch.cpu().numpy()
     assert np.all(np.abs(logits) <= 30.0)
     masks = table.cpu().numpy().view(np.uint32)
+    for s in sorted(set(states)):
+        assert np.array_equal(masks[s], ref_masks[s]), s
     ocfg = Decoding(temperature=cfg.temperature, topK=cfg.topK, topP=cfg.topP, minP=cfg.minP, typicalP=cfg.typicalP,
                     repetitionPenalty=cfg.repetitionPenalty, repetitionWindow=cfg.repetitionWindow,
                     frequencyPenalty=cfg.frequencyPenalty, presencePenalty=cfg.presencePenalty)
     for r in range(0, M, 4):
-        legal = oracle.mask_bits_to_ids(masks[states[r]], V)
+        legal = oracle.mask_bits_to_ids(ref_masks[states[r]], V)
         masked = oracle.mask_logits(logits[r], legal, [])
         t, tr = oracle.sample_token(masked, hist[r], ocfg, oracle.draw(r, 0))
         assert int(res["token"][r]) == t, (r, int(res["token"][r]), t, int(res["flags"][r]))

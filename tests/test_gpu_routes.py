@@ -31,6 +31,7 @@ def check(gs, oracle, label, out, xs, hists, cfgs, us):
     for r in range(len(cfgs)):
         t, tr = oracle.sample_token(xs[r], hists[r] if hists else [], to_oracle_cfg(cfgs[r]), us[r])
         assert int(out.tokens[r]) == t, f"{label} row {r}: {int(out.tokens[r])} != {t} (flags {int(out.flags[r])})"
+        assert not out.flags[r] & gs.GS_FLAG_INDEX_CHECK, (label, r, int(out.flags[r]))
         p = 1.0 if cfgs[r].temperature == 0 else tr.probability
         if out.flags[r] & gs.GS_FLAG_EXACT_PATH:
             exact += 1

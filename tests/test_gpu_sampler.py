@@ -36,6 +36,7 @@ def assert_rows_match(out, expected, flags_ok=None, label=""):
     gs = _gs()
     for i, (t, p) in enumerate(expected):
         assert out.tokens[i] == t, f"{label} row {i}: token {out.tokens[i]} != {t} (flags {out.flags[i]})"
+        assert not out.flags[i] & gs.GS_FLAG_INDEX_CHECK, (label, i, int(out.flags[i]))
         if out.flags[i] & gs.GS_FLAG_EXACT_PATH:
             assert out.probabilities[i] == p or (math.isnan(p) and math.isnan(out.probabilities[i])), (label, i)
         else:
@@ -388,21 +389,18 @@ def test_constrained_bf16_mixed_batch(sampler, oracle):
     assert_rows_match(out, expected, label="constrained bf16 mixed")
 
 
-def test_constrained_masks_and_samples(sampler, oracle):
+def test_constrained_masks_and_samples(sampler, oracle, synthetic_constraint):
     import torch
 
     gs = _gs()
-    offsets, data = gs.workloads.synthetic_vocab()
-    nxt, finals = gs.workloads.synthetic_dfa()
+    offsets, data, nxt, finals, ref_masks = synthetic_constraint
     sampler.set_vocab(offsets, data)
     sampler.set_dfa(nxt, finals)
-    viable = oracle.viable_states(nxt, finals)
     states = list(range(64))
     table = sampler.build_masks(states).cpu().numpy().view(np.uint32)
-    for s in states[::7]:
-        ref = oracle.dfa_legal_mask(nxt, viable, offsets, data, s)
-        assert np.array_equal(table[s], ref), s
-    frac = np.mean([oracle.mask_bits_to_ids(table[s], 262144).size for s in states]) / 262144
+    for s in states:
+        assert np.array_equal(table[s], ref_masks[s]), s
+    frac = np.mean([oracle.mask_bits_to_ids(ref_masks[s], 262144).size for s in states]) / 262144
     assert 0.005 < frac < 0.1
     rows = list(range(0, 128, 8))
     for greedy in (True, False):
@@ -413,7 +411,7 @@ def test_constrained_masks_and_samples(sampler, oracle):
         out = sampler.sample(torch.from_numpy(w.logits).cuda(), conf, mask_table=masks)
         exp = []
         for i in range(len(rows)):
-            legal = oracle.mask_bits_to_ids(table[w.states[i]], 262144)
+            legal = oracle.mask_bits_to_ids(ref_masks[w.states[i]], 262144)
             masked = oracle.mask_logits(w.logits[i], legal, [])
             t, tr = oracle.sample_token(masked, [], to_oracle_cfg(w.configs[i]), oracle.draw(w.seeds[i], 0))
             exp.append((t, tr.probability))
