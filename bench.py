@@ -88,15 +88,20 @@ def parse_args():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--workload", default="penalties",
                     choices=["penalties", "single_row", "heavy_tail", "constrained", "lmhead", "qat", "multinomial",
-                             "topk_deep", "typical"])
+                             "topk_deep", "typical", "penalties_constrained"])
+    ap.add_argument("--also", default="penalties_constrained",
+                    help="comma-separated workloads measured after the main one and reported beside it under "
+                         "'also' (default: penalties_constrained; '' for none); with the main workload only")
     ap.add_argument("--cpu-rows", type=int, default=128,
                     help="rows of the one-thread CPU baseline sample (about 13 s on one core)")
     ap.add_argument("--cpu-threads", type=int, default=16,
                     help="worker threads of the all-cores CPU baseline leg (one per host core, at most this)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
-    ap.add_argument("--copy-probe", action="store_true",
-                    help="also time a plain device copy of the logits' byte count (achievable HBM bandwidth; "
-                         "the reference kernel for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE)")
+    ap.add_argument("--copy-probe", dest="copy_probe", action="store_true", default=True,
+                    help="time a plain 256 MiB device copy in the same run (achievable HBM bandwidth, reported "
+                         "beside the peak; the reference kernel for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE); "
+                         "on by default")
+    ap.add_argument("--no-copy-probe", dest="copy_probe", action="store_false")
     return ap.parse_args()
 
 
@@ -159,8 +164,8 @@ def build_workload(name, gs, torch, device):
         out.update(rows=w.rows, sampler=s, batches=batches, copies=copies, workload=w, dtype_in=w.dtype,
                    scan_bytes_per_row=per_row, step_bytes=w.rows * (per_row + 8), dominant="scan", desc=desc)
         return out
-    if name == "constrained":
-        w = W.constrained()
+    if name in ("constrained", "penalties_constrained"):
+        w = W.constrained() if name == "constrained" else W.penalties_constrained()
         s = gs.Sampler(vocab_size=V, max_rows=w.rows)
         offsets, data = W.synthetic_vocab()
         nxt, finals = W.synthetic_dfa()
@@ -170,13 +175,20 @@ def build_workload(name, gs, torch, device):
         conf = np.stack([rt.row_config(c, seed=sd, mask_slot=int(st))
                          for c, sd, st in zip(w.configs, w.seeds, w.states)])
         copies = rotated(torch, device, w.logits, "f32")
-        batches = [s.prepare(copies[i], conf, mask_table=table) for i in range(copies.shape[0])]
-        per_row = 4 * V + (V // 8)  # logits + the row's legal-token bitmask
+        batches = [s.prepare(copies[i], conf, histories=w.histories, mask_table=table)
+                   for i in range(copies.shape[0])]
+        window = w.configs[0].repetitionWindow if w.histories is not None else 0
+        per_row = 4 * V + 4 * window + (V // 8)  # logits + window ids + the row's legal-token bitmask
+        if name == "constrained":
+            desc = (f"constrained: {w.rows} x {V} f32 logits ~ N(0, 3^2); synthetic 1-12-byte vocab, 64-state "
+                    "byte DFA (~3% legal), per-row start state; topP 0.95, T 1 (masks built once per state)")
+        else:
+            desc = (f"penalties_constrained: {w.rows} x {V} f32 logits ~ N(0, 3^2); 512-id Zipf(1.1) histories, "
+                    "repetition 1.1, presence 0.5, frequency 0.3, window 512; T 0.7, topK 50, topP 0.9; the "
+                    "constrained workload's 64-state byte DFA masks (~3% legal, per-row start state); seed = row")
         out.update(rows=w.rows, sampler=s, batches=batches, copies=copies, workload=w, dtype_in="f32",
                    scan_bytes_per_row=per_row, step_bytes=w.rows * (per_row + 8), dominant="scan",
-                   masks=table, dfa=(offsets, data, nxt, finals),
-                   desc=f"constrained: {w.rows} x {V} f32 logits ~ N(0, 3^2); synthetic 1-12-byte vocab, 64-state "
-                        "byte DFA (~3% legal), per-row start state; topP 0.95, T 1 (masks built once per state)")
+                   masks=table, dfa=(offsets, data, nxt, finals), desc=desc)
         return out
     if name == "lmhead":
         M, D = 64, 2048
@@ -269,8 +281,7 @@ def cpu_inputs(wl):
     if wl["name"] == "qat":
         return wl["scratch"].cpu().numpy(), "f32", [wl["config_obj"]] * wl["rows"], [42], None, None
     w = wl["workload"]
-    return w.logits, wl["dtype_in"], w.configs, w.seeds, w.histories, (w.states if wl["name"] == "constrained"
-                                                                       else None)
+    return w.logits, wl["dtype_in"], w.configs, w.seeds, w.histories, w.states
 
 
 def run_node_leg(wl, node, pick, threads, tmp):
@@ -341,7 +352,7 @@ def cpu_baseline(wl, tokens, probs, n_rows, threads_cap):
             p = res["probabilities"][k]
             if p:
                 rel = max(rel, abs(probs[r] - p) / abs(p))
-    what = "the sampler" if wl["name"] not in ("constrained", "lmhead") else (
+    what = "the sampler" if wl["name"] not in ("constrained", "penalties_constrained", "lmhead") else (
         "legal-id walk (cached per state) + maskConstraintLogits + the sampler")
     if wl["name"] == "lmhead":
         what += " on the GPU-produced logits (no CPU bf16 GEMM exists in the reference)"
@@ -381,76 +392,74 @@ def qat_cpu_leg(wl):
 # ---------------------------------------------------------------------- main
 
 
-def main():
-    args = parse_args()
-    world = int(os.environ.get("WORLD_SIZE", "1"))
-    if args.gpus != 1 or world != 1:
-        print(json.dumps({"error": "this build runs on one GPU only: the sampling stage shards by rows (C1-C4) or "
-                                   "by vocab (lm_head) across GPUs, which is not built; run with --gpus 1"}))
-        sys.exit(2)
-    import torch
-
-    import gsample as gs
-
-    if not torch.cuda.is_available():
-        raise SystemExit("bench.py needs a GPU")
-    device = torch.device("cuda", 0)
-    log(f"building workload {args.workload}")
-    t0 = time.time()
-    wl = build_workload(args.workload, gs, torch, device)
+def copy_probe(torch, device, stream, steps):
+    """A plain 256 MiB device-to-device copy (reads and writes each byte once):
+    the achievable HBM bandwidth in the same run."""
+    src = torch.ones(64 << 20, dtype=torch.float32, device=device)
+    dst = torch.empty_like(src)
+    with torch.cuda.stream(stream):
+        for _ in range(3):
+            dst.copy_(src)
+        c0, c1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        c0.record(stream)
+        for _ in range(steps):
+            dst.copy_(src)
+        c1.record(stream)
     torch.cuda.synchronize()
-    n_rot = len(wl["batches"])
-    log(f"workload ready in {time.time() - t0:.1f} s ({n_rot} rotated logits buffers)")
+    copy_ms = c0.elapsed_time(c1) / steps
+    nbytes = src.numel() * src.element_size()
+    del dst, src
+    return {"bytes_read": nbytes, "bytes_written": nbytes, "avg_us": round(copy_ms * 1000, 2),
+            "gbps_read_plus_write": round(2 * nbytes / (copy_ms * 1e6), 1)}
+
+
+def measure(wl, gs, torch, stream, steps, warmup):
+    """Warmup, K timed steps (step rate), K more steps with per-kernel events.
+    Returns (ms_per_step, stages, tokens, probs, flags) of the workload."""
     s = wl["sampler"]
-    # a dedicated stream at the default priority: torch's default stream has a
-    # null handle, which the library would read as "use the context's stream"
-    stream = torch.cuda.Stream(device)
     sp = stream.cuda_stream
-    torch.cuda.synchronize()
-
-    for i in range(args.warmup):
+    n_rot = len(wl["batches"])
+    for i in range(warmup):
         launch_step(wl, i, sp)
     torch.cuda.synchronize()
-    log(f"warmup {args.warmup} steps done")
+    log(f"{wl['name']}: warmup {warmup} steps done")
 
     # the step rate: K steps bracketed by two events on the launch stream,
     # step i reading logits copy i mod n
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
     start.record(stream)
-    for i in range(args.steps):
+    for i in range(steps):
         launch_step(wl, i, sp)
     end.record(stream)
     torch.cuda.synchronize()
-    total_ms = start.elapsed_time(end)
-    ms_per_step = total_ms / args.steps
-    log(f"timed {args.steps} steps: {ms_per_step * 1000:.1f} us/step")
+    ms_per_step = start.elapsed_time(end) / steps
+    log(f"{wl['name']}: timed {steps} steps: {ms_per_step * 1000:.1f} us/step")
 
     # kernel durations: K more steps, every kernel launched with start/stop
     # HIP events on the stream it runs on (the events slow a step down, so
     # the step rate above is timed without them)
-    s.timing_begin(args.steps)
-    for i in range(args.steps):
+    s.timing_begin(steps)
+    for i in range(steps):
         launch_step(wl, i, sp)
     torch.cuda.synchronize()
     stages = s.timing_end()
-    log(f"stage timing over {args.steps} more steps: {stages}")
+    log(f"{wl['name']}: stage timing over {steps} more steps: {stages}")
 
     # results of the last step (each loop above counts its steps from 0, so
     # the last launch used buffer (steps - 1) mod n_rot)
-    last = (args.steps - 1) % n_rot
+    last = (steps - 1) % n_rot
     res = wl["batches"][last][1][-1] if wl["name"] != "lmhead" else wl["batches"][0][1][-4]
     if wl["name"] == "qat":
         res = wl["batches"][0][1][-1]
     raw = res.cpu().numpy().view(np.uint8).reshape(-1)[: wl["rows"] * 16]
     rr = raw.view(gs.runtime.RESULT_DTYPE)
-    tokens, probs, flags = rr["token"], rr["probability"], rr["flags"]
-    bad = int(np.sum(tokens < 0))
-    exact_rows = int(np.sum((flags & gs.GS_FLAG_EXACT_PATH) != 0))
-    tie_rows = int(np.sum((flags & gs.GS_FLAG_TOPP_TIE) != 0))
+    return ms_per_step, stages, rr["token"].copy(), rr["probability"].copy(), rr["flags"].copy()
 
+
+def roofline_of(wl, stages):
+    """The dominant kernel's roofline object from the per-kernel timings."""
     rows = wl["rows"]
-    value = rows / (ms_per_step / 1000.0)
     dom = wl["dominant"]
     dom_ms, dom_calls = stages[dom]
     dom_avg_ms = dom_ms / max(1, dom_calls)
@@ -467,7 +476,7 @@ def main():
                 "kernel": kname, "algorithmic_bytes_per_launch": int(algo),
                 "kernel_avg_us": round(dom_avg_ms * 1000, 2),
                 "stage_avg_us": {k: round(v[0] / v[1] * 1000, 2) for k, v in stages.items() if v[1]},
-                "rotated_logits_buffers": n_rot}
+                "rotated_logits_buffers": len(wl["batches"])}
     if wl["name"] == "qat":
         # binary64 fused multiply-adds on the vector units, not MFMA
         roofline["f64_tflops"] = round(mfma_tflops, 2)
@@ -480,52 +489,105 @@ def main():
         # the unfused logits write, reported beside the weight-streaming figure
         roofline["logits_write_bytes"] = wl["lm_logits_bytes"]
         roofline["achieved_with_logits_write"] = round((algo + wl["lm_logits_bytes"]) / (dom_avg_ms * 1e6), 1)
+    return roofline
+
+
+def step_figures(wl, ms_per_step, flags, tokens):
+    return {"value": round(wl["rows"] / (ms_per_step / 1000.0), 1), "ms_per_step": round(ms_per_step, 5),
+            "step_hbm_gbps": round(wl["step_bytes"] / (ms_per_step * 1e6), 1),
+            "step_hbm_frac": round(wl["step_bytes"] / (ms_per_step * 1e6) / HBM_PEAK_GBPS, 4),
+            "rows_failed": int(np.sum(tokens < 0)),
+            "rows_exact_path": int(np.sum((flags & 2) != 0)),
+            "rows_topp_tie": int(np.sum((flags & 1) != 0))}
+
+
+def main():
+    args = parse_args()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print(json.dumps({"error": "this build runs on one GPU only: the sampling stage shards by rows (C1-C4) or "
+                                   "by vocab (lm_head) across GPUs, which is not built; run with --gpus 1"}))
+        sys.exit(2)
+    import torch
+
+    import gsample as gs
+
+    if not torch.cuda.is_available():
+        raise SystemExit("bench.py needs a GPU")
+    device = torch.device("cuda", 0)
+    # a dedicated stream at the default priority: torch's default stream has a
+    # null handle, which the library would read as "use the context's stream"
+    stream = torch.cuda.Stream(device)
+    log(f"building workload {args.workload}")
+    t0 = time.time()
+    wl = build_workload(args.workload, gs, torch, device)
+    torch.cuda.synchronize()
+    log(f"workload ready in {time.time() - t0:.1f} s ({len(wl['batches'])} rotated logits buffers)")
+    ms_per_step, stages, tokens, probs, flags = measure(wl, gs, torch, stream, args.steps, args.warmup)
+    roofline = roofline_of(wl, stages)
+    fig = step_figures(wl, ms_per_step, flags, tokens)
+    config = {"workload": wl["desc"], "rows": wl["rows"], "vocab": V, "logits_dtype": wl["dtype_in"]}
 
     if args.copy_probe:
-        # a plain 256 MiB device-to-device copy: reads and writes each byte once
-        src = torch.ones(64 << 20, dtype=torch.float32, device=device)
-        dst = torch.empty_like(src)
-        with torch.cuda.stream(stream):
-            for _ in range(3):
-                dst.copy_(src)
-            c0, c1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-            c0.record(stream)
-            for _ in range(args.steps):
-                dst.copy_(src)
-            c1.record(stream)
-        torch.cuda.synchronize()
-        copy_ms = c0.elapsed_time(c1) / args.steps
-        nbytes = src.numel() * src.element_size()
-        roofline["copy_probe"] = {"bytes_read": nbytes, "bytes_written": nbytes, "avg_us": round(copy_ms * 1000, 2),
-                                  "gbps_read_plus_write": round(2 * nbytes / (copy_ms * 1e6), 1)}
-        del dst, src
+        cp = copy_probe(torch, device, stream, args.steps)
+        # the dominant kernel against the copy's read + write rate (its own
+        # traffic is almost all reads)
+        cp["dominant_frac_of_copy"] = round(roofline["achieved"] / cp["gbps_read_plus_write"], 4)
+        cp["step_frac_of_copy"] = round(fig["step_hbm_gbps"] / cp["gbps_read_plus_write"], 4)
+        roofline["copy_probe"] = cp
 
     base, parity = (None, None)
     if not args.no_cpu:
         base, parity = cpu_baseline(wl, tokens, probs, args.cpu_rows, args.cpu_threads)
     qat_cpu = qat_cpu_leg(wl) if wl["name"] == "qat" and not args.no_cpu else None
+    s = wl["sampler"]
+    s.synchronize()
+    s.close()
+    del wl
+    torch.cuda.empty_cache()
+
+    also = {}
+    for name in [n for n in args.also.split(",") if n and n != args.workload]:
+        log(f"building workload {name}")
+        w2 = build_workload(name, gs, torch, device)
+        torch.cuda.synchronize()
+        m2, st2, tok2, pr2, fl2 = measure(w2, gs, torch, stream, args.steps, args.warmup)
+        entry = {"config": {"workload": w2["desc"], "rows": w2["rows"], "vocab": V, "logits_dtype": w2["dtype_in"]}}
+        entry.update(step_figures(w2, m2, fl2, tok2))
+        entry["roofline"] = roofline_of(w2, st2)
+        if not args.no_cpu:
+            b2, p2 = cpu_baseline(w2, tok2, pr2, max(8, args.cpu_rows // 4), args.cpu_threads)
+            entry["cpu_baseline"] = b2
+            if p2 is not None:
+                entry["parity_sample"] = p2
+        also[name] = entry
+        w2["sampler"].close()
+        del w2
+        torch.cuda.empty_cache()
 
     line = {
-        "metric": METRIC, "value": round(value, 1), "unit": "rows/s", "n_gpus": 1, "steps": args.steps,
-        "warmup": args.warmup, "ms_per_step": round(ms_per_step, 5), "higher_is_better": True, "scaling": "weak",
+        "metric": METRIC, "value": fig["value"], "unit": "rows/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": fig["ms_per_step"], "higher_is_better": True, "scaling": "weak",
         "vs_baseline": None, "dtype": "f32/f64",
         "precision": ("logits f32 (bf16 widened exactly); normaliser terms binary32 hardware exp2 summed in "
                       "binary64; every ranking, cut and draw decided in binary64 as the reference does"),
         "data": "synthetic",
-        "config": {"workload": wl["desc"], "rows": rows, "vocab": V, "logits_dtype": wl["dtype_in"]},
-        "step_hbm_gbps": round(wl["step_bytes"] / (ms_per_step * 1e6), 1),
-        "step_hbm_frac": round(wl["step_bytes"] / (ms_per_step * 1e6) / HBM_PEAK_GBPS, 4),
+        "config": config,
+        "step_hbm_gbps": fig["step_hbm_gbps"], "step_hbm_frac": fig["step_hbm_frac"],
         "roofline": roofline, "cpu_baseline": base,
-        "rows_failed": bad, "rows_exact_path": exact_rows, "rows_topp_tie": tie_rows,
+        "rows_failed": fig["rows_failed"], "rows_exact_path": fig["rows_exact_path"],
+        "rows_topp_tie": fig["rows_topp_tie"],
     }
     if parity is not None:
         line["parity_sample"] = parity
     if qat_cpu is not None:
         line["qat_cpu"] = qat_cpu
-    s.synchronize()
+    if also:
+        line["also"] = also
     print(json.dumps(line), flush=True)
-    s.close()
-    if parity is not None and parity["token_mismatches"]:
+    bad = (parity is not None and parity["token_mismatches"]) or any(
+        e.get("parity_sample", {}).get("token_mismatches") for e in also.values())
+    if bad:
         sys.exit(1)
 
 

@@ -20,6 +20,12 @@ the batch, and buffers are identical on every machine.
                  generate() defaults with a temperature (a full-vocabulary draw)
   topk_deep      256 x 262144 f32 ~ N(0, 3^2); T 0.8, topK 200, topP 0.95
   typical        256 x 262144 f32 ~ N(0, 3^2); T 0.8, topK 40, typicalP 0.9
+  penalties_constrained
+                 256 x 262144 f32 ~ N(0, 3^2); the penalties workload's
+                 histories and options (window 512, T 0.7, topK 50, topP 0.9)
+                 on logits masked by the constrained workload's 64-state DFA
+                 (start state per row): top-k / top-p + penalties + grammar
+                 mask in one batch
 """
 from __future__ import annotations
 
@@ -121,6 +127,16 @@ def synthetic_dfa(seed: int = 5, n_states: int = 64, edges_per_state: int = 25):
     finals = np.zeros(n_states, dtype=np.uint8)
     finals[:4] = 1
     return nxt, finals
+
+
+def penalties_constrained(rows: Optional[List[int]] = None, n_rows: int = 256, vocab: int = V) -> Workload:
+    rows = list(range(n_rows)) if rows is None else rows
+    logits = normal_logits(15, rows, vocab=vocab)
+    hist = [zipf_ids(rng(16, r), 512, vocab=vocab) for r in rows]
+    states = np.array([int(rng(17, r).integers(0, 64)) for r in rows], dtype=np.int32)
+    cfgs = [PENALTY_CONFIG.merged(seed=r) for r in rows]
+    return Workload("penalties_constrained", len(rows), logits, "f32", cfgs, list(rows), histories=hist,
+                    states=states)
 
 
 CONSTRAINED_TOPP = DecodingConfig(temperature=1.0, topK=0, topP=0.95, minP=0.0, typicalP=1.0, repetitionPenalty=1.0,
