@@ -33,7 +33,11 @@ constexpr int kSpecialCap = 2048;                 // distinct (window + forced) 
 constexpr int kHashSize = 4096;                   // open-addressing table for those ids
 constexpr int kExactThreads = 1024;
 constexpr int kExactTile = 4096;                  // LDS tile of the exact path's bitonic sort
-constexpr int64_t kExactScratchBudget = 2560ll << 20;  // bytes of exact-path row scratch per context
+// bytes of exact-path row scratch per context: one slot per row up to this
+// (1024 rows at V = 262144 take 9 GiB, a small share of a 288 GB part), so a
+// batch of that size replays its exact rows in place and never launches the
+// exact kernel
+constexpr int64_t kExactScratchBudget = 12ll << 30;
 
 // relative margin under which a fast-path decision is re-resolved exactly;
 // it bounds the reference's own sequential-sum error (V * 2^-53 ~ 3e-11)

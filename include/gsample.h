@@ -153,7 +153,7 @@ int gs_validate_configs(gs_context* ctx, const gs_row_config* configs, int32_t n
  * share its scratch memory, so they must be ordered on one stream. Device
  * memory: per row about V / 2 bytes of chunk statistics and lists, plus
  * 36 * 2^ceil(log2 V) bytes of exact-path scratch for each of
- * min(max_rows, max(64, 2.5 GiB / that)) rows -- rows beyond those, in
+ * min(max_rows, max(64, 12 GiB / that)) rows -- rows beyond those, in
  * larger batches, share the slots through a second kernel.
  * (no reference counterpart: the reference keeps its WebGPU device in a
  *  module singleton, src/webgpu/device.ts:4-40) */

@@ -155,17 +155,18 @@ def test_exact_rows_beyond_the_context_slots(oracle):
     """A finish workgroup replays an exact-path row itself when the row has a
     scratch slot of its own (row < slots); the rows past the slots wait in the
     device queue for the exact kernel, which the call launches only for batches
-    with more rows than slots. At V = 2^21 a context keeps 64 slots, so in a
-    72-row batch forced onto the exact path rows 60-63 are replayed in place and
-    rows 64-71 by the exact kernel: both give the oracle's ids and bit-exact
-    probabilities."""
+    with more rows than slots. At V = 2^21 a context keeps 170 slots, so in a
+    180-row batch with rows 166-179 forced onto the exact path rows 166-169 are
+    replayed in place and rows 170-179 by the exact kernel: both give the
+    oracle's ids and bit-exact probabilities."""
     import torch
 
     gs = _gs()
-    V, rows = 1 << 21, 72
+    V, rows = 1 << 21, 180
+    slots = 12 * 2**30 // (36 * V)  # 170 slots of 36 * 2^21 bytes in the 12 GiB budget
     rng = np.random.default_rng(17)
-    logits = rng.normal(0, 2.5, (rows, V)).astype(np.float32)
-    forced = list(range(60, rows))
+    logits = rng.standard_normal((rows, V), dtype=np.float32) * np.float32(2.5)
+    forced = list(range(slots - 4, rows))
     cfg_forced = gs.DecodingConfig(temperature=0.8, topK=40, topP=0.9)
     cfg_greedy = gs.DecodingConfig(temperature=0.0)
     us = [float(u) for u in rng.random(rows)]
@@ -176,11 +177,11 @@ def test_exact_rows_beyond_the_context_slots(oracle):
         x = torch.from_numpy(logits).cuda()
         s.timing_begin(2)
         out = s.sample(x, conf)
-        out_small = s.sample(x[:64], conf[:64])
+        out_small = s.sample(x[:slots], conf[:slots])
         stages = s.timing_end()
     finally:
         s.close()
-    assert stages["exact"][1] == 1, stages  # launched for the 72-row batch only
+    assert stages["exact"][1] == 1, stages  # launched for the 180-row batch only
     for r in range(rows):
         if r in forced:
             t, tr = oracle.sample_token(logits[r], [], to_oracle_cfg(cfg_forced), us[r])
@@ -188,7 +189,7 @@ def test_exact_rows_beyond_the_context_slots(oracle):
             assert int(out.tokens[r]) == t and out.probabilities[r] == tr.probability, (r, int(out.tokens[r]), t)
         else:
             assert int(out.tokens[r]) == int(np.argmax(logits[r])), r
-    assert list(out_small.tokens) == list(out.tokens[:64])
+    assert list(out_small.tokens) == list(out.tokens[:slots])
 
 
 def test_topk_deeper_than_chunk_lists(sampler, oracle):
