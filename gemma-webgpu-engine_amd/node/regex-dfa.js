@@ -269,11 +269,17 @@ function parseRegex(source) {
 
 // --------------------------------------------------------------------- NFA
 // Thompson construction: states hold eps[] and edges [[lo, hi, to]].
+// maxPositions bounds the character positions (one per character-set leaf
+// of the expanded pattern): an epsilon-free automaton of the pattern has one
+// node per position plus its initial node, the count the reference's NFA
+// node limit applies to (constraints.ts:9,205-210).
 class Nfa {
-  constructor(maxStates) {
+  constructor(maxStates, maxPositions) {
     this.eps = [];
     this.edges = [];
     this.maxStates = maxStates;
+    this.maxPositions = maxPositions || Infinity;
+    this.positions = 0;
   }
   add() {
     if (this.eps.length >= this.maxStates) throw new RegexLimitError(`more than ${this.maxStates} NFA states`);
@@ -284,6 +290,10 @@ class Nfa {
   // fragment of node between fresh states; returns [start, end]
   build(node) {
     if (node.k === "set") {
+      this.positions += 1;
+      if (this.positions >= this.maxPositions) {
+        throw new RegexLimitError(`more than ${this.maxPositions - 1} NFA nodes`);
+      }
       const s = this.add();
       const e = this.add();
       for (const [lo, hi] of node.set) this.edges[s].push([lo, hi, e]);
@@ -563,15 +573,16 @@ function minimize(next, finals, initial) {
 function compileRegexToCodePointDfa(source, options) {
   const maxStates = (options && options.maxStates) || 1000000;
   const ast = parseRegex(source);
-  const nfa = new Nfa(Math.max(maxStates * 8, 400000));
+  const nfa = new Nfa(Math.max(maxStates * 8, 400000), options && options.maxStates);
   const [start, end] = nfa.build(ast);
   const states = subsetConstruction(nfa, start, end, maxStates);
   return { states, viable: viableStates(states) };
 }
 
-/* The byte-level DFA of a pattern. options.maxStates bounds the NFA, the
- * code-point DFA and the byte table (the reference bounds its automata at
- * 50 000 nodes for JSON grammars, constraints.ts:9,196-203). Throws Error
+/* The byte-level DFA of a pattern. options.maxStates bounds the NFA's
+ * positions (an epsilon-free automaton's nodes), the code-point DFA and the
+ * byte table (the reference bounds its automata at 50 000 nodes for JSON
+ * grammars, constraints.ts:9,196-212). Throws Error
  * with the reason; the caller adds the "Unsupported generation constraint"
  * prefix. */
 function compileRegexToByteDfa(source, options) {
