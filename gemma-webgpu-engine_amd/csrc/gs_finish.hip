@@ -36,6 +36,39 @@
 namespace gs {
 namespace {
 
+// The checked build (-DGS_CHECKED): every index into the LDS candidate,
+// region, special, hash, histogram and stage arrays, into a deep record's
+// arrays and into the row's chunk lists goes through GS_CK(index, bound). An
+// index out of range reads or writes element 0 instead and sets
+// g_check_fail; the kernel then sends the row to the exact replay with
+// GS_FLAG_INDEX_CHECK in place of any result it wrote, so a bad index shows
+// as a flagged row, never as a fault or a silent wrong token. In the normal
+// build GS_CK(i, n) is i.
+#ifdef GS_CHECKED
+__shared__ uint32_t g_check_fail;
+template <typename I>
+__device__ __forceinline__ I gs_ck(I i, int64_t n) {
+  if ((uint64_t)(int64_t)i >= (uint64_t)n) {
+    g_check_fail = 1u;
+    return (I)0;
+  }
+  return i;
+}
+#define GS_CK(i, n) gs_ck((i), (int64_t)(n))
+#define GS_CHECK_RESET()                          \
+  do {                                            \
+    if (threadIdx.x == 0) g_check_fail = 0u;      \
+  } while (0)
+#define GS_CHECK_FAILED() (g_check_fail != 0u)
+#else
+#define GS_CK(i, n) (i)
+#define GS_CHECK_RESET() \
+  do {                   \
+  } while (0)
+#define GS_CHECK_FAILED() false
+#endif
+#define GS_LEN(x) ((int64_t)(sizeof(x) / sizeof((x)[0])))
+
 constexpr int kWaves = kFinishThreads / 64;
 constexpr int kTopR = 64;                             // entries the fast path ranks exactly
 constexpr int kSubThreads = 8;                        // threads that read one wave sub-list
@@ -254,13 +287,13 @@ __device__ void top_r(const uint64_t* s, int n, uint64_t* tmp, uint64_t* top) {
 #pragma unroll
   for (int q = 0; q < E; ++q) {
     const int i = lane * E + q;
-    if (i < 64) tmp[wave * 64 + i] = v[q];
+    if (i < 64) tmp[GS_CK(wave * 64 + i, kFinishCap)] = v[q];
   }
   __syncthreads();
   for (int half = kWaves / 2; half >= 1; half >>= 1) {
     uint64_t x = 0;
     if (wave < half) {
-      x = umax64(tmp[wave * 64 + lane], tmp[(wave + half) * 64 + 63 - lane]);
+      x = umax64(tmp[GS_CK(wave * 64 + lane, kFinishCap)], tmp[GS_CK((wave + half) * 64 + 63 - lane, kFinishCap)]);
 #pragma unroll
       for (int j = 32; j > 0; j >>= 1) {
         const uint64_t y = xlane_u64(x, j);
@@ -268,10 +301,10 @@ __device__ void top_r(const uint64_t* s, int n, uint64_t* tmp, uint64_t* top) {
       }
     }
     __syncthreads();
-    if (wave < half) tmp[wave * 64 + lane] = x;
+    if (wave < half) tmp[GS_CK(wave * 64 + lane, kFinishCap)] = x;
     __syncthreads();
   }
-  if (tid < kTopR) top[tid] = tmp[tid];
+  if (tid < kTopR) top[tid] = tmp[GS_CK(tid, kFinishCap)];
   __syncthreads();
 }
 
@@ -333,7 +366,7 @@ __device__ __forceinline__ uint32_t prefix_floor(const uint64_t* region, int n_n
   // higher than their value times T (the lowest bin below sel_lo): a
   // boundary at or below that bin keeps them among the ranked candidates
   for (int j = tid; j < n_sp_in; j += kFinishThreads) {
-    const double v = key_f64(in_key[j]);
+    const double v = key_f64(in_key[GS_CK(j, kHashSize / 2)]);
     const double l = v * T;
     const double l_lo = l - (l < 0 ? -l : l) * 0x1p-40;
     const float lf = (float)l_lo;
@@ -1145,7 +1178,7 @@ __device__ __forceinline__ uint32_t finish_row(const SampleArgs& a, FinishLds& U
   const int sl0 = tid / kSubThreads, k0 = tid % kSubThreads;
   uint64_t lv[kSubPerThread];
 #pragma unroll
-  for (int q = 0; q < kSpecQ; ++q) lv[q] = lists[(int64_t)(sl0 < n_subs ? sl0 : 0) * kSubCap + k0 + q * kSubThreads];
+  for (int q = 0; q < kSpecQ; ++q) lv[q] = lists[GS_CK((int64_t)(sl0 < n_subs ? sl0 : 0) * kSubCap + k0 + q * kSubThreads, (int64_t)a.n_chunks * kGatherCap)];
   const Plan plan = plan_row_flat(cfg);
   if (cfg.mask_slot >= a.mask_slots) {
     // a constrained row whose mask is not in the table: never sampled unmasked
@@ -1199,17 +1232,17 @@ __device__ __forceinline__ uint32_t finish_row(const SampleArgs& a, FinishLds& U
 
   if (tid == 0) {
     S.flags = 0; S.max_key = 0; S.thr_max = 0; S.any_truncated = 0; S.n_sorted = 0; S.n_special = 0;
-    S.sel[3] = 0;
+    S.sel[GS_CK(3, GS_LEN(S.sel))] = 0;
     S.n_sp_in = 0; S.route_exact = 0; S.status_flags = 0; S.first_idx = 0xFFFFFFFFu; S.legal_bits = 0;
     S.special_legal = 0; S.best_entry = 0; S.sp_max = 0; S.fast_done = 0; S.short_sum = 0;
   }
-  for (int h = tid; h < kHashSize; h += kFinishThreads) { S.hash_ids[h] = 0xFFFFFFFFu; S.hash_counts[h] = 0; }
-  if (tid < 256) S.hist[tid] = 0;
+  for (int h = tid; h < kHashSize; h += kFinishThreads) { S.hash_ids[GS_CK(h, GS_LEN(S.hash_ids))] = 0xFFFFFFFFu; S.hash_counts[GS_CK(h, GS_LEN(S.hash_counts))] = 0; }
+  if (tid < 256) S.hist[GS_CK(tid, GS_LEN(S.hist))] = 0;
   __syncthreads();
 
   // ---- 1. statistics: sub-list lengths into LDS; the flags, the maximum and
   // the truncation threshold reduced per wave (one LDS atomic each)
-  if (has_w) S.c_nsub[tid] = (uint16_t)(w_nsub > (uint32_t)kSubCap ? (uint32_t)kSubCap : w_nsub);
+  if (has_w) S.c_nsub[GS_CK(tid, GS_LEN(S.c_nsub))] = (uint16_t)(w_nsub > (uint32_t)kSubCap ? (uint32_t)kSubCap : w_nsub);
   {
     // a sub-list length above kSubCap: the sub-list overflowed
     const uint32_t fl = wave_or_u32(has_w ? w_flags | (w_nsub > (uint32_t)kSubCap ? kChunkOverflow : 0u) |
@@ -1235,7 +1268,7 @@ __device__ __forceinline__ uint32_t finish_row(const SampleArgs& a, FinishLds& U
       wave_max_min_u32(key, &khi, &klo);
       const uint32_t live = (uint32_t)__popcll(__ballot(key != 0u));
       const uint32_t f = live >= d ? wave_kth_key(key, d, klo, khi) : 0u;
-      if (lane == 0) S.top_floor[wave] = f;
+      if (lane == 0) S.top_floor[GS_CK(wave, GS_LEN(S.top_floor))] = f;
     }
   }
   // the owned specials' logits and mask words start loading now; they are
@@ -1329,15 +1362,15 @@ __device__ __forceinline__ uint32_t finish_row(const SampleArgs& a, FinishLds& U
     for (int r = 0; r < kEval; ++r) {
       const bool mine = r < kOwn && ofirst[r];
       hid[r] = mine ? (uint32_t)oid[r] : 0xFFFFFFFFu;
-      hpk[r] = mine ? S.hash_counts[oslot[r]] : 0u;
+      hpk[r] = mine ? S.hash_counts[GS_CK(oslot[r], GS_LEN(S.hash_counts))] : 0u;
       raw[r] = 0.0f;  // the owned loads are read where the special is evaluated
       mw[r] = 0u;
     }
   } else {
 #pragma unroll
     for (int r = 0; r < kEval; ++r) {
-      hid[r] = r < kSlotsPerThread ? S.hash_ids[tid + r * kFinishThreads] : 0xFFFFFFFFu;
-      hpk[r] = r < kSlotsPerThread ? S.hash_counts[tid + r * kFinishThreads] : 0u;
+      hid[r] = r < kSlotsPerThread ? S.hash_ids[GS_CK(tid + r * kFinishThreads, GS_LEN(S.hash_ids))] : 0xFFFFFFFFu;
+      hpk[r] = r < kSlotsPerThread ? S.hash_counts[GS_CK(tid + r * kFinishThreads, GS_LEN(S.hash_counts))] : 0u;
     }
 #pragma unroll
     for (int r = 0; r < kEval; ++r) {
@@ -1373,7 +1406,7 @@ __device__ __forceinline__ uint32_t finish_row(const SampleArgs& a, FinishLds& U
 #pragma unroll
     for (int q = 0; q < kSubPerThread; ++q) {
       if ((keep >> q) & 1u) {
-        if (pos < (uint32_t)kFinishCap) S.sorted[pos] = e[q];
+        if (pos < (uint32_t)kFinishCap) S.sorted[GS_CK(pos, GS_LEN(S.sorted))] = e[q];
         ++pos;
       }
     }
@@ -1386,7 +1419,7 @@ __device__ __forceinline__ uint32_t finish_row(const SampleArgs& a, FinishLds& U
   // pass of their own, so that the common path never waits for loads issued
   // after the special gathers.
   constexpr int kHead = kSpecQ * kSubThreads;
-  const int cnt0 = sl0 < n_subs ? (int)S.c_nsub[sl0] : 0;
+  const int cnt0 = sl0 < n_subs ? (int)S.c_nsub[GS_CK(sl0, GS_LEN(S.c_nsub))] : 0;
   bool region_in_lds = false;
   int n_region = 0;
   auto fill_region = [&]() {  // block-wide, ends with a barrier
@@ -1398,19 +1431,19 @@ __device__ __forceinline__ uint32_t finish_row(const SampleArgs& a, FinishLds& U
 #pragma unroll
       for (int q = 0; q < kSubPerThread; ++q) {
         const int k = k0 + q * kSubThreads;
-        v[q] = (k >= kHead && k < cnt0) ? lists[(int64_t)sl0 * kSubCap + k] : 0ull;
+        v[q] = (k >= kHead && k < cnt0) ? lists[GS_CK((int64_t)sl0 * kSubCap + k, (int64_t)a.n_chunks * kGatherCap)] : 0ull;
       }
       append(v, kHead, cnt0);
     }
     // sub-lists past the first kFinishThreads / kSubThreads (more than 32 chunks)
     for (int s0 = kFinishThreads / kSubThreads; s0 < n_subs; s0 += kFinishThreads / kSubThreads) {
       const int sl = s0 + tid / kSubThreads;
-      const int cnt = sl < n_subs ? (int)S.c_nsub[sl] : 0;
+      const int cnt = sl < n_subs ? (int)S.c_nsub[GS_CK(sl, GS_LEN(S.c_nsub))] : 0;
       uint64_t v[kSubPerThread];
 #pragma unroll
       for (int q = 0; q < kSubPerThread; ++q) {
         const int k = k0 + q * kSubThreads;
-        v[q] = k < cnt ? lists[(int64_t)sl * kSubCap + k] : 0ull;
+        v[q] = k < cnt ? lists[GS_CK((int64_t)sl * kSubCap + k, (int64_t)a.n_chunks * kGatherCap)] : 0ull;
       }
       append(v, 0, cnt);
     }
@@ -1435,7 +1468,7 @@ __device__ __forceinline__ uint32_t finish_row(const SampleArgs& a, FinishLds& U
       }
       // the tightest floor the wave maxima give (every stats wave found one)
       uint32_t tfl = 0xFFFFFFFFu;
-      for (int w = 0; w < (n_wstats + 63) / 64; ++w) tfl = S.top_floor[w] < tfl ? S.top_floor[w] : tfl;
+      for (int w = 0; w < (n_wstats + 63) / 64; ++w) tfl = S.top_floor[GS_CK(w, GS_LEN(S.top_floor))] < tfl ? S.top_floor[GS_CK(w, GS_LEN(S.top_floor))] : tfl;
       if (tfl > sel_lo && tfl != 0xFFFFFFFFu)
         top_ok = top_select_regs_floor<kSpecQ>(e, valid, tfl, sel_hi, S.hist, S.sel, (uint64_t*)S.cand_p, S.top,
                                                &S.n_sorted);
@@ -1453,13 +1486,13 @@ __device__ __forceinline__ uint32_t finish_row(const SampleArgs& a, FinishLds& U
         const int shift = top_select_shift(sel_lo, sel_hi);
         for (int s0 = 0; s0 < n_subs; s0 += kFinishThreads / kSubThreads) {
           const int sl = s0 + tid / kSubThreads;
-          const int cnt = sl < n_subs ? (int)S.c_nsub[sl] : 0;
+          const int cnt = sl < n_subs ? (int)S.c_nsub[GS_CK(sl, GS_LEN(S.c_nsub))] : 0;
 #pragma unroll 1
           for (int k = k0; k < cnt; k += kSubThreads) {
-            const uint32_t key = entry_key(list_rank(lists[(int64_t)sl * kSubCap + k]));
+            const uint32_t key = entry_key(list_rank(lists[GS_CK((int64_t)sl * kSubCap + k, (int64_t)a.n_chunks * kGatherCap)]));
             if (key >= thr) {
               const uint32_t bin = (key - sel_lo) >> shift;
-              atomicAdd(&S.hist[bin < 255u ? bin : 255u], 1u);
+              atomicAdd(&S.hist[GS_CK(bin < 255u ? bin : 255u, GS_LEN(S.hist))], 1u);
             }
           }
         }
@@ -1468,7 +1501,7 @@ __device__ __forceinline__ uint32_t finish_row(const SampleArgs& a, FinishLds& U
           // lane l holds bins 255-4l .. 252-4l, highest first
           uint32_t h[4], c = 0;
 #pragma unroll
-          for (int q = 0; q < 4; ++q) { h[q] = S.hist[255 - 4 * lane - q]; c += h[q]; }
+          for (int q = 0; q < 4; ++q) { h[q] = S.hist[GS_CK(255 - 4 * lane - q, GS_LEN(S.hist))]; c += h[q]; }
           const uint32_t incl = wave_scan_u32(c);
           const uint64_t hit = __ballot(incl > (uint32_t)kFinishCap);
           const int first = hit ? __ffsll((unsigned long long)hit) - 1 : 64;
@@ -1476,13 +1509,13 @@ __device__ __forceinline__ uint32_t finish_row(const SampleArgs& a, FinishLds& U
             uint32_t cum = incl - c;
             int q = 0;
             while (cum + h[q] <= (uint32_t)kFinishCap) { cum += h[q]; ++q; }
-            S.sel[0] = (uint32_t)(255 - 4 * lane - q) + 1u;  // the lowest bin kept (256: none)
+            S.sel[GS_CK(0, GS_LEN(S.sel))] = (uint32_t)(255 - 4 * lane - q) + 1u;  // the lowest bin kept (256: none)
           }
-          if (first == 64 && lane == 0) S.sel[0] = 0u;
+          if (first == 64 && lane == 0) S.sel[GS_CK(0, GS_LEN(S.sel))] = 0u;
         }
         __syncthreads();
-        const uint32_t b = S.sel[0];
-        if (tid < 256) S.hist[tid] = 0;
+        const uint32_t b = S.sel[GS_CK(0, GS_LEN(S.sel))];
+        if (tid < 256) S.hist[GS_CK(tid, GS_LEN(S.hist))] = 0;
         if (b == 0u || b > 255u) return kExactRequest | 0u;  // all of it fits, or no boundary fits
         thr = sel_lo + (b << shift);
         if (tid == 0) { S.n_sorted = 0; S.any_truncated = 1u; }
@@ -1545,8 +1578,8 @@ __device__ __forceinline__ uint32_t finish_row(const SampleArgs& a, FinishLds& U
       }
       const double v = greedy ? x : x / T;
       const uint64_t key = f64_key(v);
-      S.sp_key[idx] = key;
-      S.sp_id[idx] = id;
+      S.sp_key[GS_CK(idx, GS_LEN(S.sp_key))] = key;
+      S.sp_id[GS_CK(idx, GS_LEN(S.sp_id))] = id;
       my_max = key > my_max ? key : my_max;
     }
     const uint64_t legal_w = __ballot(my_legal), bad_w = __ballot(my_nonfinite);
@@ -1585,7 +1618,7 @@ __device__ __forceinline__ uint32_t finish_row(const SampleArgs& a, FinishLds& U
       for (int w = tid; w < a.mask_words; w += kFinishThreads) {
         uint32_t word = m[w];
         for (int i = 0; i < n_sp; ++i) {
-          const uint32_t id = S.sp_id[i];
+          const uint32_t id = S.sp_id[GS_CK(i, GS_LEN(S.sp_id))];
           if ((int)(id >> 5) == w) word &= ~(1u << (id & 31));
         }
         if (word) atomicOr(&S.legal_bits, 1u);
@@ -1601,8 +1634,8 @@ __device__ __forceinline__ uint32_t finish_row(const SampleArgs& a, FinishLds& U
   // ---- greedy: first maximum of the penalised logits (sampling.ts:31,92-96)
   if (greedy) {
     for (int c = tid; c < a.n_chunks; c += kFinishThreads) {
-      if (S.c_nsub[c * kScanWaves]) {
-        atomicMax((unsigned long long*)&S.best_entry, (unsigned long long)list_rank(lists[(int64_t)c * kGatherCap]));
+      if (S.c_nsub[GS_CK(c * kScanWaves, GS_LEN(S.c_nsub))]) {
+        atomicMax((unsigned long long*)&S.best_entry, (unsigned long long)list_rank(lists[GS_CK((int64_t)c * kGatherCap, (int64_t)a.n_chunks * kGatherCap)]));
       }
     }
     __syncthreads();
@@ -1610,15 +1643,15 @@ __device__ __forceinline__ uint32_t finish_row(const SampleArgs& a, FinishLds& U
       // best special by (value desc, id asc)
       int bs = -1;
       for (int i = 0; i < n_sp; ++i) {
-        if (bs < 0 || ranks_before(S.sp_key[i], S.sp_id[i], S.sp_key[bs], S.sp_id[bs])) bs = i;
+        if (bs < 0 || ranks_before(S.sp_key[GS_CK(i, GS_LEN(S.sp_key))], S.sp_id[GS_CK(i, GS_LEN(S.sp_id))], S.sp_key[GS_CK(bs, GS_LEN(S.sp_key))], S.sp_id[GS_CK(bs, GS_LEN(S.sp_id))])) bs = i;
       }
       int32_t token;
       if (S.best_entry == 0) {
-        token = bs >= 0 ? (int32_t)S.sp_id[bs] : 0;
+        token = bs >= 0 ? (int32_t)S.sp_id[GS_CK(bs, GS_LEN(S.sp_id))] : 0;
       } else {
         const uint32_t nid = entry_id(S.best_entry);
         const uint64_t nkey = f64_key((double)key_f32(entry_key(S.best_entry)));
-        token = (bs >= 0 && ranks_before(S.sp_key[bs], S.sp_id[bs], nkey, nid)) ? (int32_t)S.sp_id[bs]
+        token = (bs >= 0 && ranks_before(S.sp_key[GS_CK(bs, GS_LEN(S.sp_key))], S.sp_id[GS_CK(bs, GS_LEN(S.sp_id))], nkey, nid)) ? (int32_t)S.sp_id[GS_CK(bs, GS_LEN(S.sp_id))]
                                                                                  : (int32_t)nid;
       }
       write_result(a, row, token, GS_FLAG_GREEDY, 1.0);
@@ -1665,7 +1698,7 @@ __device__ __forceinline__ uint32_t finish_row(const SampleArgs& a, FinishLds& U
   {
     double part = 0.0, spart = 0.0;
     if (has_w && w_sum > 0.0 && w_max > kKeyNegInf) part = w_sum * gsm::js_exp((double)key_f32(w_max) / T - M);
-    for (int i = kFinishThreads - 1 - tid; i < n_sp; i += kFinishThreads) spart += gsm::js_exp(key_f64(S.sp_key[i]) - M);
+    for (int i = kFinishThreads - 1 - tid; i < n_sp; i += kFinishThreads) spart += gsm::js_exp(key_f64(S.sp_key[GS_CK(i, GS_LEN(S.sp_key))]) - M);
     block_sum2_f64(part, spart, S.wsum2, &t_chunks, &t_sp);
     if (tid == 0) { S.total = t_chunks + t_sp; S.total_sp = t_sp; }
   }
@@ -1683,34 +1716,34 @@ __device__ __forceinline__ uint32_t finish_row(const SampleArgs& a, FinishLds& U
   const uint64_t region_floor = thr ? f64_key((double)key_f32(thr) / T) : 0;
   for (int i0 = 0; i0 < n_sp; i0 += kFinishThreads) {
     const int i = i0 + tid;
-    const bool in = i < n_sp && S.sp_key[i] >= region_floor;
+    const bool in = i < n_sp && S.sp_key[GS_CK(i, GS_LEN(S.sp_key))] >= region_floor;
     const uint64_t m = __ballot(in);
     uint32_t base = 0;
     if (lane == 0 && m) base = atomicAdd(&S.n_sp_in, (uint32_t)__popcll(m));
     base = readlane_u32(base, 0);
     if (in) {
       const uint32_t p = base + __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
-      in_key[p] = S.sp_key[i];
-      in_id[p] = S.sp_id[i];
+      in_key[GS_CK(p, kHashSize / 2)] = S.sp_key[GS_CK(i, GS_LEN(S.sp_key))];
+      in_id[GS_CK(p, kHashSize)] = S.sp_id[GS_CK(i, GS_LEN(S.sp_id))];
     }
   }
   __syncthreads();
   const int n_sp_in = (int)S.n_sp_in;
   if (n_sp_in <= 64) {
     if (n_sp_in > 1 && wave == 0) {
-      const uint64_t k = lane < n_sp_in ? in_key[lane] : 0ull;
-      const uint32_t id = lane < n_sp_in ? in_id[lane] : 0xFFFFFFFFu;
+      const uint64_t k = lane < n_sp_in ? in_key[GS_CK(lane, kHashSize / 2)] : 0ull;
+      const uint32_t id = lane < n_sp_in ? in_id[GS_CK(lane, kHashSize)] : 0xFFFFFFFFu;
       int rank = 0;  // the ids are distinct, so the ranks are too
       for (int j = 0; j < n_sp_in; ++j) rank += ranks_before(readlane_u64(k, j), readlane_u32(id, j), k, id) ? 1 : 0;
       if (lane < n_sp_in) {
-        in_key[rank] = k;
-        in_id[rank] = id;
+        in_key[GS_CK(rank, kHashSize / 2)] = k;
+        in_id[GS_CK(rank, kHashSize)] = id;
       }
     }
     __syncthreads();
   } else {
     const int m2 = pow2_at_least(n_sp_in);
-    for (int i = n_sp_in + tid; i < m2; i += kFinishThreads) { in_key[i] = 0; in_id[i] = 0xFFFFFFFFu; }
+    for (int i = n_sp_in + tid; i < m2; i += kFinishThreads) { in_key[GS_CK(i, kHashSize / 2)] = 0; in_id[GS_CK(i, kHashSize)] = 0xFFFFFFFFu; }
     __syncthreads();
     block_sort_pairs_desc(in_key, in_id, m2);
   }
@@ -1723,7 +1756,7 @@ __device__ __forceinline__ uint32_t finish_row(const SampleArgs& a, FinishLds& U
   // whole block calls it; false when the row must take the exact path)
   auto refine = [&]() -> bool {
     // the table exponential's table into LDS (the deep draw's copy, if any, is the same)
-    if (tid < 256) S.tab[tid] = c_exp2_256[tid];
+    if (tid < 256) S.tab[GS_CK(tid, GS_LEN(S.tab))] = c_exp2_256[tid];
     __syncthreads();
     const double part = recompute_nonspecial_sum(a, row, cfg, constrained, M, n_sp, S.sp_id, S.wsum, S.tab);
     if (!(part >= 0)) return false;
@@ -1753,39 +1786,39 @@ __device__ __forceinline__ uint32_t finish_row(const SampleArgs& a, FinishLds& U
       const int n_top = n_ns < kTopR ? n_ns : kTopR;
       const int n_sp_use = n_sp_in;
       for (int i = lane; i < n_top; i += 64) {
-        const uint64_t e = S.top[i];
+        const uint64_t e = S.top[GS_CK(i, GS_LEN(S.top))];
         const uint32_t id = entry_id(e);
         const uint64_t k = f64_key(nonspecial_value(e, T));
         int lo = 0, hi = n_sp_use;  // specials ranked before this entry
         while (lo < hi) {
           const int mid = (lo + hi) >> 1;
-          if (ranks_before(in_key[mid], in_id[mid], k, id)) lo = mid + 1; else hi = mid;
+          if (ranks_before(in_key[GS_CK(mid, kHashSize / 2)], in_id[GS_CK(mid, kHashSize)], k, id)) lo = mid + 1; else hi = mid;
         }
-        fp[i + lo] = key_f64(k);
-        fid[i + lo] = id;
+        fp[GS_CK(i + lo, (kFinishCap - kWaves * 64))] = key_f64(k);
+        fid[GS_CK(i + lo, kFinishCap)] = id;
       }
       for (int j = lane; j < n_sp_use; j += 64) {
-        const uint64_t k = in_key[j];
-        const uint32_t id = in_id[j];
+        const uint64_t k = in_key[GS_CK(j, kHashSize / 2)];
+        const uint32_t id = in_id[GS_CK(j, kHashSize)];
         int lo = 0, hi = n_top;  // ranked non-specials before this special
         while (lo < hi) {
           const int mid = (lo + hi) >> 1;
-          const uint64_t e = S.top[mid];
+          const uint64_t e = S.top[GS_CK(mid, GS_LEN(S.top))];
           if (ranks_before(f64_key(nonspecial_value(e, T)), entry_id(e), k, id)) lo = mid + 1; else hi = mid;
         }
-        fp[j + lo] = key_f64(k);
-        fid[j + lo] = id;
+        fp[GS_CK(j + lo, (kFinishCap - kWaves * 64))] = key_f64(k);
+        fid[GS_CK(j + lo, kFinishCap)] = id;
       }
       // the merged list equals the row's list up to the last ranked
       // non-special; specials below it may sit under unranked non-specials
       n_valid = n_top + n_sp_use;
       complete = region_complete && n_ns <= kTopR;
       if (n_ns > kTopR) {
-        const uint64_t e = S.top[kTopR - 1];
+        const uint64_t e = S.top[GS_CK(kTopR - 1, GS_LEN(S.top))];
         const uint64_t lk = f64_key(nonspecial_value(e, T));
         int after = 0;
         for (int j = lane; j < n_sp_use; j += 64) {
-          if (!ranks_before(in_key[j], in_id[j], lk, entry_id(e))) ++after;
+          if (!ranks_before(in_key[GS_CK(j, kHashSize / 2)], in_id[GS_CK(j, kHashSize)], lk, entry_id(e))) ++after;
         }
         after = (int)wave_sum_u32((uint32_t)after);
         n_valid -= after;
@@ -1797,7 +1830,7 @@ __device__ __forceinline__ uint32_t finish_row(const SampleArgs& a, FinishLds& U
         complete = true;
       }
       __builtin_amdgcn_wave_barrier();
-      for (int i = lane; i < n_valid; i += 64) fp[i] = gsm::js_exp(fp[i] - M);
+      for (int i = lane; i < n_valid; i += 64) fp[GS_CK(i, (kFinishCap - kWaves * 64))] = gsm::js_exp(fp[GS_CK(i, (kFinishCap - kWaves * 64))] - M);
       __builtin_amdgcn_wave_barrier();
       uint32_t xf = 0;
       const int r = filters_and_draw_wave(a, row, cfg, fp, total, fid, n_valid, complete, margin, true, full_mass_rel,
@@ -1866,13 +1899,13 @@ __device__ __forceinline__ uint32_t finish_row(const SampleArgs& a, FinishLds& U
       // the cursor lies past the region, with room: the deep draw needs only
       // the candidates' exact terms, in any order
       for (int i = tid; i < n_ns; i += kFinishThreads) {
-        const uint64_t e = S.sorted[i];
-        S.cand_p[i] = gsm::js_exp(nonspecial_value(e, T) - M);
-        S.cand_id[i] = entry_id(e);
+        const uint64_t e = S.sorted[GS_CK(i, GS_LEN(S.sorted))];
+        S.cand_p[GS_CK(i, GS_LEN(S.cand_p))] = gsm::js_exp(nonspecial_value(e, T) - M);
+        S.cand_id[GS_CK(i, GS_LEN(S.cand_id))] = entry_id(e);
       }
       for (int j = tid; j < n_sp_in; j += kFinishThreads) {
-        S.cand_p[n_ns + j] = gsm::js_exp(key_f64(in_key[j]) - M);
-        S.cand_id[n_ns + j] = in_id[j];
+        S.cand_p[GS_CK(n_ns + j, GS_LEN(S.cand_p))] = gsm::js_exp(key_f64(in_key[GS_CK(j, kHashSize / 2)]) - M);
+        S.cand_id[GS_CK(n_ns + j, GS_LEN(S.cand_id))] = in_id[GS_CK(j, kHashSize)];
       }
       if (tid == 0) {
         S.deep_m = M;
@@ -1886,13 +1919,13 @@ __device__ __forceinline__ uint32_t finish_row(const SampleArgs& a, FinishLds& U
       return kDeepRequest;
     }
     if (floor_key) {
-      n_pre = (int)S.sel[3];
+      n_pre = (int)S.sel[GS_CK(3, GS_LEN(S.sel))];
       // specials at or above the boundary's value (in_key is descending)
       const uint64_t vfloor = f64_key((double)key_f32(floor_key) / T);
       int lo = 0, hi = n_sp_in;
       while (lo < hi) {
         const int mid = (lo + hi) >> 1;
-        if (in_key[mid] >= vfloor) lo = mid + 1; else hi = mid;
+        if (in_key[GS_CK(mid, kHashSize / 2)] >= vfloor) lo = mid + 1; else hi = mid;
       }
       n_sp_pre = lo;
       pre_cut = true;
@@ -1909,32 +1942,32 @@ __device__ __forceinline__ uint32_t finish_row(const SampleArgs& a, FinishLds& U
   }
   // merge by rank into (value, id), then probabilities (sampling.ts:39,42)
   for (int i = tid; i < n_pre; i += kFinishThreads) {
-    const uint64_t e = S.sorted[i];
+    const uint64_t e = S.sorted[GS_CK(i, GS_LEN(S.sorted))];
     const uint32_t id = entry_id(e);
     const uint64_t k = f64_key(nonspecial_value(e, T));
     int lo = 0, hi = n_sp_pre;  // specials ranked before this entry
     while (lo < hi) {
       const int mid = (lo + hi) >> 1;
-      if (ranks_before(in_key[mid], in_id[mid], k, id)) lo = mid + 1; else hi = mid;
+      if (ranks_before(in_key[GS_CK(mid, kHashSize / 2)], in_id[GS_CK(mid, kHashSize)], k, id)) lo = mid + 1; else hi = mid;
     }
-    S.cand_p[i + lo] = key_f64(k);
-    S.cand_id[i + lo] = id;
+    S.cand_p[GS_CK(i + lo, GS_LEN(S.cand_p))] = key_f64(k);
+    S.cand_id[GS_CK(i + lo, GS_LEN(S.cand_id))] = id;
   }
   for (int j = tid; j < n_sp_pre; j += kFinishThreads) {
-    const uint64_t k = in_key[j];
-    const uint32_t id = in_id[j];
+    const uint64_t k = in_key[GS_CK(j, kHashSize / 2)];
+    const uint32_t id = in_id[GS_CK(j, kHashSize)];
     int lo = 0, hi = n_pre;  // non-specials ranked before this special
     while (lo < hi) {
       const int mid = (lo + hi) >> 1;
-      const uint64_t e = S.sorted[mid];
+      const uint64_t e = S.sorted[GS_CK(mid, GS_LEN(S.sorted))];
       if (ranks_before(f64_key(nonspecial_value(e, T)), entry_id(e), k, id)) lo = mid + 1; else hi = mid;
     }
-    S.cand_p[j + lo] = key_f64(k);
-    S.cand_id[j + lo] = id;
+    S.cand_p[GS_CK(j + lo, GS_LEN(S.cand_p))] = key_f64(k);
+    S.cand_id[GS_CK(j + lo, GS_LEN(S.cand_id))] = id;
   }
   __syncthreads();
   // exponentials; probability = e / total where the filters read them
-  for (int i = tid; i < n_cand; i += kFinishThreads) S.cand_p[i] = gsm::js_exp(S.cand_p[i] - M);
+  for (int i = tid; i < n_cand; i += kFinishThreads) S.cand_p[GS_CK(i, GS_LEN(S.cand_p))] = gsm::js_exp(S.cand_p[GS_CK(i, GS_LEN(S.cand_p))] - M);
   __syncthreads();
 
   // ---- top-k (sampling.ts:44)
@@ -1946,11 +1979,11 @@ __device__ __forceinline__ uint32_t finish_row(const SampleArgs& a, FinishLds& U
   }
   // ---- min-p (sampling.ts:45-48): p is non-increasing along the list
   if (cfg.min_p > 0) {
-    const double floor_p = S.cand_p[0] / total * cfg.min_p;
+    const double floor_p = S.cand_p[GS_CK(0, GS_LEN(S.cand_p))] / total * cfg.min_p;
     uint32_t my_first = 0xFFFFFFFFu, my_route = 0;
     for (int i = tid; i < n; i += kFinishThreads) {
-      const double p = S.cand_p[i] / total;
-      if (i + 1 < n && S.cand_p[i + 1] / total > p) my_route |= 1u;  // not monotone: replay
+      const double p = S.cand_p[GS_CK(i, GS_LEN(S.cand_p))] / total;
+      if (i + 1 < n && S.cand_p[GS_CK(i + 1, GS_LEN(S.cand_p))] / total > p) my_route |= 1u;  // not monotone: replay
       if (!(p >= floor_p) && (uint32_t)i < my_first) my_first = (uint32_t)i;
       const double d = p >= floor_p ? p - floor_p : floor_p - p;
       if (d < kNearTie * floor_p) my_route |= 2u;
@@ -1985,7 +2018,7 @@ __device__ __forceinline__ uint32_t finish_row(const SampleArgs& a, FinishLds& U
       double s = 0.0;
       for (int q = 0; q < kPer; ++q) {
         const int i = tid * kPer + q;
-        s += i < n ? S.cand_p[i] / total : 0.0;
+        s += i < n ? S.cand_p[GS_CK(i, GS_LEN(S.cand_p))] / total : 0.0;
         local[q] = s;
       }
       double tot;
@@ -2033,7 +2066,7 @@ __device__ __forceinline__ uint32_t finish_row(const SampleArgs& a, FinishLds& U
     } else if (tid == cut / kPer) {
       // 1e-6 boundary ties, as the reference comparison plan reports them
       const double cum = base + local[cut % kPer];
-      const double prev = cum - S.cand_p[cut] / total;
+      const double prev = cum - S.cand_p[GS_CK(cut, GS_LEN(S.cand_p))] / total;
       if (cum - cfg.top_p <= kTieReport * cfg.top_p || (cut > 0 && cfg.top_p - prev <= kTieReport * cfg.top_p)) {
         atomicOr(&S.status_flags, GS_FLAG_TOPP_TIE);
       }
@@ -2061,7 +2094,7 @@ __device__ __forceinline__ uint32_t finish_row(const SampleArgs& a, FinishLds& U
     double s = 0.0;
     for (int q = 0; q < kPer; ++q) {
       const int i = tid * kPer + q;
-      s += i < n ? S.cand_p[i] / total : 0.0;
+      s += i < n ? S.cand_p[GS_CK(i, GS_LEN(S.cand_p))] / total : 0.0;
       local[q] = s;
     }
     double ctotal;
@@ -2111,7 +2144,7 @@ __device__ __forceinline__ uint32_t finish_row(const SampleArgs& a, FinishLds& U
     }
     const uint32_t i = S.first_idx;
     if (i >= (uint32_t)n) return kExactRequest | GS_FLAG_INDEX_CHECK;
-    if (tid == 0) write_result(a, row, (int32_t)S.cand_id[i], tie_report, S.cand_p[i] / total);
+    if (tid == 0) write_result(a, row, (int32_t)S.cand_id[GS_CK(i, GS_LEN(S.cand_id))], tie_report, S.cand_p[GS_CK(i, GS_LEN(S.cand_p))] / total);
     return 0;
   }
 }
@@ -2162,7 +2195,7 @@ __device__ __forceinline__ void deep_add(double v, double vfc, double M, const d
   if (z < (double)(kDeepBins - 1)) {
     const int b = (int)z;
     const uint64_t n = deep_units(z, b);
-    atomicAdd(&mass[b], negate ? 0ull - n : n);
+    atomicAdd(&mass[GS_CK(b, kFinishCap)], negate ? 0ull - n : n);
   } else {
     const double t = deep_term(v, M, tab);
     *tail += negate ? -t : t;
@@ -2292,7 +2325,7 @@ __device__ __noinline__ void deep_stage(const SampleArgs& a, int64_t row, double
     if (lane == leader) base = atomicAdd(counter, (uint32_t)__popcll(m));
     base = (uint32_t)__shfl((int)base, leader, 64);
     const uint32_t pos = base + (uint32_t)__popcll(m & ((1ull << lane) - 1ull));
-    if (pass && pos < (uint32_t)kFinishCap) stage[pos] = ((uint64_t)__builtin_bit_cast(uint32_t, l) << 32) | id;
+    if (pass && pos < (uint32_t)kFinishCap) stage[GS_CK(pos, kFinishCap)] = ((uint64_t)__builtin_bit_cast(uint32_t, l) << 32) | id;
   }, l_lo, l_hi);
 }
 
@@ -2313,16 +2346,16 @@ __device__ __forceinline__ void deep_set_insert(uint32_t* set, uint32_t id) {
 __device__ __noinline__ void deep_setup(Shared& S, int n_sp, bool zero_mass) {
   const int tid = threadIdx.x;
   for (int b = tid; b < kDeepBins; b += kFinishThreads) {
-    if (zero_mass) S.sorted[b] = 0ull;
-    S.hash_counts[b] = 0xFFFFFFFFu;
+    if (zero_mass) S.sorted[GS_CK(b, GS_LEN(S.sorted))] = 0ull;
+    S.hash_counts[GS_CK(b, GS_LEN(S.hash_counts))] = 0xFFFFFFFFu;
   }
-  if (tid < 256) S.tab[tid] = c_exp2_256[tid];
+  if (tid < 256) S.tab[GS_CK(tid, GS_LEN(S.tab))] = c_exp2_256[tid];
   if (tid == 0) {
     S.deep_count = 0;
     S.deep_final = 0;
   }
   __syncthreads();
-  for (int i = tid; i < n_sp; i += kFinishThreads) deep_set_insert(S.hash_counts, S.sp_id[i]);
+  for (int i = tid; i < n_sp; i += kFinishThreads) deep_set_insert(S.hash_counts, S.sp_id[GS_CK(i, GS_LEN(S.sp_id))]);
   __syncthreads();
 }
 
@@ -2347,7 +2380,7 @@ __device__ __noinline__ double deep_prefix_masses(Shared& S, int n_reg, double t
   static_assert(kDeepBins == kFinishCap, "kPer bins per thread");
   const uint64_t* mass = S.sorted;
   Fix128 r_fix{0ull, 0ull};
-  for (int i = tid; i < n_reg; i += kFinishThreads) r_fix = fix_add(r_fix, fix_of(S.cand_p[i]));
+  for (int i = tid; i < n_reg; i += kFinishThreads) r_fix = fix_add(r_fix, fix_of(S.cand_p[GS_CK(i, GS_LEN(S.cand_p))]));
   r_fix = block_fix_sum(r_fix, (uint64_t*)S.top);
   *r_total = fix_to_double(r_fix);
   double* after = (double*)S.sorted;
@@ -2360,7 +2393,7 @@ __device__ __noinline__ double deep_prefix_masses(Shared& S, int n_reg, double t
     if (b < kDeepBins - 1) {
       // e^(c_b - M), c_b = vf - (b + 1/2) w
       const double y = __builtin_fma(-(b + 0.5), kDeepSpan / kDeepBins, vf - M) * GS_256_LOG2E;
-      m = (double)mass[b] * 0x1p-40 * exp2_256_tight(y, S.tab);
+      m = (double)mass[GS_CK(b, kFinishCap)] * 0x1p-40 * exp2_256_tight(y, S.tab);
     }
     sum = fix_add(sum, fix_of(m));
     f[q] = sum;
@@ -2368,7 +2401,7 @@ __device__ __noinline__ double deep_prefix_masses(Shared& S, int n_reg, double t
   Fix128 t_fix;
   const Fix128 base = fix_add(r_fix, block_fix_scan(sum, (uint64_t*)S.top, &t_fix));
 #pragma unroll
-  for (int q = 0; q < kPer; ++q) after[tid * kPer + q] = fix_to_double(fix_add(base, f[q]));
+  for (int q = 0; q < kPer; ++q) after[GS_CK(tid * kPer + q, kFinishCap)] = fix_to_double(fix_add(base, f[q]));
   return fix_to_double(fix_add(r_fix, t_fix));
 }
 
@@ -2396,14 +2429,14 @@ __device__ __noinline__ uint32_t deep_mid(const SampleArgs& a, Shared& S, int64_
   // specials: out with their raw values (where pass 1 counted them; the
   // same units, so exactly), in with their penalised ones below the floor
   for (int i = tid; i < n_sp; i += kFinishThreads) {
-    const uint32_t id = S.sp_id[i];
+    const uint32_t id = S.sp_id[GS_CK(i, GS_LEN(S.sp_id))];
     float l = load_logit(a, row, id);
     if (cfg.softcap > 0) l = softcap_call(l, cfg.softcap);
     if (l > -__builtin_inff() && f32_key(l) < thr) {
       deep_add(div_by_temperature((double)l, T, rT), vfc, M, S.tab, mass, &tail, true);
     }
-    const double vs = key_f64(S.sp_key[i]);
-    if (S.sp_key[i] < S.deep_floor && vs > -__builtin_inf()) deep_add(vs, vfc, M, S.tab, mass, &tail, false);
+    const double vs = key_f64(S.sp_key[GS_CK(i, GS_LEN(S.sp_key))]);
+    if (S.sp_key[GS_CK(i, GS_LEN(S.sp_key))] < S.deep_floor && vs > -__builtin_inf()) deep_add(vs, vfc, M, S.tab, mass, &tail, false);
   }
   double tail_mass;
   block_scan_f64(tail, S.wtmp, &tail_mass);  // the last bin's mass (a fixed order)
@@ -2427,7 +2460,7 @@ __device__ __noinline__ uint32_t deep_mid(const SampleArgs& a, Shared& S, int64_
 #pragma unroll
     for (int q = 0; q < kPer; ++q) {
       const int i = tid * kPer + q;
-      sum += i < n_reg ? S.cand_p[i] : 0.0;
+      sum += i < n_reg ? S.cand_p[GS_CK(i, GS_LEN(S.cand_p))] : 0.0;
       local[q] = sum;
     }
     const double r_base = block_scan_f64(sum, S.wtmp, &r_mass) - sum;
@@ -2458,7 +2491,7 @@ __device__ __noinline__ uint32_t deep_mid(const SampleArgs& a, Shared& S, int64_
   if (walk_near) return kExactRequest | GS_FLAG_NEAR_TIE;
   if (walk_first != 0xFFFFFFFFu) {
     if (walk_first >= (uint32_t)n_reg) return kExactRequest | GS_FLAG_INDEX_CHECK;
-    if (tid == 0) write_result(a, row, (int32_t)S.cand_id[walk_first], 0u, S.cand_p[walk_first] / total);
+    if (tid == 0) write_result(a, row, (int32_t)S.cand_id[GS_CK(walk_first, GS_LEN(S.cand_id))], 0u, S.cand_p[GS_CK(walk_first, GS_LEN(S.cand_p))] / total);
     return 0;
   }
   // ---- the bin the cursor falls in, and a neighbour where a boundary lies
@@ -2467,7 +2500,7 @@ __device__ __noinline__ uint32_t deep_mid(const SampleArgs& a, Shared& S, int64_
     uint32_t first = 0xFFFFFFFFu;
 #pragma unroll
     for (int q = kPer - 1; q >= 0; --q) {
-      if (after[tid * kPer + q] >= target) first = (uint32_t)(tid * kPer + q);
+      if (after[GS_CK(tid * kPer + q, kFinishCap)] >= target) first = (uint32_t)(tid * kPer + q);
     }
     first = wave_min_u32(first);
     if (lane == 0 && first != 0xFFFFFFFFu) atomicMin(&S.first_idx, first);
@@ -2475,11 +2508,11 @@ __device__ __noinline__ uint32_t deep_mid(const SampleArgs& a, Shared& S, int64_
   __syncthreads();
   const int bc = (int)S.first_idx;
   if (bc < 0 || bc >= kDeepBins - 1) return kExactRequest | 0u;  // past the bins' span
-  const int b_hi = after[bc] < target + mrg ? bc + 1 : bc;
+  const int b_hi = after[GS_CK(bc, kFinishCap)] < target + mrg ? bc + 1 : bc;
   // bin bc - 1 taken in too when the mass before bc lies within the margin
-  const bool take_prev = bc > 0 && after[bc - 1] >= target - mrg;
+  const bool take_prev = bc > 0 && after[GS_CK(bc - 1, kFinishCap)] >= target - mrg;
   const int b_lo = take_prev ? bc - 1 : bc;
-  const double pre_before = b_lo > 0 ? after[b_lo - 1] : r_total;
+  const double pre_before = b_lo > 0 ? after[GS_CK(b_lo - 1, kFinishCap)] : r_total;
   // the walk below starts after pre_before: the cursor must lie clearly past it
   if (pre_before >= target - mrg) return kExactRequest | GS_FLAG_NEAR_TIE;
   if (b_hi >= kDeepBins - 1) return kExactRequest | 0u;
@@ -2527,18 +2560,18 @@ __device__ __noinline__ uint32_t deep_final(const SampleArgs& a, Shared& S, int6
     const int b = deep_bin(v, vfc);
     if (b < plan.b_lo || b > plan.b_hi) return;
     const uint32_t pos = atomicAdd(&S.deep_final, 1u);
-    if (pos < (uint32_t)kFinishCap) { gkey[pos] = f64_key(v); gid[pos] = id; }
+    if (pos < (uint32_t)kFinishCap) { gkey[GS_CK(pos, kFinishCap)] = f64_key(v); gid[GS_CK(pos, kHashSize)] = id; }
   };
   for (int i = tid; i < n_s; i += kFinishThreads) {
-    const uint64_t e = stage[i];
+    const uint64_t e = stage[GS_CK(i, kFinishCap)];
     const uint32_t id = (uint32_t)e;
     if (!deep_is_special(spset, id)) {
       gather(div_by_temperature((double)__builtin_bit_cast(float, (uint32_t)(e >> 32)), T, rT), id);
     }
   }
   for (int i = tid; i < n_sp; i += kFinishThreads) {
-    const double vs = key_f64(S.sp_key[i]);
-    if (S.sp_key[i] < S.deep_floor && vs > -__builtin_inf()) gather(vs, S.sp_id[i]);
+    const double vs = key_f64(S.sp_key[GS_CK(i, GS_LEN(S.sp_key))]);
+    if (S.sp_key[GS_CK(i, GS_LEN(S.sp_key))] < S.deep_floor && vs > -__builtin_inf()) gather(vs, S.sp_id[GS_CK(i, GS_LEN(S.sp_id))]);
   }
   __syncthreads();
   const int n_g = (int)S.deep_final;
@@ -2551,23 +2584,23 @@ __device__ __noinline__ uint32_t deep_final(const SampleArgs& a, Shared& S, int6
     uint32_t id = 0;
     int rank = 0;
     if (tid < n_g) {
-      k = gkey[tid];
-      id = gid[tid];
-      for (int j = 0; j < n_g; ++j) rank += ranks_before(gkey[j], gid[j], k, id) ? 1 : 0;
+      k = gkey[GS_CK(tid, kFinishCap)];
+      id = gid[GS_CK(tid, kHashSize)];
+      for (int j = 0; j < n_g; ++j) rank += ranks_before(gkey[GS_CK(j, kFinishCap)], gid[GS_CK(j, kHashSize)], k, id) ? 1 : 0;
     }
     __syncthreads();
     if (tid < n_g) {
-      gkey[rank] = k;
-      gid[rank] = id;
+      gkey[GS_CK(rank, kFinishCap)] = k;
+      gid[GS_CK(rank, kHashSize)] = id;
     }
     __syncthreads();
   } else {
     const int m2 = pow2_at_least(n_g);
-    for (int i = n_g + tid; i < m2; i += kFinishThreads) { gkey[i] = 0; gid[i] = 0xFFFFFFFFu; }
+    for (int i = n_g + tid; i < m2; i += kFinishThreads) { gkey[GS_CK(i, kFinishCap)] = 0; gid[GS_CK(i, kHashSize)] = 0xFFFFFFFFu; }
     __syncthreads();
     block_sort_pairs_desc(gkey, gid, m2);
   }
-  for (int i = tid; i < n_g; i += kFinishThreads) S.cand_p[i] = gsm::js_exp(key_f64(gkey[i]) - M);
+  for (int i = tid; i < n_g; i += kFinishThreads) S.cand_p[GS_CK(i, GS_LEN(S.cand_p))] = gsm::js_exp(key_f64(gkey[GS_CK(i, kFinishCap)]) - M);
   if (tid == 0) { S.first_idx = 0xFFFFFFFFu; S.route_exact = 0; }
   __syncthreads();
   {
@@ -2576,7 +2609,7 @@ __device__ __noinline__ uint32_t deep_final(const SampleArgs& a, Shared& S, int6
 #pragma unroll
     for (int q = 0; q < kPer; ++q) {
       const int i = tid * kPer + q;
-      sum += i < n_g ? S.cand_p[i] : 0.0;
+      sum += i < n_g ? S.cand_p[GS_CK(i, GS_LEN(S.cand_p))] : 0.0;
       g_local[q] = sum;
     }
     double g_total;
@@ -2603,7 +2636,7 @@ __device__ __noinline__ uint32_t deep_final(const SampleArgs& a, Shared& S, int6
   const uint32_t first = S.first_idx;
   if (first == 0xFFFFFFFFu) return kExactRequest | 0u;
   if (first >= (uint32_t)n_g) return kExactRequest | GS_FLAG_INDEX_CHECK;
-  if (tid == 0) write_result(a, row, (int32_t)gid[first], 0u, S.cand_p[first] / plan.total);
+  if (tid == 0) write_result(a, row, (int32_t)gid[GS_CK(first, kHashSize)], 0u, S.cand_p[GS_CK(first, GS_LEN(S.cand_p))] / plan.total);
   return 0;
 }
 
@@ -2670,9 +2703,13 @@ __device__ __noinline__ uint32_t deep_export(const SampleArgs& a, Shared& S) {
   DeepRow& D = a.deep_rows[row];
   const int n_reg = (int)S.deep_n;
   const int n_sp = (int)(S.n_special < (uint32_t)kSpecialCap ? S.n_special : (uint32_t)kSpecialCap);
-  for (int i = tid; i < n_reg; i += kFinishThreads) { D.cand_p[i] = S.cand_p[i]; D.cand_id[i] = S.cand_id[i]; }
-  for (int i = tid; i < n_sp; i += kFinishThreads) { D.sp_key[i] = S.sp_key[i]; D.sp_id[i] = S.sp_id[i]; }
-  for (int b = tid; b < kDeepBins; b += kFinishThreads) D.hist[b] = 0ull;
+  for (int i = tid; i < n_reg; i += kFinishThreads) { D.cand_p[GS_CK(i, GS_LEN(D.cand_p))] = S.cand_p[GS_CK(i, GS_LEN(S.cand_p))]; D.cand_id[GS_CK(i, GS_LEN(D.cand_id))] = S.cand_id[GS_CK(i, GS_LEN(S.cand_id))]; }
+  for (int i = tid; i < n_sp; i += kFinishThreads) { D.sp_key[GS_CK(i, GS_LEN(D.sp_key))] = S.sp_key[GS_CK(i, GS_LEN(S.sp_key))]; D.sp_id[GS_CK(i, GS_LEN(D.sp_id))] = S.sp_id[GS_CK(i, GS_LEN(S.sp_id))]; }
+  for (int b = tid; b < kDeepBins; b += kFinishThreads) D.hist[GS_CK(b, GS_LEN(D.hist))] = 0ull;
+#ifdef GS_CHECKED
+  __syncthreads();
+  if (GS_CHECK_FAILED()) return kExactRequest | GS_FLAG_INDEX_CHECK;
+#endif
   if (tid == 0) {
     D.M = S.deep_m;
     D.u = S.deep_u;
@@ -2682,6 +2719,8 @@ __device__ __noinline__ uint32_t deep_export(const SampleArgs& a, Shared& S) {
     D.n_reg = (uint32_t)n_reg;
     D.n_sp = (uint32_t)n_sp;
     D.n_stage = 0;
+    D.index_check = 0;
+    D.index_check2 = 0;
     const uint32_t q = atomicAdd(&a.deep_queue->count1, 1u);
     a.deep_queue->rows[q] = (uint32_t)row;
   }
@@ -2759,9 +2798,9 @@ __device__ __forceinline__ uint32_t deep_parts(const SampleArgs& a, uint32_t row
 
 // Takes the next work item (every thread of the block gets it).
 __device__ __forceinline__ uint32_t deep_take(Shared& S, uint32_t* next) {
-  if (threadIdx.x == 0) S.sel[0] = atomicAdd(next, 1u);
+  if (threadIdx.x == 0) S.sel[GS_CK(0, GS_LEN(S.sel))] = atomicAdd(next, 1u);
   __syncthreads();
-  const uint32_t item = S.sel[0];
+  const uint32_t item = S.sel[GS_CK(0, GS_LEN(S.sel))];
   __syncthreads();
   return item;
 }
@@ -2770,10 +2809,10 @@ __device__ __forceinline__ uint32_t deep_take(Shared& S, uint32_t* next) {
 __device__ __noinline__ void deep_import(const DeepRow& D, Shared& S, bool with_region) {
   const int tid = threadIdx.x;
   const int n_sp = (int)D.n_sp;
-  for (int i = tid; i < n_sp; i += kFinishThreads) { S.sp_key[i] = D.sp_key[i]; S.sp_id[i] = D.sp_id[i]; }
+  for (int i = tid; i < n_sp; i += kFinishThreads) { S.sp_key[GS_CK(i, GS_LEN(S.sp_key))] = D.sp_key[GS_CK(i, GS_LEN(D.sp_key))]; S.sp_id[GS_CK(i, GS_LEN(S.sp_id))] = D.sp_id[GS_CK(i, GS_LEN(D.sp_id))]; }
   if (with_region) {
     const int n_reg = (int)D.n_reg;
-    for (int i = tid; i < n_reg; i += kFinishThreads) { S.cand_p[i] = D.cand_p[i]; S.cand_id[i] = D.cand_id[i]; }
+    for (int i = tid; i < n_reg; i += kFinishThreads) { S.cand_p[GS_CK(i, GS_LEN(S.cand_p))] = D.cand_p[GS_CK(i, GS_LEN(D.cand_p))]; S.cand_id[GS_CK(i, GS_LEN(S.cand_id))] = D.cand_id[GS_CK(i, GS_LEN(D.cand_id))]; }
   }
   if (tid == 0) {
     S.deep_m = D.M;
@@ -2800,8 +2839,9 @@ __device__ __noinline__ void deep1_part(const SampleArgs& a, Shared& S, int64_t 
   const double vfc = (double)key_f32(thr) / T * ((double)kDeepBins / kDeepSpan);
   const float l_below = key_f32(thr - 1u);
   uint64_t* mass = S.sorted;
-  for (int b = tid; b < kDeepBins; b += kFinishThreads) mass[b] = 0ull;
-  if (tid < 256) S.tab[tid] = c_exp2_256[tid];
+  GS_CHECK_RESET();
+  for (int b = tid; b < kDeepBins; b += kFinishThreads) mass[GS_CK(b, kFinishCap)] = 0ull;
+  if (tid < 256) S.tab[GS_CK(tid, GS_LEN(S.tab))] = c_exp2_256[tid];
   __syncthreads();
   double tail = 0.0;
   visit_range<false>(a, row, cfg.softcap, i0, i1, [&](float l, uint32_t) {
@@ -2812,10 +2852,14 @@ __device__ __noinline__ void deep1_part(const SampleArgs& a, Shared& S, int64_t 
   block_scan_f64(tail, S.wtmp, &t_all);
   __syncthreads();
   for (int b = tid; b < kDeepBins; b += kFinishThreads) {
-    const uint64_t m = mass[b];
-    if (m) atomicAdd((unsigned long long*)&D.hist[b], (unsigned long long)m);
+    const uint64_t m = mass[GS_CK(b, kFinishCap)];
+    if (m) atomicAdd((unsigned long long*)&D.hist[GS_CK(b, GS_LEN(D.hist))], (unsigned long long)m);
   }
-  if (tid == 0) D.tail[part] = t_all;
+  if (tid == 0) D.tail[GS_CK(part, GS_LEN(D.tail))] = t_all;
+#ifdef GS_CHECKED
+  __syncthreads();
+  if (GS_CHECK_FAILED() && tid == 0) D.index_check = 1u;
+#endif
 }
 
 __global__ __launch_bounds__(kFinishThreads) void deep1_kernel(SampleArgs) {
@@ -2843,11 +2887,19 @@ __global__ __launch_bounds__(kFinishThreads) void deep1_kernel(SampleArgs) {
 __device__ __noinline__ uint32_t deep_mid_row(const SampleArgs& a, Shared& S, int64_t row, uint32_t parts) {
   const int tid = threadIdx.x;
   DeepRow& D = a.deep_rows[row];
+#ifdef GS_CHECKED
+  if (D.index_check) return kExactRequest | GS_FLAG_INDEX_CHECK;
+#endif
+  GS_CHECK_RESET();
   deep_import(D, S, true);
-  for (int b = tid; b < kDeepBins; b += kFinishThreads) S.sorted[b] = D.hist[b];
+  for (int b = tid; b < kDeepBins; b += kFinishThreads) S.sorted[GS_CK(b, GS_LEN(S.sorted))] = D.hist[GS_CK(b, GS_LEN(D.hist))];
   deep_setup(S, (int)D.n_sp, false);
-  const double tail = tid < (int)parts ? D.tail[tid] : 0.0;
+  const double tail = tid < (int)parts ? D.tail[GS_CK(tid, GS_LEN(D.tail))] : 0.0;
   const uint32_t r = deep_mid(a, S, row, (int)D.n_sp, tail);
+#ifdef GS_CHECKED
+  __syncthreads();
+  if (GS_CHECK_FAILED()) return kExactRequest | GS_FLAG_INDEX_CHECK;
+#endif
   if (r != kDeepPass2) return r;
   if (tid == 0) {
     D.plan = S.plan;
@@ -2878,6 +2930,10 @@ __global__ __launch_bounds__(kFinishThreads) void deep_mid_kernel(SampleArgs) {
 __device__ __noinline__ void deep2_part(const SampleArgs& a, int64_t row, int64_t i0, int64_t i1) {
   const int lane = threadIdx.x & 63;
   DeepRow& D = a.deep_rows[row];
+  GS_CHECK_RESET();
+#ifdef GS_CHECKED
+  __syncthreads();
+#endif
   const float l_lo = D.plan.l_lo, l_top = D.plan.l_top;
   visit_range<true>(a, row, a.configs[row].softcap, i0, i1, [&](float l, uint32_t id) {
     const bool pass = l >= l_lo && l <= l_top;
@@ -2888,8 +2944,12 @@ __device__ __noinline__ void deep2_part(const SampleArgs& a, int64_t row, int64_
     if (lane == leader) base = atomicAdd(&D.n_stage, (uint32_t)__popcll(m));
     base = (uint32_t)__shfl((int)base, leader, 64);
     const uint32_t pos = base + (uint32_t)__popcll(m & ((1ull << lane) - 1ull));
-    if (pass && pos < (uint32_t)kFinishCap) D.stage[pos] = ((uint64_t)__builtin_bit_cast(uint32_t, l) << 32) | id;
+    if (pass && pos < (uint32_t)kFinishCap) D.stage[GS_CK(pos, GS_LEN(D.stage))] = ((uint64_t)__builtin_bit_cast(uint32_t, l) << 32) | id;
   }, l_lo, l_top);
+#ifdef GS_CHECKED
+  __syncthreads();
+  if (GS_CHECK_FAILED() && threadIdx.x == 0) D.index_check2 = 1u;
+#endif
 }
 
 __global__ __launch_bounds__(kFinishThreads) void deep2_kernel(SampleArgs) {
@@ -2915,17 +2975,26 @@ __global__ __launch_bounds__(kFinishThreads) void deep2_kernel(SampleArgs) {
 __device__ __noinline__ uint32_t deep_final_row(const SampleArgs& a, Shared& S, int64_t row) {
   const int tid = threadIdx.x;
   const DeepRow& D = a.deep_rows[row];
+#ifdef GS_CHECKED
+  if (D.index_check || D.index_check2) return kExactRequest | GS_FLAG_INDEX_CHECK;
+#endif
+  GS_CHECK_RESET();
   deep_import(D, S, false);
   deep_setup(S, (int)D.n_sp, false);
   const uint32_t n_stage = D.n_stage;
   const int n_keep = (int)(n_stage < (uint32_t)kFinishCap ? n_stage : (uint32_t)kFinishCap);
-  for (int i = tid; i < n_keep; i += kFinishThreads) ((uint64_t*)S.cand_p)[i] = D.stage[i];
+  for (int i = tid; i < n_keep; i += kFinishThreads) ((uint64_t*)S.cand_p)[i] = D.stage[GS_CK(i, GS_LEN(D.stage))];
   if (tid == 0) {
     S.plan = D.plan;
     S.deep_count = n_stage;
   }
   __syncthreads();
-  return deep_final(a, S, row, (int)D.n_sp);
+  const uint32_t r = deep_final(a, S, row, (int)D.n_sp);
+#ifdef GS_CHECKED
+  __syncthreads();
+  if (GS_CHECK_FAILED()) return kExactRequest | GS_FLAG_INDEX_CHECK;
+#endif
+  return r;
 }
 
 __global__ __launch_bounds__(kFinishThreads) void deep_final_kernel(SampleArgs) {
@@ -2943,7 +3012,12 @@ __global__ __launch_bounds__(kFinishThreads) void deep_final_kernel(SampleArgs) 
 
 __global__ __launch_bounds__(kFinishThreads) void finish_kernel(SampleArgs a) {
   __shared__ FinishLds U;
+  GS_CHECK_RESET();
   uint32_t r = finish_row(a, U);
+#ifdef GS_CHECKED
+  __syncthreads();
+  if (GS_CHECK_FAILED()) r = kExactRequest | GS_FLAG_INDEX_CHECK;
+#endif
   if (r == kDeepRequest) {
     __syncthreads();
     // calls of their own that read the arguments where the kernel received
@@ -2951,6 +3025,10 @@ __global__ __launch_bounds__(kFinishThreads) void finish_kernel(SampleArgs a) {
     // the deep kernels take the row from here
     const SampleArgs& ka = *(const SampleArgs*)__builtin_amdgcn_kernarg_segment_ptr();
     r = a.deep_rows ? deep_export(ka, U.fin) : deep_draw(ka, U);
+#ifdef GS_CHECKED
+    __syncthreads();
+    if (GS_CHECK_FAILED()) r = kExactRequest | GS_FLAG_INDEX_CHECK;
+#endif
   }
   // the exact path is entered from here only, where nothing else is live
   if (r & kExactRequest) to_exact(a, U, blockIdx.x, r & ~kExactRequest);

@@ -195,9 +195,11 @@ struct DeepPlan {
 struct DeepRow {
   double M, u, margin;   // the row's maximum value, its uniform, the reference's rounding margin
   uint64_t floor;        // the region floor's value key
-  uint32_t thr, n_reg, n_sp, pad;  // the region floor's logit key, region candidates, specials
+  uint32_t thr, n_reg, n_sp;  // the region floor's logit key, region candidates, specials
+  uint32_t index_check;       // checked build: a pass-1 part failed an index check
   DeepPlan plan;
-  uint32_t n_stage, pad2;                // pass-2 entries staged
+  uint32_t n_stage;           // pass-2 entries staged
+  uint32_t index_check2;      // checked build: a pass-2 part failed an index check
   double tail[kFinishMaxChunks];         // pass 1: each part's last-bin sum
   uint64_t hist[kDeepBins];              // pass 1: bin sums in fixed point (global atomics)
   double cand_p[kFinishCap];             // the region's candidates: exact exponentials

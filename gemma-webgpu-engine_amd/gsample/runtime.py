@@ -16,7 +16,11 @@ from .config import DecodingConfig, validate_decoding_config
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 PKG = os.path.dirname(HERE)
-LIB_PATH = os.path.join(PKG, "lib", "libgsample.so")
+# GSAMPLE_CHECKED=1 loads the checked build (range checks on the finish's
+# array indices; a violation flags the row GS_FLAG_INDEX_CHECK and replays it
+# on the exact path)
+LIB_PATH = os.path.join(PKG, "lib", "libgsample_checked.so" if os.environ.get("GSAMPLE_CHECKED") == "1"
+                        else "libgsample.so")
 
 GS_F32, GS_BF16 = 0, 1
 GS_QAT_ROW_MAJOR, GS_QAT_BLOCK_MAJOR = 0, 1

@@ -22,12 +22,15 @@ def test_header_declares_the_entry_points():
         assert required in names
 
 
-def test_library_exports_every_declared_symbol():
+@pytest.mark.parametrize("name", ["libgsample.so", "libgsample_checked.so"])
+def test_library_exports_every_declared_symbol(name):
+    """The library and its checked build (range-checked finish indices)."""
     import gsample.runtime as rt
 
-    if not os.path.exists(rt.LIB_PATH):
-        pytest.fail("libgsample.so is not built; run __graft_entry__.build()")
-    lib = ctypes.CDLL(rt.LIB_PATH)
+    path = os.path.join(os.path.dirname(rt.LIB_PATH), name)
+    if not os.path.exists(path):
+        pytest.fail(f"{name} is not built; run __graft_entry__.build()")
+    lib = ctypes.CDLL(path)
     missing = [n for n in declared_functions() if not hasattr(lib, n)]
     assert not missing, missing
     assert set(declared_functions()) <= set(rt.EXPORTED_SYMBOLS) | set(declared_functions())
