@@ -106,6 +106,43 @@ __device__ __forceinline__ double block_scan_f64(double v, double* s_w, double* 
   return incl + off;
 }
 
+// The block-wide sum of one 64-bit integer per thread, in every thread
+// (integer addition: the same sum in any order); s_w holds kWaves values.
+__device__ __forceinline__ uint64_t block_sum_u64(uint64_t v, uint64_t* s_w) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  v = wave_sum_u64(v);
+  __syncthreads();  // earlier readers of s_w are done
+  if (lane == 0) s_w[wave] = v;
+  __syncthreads();
+  uint64_t t = 0ull;
+  for (int w = 0; w < kWaves; ++w) t += s_w[w];
+  __syncthreads();
+  return t;
+}
+// the same for two values at once; s_w holds 2 kWaves values
+__device__ __forceinline__ void block_sum2_u64(uint64_t x, uint64_t y, uint64_t* s_w, uint64_t* tx, uint64_t* ty) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  x = wave_sum_u64(x);
+  y = wave_sum_u64(y);
+  __syncthreads();  // earlier readers of s_w are done
+  if (lane == 0) { s_w[wave] = x; s_w[kWaves + wave] = y; }
+  __syncthreads();
+  uint64_t a = 0ull, b = 0ull;
+  for (int w = 0; w < kWaves; ++w) { a += s_w[w]; b += s_w[kWaves + w]; }
+  __syncthreads();
+  *tx = a;
+  *ty = b;
+}
+// Sums of terms whose order in LDS depends on atomics (the deep draw's
+// region and gathered candidates) go through 64-bit integers in units of
+// 2^-50 of a reference scale, so that every run gives the same sum: a term
+// up to the scale is at most 2^50 units, 4096 of them stay below 2^62, and
+// each rounds by at most 2^-51 of the scale.
+constexpr double kUnitScale = 0x1p50;
+__device__ __forceinline__ uint64_t to_units(double x, double inv_scale) {
+  return (uint64_t)__builtin_rint(x * inv_scale * kUnitScale);
+}
+
 // Block-wide sums of two binary64 values in every thread, in a fixed order
 // (per wave, then the waves in order); s_w holds 2 * kWaves values and is
 // used once per kernel, so no barrier follows the reads.
@@ -1140,6 +1177,15 @@ __device__ double recompute_nonspecial_sum(const SampleArgs& a, int64_t row, con
   return (t_all < __builtin_inf() && t_sp <= 0.5 * t_all) ? t_all - t_sp : -1.0;
 }
 
+constexpr int kCountRank = 512;    // candidates the bin walk ranks by counting
+constexpr int kCountSmall = 128;  // gathered candidates ranked by counting without the bins
+constexpr int kWalkMin = 2048;    // a full draw's prefix past this many entries is walked, not sorted
+__device__ __noinline__ uint32_t walk_cursor_by_bins(const uint64_t* list, int n_list, double T, const uint64_t* keys,
+                                                     const uint32_t* ids, int n, double M, double range_lo,
+                                                     double p0, double target, double mrg, uint64_t* bmass,
+                                                     uint32_t* sel, double* wtmp, uint64_t* kminmax,
+                                                     uint32_t* cscratch, uint32_t* hit_id, double* hit_term);
+
 // The finish of row blockIdx.x. Returns 0 when the row's result is written,
 // else kExactRequest | the result flags the exact path keeps.
 __device__ __forceinline__ uint32_t finish_row(const SampleArgs& a, FinishLds& U) {
@@ -1918,6 +1964,25 @@ __device__ __forceinline__ uint32_t finish_row(const SampleArgs& a, FinishLds& U
       __syncthreads();
       return kDeepRequest;
     }
+    const int n_rank = floor_key ? (int)S.sel[GS_CK(3, GS_LEN(S.sel))] : n_ns;
+    if (draw_pool && n_rank > kWalkMin && thr > kKeyNegInf && n_sp_in <= kHashSize - 5 * kCountRank) {
+      // a full-vocabulary draw whose cursor falls deep in the complete
+      // region: walk only the value bin it falls in (the region left
+      // unsorted; every candidate's value lies in [floor value, M]);
+      // cursors near a prefix, a wrong bin or a crowded one go the sorted
+      // way below (the walk's scratch, the end of the in-region specials' id
+      // array, lies past their n_sp_in entries)
+      uint32_t hit_id = 0;
+      double hit_term = 0.0;
+      const uint32_t w = walk_cursor_by_bins(S.sorted, n_ns, T, in_key, in_id, n_ns + n_sp_in, M,
+                                             (double)key_f32(thr) / T, 0.0, u_draw * total, draw_margin * total,
+                                             (uint64_t*)S.tab, (uint32_t*)(S.top + 2), S.wsum2, S.top,
+                                             S.hash_counts + (kHashSize - 5 * kCountRank), &hit_id, &hit_term);
+      if (w == 0u) {
+        if (tid == 0) write_result(a, row, (int32_t)hit_id, S.status_flags, hit_term / total);
+        return 0;
+      }
+    }
     if (floor_key) {
       n_pre = (int)S.sel[GS_CK(3, GS_LEN(S.sel))];
       // specials at or above the boundary's value (in_key is descending)
@@ -2202,84 +2267,6 @@ __device__ __forceinline__ void deep_add(double v, double vfc, double M, const d
   }
 }
 
-// Exact sums of exponentials in 128-bit fixed point (units of 2^-100): a
-// term e in (0, 1] is its 53-bit mantissa shifted to that scale, truncated
-// below 2^-100 (at most V 2^-100 over a row); integer addition is exact and
-// associative, so any summation order gives the same sum.
-struct Fix128 {
-  uint64_t lo, hi;
-};
-__device__ __forceinline__ Fix128 fix_add(Fix128 a, Fix128 b) {
-  Fix128 r;
-  r.lo = a.lo + b.lo;
-  r.hi = a.hi + b.hi + (r.lo < a.lo ? 1ull : 0ull);
-  return r;
-}
-// u 2^s in units of 2^-100 (the bits below 2^-100 dropped)
-__device__ __forceinline__ Fix128 fix_shift(uint64_t u, int s) {
-  if (s <= -64) return Fix128{0ull, 0ull};
-  if (s < 0) return Fix128{u >> (-s), 0ull};
-  if (s == 0) return Fix128{u, 0ull};
-  if (s < 64) return Fix128{u << s, u >> (64 - s)};
-  if (s < 128) return Fix128{0ull, u << (s - 64)};
-  return Fix128{0ull, 0ull};
-}
-__device__ __forceinline__ Fix128 fix_of(double e) {
-  if (!(e > 0)) return Fix128{0ull, 0ull};
-  int ex;
-  const double m = __builtin_frexp(e, &ex);            // e = m 2^ex, m in [0.5, 1)
-  const uint64_t mi = (uint64_t)__builtin_ldexp(m, 53);  // 53-bit integer mantissa
-  return fix_shift(mi, ex - 53 + 100);                 // e 2^100 = mi 2^(ex - 53 + 100)
-}
-__device__ __forceinline__ double fix_to_double(Fix128 a) {
-  return __builtin_ldexp((double)a.hi, -36) + __builtin_ldexp((double)a.lo, -100);
-}
-// the block-wide sum of one Fix128 per thread, in every thread; s_w holds
-// 2 * kWaves u64 of LDS
-__device__ __forceinline__ Fix128 block_fix_sum(Fix128 v, uint64_t* s_w) {
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  for (int m = 32; m > 0; m >>= 1) {
-    Fix128 o;
-    o.lo = shfl_xor_u64(v.lo, m);
-    o.hi = shfl_xor_u64(v.hi, m);
-    v = fix_add(v, o);
-  }
-  __syncthreads();
-  if (lane == 0) { s_w[2 * wave] = v.lo; s_w[2 * wave + 1] = v.hi; }
-  __syncthreads();
-  Fix128 t{0ull, 0ull};
-  for (int w = 0; w < kWaves; ++w) t = fix_add(t, Fix128{s_w[2 * w], s_w[2 * w + 1]});
-  __syncthreads();
-  return t;
-}
-// the exclusive block-wide prefix of one Fix128 per thread (thread order),
-// and the block total in *total; s_w holds 2 * kWaves u64 of LDS
-__device__ __forceinline__ Fix128 block_fix_scan(Fix128 v, uint64_t* s_w, Fix128* total) {
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  // the wave's exclusive prefix: a butterfly that keeps, per lane, the sum of
-  // the lower lanes of each pair of halves it joins
-  Fix128 incl = v, pre{0ull, 0ull};
-  for (int m = 1; m < 64; m <<= 1) {
-    Fix128 o;
-    o.lo = shfl_xor_u64(incl.lo, m);
-    o.hi = shfl_xor_u64(incl.hi, m);
-    if (lane & m) pre = fix_add(pre, o);
-    incl = fix_add(incl, o);  // the sum of the 2m lanes of this lane's group
-  }
-  __syncthreads();
-  if (lane == 0) { s_w[2 * wave] = incl.lo; s_w[2 * wave + 1] = incl.hi; }
-  __syncthreads();
-  Fix128 off{0ull, 0ull}, t{0ull, 0ull};
-  for (int w = 0; w < kWaves; ++w) {
-    const Fix128 x{s_w[2 * w], s_w[2 * w + 1]};
-    if (w < wave) off = fix_add(off, x);
-    t = fix_add(t, x);
-  }
-  __syncthreads();
-  *total = t;
-  return fix_add(off, pre);
-}
-
 // Slot of id in the LDS hash set of the row's special ids (-1: absent).
 __device__ __forceinline__ bool deep_is_special(const uint32_t* set, uint32_t id) {
   uint32_t h = hash_id(id) & (kHashSize - 1);
@@ -2368,24 +2355,30 @@ __device__ __forceinline__ bool deep_inputs_ok(const Shared& S, double T) {
   return vf <= S.deep_m && T >= 0x1p-20 && T <= 0x1p20;
 }
 
-// The deep draw's exact masses: the region's (over cand_p[0..n_reg)) into
+// The deep draw's masses: the region's (over cand_p[0..n_reg)) into
 // *r_total, and after[b] (over the histogram in sorted, in place) the mass of
-// the region and of bins 0 .. b, in binary64 from exact fixed-point sums of
-// the bins' masses (units x 2^-40 x e^(c_b - M), the last bin tail_mass).
-// Returns the normaliser. The whole block calls it.
+// the region and of bins 0 .. b (a bin's mass: units x 2^-40 x e^(c_b - M),
+// the last bin tail_mass). Returns the normaliser. The region's terms (in
+// (0, 1], in an order atomics chose) are summed as integers in units of
+// 2^-50 (under 4096 2^-51 < 2e-12 off, and the normaliser is at least 1);
+// the bins, whose order is fixed, in binary64 (each thread's kPer
+// consecutive bins in order, then block_scan_f64's waves in thread order),
+// within 32 additions' rounding (under 4e-15 relative). Every run and both
+// the single-workgroup and the many-workgroup draws get the same values,
+// within the 2^-38 the walk's margin allows for the histogram. The whole
+// block calls it.
 __device__ __noinline__ double deep_prefix_masses(Shared& S, int n_reg, double tail_mass, double vf, double M,
                                                   double* r_total) {
   const int tid = threadIdx.x;
   constexpr int kPer = kFinishCap / kFinishThreads;  // region entries per thread (and bins)
   static_assert(kDeepBins == kFinishCap, "kPer bins per thread");
   const uint64_t* mass = S.sorted;
-  Fix128 r_fix{0ull, 0ull};
-  for (int i = tid; i < n_reg; i += kFinishThreads) r_fix = fix_add(r_fix, fix_of(S.cand_p[GS_CK(i, GS_LEN(S.cand_p))]));
-  r_fix = block_fix_sum(r_fix, (uint64_t*)S.top);
-  *r_total = fix_to_double(r_fix);
-  double* after = (double*)S.sorted;
-  Fix128 f[kPer];
-  Fix128 sum{0ull, 0ull};
+  uint64_t r = 0ull;
+  for (int i = tid; i < n_reg; i += kFinishThreads) r += to_units(S.cand_p[GS_CK(i, GS_LEN(S.cand_p))], 1.0);
+  const double r_tot = (double)block_sum_u64(r, (uint64_t*)S.wsum) / kUnitScale;
+  *r_total = r_tot;
+  double f[kPer];
+  double sum = 0.0;
 #pragma unroll
   for (int q = 0; q < kPer; ++q) {
     const int b = tid * kPer + q;
@@ -2395,21 +2388,23 @@ __device__ __noinline__ double deep_prefix_masses(Shared& S, int n_reg, double t
       const double y = __builtin_fma(-(b + 0.5), kDeepSpan / kDeepBins, vf - M) * GS_256_LOG2E;
       m = (double)mass[GS_CK(b, kFinishCap)] * 0x1p-40 * exp2_256_tight(y, S.tab);
     }
-    sum = fix_add(sum, fix_of(m));
+    sum += m;
     f[q] = sum;
   }
-  Fix128 t_fix;
-  const Fix128 base = fix_add(r_fix, block_fix_scan(sum, (uint64_t*)S.top, &t_fix));
+  double t;
+  // (block_scan_f64's barriers also order every read of mass[] before after[] overwrites it)
+  const double base = r_tot + (block_scan_f64(sum, S.wtmp, &t) - sum);
+  double* after = (double*)S.sorted;
 #pragma unroll
-  for (int q = 0; q < kPer; ++q) after[GS_CK(tid * kPer + q, kFinishCap)] = fix_to_double(fix_add(base, f[q]));
-  return fix_to_double(fix_add(r_fix, t_fix));
+  for (int q = 0; q < kPer; ++q) after[GS_CK(tid * kPer + q, kFinishCap)] = base + f[q];
+  return r_tot + t;
 }
 
 // What pass 1 leaves (the mass histogram in sorted, each thread's last-bin
 // sum in `tail`) is completed and used: the specials go out of the
 // histogram with their raw values and in with their penalised ones, the
-// normaliser and every bin's prefix mass are summed in fixed point, and the
-// region is walked with them. Returns 0 with the result written,
+// normaliser and every bin's prefix mass are summed in binary64 in a fixed
+// order, and the region is walked with them. Returns 0 with the result written,
 // kExactRequest | flags, or kDeepPass2 with S.plan holding the bins the
 // cursor falls in and the logit range to gather.
 constexpr uint32_t kDeepPass2 = 1u << 27;
@@ -2441,7 +2436,7 @@ __device__ __noinline__ uint32_t deep_mid(const SampleArgs& a, Shared& S, int64_
   double tail_mass;
   block_scan_f64(tail, S.wtmp, &tail_mass);  // the last bin's mass (a fixed order)
   __syncthreads();
-  // ---- the region's exact mass, and the bins' prefix masses in fixed point
+  // ---- the region's mass, and the bins' prefix masses
   constexpr int kPer = kFinishCap / kFinishThreads;  // region entries per thread (and bins)
   double r_total;
   const double total = deep_prefix_masses(S, n_reg, tail_mass, vf, M, &r_total);
@@ -2539,6 +2534,194 @@ __device__ __noinline__ uint32_t deep_mid(const SampleArgs& a, Shared& S, int64_
   return kDeepPass2;
 }
 
+// The walk of a cursor over n candidates left unsorted, without sorting
+// them all. Candidate i < n_list is the non-special list entry list[i]
+// (value l / T as the reference computes it), candidate n_list + j the
+// special keys[j] (a value key) / ids[j]. The reference walks them in
+// (value desc, id asc) order, adding their terms e^(v - M) to a prefix that
+// starts at p0, and takes the first whose prefix reaches target
+// (sampling.ts:58-64). Here a 256-bin histogram linear in the value below
+// the largest (bin(v) = floor((v_hi - v) 256 / (v_hi - v_lo)), a
+// non-increasing function of v, so each bin is a run of the sorted order),
+// holding each bin's approximate mass (binary32 terms relative to the
+// largest, in units of 2^-40, added as integers), names the bin the
+// cursor falls in; the terms of the bins above it are summed as integers in
+// units of 2^-50 of the largest term (n 2^-51 of it at most, inside mrg, and
+// the same sum in every run: the candidates' order in LDS came from
+// atomics); and only that bin's entries, when at most kCountRank, are ranked
+// (by counting; the ids are distinct) and walked with the exact terms
+// (js_exp, as the sorted walk computes them). Returns 0 with the
+// candidate's id and term in *hit_id / *hit_term, 1 when a prefix lies
+// within mrg of the target, 2 when the approximate masses named the wrong
+// bin or the bin holds more than kCountRank entries: the caller then goes
+// the sorted way. Scratch: bmass (256 words), sel (4), wtmp (2 kWaves),
+// kminmax (2) and cscratch (5 kCountRank 32-bit words). The whole block
+// calls it.
+__device__ __noinline__ uint32_t walk_cursor_by_bins(const uint64_t* list, int n_list, double T, const uint64_t* keys,
+                                                     const uint32_t* ids, int n, double M, double range_lo,
+                                                     double p0, double target, double mrg, uint64_t* bmass,
+                                                     uint32_t* sel, double* wtmp, uint64_t* kminmax,
+                                                     uint32_t* cscratch, uint32_t* hit_id, double* hit_term) {
+  const int tid = threadIdx.x, lane = tid & 63;
+  // l / T as the reference rounds it, in three operations where the
+  // quotient's conditions hold
+  const bool fast_div = T >= 0x1p-20 && T <= 0x1p20;
+  const double rT = 1.0 / T;
+  auto get = [&](int i, uint64_t* k, uint32_t* id) {
+    if (i < n_list) {
+      const uint64_t e = list[GS_CK(i, kFinishCap)];
+      const double l = (double)key_f32(entry_key(e));
+      *k = f64_key(fast_div ? div_by_temperature(l, T, rT) : l / T);
+      *id = entry_id(e);
+    } else {
+      *k = keys[GS_CK(i - n_list, kFinishCap)];
+      *id = ids[GS_CK(i - n_list, kHashSize)];
+    }
+  };
+  if (tid < 256) bmass[tid] = 0ull;
+  if (tid == 0) { kminmax[0] = 0ull; kminmax[1] = 0ull; sel[1] = 0u; sel[2] = 0xFFFFFFFFu; sel[3] = 0u; }
+  __syncthreads();
+  // the value range: [range_lo, M] when the caller knows a bound (range_lo
+  // < M), else the candidates' own (the minimum key as the maximum of the
+  // complements)
+  double v_hi = M, v_lo = range_lo;
+  if (!(range_lo < M)) {
+    uint64_t kmax = 0ull, kneg = 0ull;
+    for (int i = tid; i < n; i += kFinishThreads) {
+      uint64_t k;
+      uint32_t id;
+      get(i, &k, &id);
+      kmax = k > kmax ? k : kmax;
+      kneg = ~k > kneg ? ~k : kneg;
+    }
+    kmax = wave_max_u64(kmax);
+    kneg = wave_max_u64(kneg);
+    if (lane == 0) {
+      atomicMax((unsigned long long*)&kminmax[0], (unsigned long long)kmax);
+      atomicMax((unsigned long long*)&kminmax[1], (unsigned long long)kneg);
+    }
+    __syncthreads();
+    v_hi = key_f64(kminmax[0]);
+    v_lo = key_f64(~kminmax[1]);
+  }
+  const double bscale = v_hi > v_lo ? 256.0 / (v_hi - v_lo) : 0.0;
+  auto bin_of = [&](double v) -> uint32_t {
+    const double z = (v_hi - v) * bscale;
+    return z < 255.0 ? (uint32_t)z : 255u;
+  };
+  const double e_top = gsm::js_exp(v_hi - M);  // the largest term
+  // approximate masses: binary32 exponentials relative to the largest term
+  // (within 1e-6 relative), in units of 2^-40 of it
+  for (int i = tid; i < n; i += kFinishThreads) {
+    uint64_t k;
+    uint32_t id;
+    get(i, &k, &id);
+    const double v = key_f64(k);
+    atomicAdd((unsigned long long*)&bmass[GS_CK(bin_of(v), 256)], mass_units((float)(v - v_hi)));
+  }
+  __syncthreads();
+  if (tid < 64) {
+    // lane l holds bins 4l .. 4l+3, highest values first
+    double m[4], ms = 0.0;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      m[q] = (double)bmass[4 * lane + q] * 0x1p-40 * e_top;
+      ms += m[q];
+    }
+    const double incl = wave_scan_f64(ms);
+    const uint64_t hit_m = __ballot(p0 + incl >= target);
+    uint32_t b = 0xFFFFFFFFu;
+    if (hit_m) {
+      const int f = __ffsll((unsigned long long)hit_m) - 1;
+      if (lane == f) {
+        double cum = p0 + incl - ms;
+        int q = 0;
+        while (q < 3 && cum + m[q] < target) { cum += m[q]; ++q; }
+        b = (uint32_t)(4 * lane + q);
+      }
+      b = readlane_u32(b, f);
+    }
+    if (lane == 0) sel[0] = b;
+  }
+  __syncthreads();
+  const uint32_t bc = sel[0];
+  if (bc == 0xFFFFFFFFu) return 2u;
+  // the exact masses above the bin and in it, and the bin's entries compacted
+  uint64_t* ck = (uint64_t*)cscratch;                 // [kCountRank]
+  uint32_t* cid = cscratch + 2 * kCountRank;          // [kCountRank]
+  double* ct = (double*)(cscratch + 3 * kCountRank);  // [kCountRank]
+  const double inv_top = 1.0 / e_top;
+  uint64_t above = 0ull, inbin = 0ull;
+  for (int i = tid; i < n; i += kFinishThreads) {
+    uint64_t k;
+    uint32_t id;
+    get(i, &k, &id);
+    const double v = key_f64(k);
+    const uint32_t b = bin_of(v);
+    if (b > bc) continue;
+    const double t = gsm::js_exp(v - M);
+    if (b < bc) {
+      above += to_units(t, inv_top);
+    } else {
+      inbin += to_units(t, inv_top);
+      const uint32_t pos = atomicAdd(&sel[1], 1u);
+      if (pos < (uint32_t)kCountRank) {
+        ck[pos] = k;
+        cid[pos] = id;
+        ct[pos] = t;
+      }
+    }
+  }
+  uint64_t above_u, inbin_u;
+  block_sum2_u64(above, inbin, (uint64_t*)wtmp, &above_u, &inbin_u);
+  const double above_all = (double)above_u / kUnitScale * e_top;
+  const double inbin_all = (double)inbin_u / kUnitScale * e_top;
+  const int c = (int)sel[1];
+  const double base = p0 + above_all;
+  if ((base >= target ? base - target : target - base) < mrg) return 1u;
+  if (base >= target || base + inbin_all < target || c > kCountRank) return 2u;
+  // rank the bin's entries by counting, then walk them in order
+  uint64_t k = 0ull;
+  uint32_t id = 0u;
+  double t = 0.0;
+  int rank = 0;
+  if (tid < c) {
+    k = ck[tid];
+    id = cid[tid];
+    t = ct[tid];
+#pragma unroll 8
+    for (int j = 0; j < c; ++j) rank += ranks_before(ck[j], cid[j], k, id) ? 1 : 0;
+  }
+  __syncthreads();
+  if (tid < c) {
+    ck[rank] = k;
+    cid[rank] = id;
+    ct[rank] = t;
+  }
+  __syncthreads();
+  const double tv = tid < c ? ct[tid] : 0.0;
+  double tot;
+  const double pre = base + block_scan_f64(tv, wtmp, &tot);
+  const uint32_t mine = tid < c && pre >= target ? (uint32_t)tid : 0xFFFFFFFFu;
+  const uint32_t wfirst = wave_min_u32(mine);
+  const bool wnear = __ballot(tid < c && (pre >= target ? pre - target : target - pre) < mrg) != 0;
+  if (lane == 0) {
+    if (wfirst != 0xFFFFFFFFu) atomicMin(&sel[2], wfirst);
+    if (wnear) atomicOr(&sel[3], 1u);
+  }
+  __syncthreads();
+  const bool any_near = sel[3] != 0u;
+  const uint32_t f = sel[2];
+  if (!any_near && f < (uint32_t)c) {
+    *hit_id = cid[f];
+    *hit_term = ct[f];
+  }
+  __syncthreads();  // every thread has read sel[] and the compacted entries
+  if (any_near) return 1u;
+  if (f >= (uint32_t)c) return 2u;
+  return 0u;
+}
+
 // Pass 2's staged logits (in cand_p as (float bits << 32 | id), deep_count of
 // them) are tested against the plan's bins exactly, joined by the specials
 // whose penalised values fall there, sorted (value desc, id asc) and walked
@@ -2577,15 +2760,16 @@ __device__ __noinline__ uint32_t deep_final(const SampleArgs& a, Shared& S, int6
   const int n_g = (int)S.deep_final;
   if (n_g > kFinishCap || n_g == 0) return kExactRequest | 0u;
   // ---- sort them (value desc, id asc) and walk them with exact exponentials
-  if (n_g <= 512) {
-    // the usual few (a bin or two): each finds its place by counting the
-    // entries ranked before it (the ids are distinct)
+  if (n_g <= kCountSmall) {
+    // a few: each finds its place by counting the entries ranked before it
+    // (the ids are distinct)
     uint64_t k = 0;
     uint32_t id = 0;
     int rank = 0;
     if (tid < n_g) {
       k = gkey[GS_CK(tid, kFinishCap)];
       id = gid[GS_CK(tid, kHashSize)];
+#pragma unroll 8
       for (int j = 0; j < n_g; ++j) rank += ranks_before(gkey[GS_CK(j, kFinishCap)], gid[GS_CK(j, kHashSize)], k, id) ? 1 : 0;
     }
     __syncthreads();
@@ -2595,6 +2779,18 @@ __device__ __noinline__ uint32_t deep_final(const SampleArgs& a, Shared& S, int6
     }
     __syncthreads();
   } else {
+    // more: walk only the histogram bin the cursor falls in (the gathered
+    // bins' entries are dense in value), else sort them all
+    uint32_t hit_id = 0;
+    double hit_term = 0.0;
+    const uint32_t w = walk_cursor_by_bins(nullptr, 0, T, gkey, gid, n_g, M, M, plan.pre_before, plan.target,
+                                           plan.mrg, (uint64_t*)S.tab, (uint32_t*)(S.top + 2), S.wsum2, S.top,
+                                           S.hash_counts, &hit_id, &hit_term);
+    if (w == 1u) return kExactRequest | GS_FLAG_NEAR_TIE;
+    if (w == 0u) {
+      if (tid == 0) write_result(a, row, (int32_t)hit_id, 0u, hit_term / plan.total);
+      return 0;
+    }
     const int m2 = pow2_at_least(n_g);
     for (int i = n_g + tid; i < m2; i += kFinishThreads) { gkey[GS_CK(i, kFinishCap)] = 0; gid[GS_CK(i, kHashSize)] = 0xFFFFFFFFu; }
     __syncthreads();

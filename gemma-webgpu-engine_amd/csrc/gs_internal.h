@@ -342,6 +342,11 @@ __device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
   GS_WAVE_REDUCE(uint64_t, dpp_u64, v, 0ull, op_max_u64);
   return readlane_u64(v, 63);
 }
+__device__ __forceinline__ uint64_t op_add_u64(uint64_t a, uint64_t b) { return a + b; }
+__device__ __forceinline__ uint64_t wave_sum_u64(uint64_t v) {
+  GS_WAVE_REDUCE(uint64_t, dpp_u64, v, 0ull, op_add_u64);
+  return readlane_u64(v, 63);
+}
 // the maximum and minimum of the wave's values, in every lane (the two
 // chains interleaved step by step)
 __device__ __forceinline__ void wave_max_min_u32(uint32_t v, uint32_t* vmax, uint32_t* vmin) {
