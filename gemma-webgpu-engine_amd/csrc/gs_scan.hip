@@ -58,14 +58,13 @@ namespace {
 
 constexpr int kChunkWords = kChunk / 32;  // special-bitmap words of one chunk
 constexpr int kMaxGroupChunks = 16;       // chunks one group workgroup streams
-// Resident scan workgroups per CU (the launch bound). The constrained
-// variants carry the masked and the unmasked group scan in one kernel and
-// need more registers: bound at 4 they spill (f32: 117 VGPRs) and crawl, so
-// they run at 3 (bf16 spill-free at 163 VGPRs; f32 at 168 with 20 spilled,
-// which scans 128 constrained rows in 31.4 us against 35.4 us spill-free at
-// 2 per CU).
+// Resident scan workgroups per CU (the launch bound). A constrained row's
+// mask is folded into the special-id bitmap before its chunks stream, so the
+// constrained variants run the same loop as the others and share the bound
+// (carrying mask words through the loop took them past 128 VGPRs: at 4 per
+// CU they spilled, at 3 the masked scan of 256 x 262144 took 51 us).
 template <typename In, bool kMaskable>
-constexpr int scan_wg_per_cu() { return !kMaskable ? 4 : 3; }
+constexpr int scan_wg_per_cu() { return 4; }
 // word 3 of a raw buffer resource on gfx9-family parts (gfx950 included)
 constexpr int32_t kBufferWord3 = 0x00020000;
 
@@ -180,33 +179,60 @@ __device__ __forceinline__ void load_group_logits(const char* lbase, int lc, int
     raw[v] = make_uint4(w.x, w.y, w.z, w.w);
   }
 }
-// the chunk's 256 mask words; load v of a thread needs word (v*256 + tid)*kVec/32
+// A group chunk's mask words, one per lane: a wave's kLoads loads of kVec
+// logits per thread cover 2 kVec consecutive mask words each, 64 in all, so
+// lane l loads word j = l of its wave's share -- load v = l / (2 kVec),
+// word v 8 kVec + 2 kVec wave + l % (2 kVec) of the chunk -- and a thread
+// takes the word of its load v from lane v 2 kVec + (l kVec) / 32.
+// Chunks lc >= nc read zeros (an empty buffer range).
 template <typename In>
-__device__ __forceinline__ void load_group_masks(const char* mbase, int lc, int nc,
-                                                 uint32_t (&mword)[kElemsPerThread / VecTraits<In>::kVec]) {
+__device__ __forceinline__ uint32_t load_group_mask_lane(const char* mbase, int lc, int nc) {
   constexpr int kVec = VecTraits<In>::kVec;
-  constexpr int kLoads = kElemsPerThread / kVec;
-  const int tid = threadIdx.x;
+  static_assert(kElemsPerThread / kVec * 2 * kVec == 64, "one mask word per lane");
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int word = (lane / (2 * kVec)) * 8 * kVec + 2 * kVec * wave + lane % (2 * kVec);
   const __amdgpu_buffer_rsrc_t mk = __builtin_amdgcn_make_buffer_rsrc(
       (void*)(mbase + (int64_t)lc * (kChunkWords * 4)), (short)0, lc < nc ? kChunkWords * 4 : 0, kBufferWord3);
+  return __builtin_amdgcn_raw_buffer_load_b32(mk, word * 4, 0, 0);
+}
+// Folds a constrained group's mask into its LDS special-id bitmap (thread-
+// major: word i kChunkWords + tid, bit e = element e of thread tid in chunk
+// i): an id the mask forbids is excluded from the scan like a special id.
+// Writes every word of the group's nc chunks (the zero fill of an
+// unconstrained group).
+template <typename In>
+__device__ __forceinline__ void fold_group_mask(const char* mk, int nc, uint32_t* s_special) {
+  constexpr int kVec = VecTraits<In>::kVec;
+  constexpr int kLoads = kElemsPerThread / kVec;
+  constexpr uint32_t kLaneBits = (1u << kVec) - 1u;
+  const int tid = threadIdx.x, lane = tid & 63;
+  uint32_t w[kMaxGroupChunks];
 #pragma unroll
-  for (int v = 0; v < kLoads; ++v) {
-    mword[v] = __builtin_amdgcn_raw_buffer_load_b32(mk, ((tid * kVec) >> 5) * 4, ((v * kScanThreads * kVec) >> 5) * 4, 0);
+  for (int i = 0; i < kMaxGroupChunks; ++i) w[i] = load_group_mask_lane<In>(mk, i, nc);
+#pragma unroll
+  for (int i = 0; i < kMaxGroupChunks; ++i) {
+    if (i >= nc) break;
+    uint32_t dead = 0;
+#pragma unroll
+    for (int v = 0; v < kLoads; ++v) {
+      const int loc = (v * kScanThreads + tid) * kVec;
+      const uint32_t mw = (uint32_t)__shfl((int)w[i], v * 2 * kVec + ((lane * kVec) >> 5), 64);
+      dead |= (~(mw >> (loc & 31)) & kLaneBits) << (v * kVec);
+    }
+    s_special[i * kChunkWords + tid] = dead;
   }
 }
-
 // The statistics and candidate list of one chunk from its loaded logits.
-// kFull: all kChunk logits exist; kMasked: the row has a constraint mask.
+// kFull: all kChunk logits exist. special: the chunk's words of the LDS
+// special-id bitmap, which also holds the ids a constraint mask forbids.
 // thr_in > 0 is the group's tau (the stream path: no exchange); with
 // thr_in == 0 the chunk takes its own tau and every path passes exactly one
-// workgroup barrier. special: the chunk's words of the LDS special-id bitmap;
-// W: the LDS slots of an exchange. Returns the threshold the chunk applied
+// workgroup barrier. W: the LDS slots of an exchange. Returns the threshold the chunk applied
 // when it truncated (0 otherwise).
-template <typename In, bool kFull, bool kMasked>
+template <typename In, bool kFull>
 __device__ __forceinline__ uint32_t chunk_stats(const SampleArgs& a, const gs_row_config& cfg, const Plan plan,
                                                 const int64_t row, const int chunk, const int n_valid,
                                                 const uint4 (&raw)[kElemsPerThread / VecTraits<In>::kVec],
-                                                const uint32_t (&mword)[kElemsPerThread / VecTraits<In>::kVec],
                                                 const uint32_t* s_special, const double* s_tab, WaveSlots& W,
                                                 uint64_t* s_stage, const uint32_t thr_in) {
   using VT = VecTraits<In>;
@@ -241,13 +267,6 @@ __device__ __forceinline__ uint32_t chunk_stats(const SampleArgs& a, const gs_ro
       const int left = n_valid - (v * kScanThreads + tid) * kVec;
       const uint32_t in_range = left >= kVec ? kLaneBits : (left > 0 ? (1u << left) - 1u : 0u);
       dead |= (~in_range & kLaneBits) << (v * kVec);
-    }
-  }
-  if (kMasked) {
-#pragma unroll
-    for (int v = 0; v < kLoads; ++v) {
-      const int loc = (v * kScanThreads + tid) * kVec;
-      dead |= (~(mword[v] >> (loc & 31)) & kLaneBits) << (v * kVec);
     }
   }
   if (__ballot(dead != 0)) {
@@ -476,7 +495,7 @@ __device__ __forceinline__ void first_specials(const SampleArgs& a, const RowRan
 template <typename In, bool kFull, bool kMasked>
 __device__ __forceinline__ void scan_single(const SampleArgs& a, const gs_row_config& cfg, const Plan plan,
                                             const RowRanges rr, const int64_t row, const int chunk,
-                                            const int n_valid, ScanShared& S) {
+                                            const int n_valid, ScanShared& S, const bool row_masked) {
   using VT = VecTraits<In>;
   constexpr int kVec = VT::kVec;
   constexpr int kLoads = kElemsPerThread / kVec;
@@ -488,32 +507,38 @@ __device__ __forceinline__ void scan_single(const SampleArgs& a, const gs_row_co
 
   uint4 raw[kLoads];
   load_chunk<In, kFull>(a, row, gbase, n_valid, raw);
-  uint32_t mword[kLoads];
-  if (kMasked) {
+  // the ids the row's mask forbids start the thread's special-bitmap word
+  // (kChunkWords == kScanThreads); bits past n_valid are excluded anyway
+  uint32_t dead = 0;
+  if (kMasked && row_masked) {
+    constexpr uint32_t kLaneBits = (1u << kVec) - 1u;
     const uint32_t* maskp = a.mask_table + (int64_t)cfg.mask_slot * a.mask_words + (gbase >> 5);
 #pragma unroll
     for (int v = 0; v < kLoads; ++v) {
       const int loc = (v * kScanThreads + tid) * kVec;
-      mword[v] = maskp[(loc < n_valid ? loc : n_valid - 1) >> 5];  // bits past n_valid are cleared later
+      const uint32_t mw = maskp[(loc < n_valid ? loc : n_valid - 1) >> 5];
+      dead |= (~(mw >> (loc & 31)) & kLaneBits) << (v * kVec);
     }
   }
 
-  S.special[tid] = 0;  // kChunkWords == kScanThreads
+  S.special[tid] = dead;
   S.tab[tid] = tabv;
   lds_barrier();
   mark_specials<In, kMasked>(a, rr, gbase, n_valid, hid0, hid1, fid0, S.special);
   lds_barrier();
-  chunk_stats<In, kFull, kMasked>(a, cfg, plan, row, chunk, n_valid, raw, mword, S.special, S.tab, S.slots[0],
-                                  S.stage, 0u);
+  chunk_stats<In, kFull>(a, cfg, plan, row, chunk, n_valid, raw, S.special, S.tab, S.slots[0], S.stage, 0u);
 }
 
 // Chunks [c0, c0 + nc) of one row, all full and 16-byte aligned, as a
 // two-stage pipeline over two register buffers; the kernel has already
 // issued the loads of the first chunk's logits into cur.
+// kMasked: the kernel handles constrained rows; row_masked: this row is one
+// (its mask is folded into the special-id bitmap first).
 template <typename In, bool kMasked>
 __device__ __forceinline__ void scan_group(const SampleArgs& a, const gs_row_config& cfg, const Plan plan,
                                            const RowRanges rr, const int64_t row, const int c0, const int nc,
-                                           uint4 (&cur)[kElemsPerThread / VecTraits<In>::kVec], ScanShared& S) {
+                                           uint4 (&cur)[kElemsPerThread / VecTraits<In>::kVec], ScanShared& S,
+                                           const bool row_masked) {
   constexpr int kLoads = kElemsPerThread / VecTraits<In>::kVec;
   const int tid = threadIdx.x;
   const int64_t gbase = (int64_t)c0 * kChunk;
@@ -523,16 +548,13 @@ __device__ __forceinline__ void scan_group(const SampleArgs& a, const gs_row_con
   int32_t hid0, hid1, fid0;
   first_specials<kMasked>(a, rr, &hid0, &hid1, &fid0);
   const double tabv = c_exp2_256[tid];
-  const char* mk =
-      (const char*)(kMasked ? a.mask_table + (int64_t)cfg.mask_slot * a.mask_words + (gbase >> 5) : a.mask_table);
-  uint32_t mc[kLoads], mn[kLoads];
-  if (kMasked) {
-    load_group_masks<In>(mk, 0, nc, mc);
-    load_group_masks<In>(mk, 1, nc, mn);
-  }
-
-  for (int i = tid; i < nc * kChunkWords; i += kScanThreads) S.special[i] = 0;
   S.tab[tid] = tabv;
+  if (kMasked && row_masked) {
+    const char* mk = (const char*)(a.mask_table + (int64_t)cfg.mask_slot * a.mask_words + (gbase >> 5));
+    fold_group_mask<In>(mk, nc, S.special);
+  } else {
+    for (int i = tid; i < nc * kChunkWords; i += kScanThreads) S.special[i] = 0;
+  }
   lds_barrier();
   mark_specials<In, kMasked>(a, rr, gbase, nc * kChunk, hid0, hid1, fid0, S.special);
   lds_barrier();
@@ -550,17 +572,15 @@ __device__ __forceinline__ void scan_group(const SampleArgs& a, const gs_row_con
     // a quarter occupied; falling priority keeps them level, so the CU's
     // waves stay many until its last chunks (-3 us at 256 x 262144)
     set_wave_priority((4 * (nc - i) - 1) / nc);
-    uint32_t t = chunk_stats<In, true, kMasked>(a, cfg, plan, row, c0 + i, kChunk, cur, mc,
-                                                S.special + i * kChunkWords, S.tab, S.slots[0], S.stage, thr);
+    uint32_t t = chunk_stats<In, true>(a, cfg, plan, row, c0 + i, kChunk, cur, S.special + i * kChunkWords, S.tab,
+                                       S.slots[0], S.stage, thr);
     thr = thr ? thr : t;
     load_group_logits<In>(lg, i + 2, nc, cur);
-    if (kMasked) load_group_masks<In>(mk, i + 2, nc, mc);
     if (i + 1 >= nc) break;
-    t = chunk_stats<In, true, kMasked>(a, cfg, plan, row, c0 + i + 1, kChunk, nxt, mn,
-                                       S.special + (i + 1) * kChunkWords, S.tab, S.slots[1], S.stage, thr);
+    t = chunk_stats<In, true>(a, cfg, plan, row, c0 + i + 1, kChunk, nxt, S.special + (i + 1) * kChunkWords, S.tab,
+                              S.slots[1], S.stage, thr);
     thr = thr ? thr : t;
     load_group_logits<In>(lg, i + 3, nc, nxt);
-    if (kMasked) load_group_masks<In>(mk, i + 3, nc, mn);
   }
 }
 
@@ -598,24 +618,23 @@ __global__ __launch_bounds__(kScanThreads, (scan_wg_per_cu<In, kMaskable>())) vo
   RowRanges rr;
   history_window(a, row, cfg, &rr.w0, &rr.w1);
   rr.f0 = rr.f1 = 0;
-  if (a.forced_offsets) { rr.f0 = a.forced_offsets[row]; rr.f1 = a.forced_offsets[row + 1]; }
+  const bool masked = kMaskable && cfg.mask_slot >= 0 && cfg.mask_slot < a.mask_slots;
+  // forced ids belong to constrained rows only
+  if (a.forced_offsets && masked) { rr.f0 = a.forced_offsets[row]; rr.f1 = a.forced_offsets[row + 1]; }
   if (plan.route != kRouteExact) {
-    const bool masked = kMaskable && cfg.mask_slot >= 0 && cfg.mask_slot < a.mask_slots;
+    // One path per kernel: with a mask table every row takes the masked
+    // path, a row without a mask as if its mask were all ones (the two paths
+    // inlined side by side cost the kernel 272 B of spills per lane at 4
+    // workgroups per CU, the masked one alone 64 B).
     if (group) {
-      if (masked) scan_group<In, kMaskable>(a, cfg, plan, rr, row, c0, nc, cur, S);
-      else scan_group<In, false>(a, cfg, plan, rr, row, c0, nc, cur, S);
+      scan_group<In, kMaskable>(a, cfg, plan, rr, row, c0, nc, cur, S, masked);
     } else {
       const int chunk = g.n_grouped + ((int)blockIdx.x - g.n_groups);
       const int64_t gbase = (int64_t)chunk * kChunk;
       const int n_valid = (int)((int64_t)a.vocab - gbase < kChunk ? (int64_t)a.vocab - gbase : kChunk);
       const bool full = n_valid == kChunk && a.vector_ok;
-      if (full) {
-        if (masked) scan_single<In, true, kMaskable>(a, cfg, plan, rr, row, chunk, n_valid, S);
-        else scan_single<In, true, false>(a, cfg, plan, rr, row, chunk, n_valid, S);
-      } else {
-        if (masked) scan_single<In, false, kMaskable>(a, cfg, plan, rr, row, chunk, n_valid, S);
-        else scan_single<In, false, false>(a, cfg, plan, rr, row, chunk, n_valid, S);
-      }
+      if (full) scan_single<In, true, kMaskable>(a, cfg, plan, rr, row, chunk, n_valid, S, masked);
+      else scan_single<In, false, kMaskable>(a, cfg, plan, rr, row, chunk, n_valid, S, masked);
     }
   }
   // reset the queues the finish kernel fills for the exact and deep kernels
