@@ -87,8 +87,8 @@ def parse_args():
     ap.add_argument("--steps", type=int, default=100)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--workload", default="penalties",
-                    choices=["penalties", "single_row", "heavy_tail", "constrained", "lmhead", "qat", "multinomial",
-                             "topk_deep", "typical", "penalties_constrained"])
+                    choices=["penalties", "single_row", "heavy_tail", "constrained", "lmhead", "lmhead_fused", "qat",
+                             "multinomial", "topk_deep", "typical", "penalties_constrained"])
     ap.add_argument("--also", default="penalties_constrained",
                     help="comma-separated workloads measured after the main one and reported beside it under "
                          "'also' (default: penalties_constrained; '' for none); with the main workload only")
@@ -190,7 +190,7 @@ def build_workload(name, gs, torch, device):
                    scan_bytes_per_row=per_row, step_bytes=w.rows * (per_row + 8), dominant="scan",
                    masks=table, dfa=(offsets, data, nxt, finals), desc=desc)
         return out
-    if name == "lmhead":
+    if name in ("lmhead", "lmhead_fused"):
         M, D = 64, 2048
         hidden, weight = W.lmhead_inputs(M, D, V, device=device)
         hist = W.lmhead_histories(M)
@@ -205,12 +205,16 @@ def build_workload(name, gs, torch, device):
         conf = np.stack([rt.row_config(cfg, seed=r, softcap_value=0.0, mask_slot=states[r]) for r in range(M)])
         scratch = torch.empty((M, V), dtype=torch.float32, device=device)
         batch, keep = s.prepare(scratch, conf, histories=hist, mask_table=table)
+        if name == "lmhead_fused":
+            # the head's epilogue computes the chunk statistics (GS_BATCH_FUSED_HEAD)
+            batch.hints |= rt.GS_BATCH_FUSED_HEAD
+            out["kernel"] = "lmhead_scan_kernel"
         keep += [hidden, weight, scratch]
         out.update(rows=M, sampler=s, batches=[(batch, keep)], dtype_in="bf16", hidden=hidden, weight=weight,
                    scratch=scratch, histories=hist, states=states, masks=table, dfa=(offsets, data, nxt, finals),
                    lm_bytes=2 * V * D + 2 * M * D, lm_logits_bytes=4 * M * V, lm_flops=2 * M * D * V,
                    step_bytes=2 * V * D + 2 * M * D + 4 * 256 * M + 8 * M, dominant="lmhead",
-                   desc=f"lmhead: H {M} x {D} bf16 ~ N(0,1), W {V} x {D} bf16 ~ N(0, 0.02^2), softcap 30, "
+                   desc=f"{name}: H {M} x {D} bf16 ~ N(0,1), W {V} x {D} bf16 ~ N(0, 0.02^2), softcap 30, "
                         "256-id histories (window 256), DFA masks, topK 64, topP 0.95, T 1, seed = row")
         return out
     if name == "qat":
@@ -245,7 +249,7 @@ def build_workload(name, gs, torch, device):
 def launch_step(wl, i, stream):
     s = wl["sampler"]
     batch = wl["batches"][i % len(wl["batches"])][0]
-    if wl["name"] == "lmhead":
+    if wl["name"] in ("lmhead", "lmhead_fused"):
         s.lmhead_sample_launch(wl["hidden"], wl["weight"], 30.0, wl["scratch"], batch, stream)
     elif wl["name"] == "qat":
         x, codes, scales = wl["qat"]
@@ -272,7 +276,7 @@ def _cfg_dict(c):
 def cpu_inputs(wl):
     """(logits [rows][V] as stored, dtype, configs, seeds, histories, constraint) of the workload
     for the CPU restatement; the lm_head workload's logits are the ones the GPU produced."""
-    if wl["name"] == "lmhead":
+    if wl["name"] in ("lmhead", "lmhead_fused"):
         logits = wl["scratch"].cpu().numpy()
         import gsample
 
@@ -352,9 +356,9 @@ def cpu_baseline(wl, tokens, probs, n_rows, threads_cap):
             p = res["probabilities"][k]
             if p:
                 rel = max(rel, abs(probs[r] - p) / abs(p))
-    what = "the sampler" if wl["name"] not in ("constrained", "penalties_constrained", "lmhead") else (
+    what = "the sampler" if wl["name"] not in ("constrained", "penalties_constrained", "lmhead", "lmhead_fused") else (
         "legal-id walk (cached per state) + maskConstraintLogits + the sampler")
-    if wl["name"] == "lmhead":
+    if wl["name"] in ("lmhead", "lmhead_fused"):
         what += " on the GPU-produced logits (no CPU bf16 GEMM exists in the reference)"
     if wl["name"] == "qat":
         what += " on the GPU-produced logits (the QAT head's CPU leg is timed in qat_cpu)"
@@ -449,7 +453,7 @@ def measure(wl, gs, torch, stream, steps, warmup):
     # results of the last step (each loop above counts its steps from 0, so
     # the last launch used buffer (steps - 1) mod n_rot)
     last = (steps - 1) % n_rot
-    res = wl["batches"][last][1][-1] if wl["name"] != "lmhead" else wl["batches"][0][1][-4]
+    res = wl["batches"][last][1][-1] if wl["name"] not in ("lmhead", "lmhead_fused") else wl["batches"][0][1][-4]
     if wl["name"] == "qat":
         res = wl["batches"][0][1][-1]
     raw = res.cpu().numpy().view(np.uint8).reshape(-1)[: wl["rows"] * 16]

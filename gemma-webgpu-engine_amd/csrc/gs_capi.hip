@@ -45,6 +45,12 @@ struct gs_context {
   // device staging for the host-array entry points (grown on demand)
   uint8_t* d_stage = nullptr;
   size_t stage_cap = 0;
+  // the fused lm_head path's per-row buffers (grown on demand)
+  uint32_t* d_dead = nullptr;
+  PartStat* d_parts = nullptr;
+  uint64_t* d_plists = nullptr;
+  uint32_t* d_row_thr = nullptr;
+  int32_t fused_rows = 0;
   // kernel timing (gs_timing_begin / gs_timing_end): per timed call and stage,
   // the start and stop events of that stage's kernel launch
   std::vector<hipEvent_t> t_events;  // [max_calls][GS_STAGE_COUNT][2]
@@ -124,6 +130,41 @@ int ensure_stage(gs_context* ctx, size_t bytes) {
 
 size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
+// Grows the fused lm_head path's buffers to at least `rows` rows (in steps
+// of 64). Waits for the device first: queued work may still use the old ones.
+int ensure_fused(gs_context* ctx, int32_t rows) {
+  if (rows <= ctx->fused_rows) return GS_OK;
+  GS_HIP(ctx, hipDeviceSynchronize());
+  free_dev(ctx->d_dead);
+  free_dev(ctx->d_parts);
+  free_dev(ctx->d_plists);
+  free_dev(ctx->d_row_thr);
+  ctx->d_dead = nullptr;
+  ctx->d_parts = nullptr;
+  ctx->d_plists = nullptr;
+  ctx->d_row_thr = nullptr;
+  ctx->fused_rows = 0;
+  const size_t r = (size_t)((rows + 63) / 64 * 64);
+  const size_t n_parts = (size_t)ctx->vocab / kPartIds;
+  if (hipMalloc(&ctx->d_dead, r * ctx->mask_words * sizeof(uint32_t)) != hipSuccess ||
+      hipMalloc(&ctx->d_parts, r * n_parts * sizeof(PartStat)) != hipSuccess ||
+      hipMalloc(&ctx->d_plists, r * n_parts * kPartCap * sizeof(uint64_t)) != hipSuccess ||
+      hipMalloc(&ctx->d_row_thr, r * sizeof(uint32_t)) != hipSuccess) {
+    (void)hipGetLastError();
+    free_dev(ctx->d_dead);
+    free_dev(ctx->d_parts);
+    free_dev(ctx->d_plists);
+    free_dev(ctx->d_row_thr);
+    ctx->d_dead = nullptr;
+    ctx->d_parts = nullptr;
+    ctx->d_plists = nullptr;
+    ctx->d_row_thr = nullptr;
+    return fail(ctx, GS_ERR_HIP, "allocating the fused lm_head buffers failed");
+  }
+  ctx->fused_rows = (int32_t)r;
+  return GS_OK;
+}
+
 // Per-row failures of a finished batch, mapped to the reference's errors
 // (the first failing row decides).
 int map_row_failures(gs_context* ctx, const gs_row_result* res, int32_t rows) {
@@ -186,11 +227,8 @@ bool deep_launch(const Workspace& w, const gs_batch* b) {
          b->rows <= w.deep_max_rows;
 }
 
-// Enqueues the sampling kernels of one checked batch on stream s (ev: the
-// timing events of each stage, none when not timing). The exact-path queue is
-// reset by the chunk scan's first workgroup: no memset node, so the launch
-// stays capturable and allocates nothing.
-hipError_t launch_sample(const Workspace& w, const gs_batch* b, hipStream_t s, const LaunchEvents* ev) {
+// The kernels' arguments for one checked batch in workspace w.
+SampleArgs sample_args(const Workspace& w, const gs_batch* b) {
   const size_t esize = b->dtype == GS_BF16 ? 2 : 4;
   SampleArgs a{};
   a.logits = b->logits;
@@ -222,7 +260,21 @@ hipError_t launch_sample(const Workspace& w, const gs_batch* b, hipStream_t s, c
   a.deep_rows = deep ? w.deep_rows : nullptr;
   a.deep_queue = deep ? w.deep_queue : nullptr;
   a.deep_max_rows = deep ? w.deep_max_rows : 0;
-  launch_scan(a, s, ev[GS_STAGE_SCAN]);
+  return a;
+}
+
+// Enqueues the sampling kernels of one checked batch on stream s (ev: the
+// timing events of each stage, none when not timing). The exact-path queue is
+// reset by the chunk scan's first workgroup: no memset node, so the launch
+// stays capturable and allocates nothing. fused: the lm_head's epilogue wrote
+// the partial statistics, which the merge kernel turns into the chunk
+// statistics in the scan's place (stage GS_STAGE_SCAN).
+hipError_t launch_sample(const Workspace& w, const gs_batch* b, hipStream_t s, const LaunchEvents* ev,
+                         const FusedArgs* fused = nullptr) {
+  const SampleArgs a = sample_args(w, b);
+  const bool deep = a.deep_rows != nullptr;
+  if (fused) launch_merge_parts(a, *fused, s, ev[GS_STAGE_SCAN]);
+  else launch_scan(a, s, ev[GS_STAGE_SCAN]);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   launch_finish(a, s, ev[GS_STAGE_FINISH]);
@@ -240,6 +292,26 @@ hipError_t launch_sample(const Workspace& w, const gs_batch* b, hipStream_t s, c
     e = hipGetLastError();
   }
   return e;
+}
+
+// A context's device memory as the sampling launches' workspace.
+Workspace context_workspace(const gs_context* ctx) {
+  Workspace w;
+  w.vocab = ctx->vocab;
+  w.n_chunks = ctx->n_chunks;
+  w.mask_words = ctx->mask_words;
+  w.exact_slots = ctx->exact_slots;
+  w.cu_count = ctx->cu_count;
+  w.stats = ctx->d_stats;
+  w.lists = ctx->d_lists;
+  w.queue = ctx->d_queue;
+  w.exact = ctx->d_exact;
+  w.exact_slot_bytes = ctx->exact_slot_bytes;
+  w.exact_cap = ctx->exact_cap;
+  w.deep_rows = ctx->d_deep_rows;
+  w.deep_queue = ctx->d_deep_queue;
+  w.deep_max_rows = ctx->max_rows;
+  return w;
 }
 
 void destroy_timing(gs_context* ctx) {
@@ -426,6 +498,10 @@ int gs_destroy(gs_context* ctx) {
   free_dev(ctx->d_next);
   free_dev(ctx->d_states);
   free_dev(ctx->d_stage);
+  free_dev(ctx->d_dead);
+  free_dev(ctx->d_parts);
+  free_dev(ctx->d_plists);
+  free_dev(ctx->d_row_thr);
   destroy_timing(ctx);
   if (ctx->stream) (void)hipStreamDestroy(ctx->stream);
   delete ctx;
@@ -474,6 +550,7 @@ int gs_validate_configs(gs_context* ctx, const gs_row_config* configs, int32_t n
   return GS_OK;
 }
 
+
 int gs_sample(gs_context* ctx, const gs_batch* b, void* stream) {
   if (!ctx || !b) return fail(ctx, GS_ERR_INVALID_ARGUMENT, "null context or batch");
   if (b->rows == 0) return GS_OK;
@@ -481,21 +558,7 @@ int gs_sample(gs_context* ctx, const gs_batch* b, void* stream) {
   const char* bad = batch_error(b, ctx->vocab);
   if (bad) return fail(ctx, GS_ERR_INVALID_ARGUMENT, bad);
   GS_HIP(ctx, hipSetDevice(ctx->device));
-  Workspace w;
-  w.vocab = ctx->vocab;
-  w.n_chunks = ctx->n_chunks;
-  w.mask_words = ctx->mask_words;
-  w.exact_slots = ctx->exact_slots;
-  w.cu_count = ctx->cu_count;
-  w.stats = ctx->d_stats;
-  w.lists = ctx->d_lists;
-  w.queue = ctx->d_queue;
-  w.exact = ctx->d_exact;
-  w.exact_slot_bytes = ctx->exact_slot_bytes;
-  w.exact_cap = ctx->exact_cap;
-  w.deep_rows = ctx->d_deep_rows;
-  w.deep_queue = ctx->d_deep_queue;
-  w.deep_max_rows = ctx->max_rows;
+  const Workspace w = context_workspace(ctx);
   const int32_t slot = timing_slot(ctx);
   LaunchEvents ev[GS_STAGE_COUNT];
   for (int k = GS_STAGE_SCAN; k <= GS_STAGE_FINISH; ++k) ev[k] = stage_events(ctx, slot, k);
@@ -940,13 +1003,54 @@ int gs_qat_lmhead_sample(gs_context* ctx, const float* x, int32_t width, const u
 int gs_lmhead_sample(gs_context* ctx, const void* hidden, const void* weight, int32_t width, float softcap,
                      float* logits_scratch, const gs_batch* batch, void* stream) {
   if (!batch) return fail(ctx, GS_ERR_INVALID_ARGUMENT, "null batch");
-  int st = gs_lmhead(ctx, hidden, weight, batch->rows, width, softcap, logits_scratch, stream);
-  if (st != GS_OK) return st;
+  if (!ctx) return GS_ERR_INVALID_ARGUMENT;
+  if (!(batch->hints & GS_BATCH_FUSED_HEAD) || ctx->vocab % kChunk != 0) {
+    // the lm_head, then the chunk scan over its output (the faster of the two
+    // at 64 x 2048 x 262144, and the path for vocabularies of partial chunks)
+    int st = gs_lmhead(ctx, hidden, weight, batch->rows, width, softcap, logits_scratch, stream);
+    if (st != GS_OK) return st;
+    gs_batch b = *batch;
+    b.logits = logits_scratch;
+    b.dtype = GS_F32;
+    b.row_stride = ctx->vocab;
+    return gs_sample(ctx, &b, stream);
+  }
+  if (!hidden || !weight || !logits_scratch || width <= 0) return fail(ctx, GS_ERR_INVALID_ARGUMENT, "bad arguments");
+  if (width % 64 != 0) return fail(ctx, GS_ERR_UNSUPPORTED, "lm_head width must be a multiple of 64");
+  if (!aligned16(hidden) || !aligned16(weight) || !aligned16(logits_scratch))
+    return fail(ctx, GS_ERR_INVALID_ARGUMENT, "hidden, weight and logits_scratch must be 16-byte aligned");
   gs_batch b = *batch;
   b.logits = logits_scratch;
   b.dtype = GS_F32;
   b.row_stride = ctx->vocab;
-  return gs_sample(ctx, &b, stream);
+  if (b.rows == 0) return GS_OK;
+  if (b.rows < 0 || b.rows > ctx->max_rows) return fail(ctx, GS_ERR_INVALID_ARGUMENT, "rows outside [0, max_rows]");
+  const char* bad = batch_error(&b, ctx->vocab);
+  if (bad) return fail(ctx, GS_ERR_INVALID_ARGUMENT, bad);
+  GS_HIP(ctx, hipSetDevice(ctx->device));
+  const int st = ensure_fused(ctx, b.rows);
+  if (st != GS_OK) return st;
+  const Workspace w = context_workspace(ctx);
+  FusedArgs f{};
+  f.configs = b.configs;
+  f.dead = ctx->d_dead;
+  f.parts = ctx->d_parts;
+  f.plists = ctx->d_plists;
+  f.row_thr = ctx->d_row_thr;
+  f.n_parts = ctx->vocab / kPartIds;
+  const int32_t slot = timing_slot(ctx);
+  LaunchEvents ev[GS_STAGE_COUNT];
+  for (int k = GS_STAGE_LMHEAD; k <= GS_STAGE_FINISH; ++k) ev[k] = stage_events(ctx, slot, k);
+  if (deep_launch(w, &b)) ev[GS_STAGE_DEEP] = stage_events(ctx, slot, GS_STAGE_DEEP);
+  if (b.rows > ctx->exact_slots) ev[GS_STAGE_EXACT] = stage_events(ctx, slot, GS_STAGE_EXACT);
+  hipStream_t s = pick_stream(ctx, stream);
+  launch_lmhead_scan((const uint16_t*)hidden, (const uint16_t*)weight, b.rows, width, softcap, logits_scratch,
+                     sample_args(w, &b), f, s, ev[GS_STAGE_LMHEAD]);
+  hipError_t e = hipGetLastError();
+  if (e == hipSuccess) e = launch_sample(w, &b, s, ev, &f);
+  if (e != hipSuccess) return fail(ctx, GS_ERR_HIP, std::string("kernel launch: ") + hipGetErrorString(e));
+  if (slot >= 0) ctx->t_calls++;
+  return GS_OK;
 }
 
 int gs_timing_begin(gs_context* ctx, int32_t max_calls) {

@@ -175,6 +175,21 @@ __host__ __device__ __forceinline__ uint64_t list_rank(uint64_t slot) {
 constexpr uint32_t kChunkOverflow = 1u;
 constexpr uint32_t kChunkNonFinite = 2u;
 
+// The fused lm_head's epilogue summarises each hidden row's logits in
+// partials of kPartIds consecutive ids (one per workgroup and row), which a
+// merge kernel turns into the chunk scan's ChunkStat and lists.
+constexpr int kPartIds = 256;
+constexpr int kPartCap = 32;                          // list slots of one partial
+constexpr int kPartsPerChunk = kChunk / kPartIds;     // 32
+struct PartStat {
+  double sum;         // sum of e^((l - max)/T) over the finite non-excluded logits
+  uint32_t max_key;   // the maximum's key (0: none finite)
+  uint32_t tau;       // the list holds every finite logit with key >= tau
+  uint32_t n;         // entries at or above tau (more than kPartCap: the list is cut)
+  uint16_t flags;     // kChunkNonFinite
+  uint16_t truncated; // finite logits lie below tau
+};
+
 struct ExactQueue {
   uint32_t count;  // rows appended by the finish kernel
   uint32_t next;   // rows taken by the exact kernel
@@ -244,6 +259,16 @@ struct SampleArgs {
   DeepRow* deep_rows;      // [rows], or null: the finish's own workgroup takes its deep draws
   DeepQueue* deep_queue;
   int32_t deep_max_rows;   // pass-2 rows start at deep_queue->rows + deep_max_rows
+};
+
+// Buffers of the fused lm_head + statistics path.
+struct FusedArgs {
+  const gs_row_config* configs;
+  uint32_t* dead;      // [rows][V/32] excluded ids (mask-forbidden, window, forced)
+  PartStat* parts;     // [rows][n_parts]
+  uint64_t* plists;    // [rows][n_parts][kPartCap] list slots
+  uint32_t* row_thr;   // [rows] the largest tau of the row's truncated partials (0: none)
+  int32_t n_parts;     // V / kPartIds
 };
 
 // A 16-byte load marked non-temporal, for rows streamed once: the stream
@@ -554,5 +579,11 @@ void launch_qat_lmhead(const float* x, int32_t M, int32_t D, const uint32_t* wor
                        LaunchEvents ev);
 void launch_lmhead(const uint16_t* hidden, const uint16_t* weight, int32_t m, int32_t width, int32_t vocab,
                    float softcap, float* out, hipStream_t s, LaunchEvents ev = {});
+// The fused path (vocab a multiple of kChunk): the excluded-id bitmaps, then
+// the lm_head with the partial statistics; launch_merge_parts takes the chunk
+// scan's place before the finish.
+void launch_lmhead_scan(const uint16_t* hidden, const uint16_t* weight, int32_t m, int32_t width, float softcap,
+                        float* out, const SampleArgs& a, const FusedArgs& f, hipStream_t s, LaunchEvents ev = {});
+void launch_merge_parts(const SampleArgs& a, const FusedArgs& f, hipStream_t s, LaunchEvents ev = {});
 
 }  // namespace gs

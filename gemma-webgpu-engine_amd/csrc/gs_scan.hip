@@ -211,15 +211,16 @@ __device__ __forceinline__ void fold_group_mask(const char* mk, int nc, uint32_t
   for (int i = 0; i < kMaxGroupChunks; ++i) w[i] = load_group_mask_lane<In>(mk, i, nc);
 #pragma unroll
   for (int i = 0; i < kMaxGroupChunks; ++i) {
-    if (i >= nc) break;
-    uint32_t dead = 0;
+    if (i < nc) {
+      uint32_t dead = 0;
 #pragma unroll
-    for (int v = 0; v < kLoads; ++v) {
-      const int loc = (v * kScanThreads + tid) * kVec;
-      const uint32_t mw = (uint32_t)__shfl((int)w[i], v * 2 * kVec + ((lane * kVec) >> 5), 64);
-      dead |= (~(mw >> (loc & 31)) & kLaneBits) << (v * kVec);
+      for (int v = 0; v < kLoads; ++v) {
+        const int loc = (v * kScanThreads + tid) * kVec;
+        const uint32_t mw = (uint32_t)__shfl((int)w[i], v * 2 * kVec + ((lane * kVec) >> 5), 64);
+        dead |= (~(mw >> (loc & 31)) & kLaneBits) << (v * kVec);
+      }
+      s_special[i * kChunkWords + tid] = dead;
     }
-    s_special[i * kChunkWords + tid] = dead;
   }
 }
 // The statistics and candidate list of one chunk from its loaded logits.

@@ -27,6 +27,7 @@ GS_QAT_ROW_MAJOR, GS_QAT_BLOCK_MAJOR = 0, 1
 GS_RNG_SEEDED, GS_RNG_EXPLICIT = 0, 1
 GS_ROW_FORCE_EXACT = 1
 GS_BATCH_FULL_DRAWS = 1  # gs_batch.hints: a row may take a full-vocabulary draw
+GS_BATCH_FUSED_HEAD = 2  # gs_batch.hints: gs_lmhead_sample computes the chunk statistics in the head
 GS_FORCED_TERMINATION, GS_FORCED_EXTRA = 1, 2
 GS_FLAG_TOPP_TIE = 1
 GS_FLAG_EXACT_PATH = 2
@@ -510,6 +511,20 @@ class Sampler:
                                                   C.c_void_p(row_scales.data_ptr()), float(input_scale),
                                                   float(output_scale), C.c_void_p(logits_scratch.data_ptr()),
                                                   C.byref(batch), C.c_void_p(stream or 0)))
+
+    def lmhead_sample(self, hidden, weight, softcap_value: float, logits_scratch, configs: np.ndarray,
+                      histories=None, forced=None, mask_table=None, fused: bool = False) -> "SampleOutput":
+        """gs_lmhead_sample: the bf16 lm_head into `logits_scratch` ([rows][V] f32), then the
+        sampler, one call; returns the rows' results. fused: GS_BATCH_FUSED_HEAD (the head
+        computes the chunk statistics itself)."""
+        b, keep = self.prepare(logits_scratch, configs, histories, forced, mask_table)
+        if fused:
+            b.hints |= GS_BATCH_FUSED_HEAD
+        self.lmhead_sample_launch(hidden, weight, softcap_value, logits_scratch, b)
+        self.synchronize()
+        res = keep[-1].cpu().numpy().view(np.uint8).reshape(-1)[: b.rows * 16].view(RESULT_DTYPE)
+        del keep
+        return SampleOutput(res["token"].copy(), res["probability"].copy(), res["flags"].copy())
 
     def lmhead_sample_launch(self, hidden, weight, softcap_value: float, logits_scratch, batch: Batch,
                              stream: Optional[int] = None):

@@ -126,6 +126,16 @@ typedef struct gs_batch {
  * more than they save on average), those launches are skipped.
  * gs_sample_host sets the hint itself from its host configs. */
 #define GS_BATCH_FULL_DRAWS 1
+/* Batch hint for gs_lmhead_sample (vocabularies that are a multiple of 8192
+ * ids): the lm_head's epilogue computes the chunk scan's statistics and
+ * candidate lists itself, so the logits are written but not read back (three
+ * launches -- the rows' excluded-id bitmaps, the fused head, a merge of its
+ * per-256-id partials into the scan's chunk records -- instead of the head and
+ * the scan). Results equal the unfused path's tokens; probabilities agree
+ * within the normaliser bound. Without the hint the head and the scan run
+ * separately, which is faster at 64 x 2048 x 262144 on MI355X (279 against
+ * 305 us for the head and the streaming stage). */
+#define GS_BATCH_FUSED_HEAD 2
 
 /* Library / device identity. */
 int gs_abi_version(void);
@@ -274,7 +284,9 @@ int gs_lmhead(gs_context* ctx, const void* hidden, const void* weight, int32_t m
               float softcap, float* logits, void* stream);
 
 /* lm_head followed by gs_sample on its f32 output (batch->logits is ignored and
- * replaced by `logits_scratch`, [m_rows][V] f32 device memory). */
+ * replaced by `logits_scratch`, [m_rows][V] f32 device memory, 16-byte
+ * aligned); with GS_BATCH_FUSED_HEAD in batch->hints the head computes the
+ * sampler's per-chunk statistics itself (see the hint). */
 int gs_lmhead_sample(gs_context* ctx, const void* hidden, const void* weight, int32_t width, float softcap,
                      float* logits_scratch, const gs_batch* batch, void* stream);
 
