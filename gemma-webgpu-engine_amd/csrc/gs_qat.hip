@@ -21,6 +21,21 @@
 // + 4 M V of logits per call; the activations (M x D) are staged in LDS as
 // binary64. Work: one bit-field extract, one conversion and one fused
 // multiply-add per weight and row of x.
+//
+// Exact integer path (widths a multiple of 256 up to 2048, V a multiple of
+// 16). Every activation a_k is a binary32 value, an integer multiple of its
+// granule 2^g_k; with E the smallest granule of a row (nonzero a_k), every
+// product (code - 2) a_k and every partial sum is an integer multiple of 2^E
+// no larger than 2 sum |a_k|. When that bound is below 2^(E + 53), no partial
+// sum rounds: the sequential binary64 sum is the exact sum, and so is
+//   2^E (sum_k code_k A_k - 2 sum_k A_k),   A_k = a_k / 2^E (integers).
+// qat_tile_kernel checks the bound per row of x, writes A_k as 7 balanced
+// base-256 digits (int8 limbs), multiplies the codes (0..3, int8) by the
+// limbs on v_mfma_i32_16x16x64_i8 (exact int32 sums), combines the limbs in
+// wrapping 64-bit arithmetic (exact: the total fits in 53 bits) and applies
+// the same epilogue, so the logits equal the binary64 path's bit for bit.
+// Rows that fail the bound (a huge exponent range, subnormals, non-finite
+// values) take the binary64 path in the same launch.
 #include "gs_internal.h"
 
 namespace gs {
@@ -48,20 +63,26 @@ __device__ __forceinline__ double srq(double v, double s) {
   return (double)(float)(q * s);
 }
 
-// kRows rows of x per pass (m0 .. m0 + kRows - 1, those below M)
+// The activations of kRows rows of x from m0 (those below M) into act,
+// after the input SRQ, in binary64 (the whole block calls it).
 template <int kRows>
-__global__ __launch_bounds__(kQatThreads) void qat_lmhead_kernel(QatArgs a, int32_t m0) {
-  __shared__ double act[kQatLdsDoubles];
-  const int tid = threadIdx.x;
+__device__ __forceinline__ void qat_stage_act(const QatArgs& a, int32_t m0, double* act) {
   const int D = a.D;
   const int rows = a.M - m0 < kRows ? a.M - m0 : kRows;
-  for (int i = tid; i < kRows * D; i += kQatThreads) {
+  for (int i = threadIdx.x; i < kRows * D; i += kQatThreads) {
     const int m = i / D;
     act[i] = m < rows ? srq((double)a.x[(int64_t)(m0 + m) * D + (i - m * D)], a.in_scale) : 0.0;
   }
   __syncthreads();
-  const int64_t r = (int64_t)blockIdx.x * kQatThreads + tid;
-  if (r >= a.V) return;
+}
+
+// Logits of the staged rows (those below M and not skipped) at vocabulary
+// row r < V.
+template <int kRows>
+__device__ __forceinline__ void qat_row_binary64(const QatArgs& a, int32_t m0, const bool (&skip)[kRows],
+                                                 const double* act, int64_t r) {
+  const int D = a.D;
+  const int rows = a.M - m0 < kRows ? a.M - m0 : kRows;
   double acc[kRows];
 #pragma unroll
   for (int m = 0; m < kRows; ++m) acc[m] = 0.0;
@@ -86,7 +107,226 @@ __global__ __launch_bounds__(kQatThreads) void qat_lmhead_kernel(QatArgs a, int3
   const double scale = (double)a.scales[r];
 #pragma unroll
   for (int m = 0; m < kRows; ++m) {
-    if (m < rows) a.out[(int64_t)(m0 + m) * a.V + r] = (float)srq(acc[m] * scale, a.out_scale);
+    if (m < rows && !skip[m]) a.out[(int64_t)(m0 + m) * a.V + r] = (float)srq(acc[m] * scale, a.out_scale);
+  }
+}
+
+// kRows rows of x per pass (m0 .. m0 + kRows - 1, those below M)
+template <int kRows>
+__global__ __launch_bounds__(kQatThreads) void qat_lmhead_kernel(QatArgs a, int32_t m0) {
+  __shared__ double act[kQatLdsDoubles];
+  bool skip[kRows];
+#pragma unroll
+  for (int m = 0; m < kRows; ++m) skip[m] = false;
+  qat_stage_act<kRows>(a, m0, act);
+  const int64_t r = (int64_t)blockIdx.x * kQatThreads + threadIdx.x;
+  if (r < a.V) qat_row_binary64<kRows>(a, m0, skip, act, r);
+}
+
+// ---- the exact integer path
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+constexpr int kQatLimbs = 7;                   // balanced base-256 digits of |A_k| < 2^52
+constexpr uint64_t kQatSumBound = 1ull << 52;  // sum |A_k| below it: every partial sum exact
+
+// Operand layout of the integer path: MFMA step s takes 64 codes of a row,
+// lane row + 16 g of a 16-row tile holding 16 of them as 4 dwords, byte i of
+// dword t being code 16 W + 4 i + t of word W = 16 q + 4 g + t' (s = 4 q + t').
+// The tile kernel expands a code word into bytes in that order and writes
+// the activations' limbs at the same positions; the dot product does not
+// depend on the order of k.
+// The activation's integer significand and granule exponent (the value is
+// sig 2^g); false for a non-finite value.
+__device__ __forceinline__ bool act_parts(float f, uint32_t* sig, int* g) {
+  const uint32_t bits = __builtin_bit_cast(uint32_t, f);
+  const uint32_t ex = (bits >> 23) & 0xFFu;
+  if (ex == 0xFFu) return false;
+  *sig = ex ? (bits & 0x7FFFFFu) | 0x800000u : bits & 0x7FFFFFu;
+  *g = ex ? (int)ex - 150 : -149;
+  return true;
+}
+
+// Per-row constants of a tile's two rows of x, reduced in LDS.
+struct QatTileRows {
+  int emin[2];                  // smallest granule exponent of the nonzero activations
+  uint32_t bad[2];              // a non-finite activation, or a magnitude past the bound
+  unsigned long long sabs[2];   // sum |A_k|
+  unsigned long long ssum[2];   // sum A_k (wrapping; exact when the check passes)
+};
+
+constexpr int kQatMaxSteps = 2048 / 64;
+constexpr int kQatTileWaves = kQatThreads / 64;
+constexpr int kQatTilesPerWave = 4;  // 16-row vocabulary tiles per wave, two in flight
+constexpr int kQatF64Blocks = 256;   // workgroups of the binary64 fallback in a tile's launch
+
+// Rows 2 tile and 2 tile + 1 of x, one launch. Workgroups below n_int take
+// the exact integer path: each first checks the two rows and writes their
+// limbs into LDS as a 16-row operand tile (rows 8 r + limb, limb 7 zero; one
+// thread per code word of 16 activations), then its waves take 16-row
+// vocabulary tiles, the next tile's codes loading while the current one
+// multiplies. The kQatF64Blocks workgroups from n_int on take the rows the
+// check refused on the binary64 path (vocabulary rows 256 (b - n_int) + tid
+// + 256 kQatF64Blocks i), and return at once when there are none; placed
+// after the integer workgroups, they are dispatched as those finish.
+__global__ __launch_bounds__(kQatThreads, 4) void qat_tile_kernel(QatArgs a, int32_t tile, int32_t n_int) {
+  __shared__ union __attribute__((aligned(16))) {
+    i32x4 op[kQatMaxSteps][64];   // the integer path's operand tile
+    double act[2 * 2048];         // the binary64 path's activations
+  } L;
+  __shared__ QatTileRows R;
+  const int tid = threadIdx.x;
+  const int D = a.D, words = D / 16, quads = D / 256;
+  const int m0 = 2 * tile;
+  if (tid < 2) { R.emin[tid] = 0x7FFFFFFF; R.bad[tid] = 0; R.sabs[tid] = 0; R.ssum[tid] = 0; }
+  __syncthreads();
+  // the check: this thread's word W of row rr (activations 16 W .. 16 W + 15)
+  const int rr = tid / words, W = tid - rr * words;
+  const bool mine = tid < 2 * words;
+  const bool live = mine && m0 + rr < a.M;
+  float f[16];
+#pragma unroll
+  for (int e = 0; e < 16; ++e) f[e] = 0.0f;
+  if (live) {
+    const float4* xp = (const float4*)(a.x + (int64_t)(m0 + rr) * D + 16 * W);
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const float4 x4 = xp[v];
+      const float xs[4] = {x4.x, x4.y, x4.z, x4.w};
+#pragma unroll
+      for (int e = 0; e < 4; ++e) f[4 * v + e] = (float)srq((double)xs[e], a.in_scale);
+    }
+  }
+  int gmin = 0x7FFFFFFF;
+  bool bad = false;
+#pragma unroll
+  for (int e = 0; e < 16; ++e) {
+    uint32_t sig;
+    int g;
+    if (!act_parts(f[e], &sig, &g)) bad = true;
+    else if (sig) gmin = g < gmin ? g : gmin;
+  }
+  if (mine && gmin != 0x7FFFFFFF) atomicMin(&R.emin[rr], gmin);
+  __syncthreads();
+  const int E = mine && R.emin[rr] != 0x7FFFFFFF ? R.emin[rr] : 0;
+  int64_t A[16];
+  uint64_t sabs = 0, ssum = 0;
+#pragma unroll
+  for (int e = 0; e < 16; ++e) {
+    A[e] = 0;
+    uint32_t sig = 0;
+    int g = 0;
+    if (!act_parts(f[e], &sig, &g) || !sig) continue;
+    const int sh = g - E;
+    if (sh > 62 - 24) { bad = true; continue; }
+    const uint64_t mag = (uint64_t)sig << sh;
+    if (mag >= kQatSumBound) { bad = true; continue; }
+    A[e] = f[e] < 0.0f ? -(int64_t)mag : (int64_t)mag;
+    sabs += mag;
+    ssum += (uint64_t)A[e];
+  }
+  if (mine) {
+    // (magnitudes below 2^52, at most 2048 of them: the sums do not wrap
+    // unless the check fails anyway)
+    atomicAdd(&R.sabs[rr], (unsigned long long)sabs);
+    atomicAdd(&R.ssum[rr], (unsigned long long)ssum);
+    if (bad) atomicOr(&R.bad[rr], 1u);
+  }
+  __syncthreads();
+  bool ok[2];
+#pragma unroll
+  for (int q = 0; q < 2; ++q) ok[q] = m0 + q < a.M && !R.bad[q] && R.sabs[q] < kQatSumBound;
+
+  if ((int)blockIdx.x >= n_int) {
+    // the binary64 path for the rows the check refused
+    const bool skip[2] = {ok[0], ok[1]};
+    if (skip[0] && (skip[1] || m0 + 1 >= a.M)) return;
+    qat_stage_act<2>(a, m0, L.act);
+    for (int64_t r = (int64_t)((int)blockIdx.x - n_int) * kQatThreads + tid; r < a.V;
+         r += (int64_t)kQatF64Blocks * kQatThreads)
+      qat_row_binary64<2>(a, m0, skip, L.act, r);
+    return;
+  }
+  if (!ok[0] && !ok[1]) return;
+  // the limbs: tile row 8 rr + l, balanced base-256 digits of A (zeros for a
+  // row the check refused), at the operand positions of word W
+  if (mine) {
+    const int q = W >> 4, g = (W >> 2) & 3, tp = W & 3;
+    const int step = 4 * q + tp;
+    int64_t v[16];
+#pragma unroll
+    for (int e = 0; e < 16; ++e) v[e] = ok[rr] ? A[e] : 0;
+#pragma unroll
+    for (int l = 0; l < 8; ++l) {
+      uint32_t dw[4] = {0u, 0u, 0u, 0u};
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        int64_t d = 0;
+        if (l < kQatLimbs) {
+          d = ((v[e] + 128) & 255) - 128;
+          v[e] = (v[e] - d) >> 8;
+        }
+        // activation e = 4 i + t of the word: dword t, byte i
+        dw[e & 3] |= ((uint32_t)d & 0xFFu) << (8 * (e >> 2));
+      }
+      L.op[step][8 * rr + l + 16 * g] = i32x4{(int)dw[0], (int)dw[1], (int)dw[2], (int)dw[3]};
+    }
+  }
+  __syncthreads();
+
+  const int lane = tid & 63, wave = tid >> 6, j = lane & 15, g = lane >> 4;
+  const int n_tiles = a.V / 16;
+  const int stride = n_int * kQatTileWaves;
+  const uint4* w4 = (const uint4*)a.words;
+  const int64_t row_words = words;
+  // words 16 q + 4 g .. + 3 of vocabulary row n (block 4 q + g in block-major order)
+  auto load = [&](int vt, uint4 (&cw)[kQatMaxSteps / 4]) __attribute__((always_inline)) {
+    const int64_t n = (int64_t)vt * 16 + j;
+#pragma unroll
+    for (int q = 0; q < kQatMaxSteps / 4; ++q) {
+      if (q < quads)
+        cw[q] = load_nt16(a.block_major ? w4 + (int64_t)(4 * q + g) * a.V + n : w4 + (n * row_words + 16 * q + 4 * g) / 4);
+    }
+  };
+  auto multiply = [&](int vt, const uint4 (&cw)[kQatMaxSteps / 4]) __attribute__((always_inline)) {
+    i32x4 acc = {0, 0, 0, 0};
+#pragma unroll
+    for (int q = 0; q < kQatMaxSteps / 4; ++q) {
+      if (q < quads) {
+        const uint32_t wq[4] = {cw[q].x, cw[q].y, cw[q].z, cw[q].w};
+#pragma unroll
+        for (int tp = 0; tp < 4; ++tp) {
+          const uint32_t w = wq[tp];
+          constexpr uint32_t kLow = 0x03030303u;
+          const i32x4 b = {(int)(w & kLow), (int)((w >> 2) & kLow), (int)((w >> 4) & kLow), (int)((w >> 6) & kLow)};
+          acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(L.op[4 * q + tp][lane], b, acc, 0, 0, 0);
+        }
+      }
+    }
+    // lane (j, g) holds tile rows 4 g .. 4 g + 3: row m0 + g / 2, limbs
+    // 4 (g & 1) .. + 3; the limbs combine in wrapping 64-bit arithmetic (the
+    // total is below 2^53 in magnitude, so the wrapped sum is exact)
+    uint64_t p = 0;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) p += (uint64_t)(int64_t)acc[e] << (8 * (4 * (g & 1) + e));
+    p += shfl_xor_u64(p, 16);
+    const int r = g >> 1;
+    if ((g & 1) == 0 && ok[r]) {
+      const int64_t n = (int64_t)vt * 16 + j;
+      const int64_t T = (int64_t)(p - 2 * (uint64_t)R.ssum[r]);
+      const double dot = __builtin_ldexp((double)T, R.emin[r] != 0x7FFFFFFF ? R.emin[r] : 0);
+      a.out[(int64_t)(m0 + r) * a.V + n] = (float)srq(dot * (double)a.scales[n], a.out_scale);
+    }
+  };
+  // two register buffers with fixed roles: tile t multiplies from one while
+  // tile t + stride loads into the other
+  uint4 b0[kQatMaxSteps / 4], b1[kQatMaxSteps / 4];
+  int vt = (int)blockIdx.x * kQatTileWaves + wave;
+  if (vt < n_tiles) load(vt, b0);
+  for (; vt < n_tiles; vt += 2 * stride) {
+    const int v1 = vt + stride, v2 = vt + 2 * stride;
+    if (v1 < n_tiles) load(v1, b1);
+    multiply(vt, b0);
+    if (v2 < n_tiles) load(v2, b0);
+    if (v1 < n_tiles) multiply(v1, b1);
   }
 }
 
@@ -98,18 +338,30 @@ int qat_rows_per_pass(int32_t D) {
   return r >= 4 ? 4 : (r >= 2 ? 2 : 1);
 }
 
+
 void launch_qat_lmhead(const float* x, int32_t M, int32_t D, const uint32_t* words, int32_t block_major,
                        const float* scales, int32_t V, double in_scale, double out_scale, float* out, hipStream_t s,
                        LaunchEvents ev) {
   QatArgs a{x, words, scales, out, D, V, M, block_major, in_scale, out_scale};
+  if (D % 256 == 0 && D <= 2048 && V % 16 == 0) {
+    // one launch per pair of rows: the integer workgroups, then the binary64 ones
+    const int tiles = (M + 1) / 2;
+    const int n_vt = V / 16;
+    const int n_int = (n_vt + kQatTileWaves * kQatTilesPerWave - 1) / (kQatTileWaves * kQatTilesPerWave);
+    const int n_f64 = kQatF64Blocks;
+    for (int t = 0; t < tiles; ++t)
+      hipExtLaunchKernelGGL(qat_tile_kernel, dim3(n_int + n_f64), dim3(kQatThreads), 0, s, t == 0 ? ev.start : nullptr,
+                            t == tiles - 1 ? ev.stop : nullptr, 0, a, t, n_int);
+    return;
+  }
   const dim3 grid((unsigned)((V + kQatThreads - 1) / kQatThreads));
   const int most = qat_rows_per_pass(D);
   for (int32_t m0 = 0; m0 < M;) {
     // as many rows of x as the stage holds and remain, in a kernel made for that many
     const int left = M - m0;
     const int per = most >= 4 && left >= 4 ? 4 : (most >= 2 && left >= 2 ? 2 : 1);
-    const bool first = m0 == 0, last = m0 + per >= M;
-    hipEvent_t start = first ? ev.start : nullptr, stop = last ? ev.stop : nullptr;
+    const bool last = m0 + per >= M;
+    hipEvent_t start = m0 == 0 ? ev.start : nullptr, stop = last ? ev.stop : nullptr;
     if (per == 4) hipExtLaunchKernelGGL(qat_lmhead_kernel<4>, grid, dim3(kQatThreads), 0, s, start, stop, 0, a, m0);
     else if (per == 2) hipExtLaunchKernelGGL(qat_lmhead_kernel<2>, grid, dim3(kQatThreads), 0, s, start, stop, 0, a, m0);
     else hipExtLaunchKernelGGL(qat_lmhead_kernel<1>, grid, dim3(kQatThreads), 0, s, start, stop, 0, a, m0);

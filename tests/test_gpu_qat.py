@@ -3,8 +3,9 @@ cpuQatLinear restatement (oracle/qat_ref.c, src/reference/qat-linear.ts:
 78-148): the reference's own known answer (tests/qat-linear-gpu.spec.ts:
 1307-1397), then the full Gemma shape (V 262144, width 1536) with random
 codes, input and output SRQ, one and several rows of activations, both weight
-layouts -- logits equal bit for bit -- and the fused head + sampler against
-the oracle sampler on the oracle's logits."""
+layouts -- logits equal bit for bit, on the exact integer path and on the
+binary64 kernel it leaves rows to -- and the fused head + sampler against the
+oracle sampler on the oracle's logits."""
 import numpy as np
 import pytest
 
@@ -74,6 +75,38 @@ def test_gemma_shape_bit_exact(gemma_head, in_scale, out_scale):
                 assert bad[0].size == 0, (layout, m, bad[0][:5], bad[1][:5], got[bad][:5], want[:m][bad][:5])
         if out_scale:
             assert len(np.unique(want[0])) <= 256  # the SRQ grid
+    finally:
+        s.close()
+
+
+@pytest.mark.parametrize("in_scale", [0.0, 0.03])
+def test_integer_path_and_fallback_rows(gemma_head, in_scale):
+    """The exact integer path (int8 MFMA on limbs of the activations) takes
+    the rows whose products and partial sums are all exact in binary64; a row
+    with an activation 2^-100 beside values near 1 (an exponent range past 53
+    bits) and a row holding an f32 subnormal are left to the binary64 kernel.
+    Five rows (the last operand tile half empty), both layouts: every logit
+    equals cpuQatLinear's bit for bit."""
+    import torch
+
+    gs = _gs()
+    V, D, words, scales, x = gemma_head
+    xs = np.concatenate([x, x[:2] * 0.5]).astype(np.float32)
+    xs[1, 10] = np.float32(2.0 ** -100)
+    xs[3, 5] = np.float32(1e-40)
+    assert xs[3, 5] != 0 and xs[3, 5] < np.finfo(np.float32).tiny
+    in_scale = float(np.float32(in_scale))
+    want = np.stack([oracle.qat_linear_int2(xs[m], words, scales, D, V, in_scale, 0.0) for m in range(5)])
+    s = gs.Sampler(vocab_size=V, max_rows=8)
+    try:
+        sc = torch.from_numpy(scales).cuda()
+        xt = torch.from_numpy(xs).cuda()
+        row = torch.from_numpy(words.view(np.int32)).cuda()
+        block = torch.from_numpy(oracle.repack_block_major(words, V, D).view(np.int32)).cuda()
+        for layout, codes in ((gs.runtime.GS_QAT_ROW_MAJOR, row), (gs.runtime.GS_QAT_BLOCK_MAJOR, block)):
+            got = s.qat_lmhead(xt, codes, sc, layout=layout, input_scale=in_scale).cpu().numpy()
+            bad = np.nonzero(got.view(np.uint32) != want.view(np.uint32))
+            assert bad[0].size == 0, (layout, bad[0][:5], bad[1][:5], got[bad][:5], want[bad][:5])
     finally:
         s.close()
 
