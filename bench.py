@@ -238,7 +238,7 @@ def build_workload(name, gs, torch, device):
                    scratch=scratch, histories=None, states=None,
                    lm_bytes=V * D // 4 + 4 * V + 4 * M * D, lm_logits_bytes=4 * M * V, lm_flops=2 * M * D * V,
                    step_bytes=V * D // 4 + 4 * V + 4 * M * D + 8 * M * V + 16 * M, dominant="lmhead",
-                   kernel="qat_lmhead_kernel", config_obj=cfg,
+                   kernel="qat_tile_kernel", config_obj=cfg,
                    desc=(f"qat: 1 x {D} f32 activation ~ N(0, 1.5^2) through the int2 QAT head, {V} x {D} "
                          "2-bit codes (block-major, 3 rotated copies), row scales 0.0008 + (r mod 29) 2.5e-5, "
                          "output SRQ 0.125; then the sampler, T 0.8, topK 40, topP 0.95, seed 42"))
@@ -474,7 +474,7 @@ def roofline_of(wl, stages):
         algo = rows * wl["scan_bytes_per_row"]
         mfma_tflops = None
     achieved = algo / (dom_avg_ms * 1e6)
-    kname = wl.get("kernel") or {"scan": "scan_kernel", "lmhead": "lmhead_kernel"}[dom]
+    kname = wl.get("kernel") or {"scan": "scan_kernel", "lmhead": "lmhead_resident_kernel"}[dom]
     roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                 "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": profiled_traffic(wl["name"], kname),
                 "kernel": kname, "algorithmic_bytes_per_launch": int(algo),

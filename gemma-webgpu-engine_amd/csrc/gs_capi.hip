@@ -962,8 +962,8 @@ int gs_lmhead(gs_context* ctx, const void* hidden, const void* weight, int32_t m
   GS_HIP(ctx, hipSetDevice(ctx->device));
   hipStream_t s = pick_stream(ctx, stream);
   const int32_t slot = timing_slot(ctx);
-  launch_lmhead((const uint16_t*)hidden, (const uint16_t*)weight, m_rows, width, ctx->vocab, softcap, logits, s,
-                stage_events(ctx, slot, GS_STAGE_LMHEAD));
+  launch_lmhead((const uint16_t*)hidden, (const uint16_t*)weight, m_rows, width, ctx->vocab, softcap, logits,
+                ctx->cu_count, s, stage_events(ctx, slot, GS_STAGE_LMHEAD));
   GS_HIP(ctx, hipGetLastError());
   return GS_OK;
 }

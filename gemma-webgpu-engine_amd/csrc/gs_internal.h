@@ -273,6 +273,12 @@ struct FusedArgs {
 
 // A 16-byte load marked non-temporal, for rows streamed once: the stream
 // does not displace what the caches hold for reuse.
+// word 3 of a raw buffer resource on gfx9-family parts (gfx950 included)
+constexpr int32_t kBufferWord3 = 0x00020000;
+// a buffer offset past every resource's extent: the access returns zeros or
+// is dropped, without a memory request
+constexpr uint32_t kBufferOutOfRange = 0x80000000u;
+
 __device__ __forceinline__ uint4 load_nt16(const uint4* p) {
   typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
   const u32x4 v = __builtin_nontemporal_load((const u32x4*)p);
@@ -578,7 +584,7 @@ void launch_qat_lmhead(const float* x, int32_t M, int32_t D, const uint32_t* wor
                        const float* scales, int32_t V, double in_scale, double out_scale, float* out, hipStream_t s,
                        LaunchEvents ev = {});
 void launch_lmhead(const uint16_t* hidden, const uint16_t* weight, int32_t m, int32_t width, int32_t vocab,
-                   float softcap, float* out, hipStream_t s, LaunchEvents ev = {});
+                   float softcap, float* out, int32_t cu_count, hipStream_t s, LaunchEvents ev = {});
 // The fused path (vocab a multiple of kChunk): the excluded-id bitmaps, then
 // the lm_head with the partial statistics; launch_merge_parts takes the chunk
 // scan's place before the finish.

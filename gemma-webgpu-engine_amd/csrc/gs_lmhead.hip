@@ -127,10 +127,185 @@ __global__ __launch_bounds__(kLmThreads) void lmhead_kernel(const uint16_t* __re
   }
 }
 
+// Resident-H kernel for widths up to 2048: one workgroup per compute unit
+// holds its 64-row block of H in registers for the whole launch and streams
+// a contiguous run of W in steps of 16 vocabulary rows.
+//   * 8 waves split K: wave w owns the 32-wide K steps [w nS / 8, (w+1) nS / 8)
+//     of the nS = D / 32, its H slice (64 rows) held as MFMA A operands
+//     (v_mfma_f32_16x16x32_bf16: lane i + 16 g holds k = 32 s + 8 g .. + 7 of
+//     row i of an M tile, 4 M tiles);
+//   * per step a lane loads 16 bytes per K step of one vocabulary row (the
+//     B operand), so the workgroup reads 16 whole rows of W (16 x 2D bytes,
+//     contiguous) per step; two steps of loads are in flight per wave;
+//   * the 8 waves' partial 64x16 tiles go through LDS (double-buffered), and
+//     after one barrier each thread adds two outputs' partials in wave order
+//     and applies the cap into an LDS stage of 16 steps, which then goes out
+//     as 1 KB runs of each logits row in 16-byte stores. At M 64, D 2048,
+//     V 262144 the logits cost 73 us of 258 stored per step (64-byte pieces
+//     of 64 rows 4V bytes apart), 31 us of 216 staged over 8 steps, 19 us of
+//     204 over 16 (185 us without stores); spreading a double-buffered stage's
+//     stores over the next run's steps took 224 us, write-back stores 237 us.
+// Every global access is a buffer access with no branch around it: rows past
+// V or M, K steps a wave does not own, and the steps past a workgroup's run
+// take an out-of-range offset (zeros, no memory request; stores dropped). The
+// compiler's wait counts then cover exactly the loads a step consumes, as
+// loads and stores share one in-order counter on this part.
+constexpr int kResWaves = 8;
+constexpr int kResThreads = 64 * kResWaves;
+constexpr int kResN = 16;         // vocabulary rows per step
+constexpr int kResStride = 68;    // LDS floats per vocabulary row of a partial (64 + 4)
+constexpr int kResMaxWidth = 2048;
+constexpr int32_t kResNT = 2;     // non-temporal cache policy of the streams
+constexpr int kResStage = 16;     // steps of logits staged per flush
+constexpr int kResStageStride = kResStage * kResN + 4;  // LDS floats per staged row
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+template <int kS>  // K steps per wave, at most 8
+__global__ __launch_bounds__(kResThreads) void lmhead_resident_kernel(const uint16_t* __restrict__ H,
+                                                                      const uint16_t* __restrict__ W, int M, int D,
+                                                                      int V, float cap, float* __restrict__ out) {
+  __shared__ __attribute__((aligned(16))) float red[2][kResWaves][kResN * kResStride];
+  __shared__ __attribute__((aligned(16))) float stage[64 * kResStageStride];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int j = lane & 15, g = lane >> 4;
+  const int n_steps = D / 32;
+  const int s_lo = wave * n_steps / kResWaves, s_hi = (wave + 1) * n_steps / kResWaves;
+  const int my_steps = s_hi - s_lo;  // kS or kS - 1
+  // this workgroup's tiles of 16 vocabulary rows: a contiguous run
+  const int n_tiles = (V + kResN - 1) / kResN;
+  const int t_lo = (int)((int64_t)blockIdx.x * n_tiles / gridDim.x);
+  const int t_hi = (int)((int64_t)(blockIdx.x + 1) * n_tiles / gridDim.x);
+  // byte offsets of this lane's K step s within a row of H or W
+  uint32_t k_off[kS];
+#pragma unroll
+  for (int s = 0; s < kS; ++s) k_off[s] = s < my_steps ? (uint32_t)(64 * (s_lo + s) + 16 * g) : kBufferOutOfRange;
+
+  // H slice: rows 16 mt + j of the M tiles (rows past M read zeros)
+  const __amdgpu_buffer_rsrc_t hr =
+      __builtin_amdgcn_make_buffer_rsrc((void*)H, (short)0, M * D * 2, kBufferWord3);
+  bf16x8 hreg[4][kS];
+#pragma unroll
+  for (int mt = 0; mt < 4; ++mt) {
+#pragma unroll
+    for (int s = 0; s < kS; ++s) {
+      const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(hr, k_off[s] + (uint32_t)((16 * mt + j) * D * 2), 0, 0);
+      hreg[mt][s] = __builtin_bit_cast(bf16x8, v);
+    }
+  }
+  u32x4 wbuf[2][kS];
+  // tile t's rows in a resource of their own (empty past the run, short at V)
+  auto issue = [&](int slot, int t) __attribute__((always_inline)) {
+    const int rows = t < t_hi ? (V - t * kResN < kResN ? V - t * kResN : kResN) : 0;
+    const __amdgpu_buffer_rsrc_t wr = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)(W + (size_t)(t < t_hi ? t : t_lo) * kResN * D), (short)0, rows * D * 2, kBufferWord3);
+    const uint32_t row_off = (uint32_t)(j * D * 2);
+#pragma unroll
+    for (int s = 0; s < kS; ++s) wbuf[slot][s] = __builtin_amdgcn_raw_buffer_load_b128(wr, row_off + k_off[s], 0, kResNT);
+  };
+  // the output block: rows past M fall outside the resource
+  const __amdgpu_buffer_rsrc_t orc =
+      __builtin_amdgcn_make_buffer_rsrc((void*)out, (short)0, M * V * 4, kBufferWord3);
+  // reduction role: outputs (m, n) = (2 (tid >> 4) + e, tid & 15), e = 0, 1
+  const int rn = tid & 15, rm = 2 * (tid >> 4);
+  auto step = [&](int t, int u) __attribute__((always_inline)) {
+    const int slot = u & 1;
+    f32x4 acc[4];
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt) acc[mt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int s = 0; s < kS; ++s) {
+      const bf16x8 b = __builtin_bit_cast(bf16x8, wbuf[slot][s]);
+#pragma unroll
+      for (int mt = 0; mt < 4; ++mt) acc[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(hreg[mt][s], b, acc[mt], 0, 0, 0);
+    }
+    issue(slot, t + 2);
+    // lane (j, g) holds rows 16 mt + 4 g + e of column j
+    float* r = &red[slot][wave][j * kResStride + 4 * g];
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt) *(f32x4*)(r + 16 * mt) = acc[mt];
+    __syncthreads();
+    float x0 = 0.0f, x1 = 0.0f;
+#pragma unroll
+    for (int w = 0; w < kResWaves; ++w) {
+      const float2 p = *(const float2*)&red[slot][w][rn * kResStride + rm];
+      x0 += p.x;
+      x1 += p.y;
+    }
+    if (cap > 0.0f) {
+      x0 = cap * tanhf(x0 / cap);
+      x1 = cap * tanhf(x1 / cap);
+    }
+    stage[rm * kResStageStride + kResN * u + rn] = x0;
+    stage[(rm + 1) * kResStageStride + kResN * u + rn] = x1;
+  };
+  // a staged run: piece q = tid + 512 i is 16 bytes of row q / 64 at column
+  // 4 (q % 64), so a wave writes one row's 1 KB. Columns of tiles past the
+  // workgroup's run, or past V, are dropped (V % 4 == 0: a piece lies within
+  // its row).
+  constexpr int kRowPieces = kResStage * kResN / 4;  // 64
+  auto flush = [&](int t0) __attribute__((always_inline)) {
+#pragma unroll
+    for (int i = 0; i < 64 * kRowPieces / kResThreads; ++i) {
+      const int q = tid + kResThreads * i, row = q / kRowPieces, c = 4 * (q % kRowPieces);
+      const f32x4 v = *(const f32x4*)&stage[row * kResStageStride + c];
+      const int n = t0 * kResN + c;
+      const uint32_t o = t0 + c / kResN < t_hi && n < V ? (uint32_t)(row * V + n) * 4u : kBufferOutOfRange;
+      __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), orc, o, 0, kResNT);
+    }
+  };
+  issue(0, t_lo);
+  // keep the first tile's loads ahead of the second's (waits count in issue order)
+  __builtin_amdgcn_sched_barrier(0);
+  issue(1, t_lo + 1);
+  // Straight-line runs of kResStage steps (even, so the two load slots
+  // alternate in place); a run past the workgroup's tiles reads zeros and
+  // drops its stores. The reduction buffer of step u is u & 1: the barrier of
+  // step u + 1 orders step u's reads before step u + 2's writes; the barrier
+  // before a flush orders the stage's writes before its reads, and the next
+  // run's first barrier its reads before the next writes.
+  for (int t0 = t_lo; t0 < t_hi; t0 += kResStage) {
+#pragma unroll
+    for (int u = 0; u < kResStage; ++u) step(t0 + u, u);
+    __syncthreads();
+    flush(t0);
+  }
+}
+
 }  // namespace
 
 void launch_lmhead(const uint16_t* hidden, const uint16_t* weight, int32_t m, int32_t width, int32_t vocab,
-                   float softcap, float* out, hipStream_t s, LaunchEvents ev) {
+                   float softcap, float* out, int32_t cu_count, hipStream_t s, LaunchEvents ev) {
+  if (width <= kResMaxWidth && width % 32 == 0 && vocab % 4 == 0 && ((uintptr_t)out & 15) == 0 &&
+      (int64_t)vocab * kLmM * 4 < ((int64_t)1 << 31)) {
+    // one launch per 64-row block of H, one workgroup per compute unit
+    const int k_steps = (width / 32 + kResWaves - 1) / kResWaves;
+    const dim3 grid(cu_count > 0 ? cu_count : 256), block(kResThreads);
+    for (int m0 = 0; m0 < m; m0 += kLmM) {
+      const int mb = m - m0 < kLmM ? m - m0 : kLmM;
+      const uint16_t* h = hidden + (size_t)m0 * width;
+      float* o = out + (size_t)m0 * vocab;
+      hipEvent_t start = m0 == 0 ? ev.start : nullptr, stop = m0 + kLmM >= m ? ev.stop : nullptr;
+      switch (k_steps) {
+#define GS_RES_CASE(k)                                                                                              \
+  case k:                                                                                                           \
+    hipExtLaunchKernelGGL(lmhead_resident_kernel<k>, grid, block, 0, s, start, stop, 0, h, weight, mb, width, vocab, \
+                          softcap, o);                                                                              \
+    break;
+        GS_RES_CASE(1)
+        GS_RES_CASE(2)
+        GS_RES_CASE(3)
+        GS_RES_CASE(4)
+        GS_RES_CASE(5)
+        GS_RES_CASE(6)
+        GS_RES_CASE(7)
+        GS_RES_CASE(8)
+#undef GS_RES_CASE
+      }
+    }
+    return;
+  }
   dim3 grid((vocab + kLmRows - 1) / kLmRows, (m + kLmM - 1) / kLmM);
   hipExtLaunchKernelGGL(lmhead_kernel, grid, dim3(kLmThreads), 0, s, ev.start, ev.stop, 0, hidden, weight, m, width,
                         vocab, softcap, out);

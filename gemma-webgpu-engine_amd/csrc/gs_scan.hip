@@ -65,8 +65,6 @@ constexpr int kMaxGroupChunks = 16;       // chunks one group workgroup streams
 // CU they spilled, at 3 the masked scan of 256 x 262144 took 51 us).
 template <typename In, bool kMaskable>
 constexpr int scan_wg_per_cu() { return 4; }
-// word 3 of a raw buffer resource on gfx9-family parts (gfx950 included)
-constexpr int32_t kBufferWord3 = 0x00020000;
 
 template <typename In>
 struct VecTraits;

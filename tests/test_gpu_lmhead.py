@@ -112,3 +112,40 @@ def test_lmhead_sample_bit_exact_on_gpu_logits(sampler, lm_inputs, oracle, synth
         assert int(res["token"][r]) == t, (r, int(res["token"][r]), t, int(res["flags"][r]))
         # the scan's normaliser bound (3.9e-7 relative) plus binary64 roundings
         assert abs(res["probability"][r] - tr.probability) <= 4e-7 * tr.probability
+
+
+@pytest.mark.parametrize("vocab,width,m", [
+    (40004, 640, 96),    # K steps split unevenly over the waves; two 64-row blocks
+    (40004, 1152, 5),    # a partial row block; V ends inside a 16-row tile
+    (40004, 2048, 1),
+    (40004, 2112, 70),   # wider than 2048: the staged-H kernel
+    (40002, 1152, 64),   # V not a multiple of 4: the staged-H kernel
+])
+def test_lmhead_shapes_match_f64(vocab, width, m):
+    """Widths, row counts and vocabulary sizes off the 64 x 2048 x 262144 shape,
+    on both lm_head kernels: every column near V's end and 3000 others against
+    a float64 GEMM; rows past m stay untouched."""
+    import torch
+
+    gs = _gs()
+    s = gs.Sampler(vocab_size=vocab, max_rows=128)
+    try:
+        dev = torch.device("cuda", 0)
+        hidden, weight = gs.workloads.lmhead_inputs(m, width, vocab, device=dev)
+        cols = np.random.default_rng(width + m).choice(vocab, 3000, replace=False)
+        cols = np.unique(np.concatenate([cols, np.arange(vocab - 40, vocab), np.arange(0, 40)]))
+        h = _f64(hidden)
+        w = _f64(weight[torch.from_numpy(cols).to(dev)])
+        ref = h @ w.T
+        bound = GEMM_RTOL_OF_ABS_SUM * (np.abs(h) @ np.abs(w).T) + 1e-30
+        for cap in (0.0, 30.0):
+            out = torch.full((m + 3, vocab), 7.0, dtype=torch.float32, device=dev)
+            s.lmhead(hidden, weight, softcap_value=cap, out=out)
+            got = out[:m].cpu().numpy()[:, cols].astype(np.float64)
+            exp = cap * np.tanh(ref / cap) if cap > 0 else ref
+            err_bound = bound + (4 * np.spacing(np.abs(exp).astype(np.float32)).astype(np.float64) if cap > 0 else 0)
+            err = np.abs(got - exp)
+            assert np.all(err <= err_bound), (cap, float((err / err_bound).max()))
+            assert bool((out[m:] == 7.0).all())
+    finally:
+        s.close()

@@ -3,10 +3,11 @@ the chunk statistics that the scan would compute from the logits
 (src/webgpu/decode-model.ts:127-150 is the handoff it removes,
 src/webgpu/decode-lm-head.ts:262-340 the producer).
 
-* the logits it writes equal gs_lmhead's bit for bit (same tiles, same K
-  order, same softcap);
-* every row's token equals the unfused pipeline's (gs_lmhead, then gs_sample
-  over the same logits) over a batch mixing every route: greedy, top-k,
+* the logits it writes agree with a float64 GEMM of the same bf16 inputs
+  within the fp32-accumulation bound (its K order differs from gs_lmhead's
+  resident kernel, so the two are not bit-identical);
+* every row's token equals the unfused pipeline's (gs_sample over the logits
+  the fused call wrote) over a batch mixing every route: greedy, top-k,
   top-p, min-p, typical-p, constrained rows with and without an accepting
   state (forced termination ids), penalties, a forced exact replay, a
   full-vocabulary draw and a row of NaN logits, at 96 rows (a partial second
@@ -38,7 +39,7 @@ def weight_and_hidden():
     return hidden.to("cuda"), weight
 
 
-def test_fused_logits_equal_lmhead(sampler, weight_and_hidden):
+def test_fused_logits_match_f64(sampler, weight_and_hidden):
     import torch
 
     import gsample as gs
@@ -47,11 +48,24 @@ def test_fused_logits_equal_lmhead(sampler, weight_and_hidden):
     h = hidden[:m].contiguous()
     cfg = gs.DecodingConfig(temperature=1.0, topK=40, topP=0.95, repetitionWindow=0)
     conf = np.stack([gs.runtime.row_config(cfg, seed=r) for r in range(m)])
+    cols = np.random.default_rng(9).choice(V, 2000, replace=False)
+    cols = np.concatenate([cols, [0, 1, 255, 256, 8191, 8192, V - 1]])
+    hf = h.to(torch.float32).cpu().numpy().astype(np.float64)
+    wf = weight[cols].to(torch.float32).cpu().numpy().astype(np.float64)
+    ref = hf @ wf.T
+    # fp32 accumulation of D products: |err| <= c sqrt(D) 2^-24 sum|h w|
+    bound = 2e-5 * (np.abs(hf) @ np.abs(wf).T) + 1e-30
     for cap in (30.0, 0.0):
-        ref = sampler.lmhead(h, weight, softcap_value=cap)
         scratch = torch.full((m, V), 5.0, dtype=torch.float32, device=hidden.device)
         sampler.lmhead_sample(h, weight, cap, scratch, conf, fused=True)
-        assert torch.equal(scratch, ref), cap
+        got = scratch[:, cols].cpu().numpy().astype(np.float64)
+        if cap > 0:
+            exp = cap * np.tanh(ref / cap)
+            err_bound = bound + 4 * np.spacing(np.abs(exp).astype(np.float32)).astype(np.float64)
+        else:
+            exp, err_bound = ref, bound
+        err = np.abs(got - exp)
+        assert np.all(err <= err_bound), (cap, float((err / err_bound).max()))
 
 
 def _mixed_batch(gs, rows, states, finals):
@@ -101,14 +115,13 @@ def test_fused_matches_unfused_and_oracle(sampler, weight_and_hidden, oracle, sy
     conf, meta = _mixed_batch(gs, rows, states, finals)
     forced = gs.constraint.forced_ids_csr(rows, EOS)
 
-    ref_logits = sampler.lmhead(h, weight, softcap_value=30.0)
-    unfused = sampler.sample(ref_logits, conf, histories=hist, forced=forced, mask_table=table,
-                             raise_on_failure=False)
     scratch = torch.empty((rows, V), dtype=torch.float32, device=hidden.device)
     fused = sampler.lmhead_sample(h, weight, 30.0, scratch, conf, histories=hist, forced=forced, mask_table=table,
                                   fused=True)
-    # bit patterns: row 50's NaNs compare unequal as values
-    assert torch.equal(scratch.view(torch.int32), ref_logits.view(torch.int32))
+    assert bool(torch.isnan(scratch[50]).all())
+    # the unfused sampler over the logits the fused call wrote
+    unfused = sampler.sample(scratch.clone(), conf, histories=hist, forced=forced, mask_table=table,
+                             raise_on_failure=False)
     for r in range(rows):
         name = meta[r][0]
         assert int(fused.tokens[r]) == int(unfused.tokens[r]), (r, name, int(fused.tokens[r]),
