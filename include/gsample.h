@@ -133,8 +133,8 @@ typedef struct gs_batch {
  * per-256-id partials into the scan's chunk records -- instead of the head and
  * the scan). Results equal the unfused path's tokens; probabilities agree
  * within the normaliser bound. Without the hint the head and the scan run
- * separately, which is faster at 64 x 2048 x 262144 on MI355X (279 against
- * 305 us for the head and the streaming stage). */
+ * separately, which is faster at 64 x 2048 x 262144 on MI355X (220 against
+ * 306 us for the head and the streaming stage). */
 #define GS_BATCH_FUSED_HEAD 2
 
 /* Library / device identity. */
@@ -331,7 +331,7 @@ int gs_check_exp2(gs_context* ctx, float lo, float hi, double* max_rel_err, floa
  * those events, writes per stage the summed milliseconds
  * (stage_ms[GS_STAGE_COUNT]) and the number of calls that ran that stage
  * (calls[GS_STAGE_COUNT]), and stops timing. */
-#define GS_STAGE_LMHEAD 0 /* lmhead_kernel or qat_lmhead_kernel */
+#define GS_STAGE_LMHEAD 0 /* the lm_head kernel (bf16 or int2 QAT) */
 #define GS_STAGE_SCAN 1   /* scan_kernel: the one HBM pass over the logits */
 #define GS_STAGE_FINISH 2 /* finish_kernel: per-row merge, filters and draw */
 #define GS_STAGE_EXACT 3  /* exact_kernel: replay of rows beyond the context's exact slots */
