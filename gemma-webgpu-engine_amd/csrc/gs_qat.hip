@@ -157,6 +157,8 @@ constexpr int kQatMaxSteps = 2048 / 64;
 constexpr int kQatTileWaves = kQatThreads / 64;
 constexpr int kQatTilesPerWave = 4;  // 16-row vocabulary tiles per wave, two in flight
 constexpr int kQatF64Blocks = 256;   // workgroups of the binary64 fallback in a tile's launch
+constexpr int32_t kQatNT = 2;        // non-temporal cache policy of the code stream
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 // Rows 2 tile and 2 tile + 1 of x, one launch. Workgroups below n_int take
 // the exact integer path: each first checks the two rows and writes their
@@ -176,25 +178,68 @@ __global__ __launch_bounds__(kQatThreads, 4) void qat_tile_kernel(QatArgs a, int
   const int tid = threadIdx.x;
   const int D = a.D, words = D / 16, quads = D / 256;
   const int m0 = 2 * tile;
-  if (tid < 2) { R.emin[tid] = 0x7FFFFFFF; R.bad[tid] = 0; R.sabs[tid] = 0; R.ssum[tid] = 0; }
-  __syncthreads();
+  const int lane = tid & 63, wave = tid >> 6, j = lane & 15, g = lane >> 4;
+  const int n_tiles = a.V / 16;
+  const int stride = n_int * kQatTileWaves;
+  const bool int_wg = (int)blockIdx.x < n_int;
+  const int rows_here = a.M - m0 < 2 ? a.M - m0 : 2;
+  // Every global access below is a buffer access with no branch around it:
+  // codes of tiles past the last or of quads past the width, loads of the
+  // binary64 workgroups, activations past the rows and logits a lane does not
+  // own take an out-of-range offset (zeros, no memory request; stores
+  // dropped). Loads and stores share one in-order wait counter, and a branch
+  // around either made the compiler wait for every access in flight.
+  const __amdgpu_buffer_rsrc_t cr =
+      __builtin_amdgcn_make_buffer_rsrc((void*)a.words, (short)0, a.V * words * 4, kBufferWord3);
+  const __amdgpu_buffer_rsrc_t sr = __builtin_amdgcn_make_buffer_rsrc((void*)a.scales, (short)0, a.V * 4, kBufferWord3);
+  const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc((void*)(a.x + (int64_t)m0 * D), (short)0,
+                                                                      rows_here * D * 4, kBufferWord3);
+  const __amdgpu_buffer_rsrc_t orr = __builtin_amdgcn_make_buffer_rsrc((void*)(a.out + (int64_t)m0 * a.V), (short)0,
+                                                                       rows_here * a.V * 4, kBufferWord3);
+  // words 16 q + 4 g .. + 3 of vocabulary row n (block 4 q + g in block-major
+  // order) and the row's scale
+  auto load = [&](int vt, u32x4 (&cw)[kQatMaxSteps / 4], float& sc) __attribute__((always_inline)) {
+    const bool live = int_wg && vt < n_tiles;
+    const uint32_t n = (uint32_t)vt * 16u + (uint32_t)j;
+#pragma unroll
+    for (int q = 0; q < kQatMaxSteps / 4; ++q) {
+      const uint32_t off = a.block_major ? ((uint32_t)(4 * q + g) * (uint32_t)a.V + n) * 16u
+                                         : (n * (uint32_t)words + (uint32_t)(16 * q + 4 * g)) * 4u;
+      cw[q] = __builtin_amdgcn_raw_buffer_load_b128(cr, live && q < quads ? off : kBufferOutOfRange, 0, kQatNT);
+    }
+    sc = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(sr, live ? n * 4u : kBufferOutOfRange, 0, 0));
+  };
+
   // the check: this thread's word W of row rr (activations 16 W .. 16 W + 15)
   const int rr = tid / words, W = tid - rr * words;
   const bool mine = tid < 2 * words;
-  const bool live = mine && m0 + rr < a.M;
+  u32x4 xv[4];
+#pragma unroll
+  for (int v = 0; v < 4; ++v)
+    xv[v] = __builtin_amdgcn_raw_buffer_load_b128(xr, mine ? (uint32_t)((rr * D + 16 * W) * 4 + 16 * v) : kBufferOutOfRange,
+                                                  0, 0);
+  if (tid < 2) { R.emin[tid] = 0x7FFFFFFF; R.bad[tid] = 0; R.sabs[tid] = 0; R.ssum[tid] = 0; }
+  __syncthreads();
+  // activations of rows past M, and of threads past the words, read zeros
   float f[16];
 #pragma unroll
-  for (int e = 0; e < 16; ++e) f[e] = 0.0f;
-  if (live) {
-    const float4* xp = (const float4*)(a.x + (int64_t)(m0 + rr) * D + 16 * W);
+  for (int v = 0; v < 4; ++v) {
+    // the elements as scalars first: a bit cast of a vector element
+    // subscript reads element 0 here
+    const uint32_t xs[4] = {xv[v].x, xv[v].y, xv[v].z, xv[v].w};
 #pragma unroll
-    for (int v = 0; v < 4; ++v) {
-      const float4 x4 = xp[v];
-      const float xs[4] = {x4.x, x4.y, x4.z, x4.w};
-#pragma unroll
-      for (int e = 0; e < 4; ++e) f[4 * v + e] = (float)srq((double)xs[e], a.in_scale);
-    }
+    for (int e = 0; e < 4; ++e) f[4 * v + e] = (float)srq((double)__builtin_bit_cast(float, xs[e]), a.in_scale);
   }
+  // An integer workgroup's first codes load while the rest of the check runs.
+  // They go out once the activations are in: issued at the start, the whole
+  // grid's first tiles (24 MB at D 1536) queued ahead of the activations' own
+  // misses and tripled their latency.
+  __builtin_amdgcn_sched_barrier(0);
+  u32x4 b0[kQatMaxSteps / 4], b1[kQatMaxSteps / 4];
+  float s0, s1;
+  int vt = (int)blockIdx.x * kQatTileWaves + wave;
+  load(vt, b0, s0);
+  __builtin_amdgcn_sched_barrier(0);
   int gmin = 0x7FFFFFFF;
   bool bad = false;
 #pragma unroll
@@ -247,46 +292,38 @@ __global__ __launch_bounds__(kQatThreads, 4) void qat_tile_kernel(QatArgs a, int
   }
   if (!ok[0] && !ok[1]) return;
   // the limbs: tile row 8 rr + l, balanced base-256 digits of A (zeros for a
-  // row the check refused), at the operand positions of word W
+  // row the check refused), at the operand positions of word W. With
+  // K = sum_l 128 256^l (l < 7) and |A| < 2^52, u = A + K has the base-256
+  // digits c_l = d_l + 128 in [0, 255]; the int8 digit d_l = c_l - 128 is
+  // byte l of u ^ K (byte 7 is zero).
   if (mine) {
-    const int q = W >> 4, g = (W >> 2) & 3, tp = W & 3;
+    const int q = W >> 4, gw = (W >> 2) & 3, tp = W & 3;
     const int step = 4 * q + tp;
-    int64_t v[16];
+    constexpr uint64_t kK = 0x0080808080808080ull;
+    static_assert(kQatLimbs == 7, "K holds one 0x80 byte per limb");
+    uint32_t* op_words = (uint32_t*)&L.op[step][0];
+    // dword t of a limb's operand holds activations 4 i + t (byte i)
 #pragma unroll
-    for (int e = 0; e < 16; ++e) v[e] = ok[rr] ? A[e] : 0;
+    for (int t = 0; t < 4; ++t) {
+      uint32_t lo[4], hi[4];
 #pragma unroll
-    for (int l = 0; l < 8; ++l) {
-      uint32_t dw[4] = {0u, 0u, 0u, 0u};
-#pragma unroll
-      for (int e = 0; e < 16; ++e) {
-        int64_t d = 0;
-        if (l < kQatLimbs) {
-          d = ((v[e] + 128) & 255) - 128;
-          v[e] = (v[e] - d) >> 8;
-        }
-        // activation e = 4 i + t of the word: dword t, byte i
-        dw[e & 3] |= ((uint32_t)d & 0xFFu) << (8 * (e >> 2));
+      for (int i = 0; i < 4; ++i) {
+        const uint64_t u = ((uint64_t)(ok[rr] ? A[4 * i + t] : 0) + kK) ^ kK;
+        lo[i] = (uint32_t)u;
+        hi[i] = (uint32_t)(u >> 32);
       }
-      L.op[step][8 * rr + l + 16 * g] = i32x4{(int)dw[0], (int)dw[1], (int)dw[2], (int)dw[3]};
+#pragma unroll
+      for (int l = 0; l < 8; ++l) {
+        uint32_t dw = 0u;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) dw |= (((l < 4 ? lo[i] : hi[i]) >> (8 * (l & 3))) & 0xFFu) << (8 * i);
+        op_words[(8 * rr + l + 16 * gw) * 4 + t] = dw;
+      }
     }
   }
   __syncthreads();
 
-  const int lane = tid & 63, wave = tid >> 6, j = lane & 15, g = lane >> 4;
-  const int n_tiles = a.V / 16;
-  const int stride = n_int * kQatTileWaves;
-  const uint4* w4 = (const uint4*)a.words;
-  const int64_t row_words = words;
-  // words 16 q + 4 g .. + 3 of vocabulary row n (block 4 q + g in block-major order)
-  auto load = [&](int vt, uint4 (&cw)[kQatMaxSteps / 4]) __attribute__((always_inline)) {
-    const int64_t n = (int64_t)vt * 16 + j;
-#pragma unroll
-    for (int q = 0; q < kQatMaxSteps / 4; ++q) {
-      if (q < quads)
-        cw[q] = load_nt16(a.block_major ? w4 + (int64_t)(4 * q + g) * a.V + n : w4 + (n * row_words + 16 * q + 4 * g) / 4);
-    }
-  };
-  auto multiply = [&](int vt, const uint4 (&cw)[kQatMaxSteps / 4]) __attribute__((always_inline)) {
+  auto multiply = [&](int vt, const u32x4 (&cw)[kQatMaxSteps / 4], float sc) __attribute__((always_inline)) {
     i32x4 acc = {0, 0, 0, 0};
 #pragma unroll
     for (int q = 0; q < kQatMaxSteps / 4; ++q) {
@@ -309,24 +346,22 @@ __global__ __launch_bounds__(kQatThreads, 4) void qat_tile_kernel(QatArgs a, int
     for (int e = 0; e < 4; ++e) p += (uint64_t)(int64_t)acc[e] << (8 * (4 * (g & 1) + e));
     p += shfl_xor_u64(p, 16);
     const int r = g >> 1;
-    if ((g & 1) == 0 && ok[r]) {
-      const int64_t n = (int64_t)vt * 16 + j;
-      const int64_t T = (int64_t)(p - 2 * (uint64_t)R.ssum[r]);
-      const double dot = __builtin_ldexp((double)T, R.emin[r] != 0x7FFFFFFF ? R.emin[r] : 0);
-      a.out[(int64_t)(m0 + r) * a.V + n] = (float)srq(dot * (double)a.scales[n], a.out_scale);
-    }
+    const uint32_t n = (uint32_t)vt * 16u + (uint32_t)j;
+    const int64_t T = (int64_t)(p - 2 * (uint64_t)R.ssum[r]);
+    const double dot = __builtin_ldexp((double)T, R.emin[r] != 0x7FFFFFFF ? R.emin[r] : 0);
+    const float y = (float)srq(dot * (double)sc, a.out_scale);
+    const bool st = (g & 1) == 0 && ok[r] && vt < n_tiles;
+    __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, y), orr,
+                                          st ? ((uint32_t)r * (uint32_t)a.V + n) * 4u : kBufferOutOfRange, 0, 0);
   };
   // two register buffers with fixed roles: tile t multiplies from one while
-  // tile t + stride loads into the other
-  uint4 b0[kQatMaxSteps / 4], b1[kQatMaxSteps / 4];
-  int vt = (int)blockIdx.x * kQatTileWaves + wave;
-  if (vt < n_tiles) load(vt, b0);
+  // tile t + stride loads into the other (the first load went out at the
+  // top); tiles past the last read zeros and store nothing
   for (; vt < n_tiles; vt += 2 * stride) {
-    const int v1 = vt + stride, v2 = vt + 2 * stride;
-    if (v1 < n_tiles) load(v1, b1);
-    multiply(vt, b0);
-    if (v2 < n_tiles) load(v2, b0);
-    if (v1 < n_tiles) multiply(v1, b1);
+    load(vt + stride, b1, s1);
+    multiply(vt, b0, s0);
+    load(vt + 2 * stride, b0, s0);
+    multiply(vt + stride, b1, s1);
   }
 }
 
