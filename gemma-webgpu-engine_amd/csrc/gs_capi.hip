@@ -981,7 +981,7 @@ int gs_qat_lmhead(gs_context* ctx, const float* x, int32_t m_rows, int32_t width
   hipStream_t s = pick_stream(ctx, stream);
   const int32_t slot = timing_slot(ctx);
   launch_qat_lmhead(x, m_rows, width, packed_codes, layout == GS_QAT_BLOCK_MAJOR, row_scales, ctx->vocab, input_scale,
-                    output_scale, logits, s, stage_events(ctx, slot, GS_STAGE_LMHEAD));
+                    output_scale, logits, ctx->cu_count, s, stage_events(ctx, slot, GS_STAGE_LMHEAD));
   GS_HIP(ctx, hipGetLastError());
   return GS_OK;
 }

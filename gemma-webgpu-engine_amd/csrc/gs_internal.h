@@ -581,8 +581,8 @@ void launch_masks(const int64_t* offsets, const uint8_t* bytes, int32_t vocab, c
                   const int32_t* states, int32_t n, uint32_t* masks, int32_t mask_words, int32_t n_states,
                   hipStream_t s);
 void launch_qat_lmhead(const float* x, int32_t M, int32_t D, const uint32_t* words, int32_t block_major,
-                       const float* scales, int32_t V, double in_scale, double out_scale, float* out, hipStream_t s,
-                       LaunchEvents ev = {});
+                       const float* scales, int32_t V, double in_scale, double out_scale, float* out,
+                       int32_t cu_count, hipStream_t s, LaunchEvents ev = {});
 void launch_lmhead(const uint16_t* hidden, const uint16_t* weight, int32_t m, int32_t width, int32_t vocab,
                    float softcap, float* out, int32_t cu_count, hipStream_t s, LaunchEvents ev = {});
 // The fused path (vocab a multiple of kChunk): the excluded-id bitmaps, then

@@ -65,11 +65,11 @@ __device__ __forceinline__ double srq(double v, double s) {
 
 // The activations of kRows rows of x from m0 (those below M) into act,
 // after the input SRQ, in binary64 (the whole block calls it).
-template <int kRows>
+template <int kRows, int kThreads = kQatThreads>
 __device__ __forceinline__ void qat_stage_act(const QatArgs& a, int32_t m0, double* act) {
   const int D = a.D;
   const int rows = a.M - m0 < kRows ? a.M - m0 : kRows;
-  for (int i = threadIdx.x; i < kRows * D; i += kQatThreads) {
+  for (int i = threadIdx.x; i < kRows * D; i += kThreads) {
     const int m = i / D;
     act[i] = m < rows ? srq((double)a.x[(int64_t)(m0 + m) * D + (i - m * D)], a.in_scale) : 0.0;
   }
@@ -154,22 +154,23 @@ struct QatTileRows {
 };
 
 constexpr int kQatMaxSteps = 2048 / 64;
-constexpr int kQatTileWaves = kQatThreads / 64;
-constexpr int kQatTilesPerWave = 4;  // 16-row vocabulary tiles per wave, two in flight
-constexpr int kQatF64Blocks = 256;   // workgroups of the binary64 fallback in a tile's launch
+constexpr int kQatTileThreads = 1024;
+constexpr int kQatTileWaves = kQatTileThreads / 64;
 constexpr int32_t kQatNT = 2;        // non-temporal cache policy of the code stream
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
-// Rows 2 tile and 2 tile + 1 of x, one launch. Workgroups below n_int take
-// the exact integer path: each first checks the two rows and writes their
-// limbs into LDS as a 16-row operand tile (rows 8 r + limb, limb 7 zero; one
-// thread per code word of 16 activations), then its waves take 16-row
-// vocabulary tiles, the next tile's codes loading while the current one
-// multiplies. The kQatF64Blocks workgroups from n_int on take the rows the
-// check refused on the binary64 path (vocabulary rows 256 (b - n_int) + tid
-// + 256 kQatF64Blocks i), and return at once when there are none; placed
-// after the integer workgroups, they are dispatched as those finish.
-__global__ __launch_bounds__(kQatThreads, 4) void qat_tile_kernel(QatArgs a, int32_t tile, int32_t n_int) {
+// Rows 2 tile and 2 tile + 1 of x, one launch, one workgroup per compute unit
+// over a contiguous run of 16-row vocabulary tiles. Each workgroup checks the
+// two rows and writes their limbs into LDS as a 16-row operand tile (rows
+// 8 r + limb, limb 7 zero; one thread per code word of 16 activations); its
+// 16 waves then take the run's tiles in turn, the next tile's codes loading
+// while the current one multiplies. A row the check refused takes the
+// binary64 path over the same vocabulary rows afterwards. (Four 256-thread
+// workgroups per compute unit, each repeating the check and the limbs, took
+// 25.3 us instead of 24.4 at V 262144, D 1536; reducing the check's sums
+// through an LDS array by one wave per row instead of LDS atomics, 24.9 us
+// instead of 24.0.)
+__global__ __launch_bounds__(kQatTileThreads) void qat_tile_kernel(QatArgs a, int32_t tile) {
   __shared__ union __attribute__((aligned(16))) {
     i32x4 op[kQatMaxSteps][64];   // the integer path's operand tile
     double act[2 * 2048];         // the binary64 path's activations
@@ -180,13 +181,12 @@ __global__ __launch_bounds__(kQatThreads, 4) void qat_tile_kernel(QatArgs a, int
   const int m0 = 2 * tile;
   const int lane = tid & 63, wave = tid >> 6, j = lane & 15, g = lane >> 4;
   const int n_tiles = a.V / 16;
-  const int stride = n_int * kQatTileWaves;
-  const bool int_wg = (int)blockIdx.x < n_int;
+  const int t_lo = (int)((int64_t)blockIdx.x * n_tiles / gridDim.x);
+  const int t_hi = (int)((int64_t)(blockIdx.x + 1) * n_tiles / gridDim.x);
   const int rows_here = a.M - m0 < 2 ? a.M - m0 : 2;
   // Every global access below is a buffer access with no branch around it:
-  // codes of tiles past the last or of quads past the width, loads of the
-  // binary64 workgroups, activations past the rows and logits a lane does not
-  // own take an out-of-range offset (zeros, no memory request; stores
+  // codes of tiles past the run or of quads past the width, activations past
+  // the rows and logits a lane does not own take an out-of-range offset (zeros, no memory request; stores
   // dropped). Loads and stores share one in-order wait counter, and a branch
   // around either made the compiler wait for every access in flight.
   const __amdgpu_buffer_rsrc_t cr =
@@ -199,7 +199,7 @@ __global__ __launch_bounds__(kQatThreads, 4) void qat_tile_kernel(QatArgs a, int
   // words 16 q + 4 g .. + 3 of vocabulary row n (block 4 q + g in block-major
   // order) and the row's scale
   auto load = [&](int vt, u32x4 (&cw)[kQatMaxSteps / 4], float& sc) __attribute__((always_inline)) {
-    const bool live = int_wg && vt < n_tiles;
+    const bool live = vt < t_hi;
     const uint32_t n = (uint32_t)vt * 16u + (uint32_t)j;
 #pragma unroll
     for (int q = 0; q < kQatMaxSteps / 4; ++q) {
@@ -237,7 +237,7 @@ __global__ __launch_bounds__(kQatThreads, 4) void qat_tile_kernel(QatArgs a, int
   __builtin_amdgcn_sched_barrier(0);
   u32x4 b0[kQatMaxSteps / 4], b1[kQatMaxSteps / 4];
   float s0, s1;
-  int vt = (int)blockIdx.x * kQatTileWaves + wave;
+  int vt = t_lo + wave;
   load(vt, b0, s0);
   __builtin_amdgcn_sched_barrier(0);
   int gmin = 0x7FFFFFFF;
@@ -280,23 +280,13 @@ __global__ __launch_bounds__(kQatThreads, 4) void qat_tile_kernel(QatArgs a, int
 #pragma unroll
   for (int q = 0; q < 2; ++q) ok[q] = m0 + q < a.M && !R.bad[q] && R.sabs[q] < kQatSumBound;
 
-  if ((int)blockIdx.x >= n_int) {
-    // the binary64 path for the rows the check refused
-    const bool skip[2] = {ok[0], ok[1]};
-    if (skip[0] && (skip[1] || m0 + 1 >= a.M)) return;
-    qat_stage_act<2>(a, m0, L.act);
-    for (int64_t r = (int64_t)((int)blockIdx.x - n_int) * kQatThreads + tid; r < a.V;
-         r += (int64_t)kQatF64Blocks * kQatThreads)
-      qat_row_binary64<2>(a, m0, skip, L.act, r);
-    return;
-  }
-  if (!ok[0] && !ok[1]) return;
+  const bool any_ok = ok[0] || ok[1];
   // the limbs: tile row 8 rr + l, balanced base-256 digits of A (zeros for a
   // row the check refused), at the operand positions of word W. With
   // K = sum_l 128 256^l (l < 7) and |A| < 2^52, u = A + K has the base-256
   // digits c_l = d_l + 128 in [0, 255]; the int8 digit d_l = c_l - 128 is
   // byte l of u ^ K (byte 7 is zero).
-  if (mine) {
+  if (mine && any_ok) {
     const int q = W >> 4, gw = (W >> 2) & 3, tp = W & 3;
     const int step = 4 * q + tp;
     constexpr uint64_t kK = 0x0080808080808080ull;
@@ -350,18 +340,29 @@ __global__ __launch_bounds__(kQatThreads, 4) void qat_tile_kernel(QatArgs a, int
     const int64_t T = (int64_t)(p - 2 * (uint64_t)R.ssum[r]);
     const double dot = __builtin_ldexp((double)T, R.emin[r] != 0x7FFFFFFF ? R.emin[r] : 0);
     const float y = (float)srq(dot * (double)sc, a.out_scale);
-    const bool st = (g & 1) == 0 && ok[r] && vt < n_tiles;
+    const bool st = (g & 1) == 0 && ok[r] && vt < t_hi;
     __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, y), orr,
                                           st ? ((uint32_t)r * (uint32_t)a.V + n) * 4u : kBufferOutOfRange, 0, 0);
   };
   // two register buffers with fixed roles: tile t multiplies from one while
-  // tile t + stride loads into the other (the first load went out at the
-  // top); tiles past the last read zeros and store nothing
-  for (; vt < n_tiles; vt += 2 * stride) {
-    load(vt + stride, b1, s1);
-    multiply(vt, b0, s0);
-    load(vt + 2 * stride, b0, s0);
-    multiply(vt + stride, b1, s1);
+  // tile t + 16 loads into the other (the first load went out with the
+  // check); tiles past the run read zeros and store nothing
+  if (any_ok) {
+    for (; vt < t_hi; vt += 2 * kQatTileWaves) {
+      load(vt + kQatTileWaves, b1, s1);
+      multiply(vt, b0, s0);
+      load(vt + 2 * kQatTileWaves, b0, s0);
+      multiply(vt + kQatTileWaves, b1, s1);
+    }
+  }
+  // rows the check refused: the binary64 path over this run's vocabulary
+  // rows, the activations staged where the operand tile was
+  const bool skip[2] = {ok[0], ok[1]};
+  if (!(skip[0] && (skip[1] || m0 + 1 >= a.M))) {
+    __syncthreads();
+    qat_stage_act<2, kQatTileThreads>(a, m0, L.act);
+    for (int64_t r = (int64_t)t_lo * 16 + tid; r < (int64_t)t_hi * 16; r += kQatTileThreads)
+      qat_row_binary64<2>(a, m0, skip, L.act, r);
   }
 }
 
@@ -375,18 +376,16 @@ int qat_rows_per_pass(int32_t D) {
 
 
 void launch_qat_lmhead(const float* x, int32_t M, int32_t D, const uint32_t* words, int32_t block_major,
-                       const float* scales, int32_t V, double in_scale, double out_scale, float* out, hipStream_t s,
-                       LaunchEvents ev) {
+                       const float* scales, int32_t V, double in_scale, double out_scale, float* out,
+                       int32_t cu_count, hipStream_t s, LaunchEvents ev) {
   QatArgs a{x, words, scales, out, D, V, M, block_major, in_scale, out_scale};
   if (D % 256 == 0 && D <= 2048 && V % 16 == 0) {
-    // one launch per pair of rows: the integer workgroups, then the binary64 ones
+    // one launch per pair of rows, one workgroup per compute unit
     const int tiles = (M + 1) / 2;
-    const int n_vt = V / 16;
-    const int n_int = (n_vt + kQatTileWaves * kQatTilesPerWave - 1) / (kQatTileWaves * kQatTilesPerWave);
-    const int n_f64 = kQatF64Blocks;
-    for (int t = 0; t < tiles; ++t)
-      hipExtLaunchKernelGGL(qat_tile_kernel, dim3(n_int + n_f64), dim3(kQatThreads), 0, s, t == 0 ? ev.start : nullptr,
-                            t == tiles - 1 ? ev.stop : nullptr, 0, a, t, n_int);
+    for (int t = 0; t < tiles; ++t) {
+      hipExtLaunchKernelGGL(qat_tile_kernel, dim3(cu_count > 0 ? cu_count : 256), dim3(kQatTileThreads), 0, s,
+                            t == 0 ? ev.start : nullptr, t == tiles - 1 ? ev.stop : nullptr, 0, a, t);
+    }
     return;
   }
   const dim3 grid((unsigned)((V + kQatThreads - 1) / kQatThreads));
