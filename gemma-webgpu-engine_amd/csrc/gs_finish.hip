@@ -345,6 +345,29 @@ __device__ void top_r(const uint64_t* s, int n, uint64_t* tmp, uint64_t* top) {
   __syncthreads();
 }
 
+// hist[bin] += 1 for every lane of the wave with `take`; the whole wave is
+// active. When at least 8 such lanes share the first one's bin, they add
+// together in one LDS atomic and the others one each: tied keys put most of a
+// wave in one bin, and same-address LDS atomics from many lanes serialise
+// (a row on a 1/8 logit grid spent 14.6 us in one such histogram). Otherwise
+// every lane adds its own.
+__device__ __forceinline__ void hist_add(uint32_t* hist, uint32_t bin, bool take) {
+  const uint64_t m = __ballot(take);
+  if (!m) return;
+  const int lane = threadIdx.x & 63;
+  const int leader = __ffsll((unsigned long long)m) - 1;
+  const uint32_t lb = (uint32_t)__shfl((int)bin, leader, 64);
+  const bool same = take && bin == lb;
+  const uint64_t sm = __ballot(same);
+  if (__popcll(sm) < 8) {
+    if (take) atomicAdd(&hist[bin], 1u);
+  } else if (lane == leader) {
+    atomicAdd(&hist[lb], (uint32_t)__popcll(sm));
+  } else if (take && !same) {
+    atomicAdd(&hist[bin], 1u);
+  }
+}
+
 // The kTopR largest entries of s[0..n) into top[0..kTopR), descending and
 // zero-padded, found without sorting the region when possible. Keys lie in
 // [lo, hi]. A 256-bin histogram of (key - lo) >> shift finds the bin holding
@@ -1533,13 +1556,14 @@ __device__ __forceinline__ uint32_t finish_row(const SampleArgs& a, FinishLds& U
         for (int s0 = 0; s0 < n_subs; s0 += kFinishThreads / kSubThreads) {
           const int sl = s0 + tid / kSubThreads;
           const int cnt = sl < n_subs ? (int)S.c_nsub[GS_CK(sl, GS_LEN(S.c_nsub))] : 0;
+          // a trip count the whole wave shares (hist_add needs every lane)
 #pragma unroll 1
-          for (int k = k0; k < cnt; k += kSubThreads) {
-            const uint32_t key = entry_key(list_rank(lists[GS_CK((int64_t)sl * kSubCap + k, (int64_t)a.n_chunks * kGatherCap)]));
-            if (key >= thr) {
-              const uint32_t bin = (key - sel_lo) >> shift;
-              atomicAdd(&S.hist[GS_CK(bin < 255u ? bin : 255u, GS_LEN(S.hist))], 1u);
-            }
+          for (int k = k0; __ballot(k < cnt) != 0; k += kSubThreads) {
+            const uint32_t key =
+                k < cnt ? entry_key(list_rank(lists[GS_CK((int64_t)sl * kSubCap + k, (int64_t)a.n_chunks * kGatherCap)]))
+                        : 0u;
+            const uint32_t bin = (key - sel_lo) >> shift;
+            hist_add(S.hist, GS_CK(bin < 255u ? bin : 255u, GS_LEN(S.hist)), k < cnt && key >= thr);
           }
         }
         __syncthreads();
