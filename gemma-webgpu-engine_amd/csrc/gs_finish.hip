@@ -405,6 +405,10 @@ __device__ __forceinline__ uint32_t prefix_floor(const uint64_t* region, int n_n
   const bool by_mass = want_mass < __builtin_inf();
   if (!(by_rank || by_mass) || n_ns <= kPrefixMin) {
     if (tid == 0) *region_mass = __builtin_inf();
+    // every thread reads *region_mass after the call: without this barrier a
+    // wave could read the word before thread 0 writes it (whatever an earlier
+    // workgroup left there) and take another branch than thread 0's wave
+    __syncthreads();
     return 0;
   }
   const int shift = top_select_shift(sel_lo, sel_hi);
@@ -2880,6 +2884,7 @@ __device__ __noinline__ uint32_t deep_draw(const SampleArgs& a, FinishLds& U) {
   const gs_row_config cfg = a.configs[row];
   const double T = cfg.temperature;
   if (!deep_inputs_ok(S, T)) return kExactRequest | 0u;
+  if (S.deep_n > (uint32_t)kFinishCap) return kExactRequest | GS_FLAG_INDEX_CHECK;
   const int n_sp = (int)(S.n_special < (uint32_t)kSpecialCap ? S.n_special : (uint32_t)kSpecialCap);
   const double rT = 1.0 / T;
   const double vfc = (double)key_f32(S.deep_thr) / T * ((double)kDeepBins / kDeepSpan);
@@ -2921,6 +2926,9 @@ __device__ __noinline__ uint32_t deep_export(const SampleArgs& a, Shared& S) {
   const int64_t row = blockIdx.x;
   if (!deep_inputs_ok(S, a.configs[row].temperature)) return kExactRequest | 0u;
   DeepRow& D = a.deep_rows[row];
+  // the region count sizes the copy into the record: one past the record's
+  // capacity is never copied (block-uniform: read after the caller's barrier)
+  if (S.deep_n > (uint32_t)kFinishCap) return kExactRequest | GS_FLAG_INDEX_CHECK;
   const int n_reg = (int)S.deep_n;
   const int n_sp = (int)(S.n_special < (uint32_t)kSpecialCap ? S.n_special : (uint32_t)kSpecialCap);
   for (int i = tid; i < n_reg; i += kFinishThreads) { D.cand_p[GS_CK(i, GS_LEN(D.cand_p))] = S.cand_p[GS_CK(i, GS_LEN(S.cand_p))]; D.cand_id[GS_CK(i, GS_LEN(D.cand_id))] = S.cand_id[GS_CK(i, GS_LEN(S.cand_id))]; }
@@ -3025,6 +3033,12 @@ __device__ __forceinline__ uint32_t deep_take(Shared& S, uint32_t* next) {
   return item;
 }
 
+// The record's counts lie within its arrays (deep_export writes them so);
+// a record that says otherwise goes to the exact path, never into a copy.
+__device__ __forceinline__ bool deep_counts_ok(const DeepRow& D) {
+  return D.n_reg <= (uint32_t)kFinishCap && D.n_sp <= (uint32_t)kSpecialCap;
+}
+
 // The row's inputs back into LDS for deep_mid / deep_final (the whole block).
 __device__ __noinline__ void deep_import(const DeepRow& D, Shared& S, bool with_region) {
   const int tid = threadIdx.x;
@@ -3110,6 +3124,7 @@ __device__ __noinline__ uint32_t deep_mid_row(const SampleArgs& a, Shared& S, in
 #ifdef GS_CHECKED
   if (D.index_check) return kExactRequest | GS_FLAG_INDEX_CHECK;
 #endif
+  if (!deep_counts_ok(D)) return kExactRequest | GS_FLAG_INDEX_CHECK;
   GS_CHECK_RESET();
   deep_import(D, S, true);
   for (int b = tid; b < kDeepBins; b += kFinishThreads) S.sorted[GS_CK(b, GS_LEN(S.sorted))] = D.hist[GS_CK(b, GS_LEN(D.hist))];
@@ -3198,6 +3213,7 @@ __device__ __noinline__ uint32_t deep_final_row(const SampleArgs& a, Shared& S, 
 #ifdef GS_CHECKED
   if (D.index_check || D.index_check2) return kExactRequest | GS_FLAG_INDEX_CHECK;
 #endif
+  if (!deep_counts_ok(D)) return kExactRequest | GS_FLAG_INDEX_CHECK;
   GS_CHECK_RESET();
   deep_import(D, S, false);
   deep_setup(S, (int)D.n_sp, false);

@@ -154,6 +154,50 @@ def test_lone_row_deep_draws(sampler, oracle):
     assert deep > 0
 
 
+@pytest.mark.parametrize("Vs", [8269, 20000, 32768])
+def test_small_region_full_draws(oracle, Vs):
+    """Full-vocabulary draws on vocabularies of two to four chunks, whose
+    complete region (64 list entries per chunk) holds at most 256 entries:
+    the finish's prefix ranking returns early for them, and cursors past the
+    region go to the deep draw. Over many workgroups (the batch hint), on each
+    row's own (no hint) and as lone rows, penalty windows on some rows: the
+    oracle's ids every time."""
+    import torch
+
+    gs = _gs()
+    rng = np.random.default_rng(Vs)
+    n = 24
+    rows, cfgs, us, hists = [], [], [], []
+    for r in range(n):
+        x = rng.normal(0, [0.5, 1.0, 2.0][r % 3], Vs).astype(np.float32)
+        rows.append(x)
+        cfg = gs.DecodingConfig(temperature=[0.7, 1.0, 1.3][(r // 3) % 3], topK=0, topP=1.0, minP=0.0,
+                                typicalP=1.0, repetitionWindow=0)
+        hist = []
+        if r % 4 == 1:
+            hist = rng.integers(0, Vs, 8).tolist()
+            cfg = cfg.merged(repetitionPenalty=2.0, repetitionWindow=8)
+        cfgs.append(cfg)
+        hists.append(hist)
+        us.append(float(rng.uniform(0.3, 0.999)))
+    s = gs.Sampler(vocab_size=Vs, max_rows=n)
+    try:
+        conf = np.stack([gs.runtime.row_config(c, uniform=u) for c, u in zip(cfgs, us)])
+        x = torch.from_numpy(np.stack(rows)).cuda()
+        multi = s.sample(x, conf, histories=hists)
+        single = s.sample(x, conf, histories=hists, hints=0)
+        lone = [s.sample(x[r:r + 1], conf[r:r + 1], histories=[hists[r]]) for r in range(0, n, 5)]
+    finally:
+        s.close()
+    check(gs, oracle, f"V={Vs} multi", multi, rows, hists, cfgs, us)
+    check(gs, oracle, f"V={Vs} single", single, rows, hists, cfgs, us)
+    assert np.array_equal(multi.tokens, single.tokens)
+    for k, r in enumerate(range(0, n, 5)):
+        assert int(lone[k].tokens[0]) == int(multi.tokens[r]), (Vs, r)
+    # most rows are deep draws (one pass over the row), not exact replays
+    assert int(np.sum((multi.flags & gs.GS_FLAG_EXACT_PATH) == 0)) >= n // 2, multi.flags
+
+
 def test_topk_above_64(sampler, oracle):
     """topK 65 .. 2000 keep 64 entries per chunk; the finish ranks the
     complete region (block-wide) and cuts it at K."""

@@ -119,16 +119,14 @@ def _random_batch(seed, rows, V):
     return logits, hists, cfgs, us
 
 
-# (False, 8269, 2) faulted the GPU once inside a full-suite run, after it had
-# twice returned one wrong token for row 6 (a full-vocabulary draw: 774 for
-# 1237, flags 0), also only inside full-suite runs; alone, and under stress, it
-# never failed. Its cause is not found, so the case stays off the GPU.
-_FAULTED = "faulted the GPU once in a full-suite run; the cause is not found"
-
-
+# (False, 8269, 2) holds full-vocabulary draws (row 6 among them) whose cursor
+# lies past a region of under 256 entries: the finish's prefix ranking returns
+# early for them, and every thread reads the region mass it leaves in LDS only
+# after a barrier (without it a wave could read the word before it was written
+# and leave the workgroup's barriers out of step).
 @pytest.mark.parametrize("force_exact,V,seed", [
     (False, 3000, 1),
-    pytest.param(False, 8192 + 77, 2, marks=pytest.mark.skip(reason=_FAULTED)),
+    (False, 8192 + 77, 2),
     (False, 40000, 3),
     (True, 3000, 1),
     (True, 8192 + 77, 2),
