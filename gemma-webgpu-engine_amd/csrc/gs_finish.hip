@@ -69,6 +69,35 @@ __device__ __forceinline__ I gs_ck(I i, int64_t n) {
 #endif
 #define GS_LEN(x) ((int64_t)(sizeof(x) / sizeof((x)[0])))
 
+// The checked build also makes LDS races show. Much of this file is serial
+// work by thread 0 or wave 0 (set-up words, reductions, the one-wave filters)
+// whose results the other waves read after a barrier. A missing barrier there
+// lets a wave read the word before wave 0 writes it, which happens only when
+// wave 0 falls behind, and the read then sees whatever an earlier workgroup
+// left in LDS. Here every workgroup barrier below is followed by a sleep of
+// wave 0 (about 4000 cycles), so the other waves win such a race every time,
+// and every workgroup of these kernels starts from cleared LDS, so the word
+// they read is 0 every time. A missing barrier then changes the row's result
+// on every run instead of once in many, and the comparison with the normal
+// build shows it. Neither changes what a race-free kernel computes.
+#ifdef GS_CHECKED
+__device__ __forceinline__ void gs_checked_barrier() {
+  __syncthreads();
+  if (threadIdx.x < 64) __builtin_amdgcn_s_sleep(64);
+}
+__device__ __forceinline__ void gs_checked_clear(void* lds, size_t bytes) {
+  uint32_t* p = (uint32_t*)lds;
+  for (size_t i = threadIdx.x; i < bytes / 4; i += blockDim.x) p[i] = 0u;
+  __syncthreads();
+}
+#define __syncthreads() gs_checked_barrier()
+#define GS_CHECKED_CLEAR(u) gs_checked_clear(&(u), sizeof(u))
+#else
+#define GS_CHECKED_CLEAR(u) \
+  do {                      \
+  } while (0)
+#endif
+
 constexpr int kWaves = kFinishThreads / 64;
 constexpr int kTopR = 64;                             // entries the fast path ranks exactly
 constexpr int kSubThreads = 8;                        // threads that read one wave sub-list
@@ -3098,6 +3127,7 @@ __device__ __noinline__ void deep1_part(const SampleArgs& a, Shared& S, int64_t 
 
 __global__ __launch_bounds__(kFinishThreads) void deep1_kernel(SampleArgs) {
   __shared__ FinishLds U;
+  GS_CHECKED_CLEAR(U);
   Shared& S = U.fin;
   // the arguments read where the kernel received them (never copied to the stack)
   const SampleArgs& a = *(const SampleArgs*)__builtin_amdgcn_kernarg_segment_ptr();
@@ -3146,6 +3176,7 @@ __device__ __noinline__ uint32_t deep_mid_row(const SampleArgs& a, Shared& S, in
 
 __global__ __launch_bounds__(kFinishThreads) void deep_mid_kernel(SampleArgs) {
   __shared__ FinishLds U;
+  GS_CHECKED_CLEAR(U);
   Shared& S = U.fin;
   const SampleArgs& a = *(const SampleArgs*)__builtin_amdgcn_kernarg_segment_ptr();
   uint32_t cpp;
@@ -3189,6 +3220,7 @@ __device__ __noinline__ void deep2_part(const SampleArgs& a, int64_t row, int64_
 
 __global__ __launch_bounds__(kFinishThreads) void deep2_kernel(SampleArgs) {
   __shared__ FinishLds U;
+  GS_CHECKED_CLEAR(U);
   Shared& S = U.fin;
   const SampleArgs& a = *(const SampleArgs*)__builtin_amdgcn_kernarg_segment_ptr();
   uint32_t cpp;
@@ -3235,6 +3267,7 @@ __device__ __noinline__ uint32_t deep_final_row(const SampleArgs& a, Shared& S, 
 
 __global__ __launch_bounds__(kFinishThreads) void deep_final_kernel(SampleArgs) {
   __shared__ FinishLds U;
+  GS_CHECKED_CLEAR(U);
   Shared& S = U.fin;
   const SampleArgs& a = *(const SampleArgs*)__builtin_amdgcn_kernarg_segment_ptr();
   const uint32_t n_rows = a.deep_queue->count2;
@@ -3248,6 +3281,7 @@ __global__ __launch_bounds__(kFinishThreads) void deep_final_kernel(SampleArgs) 
 
 __global__ __launch_bounds__(kFinishThreads) void finish_kernel(SampleArgs a) {
   __shared__ FinishLds U;
+  GS_CHECKED_CLEAR(U);
   GS_CHECK_RESET();
   uint32_t r = finish_row(a, U);
 #ifdef GS_CHECKED

@@ -7,9 +7,15 @@ A child process loads the checked build (GSAMPLE_CHECKED=1; this process
 already holds the normal one) and samples the batches that exercise the
 finish's routes: the penalties batch (top-k / top-p, greedy, forced exact
 rows), full-vocabulary draws taken by the deep kernels, top-k past 64,
-typical-p, the constrained batch and heavy-tailed bf16 rows. No row may carry
-the flag, and every token, probability and flag must equal the normal
-build's on the same inputs."""
+typical-p, the constrained batch, heavy-tailed bf16 rows and full-vocabulary
+draws past small regions. No row may carry the flag, and every token,
+probability and flag must equal the normal build's on the same inputs.
+
+The checked build also delays wave 0 after every barrier of the finish and
+deep kernels and clears their LDS at each workgroup's start, so a read that
+races a write by wave 0 sees the cleared word on every run: such a race
+changes results here deterministically, where the normal build shows it
+once in many runs."""
 import json
 import os
 import subprocess
@@ -55,6 +61,18 @@ run("constrained", torch.from_numpy(w.logits).cuda(), conf, mask_table=table)
 w = W.heavy_tail(n_rows=512)
 conf = np.stack([gs.runtime.row_config(c, seed=sd) for c, sd in zip(w.configs, w.seeds)])
 run("heavy_tail", torch.from_numpy(w.logits.view(np.int16)).cuda().view(torch.bfloat16), conf)
+s.close()
+# full-vocabulary draws past regions of at most 128 entries (two chunks)
+rng = np.random.default_rng(5)
+Vs, n = 8269, 48
+s = gs.Sampler(vocab_size=Vs, max_rows=n)
+x = torch.from_numpy(rng.normal(0, 1.0, (n, Vs)).astype(np.float32)).cuda()
+cfg = gs.DecodingConfig(temperature=1.0, topK=0, topP=1.0, minP=0.0, typicalP=1.0, repetitionPenalty=2.0,
+                        repetitionWindow=8)
+hist = [rng.integers(0, Vs, 8).tolist() for _ in range(n)]
+conf = np.stack([gs.runtime.row_config(cfg, uniform=float(u)) for u in rng.uniform(0.3, 0.99, n)])
+run("small_region_multi", x, conf, histories=hist)
+run("small_region_single", x, conf, histories=hist, hints=0)
 s.close()
 with open(sys.argv[3], "w") as f:
     json.dump(out, f)
