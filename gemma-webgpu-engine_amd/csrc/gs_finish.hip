@@ -902,6 +902,15 @@ __device__ __forceinline__ int filters_and_draw_wave(const SampleArgs& a, int64_
   // (sorted by probability desc, stable: the list's own order)
   if (cfg.typical_p < 1) {
     if (!n_complete) return 1;
+    // The reference's pool is its list's first min(topK, V) entries
+    // (sampling.ts:44). A row with fewer candidates (finite values: the rest
+    // are -inf ids, masked or not) fills the pool with entries of probability
+    // 0, whose p ln p turns the entropy NaN (sampling.ts:50), unless min-p
+    // dropped them; the exact replay follows that arithmetic.
+    if (complete && !(cfg.min_p > 0) && cfg.top_k > n_avail && a.vocab > n_avail) {
+      *exact_flags = 0u;
+      return 3;
+    }
     double t = 0.0;
 #pragma unroll
     for (int q = 0; q < kPerLane; ++q) t += kept[q] ? pl[q] * gsm::js_log(pl[q]) : 0.0;

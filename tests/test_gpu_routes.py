@@ -198,6 +198,49 @@ def test_small_region_full_draws(oracle, Vs):
     assert int(np.sum((multi.flags & gs.GS_FLAG_EXACT_PATH) == 0)) >= n // 2, multi.flags
 
 
+@pytest.mark.parametrize("Vs", [3000, 40000])
+def test_typical_p_pool_past_finite_logits(oracle, Vs):
+    """typical-p with top-k on rows holding fewer finite logits than topK (a
+    mask with few legal ids, or mostly -inf logits): the reference's pool is
+    still the first topK entries of its list, so entries of probability 0
+    join it and their p ln p turns the entropy NaN (sampling.ts:44,49-55),
+    which leaves the pool in list order for the typicalP cut. With min-p those
+    entries leave the pool first. The oracle's ids (the same as V8's) on every
+    row, constrained and not."""
+    import torch
+
+    gs = _gs()
+    rng = np.random.default_rng(Vs + 1)
+    n_legal = [1, 4, 33, 63, 64, 200]
+    words = np.zeros((len(n_legal), (Vs + 31) // 32), np.uint32)
+    legal_sets = []
+    for k, m in enumerate(n_legal):
+        legal = np.sort(rng.choice(Vs, m, replace=False)).astype(np.int32)
+        np.bitwise_or.at(words[k], legal >> 5, np.left_shift(np.uint32(1), (legal & 31).astype(np.uint32)))
+        legal_sets.append(legal)
+    rows, cfgs, us, slots, vals = [], [], [], [], []
+    for r in range(36):
+        x = rng.normal(0, [0.5, 2.0, 4.0][r % 3], Vs).astype(np.float32)
+        slot = r % 7 - 1  # -1: unconstrained
+        if slot < 0 and r % 2:
+            x[rng.random(Vs) < 0.99] = -np.inf  # about 30 (V 3000) or 400 finite logits
+        rows.append(x)
+        slots.append(slot)
+        vals.append(oracle.mask_logits(x, legal_sets[slot], []) if slot >= 0 else x)
+        cfgs.append(gs.DecodingConfig(temperature=[0.7, 1.0, 1.5][r % 3], topK=[64, 40, 5, 64][r % 4],
+                                      typicalP=[0.3, 0.9, 0.6][(r // 3) % 3], topP=[1.0, 0.95][r % 2],
+                                      minP=0.05 if r % 5 == 4 else 0.0, repetitionWindow=0))
+        us.append(float(rng.random()))
+    s = gs.Sampler(vocab_size=Vs, max_rows=64)
+    try:
+        conf = np.stack([gs.runtime.row_config(c, uniform=u, mask_slot=m) for c, u, m in zip(cfgs, us, slots)])
+        table = torch.from_numpy(words.view(np.int32)).cuda()
+        out = s.sample(torch.from_numpy(np.stack(rows)).cuda(), conf, mask_table=table)
+    finally:
+        s.close()
+    check(gs, oracle, f"typical past finite V={Vs}", out, vals, None, cfgs, us)
+
+
 def test_topk_above_64(sampler, oracle):
     """topK 65 .. 2000 keep 64 entries per chunk; the finish ranks the
     complete region (block-wide) and cuts it at K."""
