@@ -3,11 +3,13 @@
 bf16 logits, the softcap, quantised logits (exact ties), mostly -inf rows, a
 few huge logits, penalty windows with out-of-range ids, every filter
 (top-k, min-p, typical-p, top-p, full-vocabulary draws, greedy), uniforms at
-0 and near 1, and mask tables of one to three slots with 0.1% to 50% legal
-ids. Each batch runs with the batch hint (deep draws over many workgroups)
-and without it; every row's id must be the oracle's (sampling.ts:18-65,
-constraints.ts:159-173), with probabilities as in the other parity tests.
-A wider run of the same generator (tens of thousands of batches) found the
+0 and near 1 or seeded draws at a draw index, forced exact replays, and mask
+tables of one to three slots with 0.1% to 50% legal ids, with termination and
+extra ids on some (gemma-session.ts:1305-1329, dead ends included). Each batch
+runs with the batch hint (deep draws over many workgroups) and without it;
+every row's id must be the oracle's (sampling.ts:18-65,
+constraints.ts:159-173), with probabilities as in the other parity tests. A
+wider run of the same generator (tens of thousands of batches) found the
 typical-p pool that reaches past a row's finite logits."""
 import math
 
@@ -64,7 +66,8 @@ def _batch(gs, oracle, seed):
         bits = W.to_bf16_bits(X)
         X = W.bf16_bits_to_f32(bits).reshape(R, V)
     vals = [oracle.softcap(X[r], cap) if cap > 0 else X[r] for r in range(R)]
-    words, slots = None, [-1] * R
+    words, slots, forced = None, [-1] * R, None
+    accepting, dead = [False] * R, [False] * R
     if rng.random() < 0.3:
         n_slots = int(rng.integers(1, 4))
         words = np.zeros((n_slots, (V + 31) // 32), np.uint32)
@@ -76,9 +79,46 @@ def _batch(gs, oracle, seed):
             np.bitwise_or.at(words[k], legal >> 5, np.left_shift(np.uint32(1), (legal & 31).astype(np.uint32)))
             legal_sets.append(legal.astype(np.int32))
         slots = [int(rng.integers(-1, n_slots)) for _ in range(R)]
-        vals = [oracle.mask_logits(vals[r], legal_sets[slots[r]], []) if slots[r] >= 0 else vals[r]
-                for r in range(R)]
-    return V, R, X, bits, cap, vals, hists, cfgs, us, words, slots
+        if rng.random() < 0.5:
+            # forced ids (gemma-session.ts:1305-1329): termination ids, legal only when the
+            # constraint is accepting, and extra legal ids, some of them termination ids too
+            f_ids, f_kinds, f_off = [], [], [0]
+            for r in range(R):
+                if slots[r] >= 0:
+                    term = rng.integers(0, V, int(rng.integers(0, 4))).tolist()
+                    extra = rng.integers(0, V, int(rng.integers(0, 5))).tolist()
+                    if term and rng.random() < 0.3:
+                        extra.append(term[0])
+                    if rng.random() < 0.3:
+                        term.append(int(legal_sets[slots[r]][0]))
+                    accepting[r] = bool(rng.random() < 0.5)
+                    f_ids += term + extra
+                    f_kinds += [gs.runtime.GS_FORCED_TERMINATION] * len(term) + [gs.runtime.GS_FORCED_EXTRA] * len(extra)
+                    tset = set(term)
+                    legal = [t for t in set(legal_sets[slots[r]].tolist()) | set(extra) if t not in tset]
+                    lterm = sorted(tset) if accepting[r] else []
+                    dead[r] = not legal and not lterm
+                    vals[r] = oracle.mask_logits(vals[r], legal, lterm)
+                f_off.append(len(f_ids))
+            forced = (np.asarray(f_off, np.int64), np.asarray(f_ids or [0], np.int32),
+                      np.asarray(f_kinds or [0], np.uint8))
+        else:
+            vals = [oracle.mask_logits(vals[r], legal_sets[slots[r]], []) if slots[r] >= 0 else vals[r]
+                    for r in range(R)]
+    # seeded draws (SeededRandom(seed) at a draw index) on some rows, forced exact replays on a few
+    seeded = [rng.random() < 0.3 for _ in range(R)]
+    seeds = [int(rng.integers(0, 2 ** 32)) for _ in range(R)]
+    didx = [int(rng.integers(0, 50)) for _ in range(R)]
+    fexact = [rng.random() < 0.05 for _ in range(R)]
+    confs = []
+    for r in range(R):
+        if seeded[r]:
+            us[r] = float(oracle.draw(seeds[r], didx[r]))
+        confs.append(gs.runtime.row_config(cfgs[r], uniform=None if seeded[r] else us[r],
+                                           seed=seeds[r] if seeded[r] else None, draw_index=didx[r] if seeded[r] else 0,
+                                           softcap_value=cap, mask_slot=slots[r], accepting=accepting[r],
+                                           force_exact=fexact[r]))
+    return V, R, X, bits, vals, hists, cfgs, us, words, forced, dead, np.stack(confs)
 
 
 def _ocfg(c):
@@ -97,19 +137,24 @@ def test_random_sweep_matches_oracle(oracle):
     n_rows = 0
     try:
         for seed in range(300):
-            V, R, X, bits, cap, vals, hists, cfgs, us, words, slots = _batch(gs, oracle, 900000 + seed)
+            V, R, X, bits, vals, hists, cfgs, us, words, forced, dead, conf = _batch(gs, oracle, 900000 + seed)
             if V not in samplers:
                 samplers[V] = gs.Sampler(vocab_size=V, max_rows=64)
             s = samplers[V]
             dev = (torch.from_numpy(bits.view(np.int16)).cuda().view(torch.bfloat16) if bits is not None
                    else torch.from_numpy(X).cuda())
             table = torch.from_numpy(words.view(np.int32)).cuda() if words is not None else None
-            conf = np.stack([gs.runtime.row_config(c, uniform=u, softcap_value=cap, mask_slot=m)
-                             for c, u, m in zip(cfgs, us, slots)])
-            outs = {"hint": s.sample(dev, conf, histories=hists, mask_table=table, raise_on_failure=False),
-                    "no hint": s.sample(dev, conf, histories=hists, mask_table=table, raise_on_failure=False,
-                                        hints=0)}
+            outs = {"hint": s.sample(dev, conf, histories=hists, forced=forced, mask_table=table,
+                                     raise_on_failure=False),
+                    "no hint": s.sample(dev, conf, histories=hists, forced=forced, mask_table=table,
+                                        raise_on_failure=False, hints=0)}
             for r in range(R):
+                if dead[r]:
+                    # no legal id and no legal termination id: the reference throws
+                    for tag, out in outs.items():
+                        if not int(out.flags[r]) & gs.GS_FLAG_DEAD_END:
+                            bad.append(f"seed {900000 + seed} row {r} {tag}: flags {int(out.flags[r])}, no dead end")
+                    continue
                 t, tr = oracle.sample_token(vals[r], hists[r], _ocfg(cfgs[r]), us[r])
                 p = tr.probability if t >= 0 else 0.0
                 for tag, out in outs.items():
@@ -124,7 +169,7 @@ def test_random_sweep_matches_oracle(oracle):
                             else:
                                 ok = abs(pr - p) <= PROB_RTOL * abs(p)
                     if not ok:
-                        bad.append(f"seed {900000 + seed} V {V} row {r} slot {slots[r]} {tag}: {tok} (flags {fl}, "
+                        bad.append(f"seed {900000 + seed} V {V} row {r} slot {int(conf[r]['mask_slot'])} {tag}: {tok} (flags {fl}, "
                                    f"p {pr}) != {t} (p {p}); {cfgs[r]} u {us[r]}")
             n_rows += R
     finally:
