@@ -172,18 +172,20 @@ __device__ __forceinline__ uint64_t to_units(double x, double inv_scale) {
   return (uint64_t)__builtin_rint(x * inv_scale * kUnitScale);
 }
 
-// Block-wide sums of two binary64 values in every thread, in a fixed order
-// (per wave, then the waves in order); s_w holds 2 * kWaves values and is
+// Block-wide sums, in every thread, of one binary64 value per thread in a
+// fixed order (per wave, then the waves in order) and of one 64-bit integer
+// per thread (the same sum in any order); s_w holds 2 * kWaves words and is
 // used once per kernel, so no barrier follows the reads.
-__device__ __forceinline__ void block_sum2_f64(double x, double y, double* s_w, double* tx, double* ty) {
+__device__ __forceinline__ void block_sum_f64_u64(double x, uint64_t y, double* s_w, double* tx, uint64_t* ty) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  uint64_t* s_u = (uint64_t*)(s_w + kWaves);
   x = wave_sum_f64_dpp(x);
-  y = wave_sum_f64_dpp(y);
-  if (lane == 0) { s_w[wave] = x; s_w[kWaves + wave] = y; }
+  y = wave_sum_u64(y);
+  if (lane == 0) { s_w[wave] = x; s_u[wave] = y; }
   __syncthreads();
-  // lane l < kWaves holds wave l's totals; the same DPP reduction then sums them
+  // lane l < kWaves holds wave l's totals; the same reductions then sum them
   *tx = wave_sum_f64_dpp(lane < kWaves ? s_w[lane] : 0.0);
-  *ty = wave_sum_f64_dpp(lane < kWaves ? s_w[kWaves + lane] : 0.0);
+  *ty = wave_sum_u64(lane < kWaves ? s_u[lane] : 0ull);
 }
 
 // (value key desc, id asc) on parallel arrays
@@ -1167,8 +1169,8 @@ __device__ __forceinline__ void visit_row(const SampleArgs& a, int64_t row, doub
 // allowed special ids, which the normaliser counts with their penalised
 // values instead. Identical terms cancel exactly, so the difference keeps the
 // sum's accuracy while the specials hold at most half of it; otherwise, or
-// when a sum overflows, it returns -1. tab: the exponential's table in LDS.
-// The whole block calls it.
+// when a sum overflows, it returns -1. s_w: 2 kWaves words of LDS scratch;
+// tab: the exponential's table in LDS. The whole block calls it.
 __device__ double recompute_nonspecial_sum(const SampleArgs& a, int64_t row, const gs_row_config& cfg,
                                            bool constrained, double M, int n_sp, const uint32_t* sp_id,
                                            double* s_w, const double* tab) {
@@ -1190,7 +1192,7 @@ __device__ double recompute_nonspecial_sum(const SampleArgs& a, int64_t row, con
     if (cfg.softcap > 0) l = softcap_call(l, cfg.softcap);
     return term_of_capped(l);
   };
-  double all = 0.0, sp = 0.0;
+  double all = 0.0;
   const int64_t V = a.vocab;
   if (mrow) {
     // constrained rows: only legal ids contribute (masked logits are -inf).
@@ -1231,15 +1233,26 @@ __device__ double recompute_nonspecial_sum(const SampleArgs& a, int64_t row, con
   // unconstrained rows: every id, four 16-byte loads per thread in flight
   // (visit_row); the sum keeps each thread's order
   if (!mrow) visit_row<4>(a, row, cfg.softcap, [&](float l, uint32_t) { all += term_of_capped(l); });
+  double t_all;
+  block_scan_f64(all, s_w, &t_all);
+  if (!(t_all < __builtin_inf() && t_all > 0.0)) return -1.0;
+  // the specials' terms in units of 2^-50 t_all, summed as integers: the
+  // specials sit in an order that atomics chose, so a binary64 sum could
+  // differ in its last bits from run to run (at most 2048 2^-51 t_all off);
+  // a term above t_all / 2 is counted apart
+  const double inv = 1.0 / t_all;
+  uint64_t su = 0ull, big = 0ull;
   for (int i = tid; i < n_sp; i += kFinishThreads) {
     const uint32_t id = sp_id[i];
     if (mrow && !((mrow[id >> 5] >> (id & 31)) & 1u)) continue;
-    sp += term(load_logit(a, row, id));
+    const double t = term(load_logit(a, row, id));
+    if (t <= 0.5 * t_all) su += to_units(t, inv);
+    else big = 1ull;
   }
-  double t_all, t_sp;
-  block_scan_f64(all, s_w, &t_all);
-  block_scan_f64(sp, s_w, &t_sp);
-  return (t_all < __builtin_inf() && t_sp <= 0.5 * t_all) ? t_all - t_sp : -1.0;
+  uint64_t su_all, big_all;
+  block_sum2_u64(su, big, (uint64_t*)s_w, &su_all, &big_all);
+  const double t_sp = (double)su_all / kUnitScale * t_all;
+  return (big_all == 0ull && t_sp <= 0.5 * t_all) ? t_all - t_sp : -1.0;
 }
 
 constexpr int kCountRank = 512;    // candidates the bin walk ranks by counting
@@ -1805,13 +1818,20 @@ __device__ __forceinline__ uint32_t finish_row(const SampleArgs& a, FinishLds& U
   // ---- normaliser: the scan's per-wave partial sums rescaled from their wave
   // maximum to M (the rescale argument computed as the reference computes
   // l/T - M for that logit), plus every special (threads from the top down,
-  // so that they are not the ones holding wave sums)
+  // so that they are not the ones holding wave sums). The specials sit in
+  // LDS in an order that atomics chose, so their terms (each at most 1: M is
+  // at least every special's value) are summed as integers in units of
+  // 2^-50 (at most 2048 2^-51 < 1e-12 off, against a normaliser of at least
+  // 1): every run of a row gets the same normaliser, bit for bit.
   double t_chunks, t_sp;
   {
-    double part = 0.0, spart = 0.0;
+    double part = 0.0;
+    uint64_t spart = 0ull;
     if (has_w && w_sum > 0.0 && w_max > kKeyNegInf) part = w_sum * gsm::js_exp((double)key_f32(w_max) / T - M);
-    for (int i = kFinishThreads - 1 - tid; i < n_sp; i += kFinishThreads) spart += gsm::js_exp(key_f64(S.sp_key[GS_CK(i, GS_LEN(S.sp_key))]) - M);
-    block_sum2_f64(part, spart, S.wsum2, &t_chunks, &t_sp);
+    for (int i = kFinishThreads - 1 - tid; i < n_sp; i += kFinishThreads) spart += to_units(gsm::js_exp(key_f64(S.sp_key[GS_CK(i, GS_LEN(S.sp_key))]) - M), 1.0);
+    uint64_t sp_units;
+    block_sum_f64_u64(part, spart, S.wsum2, &t_chunks, &sp_units);
+    t_sp = (double)sp_units / kUnitScale;
     if (tid == 0) { S.total = t_chunks + t_sp; S.total_sp = t_sp; }
   }
   if (!(t_chunks + t_sp < __builtin_inf())) {
@@ -1870,7 +1890,7 @@ __device__ __forceinline__ uint32_t finish_row(const SampleArgs& a, FinishLds& U
     // the table exponential's table into LDS (the deep draw's copy, if any, is the same)
     if (tid < 256) S.tab[GS_CK(tid, GS_LEN(S.tab))] = c_exp2_256[tid];
     __syncthreads();
-    const double part = recompute_nonspecial_sum(a, row, cfg, constrained, M, n_sp, S.sp_id, S.wsum, S.tab);
+    const double part = recompute_nonspecial_sum(a, row, cfg, constrained, M, n_sp, S.sp_id, S.wsum2, S.tab);
     if (!(part >= 0)) return false;
     total = part + S.total_sp;
     margin = margin_fine;

@@ -246,3 +246,47 @@ def test_full_penalty_batch_mixed_routes_repeated(sampler, oracle):
         check_row(gs, "mixed routes", r, out.tokens[r], out.probabilities[r], out.flags[r], t, tr.probability)
     for r in force:
         assert out.flags[r] & gs.GS_FLAG_EXACT_PATH
+
+
+def test_results_identical_across_calls(sampler, synthetic_constraint):
+    """Every result is the same bit for bit on every call of the same batch:
+    the finish sums the specials (window and forced ids, which sit in LDS in
+    an order that atomics chose) as integers, and every other sum runs in a
+    fixed order. The full penalty batch (512-id windows on every row), a
+    constrained batch with windows and forced termination ids, and the
+    typical-p and full-draw workloads (the binary64 normaliser recompute and
+    the deep draws), each sampled 8 times."""
+    import torch
+
+    gs = _gs()
+    W = gs.workloads
+    batches = []
+    w = W.penalties()
+    conf = np.stack([gs.runtime.row_config(c, seed=sd) for c, sd in zip(w.configs, w.seeds)])
+    batches.append(("penalties", torch.from_numpy(w.logits).cuda(), conf, dict(histories=w.histories)))
+    offsets, data, nxt, finals, _ = synthetic_constraint
+    sampler.set_vocab(offsets, data)
+    sampler.set_dfa(nxt, finals)
+    table = sampler.build_masks(list(range(64)))
+    w = W.constrained(rows=list(range(0, 128, 2)))
+    cfgs = [c.merged(repetitionPenalty=1.3, repetitionWindow=256, presencePenalty=0.4) for c in w.configs]
+    hists = W.lmhead_histories(len(cfgs))
+    conf = np.stack([gs.runtime.row_config(c, seed=sd, mask_slot=int(st), accepting=bool(finals[st]))
+                     for c, sd, st in zip(cfgs, w.seeds, w.states)])
+    batches.append(("constrained", torch.from_numpy(w.logits).cuda(), conf,
+                    dict(histories=hists, forced=gs.constraint.forced_ids_csr(len(cfgs), (1, 50, 106)),
+                         mask_table=table)))
+    for name in ("typical", "multinomial"):
+        w = getattr(W, name)(rows=list(range(64)))
+        cfgs = [c.merged(repetitionPenalty=1.2, repetitionWindow=128) for c in w.configs]
+        hists = W.lmhead_histories(64)
+        conf = np.stack([gs.runtime.row_config(c, seed=sd) for c, sd in zip(cfgs, w.seeds)])
+        batches.append((name, torch.from_numpy(w.logits).cuda(), conf, dict(histories=hists)))
+    for name, x, conf, kw in batches:
+        first = sampler.sample(x, conf, raise_on_failure=False, **kw)
+        for k in range(7):
+            out = sampler.sample(x, conf, raise_on_failure=False, **kw)
+            assert np.array_equal(out.tokens, first.tokens), (name, k)
+            assert np.array_equal(out.flags, first.flags), (name, k)
+            same = out.probabilities.view(np.uint64) == first.probabilities.view(np.uint64)
+            assert same.all(), (name, k, np.nonzero(~same)[0][:8])
