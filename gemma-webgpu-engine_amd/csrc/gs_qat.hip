@@ -56,9 +56,13 @@ struct QatArgs {
 
 __device__ __forceinline__ double srq(double v, double s) {
   if (s == 0) return v;
-  // + 0.0 turns a -0 from rint into +0, as the reference's floor-based
-  // rounding returns for ratios in [-1/2, 0)
-  double q = __builtin_rint(v / s) + 0.0;
+  // the reference's floor-based rounding (qat-linear.ts:142-148) returns +0
+  // for ratios in [-1/2, 0), where rint gives -0, and keeps a ratio of -0
+  // (floor(-0) is -0): a zero from rint becomes the ratio itself when that
+  // is a zero, else +0
+  const double r = v / s;
+  double q = __builtin_rint(r);
+  if (q == 0.0) q = r == 0.0 ? r : 0.0;
   q = q < -128.0 ? -128.0 : (q > 127.0 ? 127.0 : q);
   return (double)(float)(q * s);
 }

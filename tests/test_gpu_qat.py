@@ -134,3 +134,39 @@ def test_fused_head_and_sampler(gemma_head):
             assert int(out.tokens[m]) == t
     finally:
         s.close()
+
+
+def test_signed_zero_logits():
+    """Rows whose scale is 0 turn a negative dot into -0, and the output SRQ
+    keeps a -0 ratio as -0 while ratios in [-1/2, 0) round to +0
+    (qat-linear.ts:120-148); activations of -0 beside +0: every logit's bits,
+    sign of zero included, equal cpuQatLinear's, on both layouts."""
+    import torch
+
+    gs = _gs()
+    rng = np.random.default_rng(23)
+    V, D = 100, 1536
+    codes = rng.integers(0, 4, V * D, dtype=np.uint8)
+    words = oracle.pack_int2_rows(codes, V, D)
+    scales = rng.uniform(0.0005, 0.005, V).astype(np.float32)
+    scales[::7] = 0.0
+    x = rng.normal(0, 1.0, (4, D)).astype(np.float32)
+    x[1, ::3] = np.float32(-0.0)
+    x[2] = np.float32(-0.0)
+    s = gs.Sampler(vocab_size=V, max_rows=4)
+    try:
+        sc = torch.from_numpy(scales).cuda()
+        xs = torch.from_numpy(x).cuda()
+        row = torch.from_numpy(words.view(np.int32)).cuda()
+        block = torch.from_numpy(oracle.repack_block_major(words, V, D).view(np.int32)).cuda()
+        for in_s, out_s in ((0.0, 0.02), (0.03, 0.125), (0.0, 0.0)):
+            in_s, out_s = float(np.float32(in_s)), float(np.float32(out_s))
+            want = np.stack([oracle.qat_linear_int2(x[m], words, scales, D, V, in_s, out_s) for m in range(4)])
+            if out_s:
+                assert np.any(np.signbit(want) & (want == 0)) and np.any(~np.signbit(want) & (want == 0))
+            for layout, cw in ((gs.runtime.GS_QAT_ROW_MAJOR, row), (gs.runtime.GS_QAT_BLOCK_MAJOR, block)):
+                got = s.qat_lmhead(xs, cw, sc, layout=layout, input_scale=in_s, output_scale=out_s).cpu().numpy()
+                bad = np.nonzero(got.view(np.uint32) != want.view(np.uint32))
+                assert bad[0].size == 0, (in_s, out_s, layout, bad[0][:5], bad[1][:5], got[bad][:5], want[bad][:5])
+    finally:
+        s.close()

@@ -37,6 +37,26 @@ def test_srq_ties_to_even_and_clamp():
     assert oracle.apply_srq(0.31, 0.1) == float(np.float32(3 * 0.1))
 
 
+def test_srq_signed_zeros():
+    """roundTiesToEven (qat-linear.ts:142-148) is floor-based: a ratio in
+    [-1/2, 0) gives floor -1 plus 1, which is +0, and a ratio of -0 gives
+    floor(-0), which is -0 (then -0 times the scale stays -0); Math.min and
+    Math.max keep -0 against 127 and -128."""
+    def sign_bit(v):
+        return np.signbit(np.float64(v))
+
+    for v, neg in ((-0.0, True), (0.0, False), (-0.3, False), (-0.5, False), (-0.49, False), (0.4, False),
+                   (-0.51, True), (-1e-300, False)):
+        out = oracle.apply_srq(v, 1.0)
+        assert (out == 0.0) == (abs(v) <= 0.5), (v, out)
+        assert sign_bit(out) == neg, (v, out)
+    # a whole row: scale 0 turns a negative dot into -0, which the output SRQ keeps
+    x = np.ones(16, np.float32)
+    codes = [0] * 16  # every weight -2: dot = -32
+    out = oracle.qat_linear_int2(x, oracle.pack_int2_rows(codes, 1, 16), [0.0], 16, 1, 0.0, 0.02)
+    assert out[0] == 0.0 and np.signbit(out[0])
+
+
 def test_rejects_invalid_codes_and_shapes():
     with pytest.raises(ValueError, match="Int2 codes must be between 0 and 3"):
         oracle.pack_int2_rows([4] + [0] * 15, 1, 16)
