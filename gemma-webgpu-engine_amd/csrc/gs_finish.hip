@@ -1233,6 +1233,20 @@ __device__ double recompute_nonspecial_sum(const SampleArgs& a, int64_t row, con
   // unconstrained rows: every id, four 16-byte loads per thread in flight
   // (visit_row); the sum keeps each thread's order
   if (!mrow) visit_row<4>(a, row, cfg.softcap, [&](float l, uint32_t) { all += term_of_capped(l); });
+  // the allowed specials' raw terms (at most kSpecialCap of them, so kSpPer
+  // per thread), loaded before the row's sum is reduced
+  constexpr int kSpPer = kSpecialCap / kFinishThreads;
+  static_assert(kSpecialCap % kFinishThreads == 0, "whole specials per thread");
+  double tsp[kSpPer];
+#pragma unroll
+  for (int k = 0; k < kSpPer; ++k) {
+    const int i = tid + k * kFinishThreads;
+    tsp[k] = 0.0;
+    if (i < n_sp) {
+      const uint32_t id = sp_id[i];
+      if (!mrow || ((mrow[id >> 5] >> (id & 31)) & 1u)) tsp[k] = term(load_logit(a, row, id));
+    }
+  }
   double t_all;
   block_scan_f64(all, s_w, &t_all);
   if (!(t_all < __builtin_inf() && t_all > 0.0)) return -1.0;
@@ -1242,11 +1256,9 @@ __device__ double recompute_nonspecial_sum(const SampleArgs& a, int64_t row, con
   // a term above t_all / 2 is counted apart
   const double inv = 1.0 / t_all;
   uint64_t su = 0ull, big = 0ull;
-  for (int i = tid; i < n_sp; i += kFinishThreads) {
-    const uint32_t id = sp_id[i];
-    if (mrow && !((mrow[id >> 5] >> (id & 31)) & 1u)) continue;
-    const double t = term(load_logit(a, row, id));
-    if (t <= 0.5 * t_all) su += to_units(t, inv);
+#pragma unroll
+  for (int k = 0; k < kSpPer; ++k) {
+    if (tsp[k] <= 0.5 * t_all) su += to_units(tsp[k], inv);
     else big = 1ull;
   }
   uint64_t su_all, big_all;
