@@ -25,7 +25,7 @@ VOCABS = [700, 3000, 5000, 8192, 8269, 16384, 20000, 32768, 40000, 65549, 100000
 ROWS = [1, 2, 3, 4, 5, 8, 17, 32, 64]
 
 
-def _batch(gs, oracle, seed):
+def _batch(gs, oracle, seed, extreme=False):
     W = gs.workloads
     rng = np.random.default_rng(seed)
     V = int(rng.choice(VOCABS))
@@ -36,7 +36,8 @@ def _batch(gs, oracle, seed):
     cap = 30.0 if rng.random() < 0.15 else 0.0
     xs, hists, cfgs, us = [], [], [], []
     for _ in range(R):
-        x = rng.normal(0, rng.uniform(0.3, 5.0), V).astype(np.float32)
+        sigma = float(rng.choice([1e-3, 0.3, 5.0, 50.0, 3e3])) if extreme else rng.uniform(0.3, 5.0)
+        x = rng.normal(0, sigma, V).astype(np.float32)
         q = rng.random()
         if q < 0.15:
             x = (np.round(x * 4) / 4).astype(np.float32)
@@ -49,6 +50,20 @@ def _batch(gs, oracle, seed):
         xs.append(x)
         hists.append(rng.integers(-2, V + 2, int(rng.integers(0, 120))).tolist())
         full = rng.random() < 0.4
+        if extreme:
+            # the far ends of every option the reference accepts (decoding.ts:31-55)
+            cfgs.append(gs.DecodingConfig(
+                temperature=float(rng.choice([0.0, 1e-3, 0.05, 0.7, 20.0, 1e3])),
+                topK=0 if full else int(rng.choice([0, 1, 2, 63, 64, 4096, 4097, 100000])),
+                topP=1.0 if full else float(rng.choice([1.0, 0.999999999, 0.5, 1e-9])),
+                minP=0.0 if full else float(rng.choice([0.0, 1e-9, 0.5, 0.99])),
+                typicalP=1.0 if full else float(rng.choice([1.0, 1.0, 0.999, 0.01])),
+                repetitionPenalty=float(rng.choice([1.0, 0.5, 5.0])),
+                repetitionWindow=int(rng.choice([0, 1, 1000])),
+                frequencyPenalty=float(rng.choice([0.0, 10.0, 0.001])),
+                presencePenalty=float(rng.choice([0.0, 10.0, 1e-6]))))
+            us.append(float(rng.random()) if rng.random() < 0.8 else float(rng.choice([0.0, 1 - 2 ** -32, 0.999])))
+            continue
         cfgs.append(gs.DecodingConfig(
             temperature=float(rng.choice([0.0, 0.3, 0.7, 1.0, 1.0, 1.5])),
             topK=0 if full else int(rng.choice([0, 1, 5, 40, 64, 65, 300, 2000])),
@@ -127,7 +142,13 @@ def _ocfg(c):
                     frequencyPenalty=c.frequencyPenalty, presencePenalty=c.presencePenalty)
 
 
-def test_random_sweep_matches_oracle(oracle):
+@pytest.mark.parametrize("extreme,n_batches,seed0", [(False, 300, 900000), (True, 100, 950000)])
+def test_random_sweep_matches_oracle(oracle, extreme, n_batches, seed0):
+    """300 batches of the settings above; 100 more at the far ends of every
+    option: temperatures 1e-3 to 1e3, logit spreads 1e-3 to 3e3, topK up to
+    100000, topP 1e-9 and 1 - 1e-9, minP 0.99, typicalP 0.01, repetition
+    penalties 0.5 and 5, presence and frequency penalties of 10, windows of 1
+    and 1000 ids."""
     import torch
 
     import gsample as gs
@@ -136,8 +157,8 @@ def test_random_sweep_matches_oracle(oracle):
     bad = []
     n_rows = 0
     try:
-        for seed in range(300):
-            V, R, X, bits, vals, hists, cfgs, us, words, forced, dead, conf = _batch(gs, oracle, 900000 + seed)
+        for seed in range(seed0, seed0 + n_batches):
+            V, R, X, bits, vals, hists, cfgs, us, words, forced, dead, conf = _batch(gs, oracle, seed, extreme)
             if V not in samplers:
                 samplers[V] = gs.Sampler(vocab_size=V, max_rows=64)
             s = samplers[V]
@@ -153,7 +174,7 @@ def test_random_sweep_matches_oracle(oracle):
                     # no legal id and no legal termination id: the reference throws
                     for tag, out in outs.items():
                         if not int(out.flags[r]) & gs.GS_FLAG_DEAD_END:
-                            bad.append(f"seed {900000 + seed} row {r} {tag}: flags {int(out.flags[r])}, no dead end")
+                            bad.append(f"seed {seed} row {r} {tag}: flags {int(out.flags[r])}, no dead end")
                     continue
                 t, tr = oracle.sample_token(vals[r], hists[r], _ocfg(cfgs[r]), us[r])
                 p = tr.probability if t >= 0 else 0.0
@@ -169,11 +190,11 @@ def test_random_sweep_matches_oracle(oracle):
                             else:
                                 ok = abs(pr - p) <= PROB_RTOL * abs(p)
                     if not ok:
-                        bad.append(f"seed {900000 + seed} V {V} row {r} slot {int(conf[r]['mask_slot'])} {tag}: {tok} (flags {fl}, "
+                        bad.append(f"seed {seed} V {V} row {r} slot {int(conf[r]['mask_slot'])} {tag}: {tok} (flags {fl}, "
                                    f"p {pr}) != {t} (p {p}); {cfgs[r]} u {us[r]}")
             n_rows += R
     finally:
         for s in samplers.values():
             s.close()
     assert not bad, "\n".join(bad[:20])
-    assert n_rows > 2000, n_rows
+    assert n_rows > 6 * n_batches, n_rows
