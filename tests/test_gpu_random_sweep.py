@@ -5,7 +5,8 @@ few huge logits, penalty windows with out-of-range ids, every filter
 (top-k, min-p, typical-p, top-p, full-vocabulary draws, greedy), uniforms at
 0 and near 1 or seeded draws at a draw index, forced exact replays, and mask
 tables of one to three slots with 0.1% to 50% legal ids, with termination and
-extra ids on some (gemma-session.ts:1305-1329, dead ends included). Each batch
+extra ids on some (gemma-session.ts:1305-1329, dead ends included), and rows
+padded past V with NaN and +inf that no kernel may read. Each batch
 runs with the batch hint (deep draws over many workgroups) and without it;
 every row's id must be the oracle's (sampling.ts:18-65,
 constraints.ts:159-173), with probabilities as in the other parity tests. A
@@ -133,7 +134,28 @@ def _batch(gs, oracle, seed, extreme=False):
                                            seed=seeds[r] if seeded[r] else None, draw_index=didx[r] if seeded[r] else 0,
                                            softcap_value=cap, mask_slot=slots[r], accepting=accepting[r],
                                            force_exact=fexact[r]))
-    return V, R, X, bits, vals, hists, cfgs, us, words, forced, dead, np.stack(confs)
+    # padded rows on some batches (a row stride past V; NaN and +inf in the padding, which no kernel
+    # may read)
+    pad = int(rng.choice([1, 3, 64])) if rng.random() < 0.2 else 0
+    return V, R, X, bits, vals, hists, cfgs, us, words, forced, dead, np.stack(confs), pad
+
+
+def _device_rows(torch, X, bits, pad):
+    """The batch's logits on the device, in rows of V + pad elements when pad > 0."""
+    R, V = X.shape
+    if bits is not None:
+        if not pad:
+            return torch.from_numpy(bits.view(np.int16)).cuda().view(torch.bfloat16)
+        buf = np.zeros((R, V + pad), np.uint16)
+        buf[:, V:] = np.where(np.arange(pad) % 2 == 0, 0x7FC0, 0x7F80).astype(np.uint16)
+        buf[:, :V] = bits
+        return torch.from_numpy(buf.view(np.int16)).cuda().view(torch.bfloat16)[:, :V]
+    if not pad:
+        return torch.from_numpy(X).cuda()
+    buf = np.zeros((R, V + pad), np.float32)
+    buf[:, V:] = np.where(np.arange(pad) % 2 == 0, np.nan, np.inf).astype(np.float32)
+    buf[:, :V] = X
+    return torch.from_numpy(buf).cuda()[:, :V]
 
 
 def _ocfg(c):
@@ -158,12 +180,11 @@ def test_random_sweep_matches_oracle(oracle, extreme, n_batches, seed0):
     n_rows = 0
     try:
         for seed in range(seed0, seed0 + n_batches):
-            V, R, X, bits, vals, hists, cfgs, us, words, forced, dead, conf = _batch(gs, oracle, seed, extreme)
+            V, R, X, bits, vals, hists, cfgs, us, words, forced, dead, conf, pad = _batch(gs, oracle, seed, extreme)
             if V not in samplers:
                 samplers[V] = gs.Sampler(vocab_size=V, max_rows=64)
             s = samplers[V]
-            dev = (torch.from_numpy(bits.view(np.int16)).cuda().view(torch.bfloat16) if bits is not None
-                   else torch.from_numpy(X).cuda())
+            dev = _device_rows(torch, X, bits, pad)
             table = torch.from_numpy(words.view(np.int32)).cuda() if words is not None else None
             outs = {"hint": s.sample(dev, conf, histories=hists, forced=forced, mask_table=table,
                                      raise_on_failure=False),
