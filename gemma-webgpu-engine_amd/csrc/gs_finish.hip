@@ -921,18 +921,27 @@ __device__ __forceinline__ int filters_and_draw_wave(const SampleArgs& a, int64_
       *exact_flags = 0u;
       return 3;
     }
-    double sp[kPerLane];
+    // signed surprises a = -ln p - H (the surprise is |a|), kept in aux
+    double sa[kPerLane], sp[kPerLane];
 #pragma unroll
     for (int q = 0; q < kPerLane; ++q) {
       const int i = lane * kPerLane + q;
-      sp[q] = kept[q] ? __builtin_fabs(-gsm::js_log(pl[q]) - H) : __builtin_inf();
-      if (i < 128) aux[i] = sp[q];
+      sa[q] = kept[q] ? -gsm::js_log(pl[q]) - H : __builtin_inf();
+      sp[q] = __builtin_fabs(sa[q]);
+      if (i < 128) aux[i] = sa[q];
     }
     __builtin_amdgcn_wave_barrier();
-    // The surprises carry the normaliser's error twice (through ln p and
-    // through H): |ds| <= margin (H + 2). Two items of different value
-    // whose surprises lie within twice that may be ordered either way.
-    const double ms = 2.0 * margin * (H + 2.0) + 1e-13 * (H + 1.0);
+    // The reference's signed surprises are ours shifted by one amount common
+    // to every item: with its normaliser Z and ours Z (1 + e), every ln p
+    // moves by -ln(1 + e) and H by about e (S - H), S the pool's mass, so
+    // every a moves by about e (H + 1 - S): |shift| <= margin (H + 2). Each
+    // item also carries its own rounding, rt. Two items on the same side of the entropy (a of one sign), both
+    // clear of the shift, keep their order whatever the shift: only rounding
+    // can swap them. Items on opposite sides, or near the entropy, can swap
+    // when their surprises lie within twice the shift.
+    const double rt = 1e-13 * (H + 1.0);
+    const double shift = margin * (H + 2.0) + rt;
+    const double ms = 2.0 * margin * (H + 2.0) + rt;
     int rank[kPerLane];
     bool amb = false;
 #pragma unroll
@@ -940,10 +949,12 @@ __device__ __forceinline__ int filters_and_draw_wave(const SampleArgs& a, int64_
       const int i = lane * kPerLane + q;
       int r = 0;
       for (int j = 0; j < n; ++j) {
-        const double sj = aux[j];
+        const double aj = aux[j];
+        const double sj = __builtin_fabs(aj);
         r += (sj < sp[q] || (sj == sp[q] && j < i)) ? 1 : 0;
         const double d = sj >= sp[q] ? sj - sp[q] : sp[q] - sj;
-        if (kept[q] && j != i && sj != sp[q] && d <= ms) amb = true;
+        const bool same_side = (aj < 0.0) == (sa[q] < 0.0) && sj > shift && sp[q] > shift;
+        if (kept[q] && j != i && sj != sp[q] && d <= (same_side ? 2.0 * rt : ms)) amb = true;
       }
       rank[q] = r;
     }

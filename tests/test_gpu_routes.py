@@ -312,6 +312,23 @@ def test_typical_p_with_top_k(sampler, oracle):
     assert exact <= 4, exact
 
 
+def test_typical_workload_matches_oracle(sampler, oracle):
+    """The typical workload's 256 rows (topK 40, typicalP 0.9) against the
+    oracle. Row 180 holds two items on the same side of the entropy whose
+    surprises lie within the normaliser's margin of each other: their order
+    does not depend on the normaliser (a common shift of every signed
+    surprise), so the row is settled without the binary64 recompute."""
+    import torch
+
+    gs = _gs()
+    w = gs.workloads.typical()
+    conf = np.stack([gs.runtime.row_config(c, seed=sd) for c, sd in zip(w.configs, w.seeds)])
+    out = sampler.sample(torch.from_numpy(w.logits).cuda(), conf)
+    us = [oracle.draw(sd, 0) for sd in w.seeds]
+    exact = check(gs, oracle, "typical workload", out, w.logits, None, w.configs, us)
+    assert exact == 0, exact
+
+
 def test_typical_p_ties_and_small_pools(oracle):
     """typical-p on small vocabularies with repeated values (equal surprises,
     stable order) and a pool of one, against the oracle."""
