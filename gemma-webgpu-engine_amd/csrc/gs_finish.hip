@@ -938,7 +938,11 @@ __device__ __forceinline__ int filters_and_draw_wave(const SampleArgs& a, int64_
     // item also carries its own rounding, rt. Two items on the same side of the entropy (a of one sign), both
     // clear of the shift, keep their order whatever the shift: only rounding
     // can swap them. Items on opposite sides, or near the entropy, can swap
-    // when their surprises lie within twice the shift.
+    // when their surprises lie within twice the shift. Only equal signed
+    // surprises are a tie in the reference too (equal probabilities: the same
+    // exponential over one normaliser), kept in list order; equal surprises of
+    // opposite sign move apart under any shift, so they count as ambiguous
+    // like any other pair within twice the shift.
     const double rt = 1e-13 * (H + 1.0);
     const double shift = margin * (H + 2.0) + rt;
     const double ms = 2.0 * margin * (H + 2.0) + rt;
@@ -954,7 +958,7 @@ __device__ __forceinline__ int filters_and_draw_wave(const SampleArgs& a, int64_
         r += (sj < sp[q] || (sj == sp[q] && j < i)) ? 1 : 0;
         const double d = sj >= sp[q] ? sj - sp[q] : sp[q] - sj;
         const bool same_side = (aj < 0.0) == (sa[q] < 0.0) && sj > shift && sp[q] > shift;
-        if (kept[q] && j != i && sj != sp[q] && d <= (same_side ? 2.0 * rt : ms)) amb = true;
+        if (kept[q] && j != i && aj != sa[q] && d <= (same_side ? 2.0 * rt : ms)) amb = true;
       }
       rank[q] = r;
     }
