@@ -942,7 +942,11 @@ __device__ __forceinline__ int filters_and_draw_wave(const SampleArgs& a, int64_
     // surprises are a tie in the reference too (equal probabilities: the same
     // exponential over one normaliser), kept in list order; equal surprises of
     // opposite sign move apart under any shift, so they count as ambiguous
-    // like any other pair within twice the shift.
+    // like any other pair within twice the shift. rt needs to cover only items
+    // of probability >= margin (|a| <= 20 + H, a few 1e-15 of rounding each):
+    // a swap moves the kept set only across the cut, and a cut on an item of
+    // smaller probability leaves the cumulative mass within margin of
+    // typicalP, which the cut's own check below sends on.
     const double rt = 1e-13 * (H + 1.0);
     const double shift = margin * (H + 2.0) + rt;
     const double ms = 2.0 * margin * (H + 2.0) + rt;
