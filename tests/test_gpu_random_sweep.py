@@ -26,7 +26,7 @@ VOCABS = [700, 3000, 5000, 8192, 8269, 16384, 20000, 32768, 40000, 65549, 100000
 ROWS = [1, 2, 3, 4, 5, 8, 17, 32, 64]
 
 
-def _batch(gs, oracle, seed, extreme=False):
+def _batch(gs, oracle, seed, extreme=False, typical=False):
     W = gs.workloads
     rng = np.random.default_rng(seed)
     V = int(rng.choice(VOCABS))
@@ -39,7 +39,7 @@ def _batch(gs, oracle, seed, extreme=False):
     for _ in range(R):
         sigma = float(rng.choice([1e-3, 0.3, 5.0, 50.0, 3e3])) if extreme else rng.uniform(0.3, 5.0)
         x = rng.normal(0, sigma, V).astype(np.float32)
-        q = rng.random()
+        q = rng.random() * (0.5 if typical else 1.0)
         if q < 0.15:
             x = (np.round(x * 4) / 4).astype(np.float32)
         elif q < 0.25:
@@ -50,7 +50,20 @@ def _batch(gs, oracle, seed, extreme=False):
             x[rng.integers(0, V, 3)] = np.float32(rng.uniform(20, 60))
         xs.append(x)
         hists.append(rng.integers(-2, V + 2, int(rng.integers(0, 120))).tolist())
-        full = rng.random() < 0.4
+        full = rng.random() < 0.4 and not typical
+        if typical:
+            # typical-p on every row, half the rows on a 1/4 or 1/8 grid: exact
+            # and mirrored surprise ties (sampling.ts:49-55)
+            cfgs.append(gs.DecodingConfig(
+                temperature=float(rng.choice([0.3, 0.7, 1.0, 1.5, 3.0])),
+                topK=int(rng.choice([0, 3, 10, 40, 64, 100, 128, 300])),
+                topP=float(rng.choice([1.0, 1.0, 0.95, 0.5])),
+                minP=float(rng.choice([0.0, 0.0, 0.0, 0.05])),
+                typicalP=float(rng.choice([0.05, 0.2, 0.5, 0.8, 0.95, 0.999])),
+                repetitionPenalty=float(rng.choice([1.0, 1.1])),
+                repetitionWindow=int(rng.choice([0, 64]))))
+            us.append(float(rng.random()) if rng.random() < 0.8 else float(rng.choice([0.0, 1 - 2 ** -32, 0.999])))
+            continue
         if extreme:
             # the far ends of every option the reference accepts (decoding.ts:31-55)
             cfgs.append(gs.DecodingConfig(
@@ -164,13 +177,16 @@ def _ocfg(c):
                     frequencyPenalty=c.frequencyPenalty, presencePenalty=c.presencePenalty)
 
 
-@pytest.mark.parametrize("extreme,n_batches,seed0", [(False, 300, 900000), (True, 100, 950000)])
-def test_random_sweep_matches_oracle(oracle, extreme, n_batches, seed0):
+@pytest.mark.parametrize("extreme,typical,n_batches,seed0",
+                         [(False, False, 300, 900000), (True, False, 100, 950000), (False, True, 150, 1200000)])
+def test_random_sweep_matches_oracle(oracle, extreme, typical, n_batches, seed0):
     """300 batches of the settings above; 100 more at the far ends of every
     option: temperatures 1e-3 to 1e3, logit spreads 1e-3 to 3e3, topK up to
     100000, topP 1e-9 and 1 - 1e-9, minP 0.99, typicalP 0.01, repetition
     penalties 0.5 and 5, presence and frequency penalties of 10, windows of 1
-    and 1000 ids."""
+    and 1000 ids; 150 with typical-p (0.05 to 0.999) on every row and half the
+    rows' logits on a grid, so that surprises tie, exactly or mirrored about
+    the entropy."""
     import torch
 
     import gsample as gs
@@ -180,7 +196,7 @@ def test_random_sweep_matches_oracle(oracle, extreme, n_batches, seed0):
     n_rows = 0
     try:
         for seed in range(seed0, seed0 + n_batches):
-            V, R, X, bits, vals, hists, cfgs, us, words, forced, dead, conf, pad = _batch(gs, oracle, seed, extreme)
+            V, R, X, bits, vals, hists, cfgs, us, words, forced, dead, conf, pad = _batch(gs, oracle, seed, extreme, typical)
             if V not in samplers:
                 samplers[V] = gs.Sampler(vocab_size=V, max_rows=64)
             s = samplers[V]
