@@ -7,8 +7,8 @@ A child process loads the checked build (GSAMPLE_CHECKED=1; this process
 already holds the normal one) and samples the batches that exercise the
 finish's routes: the penalties batch (top-k / top-p, greedy, forced exact
 rows), full-vocabulary draws taken by the deep kernels, top-k past 64,
-typical-p, the constrained batch, heavy-tailed bf16 rows and full-vocabulary
-draws past small regions. No row may carry the flag, and every token,
+typical-p (also on a logit grid, where surprises tie), the constrained batch,
+heavy-tailed bf16 rows and full-vocabulary draws past small regions. No row may carry the flag, and every token,
 probability and flag must equal the normal build's on the same inputs.
 
 The checked build also delays wave 0 after every barrier of the finish and
@@ -73,6 +73,17 @@ hist = [rng.integers(0, Vs, 8).tolist() for _ in range(n)]
 conf = np.stack([gs.runtime.row_config(cfg, uniform=float(u)) for u in rng.uniform(0.3, 0.99, n)])
 run("small_region_multi", x, conf, histories=hist)
 run("small_region_single", x, conf, histories=hist, hints=0)
+s.close()
+# typical-p on every row, logits on a 1/4 grid: exact and mirrored surprise ties
+rng = np.random.default_rng(11)
+Vt, n = 40000, 64
+s = gs.Sampler(vocab_size=Vt, max_rows=n)
+xt = torch.from_numpy((np.round(rng.normal(0, 2.0, (n, Vt)) * 4) / 4).astype(np.float32)).cuda()
+conf = np.stack([gs.runtime.row_config(gs.DecodingConfig(
+    temperature=float(rng.choice([0.7, 1.0, 1.5])), topK=int(rng.choice([0, 10, 64, 128, 300])), topP=1.0,
+    minP=0.0, typicalP=float(rng.choice([0.2, 0.5, 0.9, 0.999])), repetitionPenalty=1.0),
+    uniform=float(rng.random())) for _ in range(n)])
+run("typical_grid", xt, conf)
 s.close()
 with open(sys.argv[3], "w") as f:
     json.dump(out, f)
